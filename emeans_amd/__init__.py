@@ -1,0 +1,499 @@
+"""emeans on AMD Instinct MI355X (gfx950): the reference's Device / Assigner /
+Emeans / knn / dedup interfaces over hand-written HIP kernels.
+
+Mirrors, name for name, the Rust reference (samhvw8/emeans):
+  HipDevice            core::Device + Assigner   (crates/emeans-core/src/core/mod.rs:71-178,
+                                                   assign.rs:71-117)
+  EmaStep, Mat, Select core::EmaStep / Mat / Select (core/mod.rs:27-56, 180-197)
+  Config, Emeans       model.rs:24-76, 165-919 (train, assign, iteration_stats, ...)
+  knn_self, knn        emeans-cluster/src/knn.rs:17-64
+  dedup                emeans-cluster/src/dedup.rs:163-358
+  make_assigner        emeans-cluster/src/backend.rs:170-178 for the backend name "hip"
+
+Every computation runs on the GPU through libemeans_hip.so; nothing here
+falls back to a CPU path.
+"""
+
+import ctypes as C
+from dataclasses import dataclass, field
+from typing import List, Optional, Tuple
+
+import numpy as np
+
+from ._lib import (EMH_IP, EMH_L2, Config as _CConfig, EmeansHipError, EmeansHipInvalid,
+                   EpochStats as _CEpoch, TrainOut as _CTrainOut, check, lib)
+
+__all__ = [
+    "HipDevice", "DevBuf", "EmaStep", "Mat", "Select", "Config", "Emeans", "Trained",
+    "Assignment", "EpochStats", "Neighbors", "DedupConfig", "DedupResult", "knn_self", "knn",
+    "dedup", "make_assigner", "BACKEND_NAME", "EmeansHipError", "EmeansHipInvalid",
+    "GPU_KMAX", "NONE",
+]
+
+BACKEND_NAME = "hip"
+GPU_KMAX = 16          # emeans-core/src/knn.rs:16
+NONE = 0xFFFFFFFF      # emeans-core/src/knn.rs:19
+
+
+def _metric(m) -> int:
+    if m in ("l2", "L2", EMH_L2):
+        return EMH_L2
+    if m in ("ip", "inner_product", "InnerProduct", EMH_IP):
+        return EMH_IP
+    raise ValueError(f"unknown metric {m!r}")
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _u32(a):
+    return np.ascontiguousarray(a, dtype=np.uint32)
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+class DevBuf:
+    """A backend-owned device buffer (Device::F / Device::U)."""
+
+    __slots__ = ("_dev", "h", "kind")
+
+    def __init__(self, dev, h, kind):
+        self._dev, self.h, self.kind = dev, h, kind
+
+    def __len__(self):
+        return lib().emh_buf_len(self.h)
+
+    @property
+    def ptr(self):
+        return lib().emh_buf_ptr(self.h)
+
+    def __del__(self):
+        if getattr(self, "h", None) and self._dev is not None and self._dev._ctx:
+            lib().emh_free(self._dev._ctx, self.h)
+            self.h = None
+
+
+@dataclass
+class EmaStep:
+    """Scalars of one EMA step (core/mod.rs:182-197)."""
+    alpha: float
+    decay: float
+    replace: bool
+
+    @staticmethod
+    def new(alpha: float) -> "EmaStep":
+        return EmaStep(float(np.float32(alpha)), float(np.float32(1.0 - alpha)), alpha == 1.0)
+
+
+@dataclass
+class Mat:
+    """An n x d matrix on the device (core/mod.rs:30-34)."""
+    dev: DevBuf
+    d: int
+
+
+@dataclass
+class Select:
+    """Rows `rows` of a selection: x[ids[r]] when ids is given, else x[r] (core/mod.rs:44-47)."""
+    ids: Optional[DevBuf]
+    rows: Tuple[int, int]
+
+
+class HipDevice:
+    """The gfx950 backend: core::Device + Assigner over the C ABI."""
+
+    def __init__(self, device: int = 0):
+        h = C.c_void_p()
+        check(lib().emh_create(device, C.byref(h)))
+        self._ctx = h
+
+    def close(self):
+        if self._ctx:
+            lib().emh_destroy(self._ctx)
+            self._ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- Device::name, bind, upload, zeros, write, read, flush
+    def name(self) -> str:
+        return lib().emh_name(self._ctx).decode()
+
+    def _new(self, fn, *args, kind):
+        h = C.c_void_p()
+        check(fn(self._ctx, *args, C.byref(h)))
+        return DevBuf(self, h, kind)
+
+    def bind(self, x) -> DevBuf:
+        x = _f32(x)
+        return self._new(lib().emh_bind, _p(x), x.size, kind=0)
+
+    def upload_f32(self, v) -> DevBuf:
+        v = _f32(v)
+        return self._new(lib().emh_upload_f32, _p(v), v.size, kind=0)
+
+    def upload_u32(self, v) -> DevBuf:
+        v = _u32(v)
+        return self._new(lib().emh_upload_u32, _p(v), v.size, kind=1)
+
+    def zeros_f32(self, n: int) -> DevBuf:
+        return self._new(lib().emh_zeros_f32, n, kind=0)
+
+    def zeros_u32(self, n: int) -> DevBuf:
+        return self._new(lib().emh_zeros_u32, n, kind=1)
+
+    def write_f32(self, b: DevBuf, offset: int, v):
+        v = _f32(v)
+        check(lib().emh_write_f32(self._ctx, b.h, offset, _p(v), v.size))
+
+    def write_u32(self, b: DevBuf, offset: int, v):
+        v = _u32(v)
+        check(lib().emh_write_u32(self._ctx, b.h, offset, _p(v), v.size))
+
+    def read_f32(self, b: DevBuf, rng=None) -> np.ndarray:
+        lo, hi = rng if rng is not None else (0, len(b))
+        out = np.empty(max(hi - lo, 0), np.float32)
+        check(lib().emh_read_f32(self._ctx, b.h, lo, hi, _p(out)))
+        return out
+
+    def read_u32(self, b: DevBuf, rng=None) -> np.ndarray:
+        lo, hi = rng if rng is not None else (0, len(b))
+        out = np.empty(max(hi - lo, 0), np.uint32)
+        check(lib().emh_read_u32(self._ctx, b.h, lo, hi, _p(out)))
+        return out
+
+    def flush(self):
+        check(lib().emh_flush(self._ctx))
+
+    def sync(self):
+        check(lib().emh_sync(self._ctx))
+
+    def wrap(self, ptr: int, length: int, kind: int) -> DevBuf:
+        """A non-owning view of device memory (e.g. a torch tensor's data_ptr())."""
+        h = C.c_void_p()
+        check(lib().emh_wrap(self._ctx, C.c_void_p(ptr), length, kind, C.byref(h)))
+        return DevBuf(self, h, kind)
+
+    # -- Device ops
+    def top1(self, x: Mat, sel: Select, centroids: DevBuf, cnorm: Optional[DevBuf], k: int,
+             metric, labels: DevBuf, scores: DevBuf):
+        check(lib().emh_top1(self._ctx, x.dev.h, x.d, sel.ids.h if sel.ids else None,
+                             sel.rows[0], sel.rows[1], centroids.h, cnorm.h if cnorm else None,
+                             k, _metric(metric), labels.h, scores.h))
+
+    def topk(self, queries, data, d: int, kk: int, exclude_self: bool):
+        q, x = _f32(queries), _f32(data)
+        m, n = q.size // d, x.size // d
+        ids = np.empty(m * kk, np.uint32)
+        sims = np.empty(m * kk, np.float32)
+        same = queries is data
+        check(lib().emh_topk(self._ctx, _p(q), m, _p(q) if same else _p(x), n, d, kk,
+                             int(exclude_self), _p(ids), _p(sims)))
+        return ids, sims
+
+    def topk_dev(self, q: DevBuf, m: int, data: DevBuf, n: int, d: int, kk: int,
+                 exclude_self: bool, ids: DevBuf, sims: DevBuf):
+        check(lib().emh_topk_dev(self._ctx, q.h, m, data.h, n, d, kk, int(exclude_self),
+                                 ids.h, sims.h))
+
+    def scatter_add(self, x: Mat, sel: Select, labels: DevBuf, k: int, sums: DevBuf,
+                    counts: DevBuf, acc: Optional[DevBuf] = None):
+        check(lib().emh_scatter_add(self._ctx, x.dev.h, x.d, sel.ids.h if sel.ids else None,
+                                    sel.rows[0], sel.rows[1], labels.h, k, sums.h, counts.h,
+                                    acc.h if acc else None))
+
+    def row_norms(self, m: DevBuf, rows: int, d: int, out: DevBuf):
+        check(lib().emh_row_norms(self._ctx, m.h, rows, d, out.h))
+
+    def normalize_rows(self, src: DevBuf, rows: int, d: int, dst: DevBuf):
+        check(lib().emh_normalize_rows(self._ctx, src.h, rows, d, dst.h))
+
+    def split(self, positions: DevBuf, usage: DevBuf, plan: List[Tuple[int, int]], d: int):
+        pairs = _u32(np.asarray(plan, dtype=np.uint32).reshape(-1))
+        check(lib().emh_split(self._ctx, positions.h, usage.h, _p(pairs), len(plan), d))
+
+    def ema_update(self, positions: DevBuf, usage: DevBuf, sums: DevBuf, counts: DevBuf, k: int,
+                   d: int, step: EmaStep):
+        check(lib().emh_ema_update(self._ctx, positions.h, usage.h, sums.h, counts.h, k, d,
+                                   step.alpha, step.decay, int(step.replace)))
+
+    # -- Assigner::assign (assign_all over assign_on)
+    def assign(self, x, d: int, centroids, metric, chunk: int = 65536):
+        x, c = _f32(x), _f32(centroids)
+        n, k = x.size // d, c.size // d
+        labels = np.empty(n, np.uint32)
+        scores = np.empty(n, np.float32)
+        check(lib().emh_assign(self._ctx, _p(x), n, d, _p(c), k, _metric(metric), chunk,
+                               _p(labels), _p(scores)))
+        return labels, scores
+
+    def fallback_rows(self) -> int:
+        return lib().emh_fallback_rows(self._ctx)
+
+    def set_screen(self, on: bool):
+        check(lib().emh_set_screen(self._ctx, int(on)))
+
+
+def make_assigner(backend: str = BACKEND_NAME, device: int = 0) -> HipDevice:
+    """make_assigner(Backend::Custom{name: "hip"}) (backend.rs:170-178)."""
+    if backend != BACKEND_NAME:
+        raise ValueError(f"unknown backend {backend!r} (this package provides {BACKEND_NAME!r})")
+    return HipDevice(device)
+
+
+# ---------------------------------------------------------------------- model
+@dataclass
+class Config:
+    """Emeans constructor options (model.rs:24-76); faiss defaults."""
+    d: int
+    k: int
+    nepochs: float = 5.0
+    batch_size: Optional[int] = None
+    alpha0: Optional[float] = None
+    batch_law: str = "auto"
+    seed: int = 1234
+    spherical: bool = False
+    unused_threshold: Optional[float] = None
+    max_points_per_centroid: Optional[int] = None
+    assignment_chunk_size: Optional[int] = None
+    capture_assignments: bool = True
+    verbose: bool = False
+
+    def metric(self):
+        return "ip" if self.spherical else "l2"
+
+    def _c(self):
+        laws = {"auto": 0, "throughput": 1, "quality": 2}
+        if self.batch_law not in laws:
+            raise ValueError(f"unknown batch law {self.batch_law!r} (auto, throughput, quality)")
+        return _CConfig(self.k, self.d, float(self.nepochs), self.batch_size or 0,
+                        int(self.alpha0 is not None), float(self.alpha0 or 0.0),
+                        laws[self.batch_law], self.seed & 0xFFFFFFFF, int(self.spherical),
+                        int(self.unused_threshold is not None),
+                        float(self.unused_threshold or 0.0), self.assignment_chunk_size or 0,
+                        int(self.capture_assignments), int(self.verbose))
+
+
+@dataclass
+class EpochStats:
+    obj: float
+    time: float
+    imbalance_factor: float
+    nsplit: int
+
+
+@dataclass
+class Trained:
+    centroids: np.ndarray
+    labels: Optional[np.ndarray]
+
+
+@dataclass
+class Assignment:
+    labels: np.ndarray
+    scores: np.ndarray
+
+    def mean_objective(self, spherical: bool) -> float:
+        """Mean squared distance, or mean of 2 - 2 cos (model.rs:127-141)."""
+        s = self.scores.astype(np.float64)
+        v = 2.0 - 2.0 * s if spherical else s
+        return float(np.add.reduce(v, dtype=np.float64) / max(len(v), 1))
+
+
+class Emeans:
+    """faiss NumpyEmeans (model.rs) with the device loop on the gfx950 backend."""
+
+    def __init__(self, config: Config, assigner: Optional[HipDevice] = None):
+        if config.d <= 0 or config.k <= 0:
+            raise ValueError("d and k must be positive")
+        if not (np.isfinite(config.nepochs) and config.nepochs > 0):
+            raise ValueError("nepochs must be positive")
+        if config.max_points_per_centroid is not None and config.max_points_per_centroid < 1:
+            raise ValueError("max_points_per_centroid must be >= 1 or None")
+        if config.unused_threshold is not None and config.unused_threshold < 0:
+            raise ValueError("unused_threshold must be >= 0 (0 disables revival)")
+        self.config = config
+        self.dev = assigner or make_assigner()
+        self._centroids = None
+        self._positions = None
+        self._usage = None
+        self._stats: List[EpochStats] = []
+        self._n_splits = 0
+        self._recipe = {}
+        self.failed = False
+        self.fallback_rows = 0
+
+    def _require_ok(self):
+        if self.failed:
+            raise RuntimeError("create a new object after execution failure")
+
+    def training_subset(self, n: int):
+        """Sorted rows kept by max_points_per_centroid (model.rs:752-770)."""
+        m = self.config.max_points_per_centroid
+        if m is None or n <= m * self.config.k:
+            return None
+        keep = np.empty(n, np.uint32)
+        lib().emh_host_permutation((self.config.seed ^ 0x9E3779B9) & 0xFFFFFFFF, n, _p(keep))
+        return np.sort(keep[: m * self.config.k])
+
+    def train(self, x) -> Trained:
+        self._require_ok()
+        try:
+            return self._train(x)
+        except Exception:
+            self.failed = True
+            raise
+
+    def _train(self, x) -> Trained:
+        cfg = self.config
+        x = _f32(x).reshape(-1)
+        if x.size % cfg.d:
+            raise ValueError("x must be n x d")
+        n = x.size // cfg.d
+        keep = self.training_subset(n)
+        xs = x if keep is None else x.reshape(n, cfg.d)[keep].reshape(-1)
+        m = xs.size // cfg.d
+        k, d = cfg.k, cfg.d
+        cent = np.empty(k * d, np.float32)
+        pos = np.empty(k * d, np.float32)
+        usage = np.empty(k, np.float32)
+        labels = np.empty(m, np.int32)
+        stats = (_CEpoch * 64)()
+        out = _CTrainOut(_p(cent), _p(pos), _p(usage), _p(labels), C.addressof(stats), 64)
+        ccfg = cfg._c()
+        check(lib().emh_train(self.dev._ctx, _p(xs), m, C.byref(ccfg), C.byref(out)))
+        self._centroids, self._positions, self._usage = cent, pos, usage
+        self._stats = [EpochStats(stats[e].obj, stats[e].time, stats[e].imbalance_factor,
+                                  int(stats[e].nsplit)) for e in range(out.n_epochs)]
+        self._n_splits = int(out.n_splits)
+        self._recipe = {"batch_size": int(out.batch_size), "alpha0": out.alpha0,
+                        "total_steps": int(out.total_steps)}
+        self.fallback_rows = int(out.fallback_rows)
+        lab = labels if cfg.capture_assignments else None
+        if lab is not None and keep is not None:
+            full = np.full(n, -1, np.int32)
+            full[keep] = lab
+            lab = full
+        return Trained(cent.copy(), lab)
+
+    def assign(self, x) -> Assignment:
+        self._require_ok()
+        if self._centroids is None:
+            raise RuntimeError("model is not trained")
+        labels, scores = self.dev.assign(x, self.config.d, self._centroids, self.config.metric(),
+                                         self.config.assignment_chunk_size or 65536)
+        return Assignment(labels, scores)
+
+    def centroids(self):
+        return self._centroids
+
+    def ema_state(self):
+        return (self._positions, self._usage) if self._usage is not None else None
+
+    def iteration_stats(self):
+        return list(self._stats)
+
+    def obj(self):
+        return [s.obj for s in self._stats]
+
+    def n_splits(self):
+        return self._n_splits
+
+    def recipe(self):
+        return dict(self._recipe)
+
+
+# ------------------------------------------------------------------------ kNN
+@dataclass
+class Neighbors:
+    """k nearest rows per query, best first (emeans-core/src/knn.rs:21-45)."""
+    k: int
+    ids: np.ndarray
+    sims: np.ndarray
+
+    def __len__(self):
+        return self.ids.size // max(self.k, 1)
+
+    def row(self, i: int):
+        return self.ids[i * self.k:(i + 1) * self.k], self.sims[i * self.k:(i + 1) * self.k]
+
+
+def _search(queries, data, d, k, exclude_self, dev):
+    q, x = _f32(queries).reshape(-1), _f32(data).reshape(-1)
+    if d <= 0 or q.size % d or x.size % d:
+        raise ValueError("queries and data must be n x d")
+    if k <= 0:
+        raise ValueError("k must be positive")
+    if k > GPU_KMAX:
+        raise ValueError(f"the gfx950 top-k keeps at most {GPU_KMAX} neighbours")
+    dev = dev or make_assigner()
+    ids, sims = dev.topk(q, q if exclude_self else x, d, k, exclude_self)
+    return Neighbors(k, ids, sims)
+
+
+def knn_self(data, d: int, k: int, dev: Optional[HipDevice] = None) -> Neighbors:
+    """Neighbours of every row among the other rows (knn.rs:17-19)."""
+    return _search(data, data, d, k, True, dev)
+
+
+def knn(queries, data, d: int, k: int, dev: Optional[HipDevice] = None) -> Neighbors:
+    """Neighbours of every query among the data rows (knn.rs:22-30)."""
+    return _search(queries, data, d, k, False, dev)
+
+
+# ---------------------------------------------------------------------- dedup
+@dataclass
+class DedupConfig:
+    """dedup.rs:39-62 (time and burst inputs are not supported by this backend's host code)."""
+    k: int = 10
+    sim_threshold: float = 0.95
+    rep_threshold: Optional[float] = None
+
+
+@dataclass
+class DedupResult:
+    group_of: np.ndarray
+    representatives: np.ndarray
+    anchors: np.ndarray
+    sizes: np.ndarray
+    nn_sim: np.ndarray
+    linked_pairs: int
+    split_components: int
+
+    def n_groups(self):
+        return len(self.representatives)
+
+    def expand(self, rep_labels):
+        rep_labels = np.asarray(rep_labels)
+        assert len(rep_labels) == len(self.representatives)
+        return rep_labels[self.group_of]
+
+
+def dedup(x, d: int, cfg: DedupConfig = DedupConfig(), priority=None,
+          dev: Optional[HipDevice] = None) -> DedupResult:
+    """Near-duplicate groups of unit rows (dedup.rs:163-183): GPU kNN, host groups."""
+    x = _f32(x).reshape(-1)
+    if d <= 0 or x.size % d:
+        raise ValueError("x must be n x d")
+    if not (-1.0 <= cfg.sim_threshold <= 1.0):
+        raise ValueError("sim_threshold must be in [-1, 1]")
+    n = x.size // d
+    dev = dev or make_assigner()
+    pr = None if priority is None else _f32(priority)
+    g = np.zeros(n, np.uint32)
+    reps, anchors, sizes = (np.zeros(max(n, 1), np.uint32) for _ in range(3))
+    nn = np.zeros(n, np.float32)
+    ng, lp, sc = C.c_size_t(), C.c_size_t(), C.c_size_t()
+    rep_t = cfg.sim_threshold if cfg.rep_threshold is None else cfg.rep_threshold
+    check(lib().emh_dedup(dev._ctx, _p(x), n, d, cfg.k, cfg.sim_threshold, rep_t, _p(pr),
+                          _p(g), _p(reps), _p(anchors), _p(sizes), _p(nn), C.byref(ng),
+                          C.byref(lp), C.byref(sc)))
+    m = ng.value
+    return DedupResult(g, reps[:m].copy(), anchors[:m].copy(), sizes[:m].copy(), nn,
+                       lp.value, sc.value)

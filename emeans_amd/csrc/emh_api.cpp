@@ -1,0 +1,468 @@
+// The C ABI of layer 1 (include/emeans_hip.h): context, buffers and the
+// Device ops, each validated like the reference CPU backend
+// (crates/emeans-core/src/core/cpu.rs) before anything is queued.
+
+#include <cstring>
+#include <string>
+
+#include "emh_internal.h"
+
+namespace {
+thread_local std::string g_last_error;
+
+template <class F>
+int guard(F&& f) {
+  try {
+    f();
+    return EMH_OK;
+  } catch (const emh::Invalid& e) {
+    g_last_error = e.what();
+    return EMH_INVALID;
+  } catch (const std::exception& e) {
+    g_last_error = e.what();
+    return EMH_ERROR;
+  } catch (...) {
+    g_last_error = "unknown error";
+    return EMH_ERROR;
+  }
+}
+
+void use_device(emh_ctx* c) { EMH_HIP(hipSetDevice(c->device)); }
+
+emh_buf* new_buf(emh_ctx* c, size_t len, int kind) {
+  auto* b = new emh_buf;
+  b->len = len;
+  b->kind = kind;
+  if (len > 0) {
+    hipError_t e = hipMalloc(&b->ptr, len * 4);
+    if (e != hipSuccess) {
+      delete b;
+      char m[256];
+      snprintf(m, sizeof m, "hipMalloc of %zu bytes failed: %s", len * 4, hipGetErrorString(e));
+      throw emh::Failure(m);
+    }
+  }
+  (void)c;
+  return b;
+}
+
+const float* F(const emh_buf* b, const char* what) {
+  EMH_ENSURE(b && b->kind == 0, "%s must be an f32 buffer", what);
+  return (const float*)b->ptr;
+}
+float* Fm(emh_buf* b, const char* what) {
+  EMH_ENSURE(b && b->kind == 0, "%s must be an f32 buffer", what);
+  return (float*)b->ptr;
+}
+const uint32_t* U(const emh_buf* b, const char* what) {
+  EMH_ENSURE(b && b->kind == 1, "%s must be a u32 buffer", what);
+  return (const uint32_t*)b->ptr;
+}
+uint32_t* Um(emh_buf* b, const char* what) {
+  EMH_ENSURE(b && b->kind == 1, "%s must be a u32 buffer", what);
+  return (uint32_t*)b->ptr;
+}
+
+// Errors the kernels record on the device come up at the next wait.
+void check_device_flags(emh_ctx* c) {
+  uint32_t w[emh::SW_WORDS];
+  EMH_HIP(hipMemcpyAsync(w, c->small, sizeof w, hipMemcpyDeviceToHost, c->stream));
+  EMH_HIP(hipStreamSynchronize(c->stream));
+  bool bad_label = w[emh::SW_BAD_LABEL] != 0, bad_id = w[emh::SW_BAD_ID] != 0;
+  if (bad_label || bad_id) {
+    emh::launch_fill_u32(c, c->small + emh::SW_BAD_LABEL, 1, 0);
+    emh::launch_fill_u32(c, c->small + emh::SW_BAD_ID, 1, 0);
+    EMH_HIP(hipStreamSynchronize(c->stream));
+    EMH_ENSURE(!bad_label, "scatter_add: label out of range");
+    EMH_ENSURE(!bad_id, "row id out of range");
+  }
+}
+
+// core/mod.rs:432-439 (check_select).
+void check_select(const emh_buf* ids, size_t lo, size_t hi, size_t nx) {
+  EMH_ENSURE(lo <= hi, "bad row range");
+  if (ids)
+    EMH_ENSURE(hi <= ids->len, "row range past the ids");
+  else
+    EMH_ENSURE(hi <= nx, "row range past the data");
+}
+}  // namespace
+
+namespace emh {
+void set_last_error(const std::string& m) { g_last_error = m; }
+}  // namespace emh
+
+extern "C" {
+
+const char* emh_last_error(void) { return g_last_error.c_str(); }
+
+int emh_create(int device, emh_ctx** out) {
+  return guard([&] {
+    EMH_ENSURE(out != nullptr, "out is null");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0)
+      throw emh::Failure("no HIP device");
+    EMH_ENSURE(device >= 0 && device < n, "device %d not present (%d devices)", device, n);
+    EMH_HIP(hipSetDevice(device));
+    hipDeviceProp_t p;
+    EMH_HIP(hipGetDeviceProperties(&p, device));
+    if (std::strncmp(p.gcnArchName, "gfx950", 6) != 0) {
+      char m[256];
+      snprintf(m, sizeof m, "device %d is %s; this library is built for gfx950", device,
+               p.gcnArchName);
+      throw emh::Failure(m);
+    }
+    auto* c = new emh_ctx;
+    c->device = device;
+    c->cus = p.multiProcessorCount;
+    if (const char* s = getenv("EMEANS_HIP_SCREEN")) c->screen = atoi(s) != 0;
+    try {
+      EMH_HIP(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+      EMH_HIP(hipMalloc(&c->small, emh::SW_WORDS * 4));
+      EMH_HIP(hipMemsetAsync(c->small, 0, emh::SW_WORDS * 4, c->stream));
+      EMH_HIP(hipStreamSynchronize(c->stream));
+    } catch (...) {
+      if (c->small) (void)hipFree(c->small);
+      if (c->stream) (void)hipStreamDestroy(c->stream);
+      delete c;
+      throw;
+    }
+    *out = c;
+  });
+}
+
+int emh_destroy(emh_ctx* c) {
+  return guard([&] {
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->stream);
+    for (emh::Scratch* s : {&c->cand, &c->fblist, &c->order, &c->start, &c->misc, &c->knn_tmp})
+      s->release();
+    if (c->small) (void)hipFree(c->small);
+    (void)hipStreamDestroy(c->stream);
+    delete c;
+  });
+}
+
+const char* emh_name(const emh_ctx* c) { return c ? c->name.c_str() : "hip-gfx950"; }
+
+int emh_flush(emh_ctx* c) {
+  return guard([&] {
+    EMH_ENSURE(c, "null context");
+    (void)hipStreamQuery(c->stream);
+  });
+}
+
+int emh_sync(emh_ctx* c) {
+  return guard([&] {
+    EMH_ENSURE(c, "null context");
+    use_device(c);
+    check_device_flags(c);
+  });
+}
+
+void* emh_stream(emh_ctx* c) { return c ? (void*)c->stream : nullptr; }
+
+// ------------------------------------------------------------------ buffers
+static int upload(emh_ctx* c, const void* v, size_t len, int kind, emh_buf** out) {
+  return guard([&] {
+    EMH_ENSURE(c && out, "null argument");
+    EMH_ENSURE(len == 0 || v, "null source");
+    use_device(c);
+    emh_buf* b = new_buf(c, len, kind);
+    if (len > 0) {
+      hipError_t e = hipMemcpyAsync(b->ptr, v, len * 4, hipMemcpyHostToDevice, c->stream);
+      if (e == hipSuccess) e = hipStreamSynchronize(c->stream);  // the source may go away
+      if (e != hipSuccess) {
+        (void)hipFree(b->ptr);
+        delete b;
+        throw emh::Failure(std::string("upload failed: ") + hipGetErrorString(e));
+      }
+    }
+    *out = b;
+  });
+}
+
+int emh_bind(emh_ctx* c, const float* x, size_t len, emh_buf** out) {
+  return upload(c, x, len, 0, out);
+}
+int emh_upload_f32(emh_ctx* c, const float* v, size_t len, emh_buf** out) {
+  return upload(c, v, len, 0, out);
+}
+int emh_upload_u32(emh_ctx* c, const uint32_t* v, size_t len, emh_buf** out) {
+  return upload(c, v, len, 1, out);
+}
+
+static int zeros(emh_ctx* c, size_t len, int kind, emh_buf** out) {
+  return guard([&] {
+    EMH_ENSURE(c && out, "null argument");
+    use_device(c);
+    emh_buf* b = new_buf(c, len, kind);
+    if (len > 0) emh::launch_fill_u32(c, (uint32_t*)b->ptr, len, 0);
+    *out = b;
+  });
+}
+int emh_zeros_f32(emh_ctx* c, size_t len, emh_buf** out) { return zeros(c, len, 0, out); }
+int emh_zeros_u32(emh_ctx* c, size_t len, emh_buf** out) { return zeros(c, len, 1, out); }
+
+static int write(emh_ctx* c, emh_buf* b, size_t off, const void* v, size_t len, int kind) {
+  return guard([&] {
+    EMH_ENSURE(c && b && b->kind == kind, "buffer kind mismatch");
+    EMH_ENSURE(off + len <= b->len, "write past the buffer");
+    if (len == 0) return;
+    use_device(c);
+    EMH_HIP(hipMemcpyAsync((char*)b->ptr + off * 4, v, len * 4, hipMemcpyHostToDevice,
+                           c->stream));
+    EMH_HIP(hipStreamSynchronize(c->stream));
+  });
+}
+int emh_write_f32(emh_ctx* c, emh_buf* b, size_t off, const float* v, size_t len) {
+  return write(c, b, off, v, len, 0);
+}
+int emh_write_u32(emh_ctx* c, emh_buf* b, size_t off, const uint32_t* v, size_t len) {
+  return write(c, b, off, v, len, 1);
+}
+
+static int read(emh_ctx* c, const emh_buf* b, size_t lo, size_t hi, void* dst, int kind) {
+  return guard([&] {
+    EMH_ENSURE(c && b && b->kind == kind, "buffer kind mismatch");
+    EMH_ENSURE(lo <= hi && hi <= b->len, "read past the buffer");
+    use_device(c);
+    if (hi > lo)
+      EMH_HIP(hipMemcpyAsync(dst, (const char*)b->ptr + lo * 4, (hi - lo) * 4,
+                             hipMemcpyDeviceToHost, c->stream));
+    check_device_flags(c);  // waits
+  });
+}
+int emh_read_f32(emh_ctx* c, const emh_buf* b, size_t lo, size_t hi, float* dst) {
+  return read(c, b, lo, hi, dst, 0);
+}
+int emh_read_u32(emh_ctx* c, const emh_buf* b, size_t lo, size_t hi, uint32_t* dst) {
+  return read(c, b, lo, hi, dst, 1);
+}
+
+int emh_free(emh_ctx* c, emh_buf* b) {
+  return guard([&] {
+    if (!b) return;
+    if (c) {
+      use_device(c);
+      EMH_HIP(hipStreamSynchronize(c->stream));
+    }
+    if (b->owned && b->ptr) EMH_HIP(hipFree(b->ptr));
+    delete b;
+  });
+}
+
+int emh_wrap(emh_ctx* c, void* p, size_t len, int kind, emh_buf** out) {
+  return guard([&] {
+    EMH_ENSURE(c && out, "null argument");
+    EMH_ENSURE(kind == 0 || kind == 1, "kind must be 0 (f32) or 1 (u32)");
+    EMH_ENSURE(len == 0 || p, "null pointer");
+    auto* b = new emh_buf;
+    b->ptr = p;
+    b->len = len;
+    b->kind = kind;
+    b->owned = false;
+    *out = b;
+  });
+}
+
+void* emh_buf_ptr(const emh_buf* b) { return b ? b->ptr : nullptr; }
+size_t emh_buf_len(const emh_buf* b) { return b ? b->len : 0; }
+
+// ---------------------------------------------------------------------- ops
+int emh_top1(emh_ctx* c, const emh_buf* x, size_t d, const emh_buf* ids, size_t lo, size_t hi,
+             const emh_buf* cents, const emh_buf* cnorm, size_t k, int metric, emh_buf* labels,
+             emh_buf* scores) {
+  return guard([&] {
+    EMH_ENSURE(c, "null context");
+    EMH_ENSURE(d > 0, "d must be positive");
+    EMH_ENSURE(k > 0, "k must be positive");
+    EMH_ENSURE(metric == EMH_L2 || metric == EMH_IP, "unknown metric");
+    const float* xp = F(x, "x");
+    const size_t nx = x->len / d;
+    if (ids) U(ids, "ids");
+    check_select(ids, lo, hi, nx);
+    EMH_ENSURE(cents && F(cents, "centroids") && cents->len >= k * d, "centroids must be k x d");
+    const float* cn = nullptr;
+    if (metric == EMH_L2) {
+      EMH_ENSURE(cnorm != nullptr, "L2 top1 needs the centroid norms");
+      cn = F(cnorm, "cnorm");
+      EMH_ENSURE(cnorm->len >= k, "cnorm must have k entries");
+    }
+    uint32_t* lab = Um(labels, "labels");
+    float* sco = Fm(scores, "scores");
+    EMH_ENSURE(hi <= labels->len && hi <= scores->len, "outputs too short");
+    use_device(c);
+    emh::launch_top1(c, xp, nx, d, ids ? (const uint32_t*)ids->ptr : nullptr, lo, hi,
+                     (const float*)cents->ptr, cn, k, metric == EMH_IP, lab, sco);
+  });
+}
+
+int emh_topk_dev(emh_ctx* c, const emh_buf* q, size_t m, const emh_buf* data, size_t n, size_t d,
+                 size_t kk, int exclude_self, emh_buf* ids, emh_buf* sims) {
+  return guard([&] {
+    EMH_ENSURE(c, "null context");
+    EMH_ENSURE(d > 0, "d must be positive");
+    EMH_ENSURE(kk > 0, "k must be positive");
+    EMH_ENSURE(kk <= 16, "topk keeps at most 16 neighbours (knn.rs:16), got %zu", kk);
+    EMH_ENSURE(!exclude_self || m == n, "exclude_self needs queries == data");
+    const float* qp = F(q, "queries");
+    const float* dp = F(data, "data");
+    EMH_ENSURE(q->len >= m * d && data->len >= n * d, "queries m x d, data n x d");
+    uint32_t* ip = Um(ids, "ids");
+    float* sp = Fm(sims, "sims");
+    EMH_ENSURE(ids->len >= m * kk && sims->len >= m * kk, "outputs must hold m x k");
+    use_device(c);
+    emh::launch_topk(c, qp, m, dp, n, d, kk, exclude_self != 0, ip, sp);
+  });
+}
+
+int emh_topk(emh_ctx* c, const float* queries, size_t m, const float* data, size_t n, size_t d,
+             size_t kk, int exclude_self, uint32_t* ids, float* sims) {
+  return guard([&] {
+    EMH_ENSURE(c && (m == 0 || (queries && ids && sims)) && (n == 0 || data), "null argument");
+    EMH_ENSURE(d > 0 && kk > 0 && kk <= 16, "need d > 0 and 1 <= k <= 16");
+    EMH_ENSURE(!exclude_self || m == n, "exclude_self needs queries == data");
+    if (m == 0) return;
+    use_device(c);
+    const bool same = queries == data && m == n;
+    emh_buf *qb = nullptr, *db = nullptr, *ib = nullptr, *sb = nullptr;
+    auto cleanup = [&] {
+      for (emh_buf* b : {qb, db, ib, sb})
+        if (b && b != qb) emh_free(c, b);
+      if (qb) emh_free(c, qb);
+    };
+    try {
+      if (emh_upload_f32(c, queries, m * d, &qb)) throw emh::Failure(g_last_error);
+      if (same)
+        db = nullptr;
+      else if (emh_upload_f32(c, data, n * d, &db))
+        throw emh::Failure(g_last_error);
+      if (emh_zeros_u32(c, m * kk, &ib) || emh_zeros_f32(c, m * kk, &sb))
+        throw emh::Failure(g_last_error);
+      emh::launch_topk(c, (const float*)qb->ptr, m, same ? (const float*)qb->ptr
+                                                        : (const float*)db->ptr,
+                       n, d, kk, exclude_self != 0, (uint32_t*)ib->ptr, (float*)sb->ptr);
+      EMH_HIP(hipMemcpyAsync(ids, ib->ptr, m * kk * 4, hipMemcpyDeviceToHost, c->stream));
+      EMH_HIP(hipMemcpyAsync(sims, sb->ptr, m * kk * 4, hipMemcpyDeviceToHost, c->stream));
+      check_device_flags(c);
+    } catch (...) {
+      cleanup();
+      throw;
+    }
+    cleanup();
+  });
+}
+
+int emh_scatter_add(emh_ctx* c, const emh_buf* x, size_t d, const emh_buf* ids, size_t lo,
+                    size_t hi, const emh_buf* labels, size_t k, emh_buf* sums, emh_buf* counts,
+                    emh_buf* acc) {
+  return guard([&] {
+    EMH_ENSURE(c, "null context");
+    EMH_ENSURE(d > 0 && k > 0, "d and k must be positive");
+    const float* xp = F(x, "x");
+    const size_t nx = x->len / d;
+    if (ids) U(ids, "ids");
+    check_select(ids, lo, hi, nx);
+    const uint32_t* lab = U(labels, "labels");
+    EMH_ENSURE(hi <= labels->len, "labels shorter than the selection");
+    float* sp = Fm(sums, "sums");
+    uint32_t* cp = Um(counts, "counts");
+    EMH_ENSURE(sums->len == k * d && counts->len == k, "sums k x d, counts k");
+    float* ap = nullptr;
+    if (acc) {
+      ap = Fm(acc, "acc");
+      EMH_ENSURE(acc->len == k * d, "acc must be k x d");
+    }
+    use_device(c);
+    emh::launch_scatter(c, xp, nx, d, ids ? (const uint32_t*)ids->ptr : nullptr, lo, hi, lab, k,
+                        sp, cp, ap);
+  });
+}
+
+int emh_row_norms(emh_ctx* c, const emh_buf* m, size_t rows, size_t d, emh_buf* out) {
+  return guard([&] {
+    EMH_ENSURE(c && d > 0, "bad arguments");
+    const float* mp = F(m, "m");
+    float* op = Fm(out, "out");
+    EMH_ENSURE(m->len >= rows * d && out->len >= rows, "shapes");
+    use_device(c);
+    emh::launch_row_norms(c, mp, rows, d, op);
+  });
+}
+
+int emh_normalize_rows(emh_ctx* c, const emh_buf* src, size_t rows, size_t d, emh_buf* dst) {
+  return guard([&] {
+    EMH_ENSURE(c && d > 0, "bad arguments");
+    const float* sp = F(src, "src");
+    float* dp = Fm(dst, "dst");
+    EMH_ENSURE(src->len >= rows * d && dst->len >= rows * d, "shapes");
+    EMH_ENSURE(src->ptr != dst->ptr || rows == 0, "normalize_rows: src and dst must differ");
+    use_device(c);
+    emh::launch_normalize_rows(c, sp, rows, d, dp);
+  });
+}
+
+int emh_split(emh_ctx* c, emh_buf* positions, emh_buf* usage, const uint32_t* pairs,
+              size_t npairs, size_t d) {
+  return guard([&] {
+    EMH_ENSURE(c && d > 0, "bad arguments");
+    float* pp = Fm(positions, "positions");
+    float* up = Fm(usage, "usage");
+    const size_t k = usage->len;
+    EMH_ENSURE(positions->len == k * d, "positions must be k x d");
+    if (npairs == 0) return;
+    EMH_ENSURE(pairs != nullptr, "null plan");
+    std::vector<uint8_t> seen(k, 0);
+    bool independent = true;
+    for (size_t q = 0; q < npairs; q++) {
+      uint32_t s = pairs[2 * q], t = pairs[2 * q + 1];
+      EMH_ENSURE(s < k && t < k, "split ids out of range");
+      if (seen[s] || seen[t] || s == t) independent = false;
+      seen[s] = seen[t] = 1;
+    }
+    use_device(c);
+    uint32_t* pd = (uint32_t*)c->misc.get(npairs * 8);
+    EMH_HIP(hipMemcpyAsync(pd, pairs, npairs * 8, hipMemcpyHostToDevice, c->stream));
+    EMH_HIP(hipStreamSynchronize(c->stream));
+    emh::launch_split(c, pp, up, pd, npairs, d, independent);
+  });
+}
+
+int emh_ema_update(emh_ctx* c, emh_buf* positions, emh_buf* usage, const emh_buf* sums,
+                   const emh_buf* counts, size_t k, size_t d, float alpha, float decay,
+                   int replace) {
+  return guard([&] {
+    EMH_ENSURE(c && d > 0, "bad arguments");
+    float* pp = Fm(positions, "positions");
+    float* up = Fm(usage, "usage");
+    const float* sp = F(sums, "sums");
+    const uint32_t* cp = U(counts, "counts");
+    EMH_ENSURE(positions->len == k * d && usage->len == k && sums->len == k * d &&
+                   counts->len == k,
+               "shapes");
+    use_device(c);
+    emh::launch_ema(c, pp, up, sp, cp, k, d, alpha, decay, replace);
+  });
+}
+
+uint64_t emh_fallback_rows(emh_ctx* c) {
+  if (!c) return 0;
+  uint32_t v = 0;
+  if (hipSetDevice(c->device) != hipSuccess) return 0;
+  if (hipMemcpyAsync(&v, c->small + emh::SW_FALLBACK_TOTAL, 4, hipMemcpyDeviceToHost,
+                     c->stream) != hipSuccess)
+    return 0;
+  (void)hipStreamSynchronize(c->stream);
+  return v;
+}
+
+int emh_set_screen(emh_ctx* c, int on) {
+  return guard([&] {
+    EMH_ENSURE(c, "null context");
+    c->screen = on != 0;
+  });
+}
+
+}  // extern "C"

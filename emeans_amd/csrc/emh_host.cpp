@@ -1,0 +1,746 @@
+// Host side of the device loop and its callers, on the gfx950 context:
+//  - the seeded draws the reference keeps on the host: numpy-legacy MT19937
+//    (crates/emeans-core/src/rng.rs), the recipe and cosine schedule
+//    (recipe.rs), the revival plan (core/mod.rs:339-370) and closing means
+//    (core/mod.rs:404-429);
+//  - layer 2, core::train::run (core/train.rs:60-303) and Emeans::train
+//    (model.rs:700-811): every batch op queued on the context's stream, the
+//    host waiting only for the revival check (every 5 steps), the epoch's
+//    labels and scores, and the end; the next epoch's permutation and the
+//    epoch statistics run on helper threads;
+//  - assign_all / assign_on (assign.rs:785-809, core/mod.rs:249-330),
+//    knn_self / knn (emeans-cluster/src/knn.rs:17-64) and dedup
+//    (emeans-cluster/src/dedup.rs:163-358).
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <future>
+#include <map>
+#include <set>
+#include <string>
+#include <vector>
+
+#include "emh_internal.h"
+
+namespace emh {
+namespace host {
+
+// ------------------------------------------------------------------ MT19937
+class RandomState {  // rng.rs:13-102
+ public:
+  explicit RandomState(uint32_t seed) {
+    uint32_t s = seed;
+    for (int i = 0; i < N; i++) {
+      mt_[i] = s;
+      s = 1812433253u * (s ^ (s >> 30)) + (uint32_t)(i + 1);
+    }
+    pos_ = N;
+  }
+  uint32_t next_u32() {
+    if (pos_ == N) refill();
+    uint32_t y = mt_[pos_++];
+    y ^= y >> 11;
+    y ^= (y << 7) & 0x9d2c5680u;
+    y ^= (y << 15) & 0xefc60000u;
+    return y ^ (y >> 18);
+  }
+  double random_sample() {
+    uint32_t a = next_u32() >> 5, b = next_u32() >> 6;
+    return ((double)a * 67108864.0 + (double)b) / 9007199254740992.0;
+  }
+  // numpy legacy random_interval: masked rejection in [0, max].
+  uint64_t interval(uint64_t max) {
+    if (max == 0) return 0;
+    uint64_t mask = max;
+    mask |= mask >> 1;
+    mask |= mask >> 2;
+    mask |= mask >> 4;
+    mask |= mask >> 8;
+    mask |= mask >> 16;
+    mask |= mask >> 32;
+    for (;;) {
+      uint64_t v;
+      if (max <= 0xffffffffull) {
+        v = next_u32() & mask;
+      } else {
+        uint64_t hi = next_u32();
+        v = ((hi << 32) | next_u32()) & mask;
+      }
+      if (v <= max) return v;
+    }
+  }
+  std::vector<uint32_t> permutation(size_t n) {
+    std::vector<uint32_t> p(n);
+    for (size_t i = 0; i < n; i++) p[i] = (uint32_t)i;
+    for (size_t i = n; i > 1; i--) std::swap(p[i - 1], p[interval(i - 1)]);
+    return p;
+  }
+
+ private:
+  static constexpr int N = 624, M = 397;
+  void refill() {
+    for (int i = 0; i < N; i++) {
+      uint32_t y = (mt_[i] & 0x80000000u) | (mt_[(i + 1) % N] & 0x7fffffffu);
+      mt_[i] = mt_[(i + M) % N] ^ (y >> 1) ^ ((y & 1u) ? 0x9908b0dfu : 0u);
+    }
+    pos_ = 0;
+  }
+  uint32_t mt_[N];
+  int pos_;
+};
+
+// ------------------------------------------------------------------- recipe
+struct Recipe {
+  size_t batch_size = 0;
+  double alpha0 = 0;
+  std::vector<size_t> epoch_rows;
+  size_t total_steps = 0;
+  double tau = 0;
+  size_t chunk = 65536;
+};
+
+size_t pow2_round(double v) {  // recipe.rs:69-80
+  if (v <= 1.0) return 1;
+  double lo = std::ldexp(1.0, (int)std::floor(std::log2(v)));
+  return (size_t)(v / lo < (2.0 * lo) / v ? lo : 2.0 * lo);
+}
+
+Recipe resolve(size_t n, size_t k, size_t d, const emh_config& cfg) {  // recipe.rs:200-254
+  Recipe r;
+  int law = cfg.batch_law;
+  if (law == 0) law = d <= 16 ? 2 : 1;  // auto: quality at d <= 16
+  const double T = cfg.nepochs;
+  size_t b;
+  if (cfg.batch_size > 0) {
+    b = std::min((size_t)cfg.batch_size, n);
+  } else {
+    const double cb = law == 1 ? 0.035134 : 0.00439175;
+    const double raw = cb * std::pow((double)k, 0.134749) * std::pow((double)n, 0.876473) *
+                       std::pow(T, 0.813344);
+    b = pow2_round(raw);
+    b = law == 1 ? std::min(b, pow2_round((double)n / 2.0)) : std::min(b, n / 2);
+    b = std::max<size_t>(std::min(b, n), 1);
+  }
+  r.batch_size = b;
+  if (cfg.has_alpha0) {
+    r.alpha0 = cfg.alpha0;
+  } else {
+    double a = 0.8244 * std::pow((double)k, -0.4617) * std::pow((double)b, 0.9003) *
+               std::pow((double)n, -0.4498) * std::pow(T, -0.1057);
+    r.alpha0 = std::min(std::max(a, 1e-4), 1.0);
+  }
+  // epoch_rows (recipe.rs:127-140)
+  const double whole = std::floor(T);
+  const size_t rem = (size_t)std::nearbyint((T - whole) * (double)n);
+  const size_t w = (size_t)whole;
+  if (w == 0) {
+    r.epoch_rows = {rem};
+  } else {
+    r.epoch_rows.assign(w - 1, n);
+    if (rem > 0) r.epoch_rows.push_back(rem);
+    r.epoch_rows.push_back(n);
+  }
+  for (size_t e : r.epoch_rows) r.total_steps += (e + b - 1) / b;
+  r.tau = cfg.has_unused_threshold ? cfg.unused_threshold : (d <= 2 ? 0.0 : 0.1);
+  r.chunk = cfg.assignment_chunk_size ? (size_t)cfg.assignment_chunk_size : 65536;
+  return r;
+}
+
+uint32_t epoch_seed(uint32_t seed, size_t e) {  // recipe.rs:143-145
+  return (uint32_t)(((uint64_t)seed * 1000003ull + e) & 0xffffffffull);
+}
+
+double scheduled_alpha(double a0, size_t step, size_t total) {  // recipe.rs:148-152
+  const double f = (double)std::min(step, total) / (double)std::max<size_t>(total, 1);
+  const double cosine = 0.5 * (1.0 + std::cos(M_PI * f));
+  return a0 * (0.1 + 0.9 * cosine);
+}
+
+// numpy float32 pairwise sum (model.rs:970-1002).
+float np_sum(const float* a, size_t n) {
+  if (n < 8) {
+    float s = 0.0f;
+    for (size_t i = 0; i < n; i++) s = s + a[i];
+    return s;
+  }
+  if (n <= 128) {
+    float r[8];
+    for (int j = 0; j < 8; j++) r[j] = a[j];
+    size_t i = 8;
+    const size_t stop = n - n % 8;
+    for (; i < stop; i += 8)
+      for (int j = 0; j < 8; j++) r[j] = r[j] + a[i + j];
+    float s = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+    for (; i < n; i++) s = s + a[i];
+    return s;
+  }
+  size_t h = n / 2;
+  h -= h % 8;
+  return np_sum(a, h) + np_sum(a + h, n - h);
+}
+
+// Revival plan (core/mod.rs:339-370): clusters under tau * mean mass take a
+// donor drawn by Gumbel top-k on ln N; k uniforms drawn only if a split happens.
+std::vector<uint32_t> plan_revival(const std::vector<float>& usage, double tau, RandomState& rng) {
+  const size_t k = usage.size();
+  const float thr = (np_sum(usage.data(), k) * (float)tau) / (float)k;
+  std::vector<uint32_t> dead;
+  std::vector<char> donor(k);
+  size_t ndonor = 0;
+  for (size_t j = 0; j < k; j++) {
+    const bool u = usage[j] < thr;
+    if (u) dead.push_back((uint32_t)j);
+    donor[j] = !u && usage[j] > 0.0f;
+    ndonor += donor[j];
+  }
+  const size_t nsplit = std::min(dead.size(), ndonor);
+  std::vector<uint32_t> pairs;
+  if (nsplit == 0) return pairs;
+  std::vector<double> g(k);
+  for (size_t j = 0; j < k; j++) g[j] = std::max(rng.random_sample(), 2.2250738585072014e-308);
+  struct Key {
+    int64_t ord;
+    uint32_t j;
+  };
+  std::vector<Key> keys;
+  for (size_t j = 0; j < k; j++) {
+    if (!donor[j]) continue;
+    double v = (double)std::log(usage[j]) - std::log(-std::log(g[j]));
+    int64_t b;
+    std::memcpy(&b, &v, 8);
+    b ^= (int64_t)(((uint64_t)(b >> 63)) >> 1);  // IEEE total order as an integer
+    keys.push_back({b, (uint32_t)j});
+  }
+  std::sort(keys.begin(), keys.end(), [](const Key& a, const Key& b) {
+    return a.ord != b.ord ? a.ord > b.ord : a.j > b.j;
+  });
+  for (size_t q = 0; q < nsplit; q++) {
+    pairs.push_back(keys[q].j);
+    pairs.push_back(dead[q]);
+  }
+  return pairs;
+}
+
+void normalize_row(float* r, size_t d) {  // model.rs:954-967
+  float mx = 0.0f;
+  for (size_t t = 0; t < d; t++) mx = std::fmax(mx, std::fabs(r[t]));
+  const float s = mx > 0.0f ? mx : 1.0f;
+  for (size_t t = 0; t < d; t++) r[t] = r[t] / s;
+  float q = 0.0f;
+  for (size_t t = 0; t < d; t++) {
+    float p = r[t] * r[t];
+    q = q + p;
+  }
+  const float nr = std::sqrt(q);
+  const float s2 = nr > 0.0f ? nr : 1.0f;
+  for (size_t t = 0; t < d; t++) r[t] = r[t] / s2;
+}
+
+// ------------------------------------------------------------ device buffers
+struct Buf {
+  emh_ctx* c = nullptr;
+  void* p = nullptr;
+  Buf() = default;
+  Buf(emh_ctx* ctx, size_t bytes) : c(ctx) {
+    if (bytes) EMH_HIP(hipMalloc(&p, bytes));
+  }
+  ~Buf() {
+    if (p) (void)hipFree(p);
+  }
+  Buf(const Buf&) = delete;
+  Buf& operator=(const Buf&) = delete;
+  float* f() const { return (float*)p; }
+  uint32_t* u() const { return (uint32_t*)p; }
+};
+
+void h2d(emh_ctx* c, void* dst, const void* src, size_t bytes) {
+  if (!bytes) return;
+  EMH_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream));
+  EMH_HIP(hipStreamSynchronize(c->stream));
+}
+void d2h(emh_ctx* c, void* dst, const void* src, size_t bytes) {
+  if (bytes) EMH_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream));
+  EMH_HIP(hipStreamSynchronize(c->stream));
+}
+void check_flags(emh_ctx* c) {
+  uint32_t w[SW_WORDS];
+  d2h(c, w, c->small, sizeof w);
+  if (w[SW_BAD_LABEL] || w[SW_BAD_ID]) {
+    launch_fill_u32(c, c->small + SW_BAD_LABEL, 1, 0);
+    launch_fill_u32(c, c->small + SW_BAD_ID, 1, 0);
+    EMH_HIP(hipStreamSynchronize(c->stream));
+    throw Failure(w[SW_BAD_LABEL] ? "label out of range" : "row id out of range");
+  }
+}
+
+struct EpochResult {
+  emh_epoch_stats st;
+  std::vector<uint64_t> hist;  // last epoch only
+};
+
+// core/train.rs:60-303 on the context, then closing means.
+void train_run(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
+               const std::vector<float>& init_pos, emh_train_out* out,
+               std::future<std::vector<uint32_t>> first_order,
+               std::chrono::steady_clock::time_point t_start) {
+  const size_t k = cfg.k, d = cfg.d;
+  const bool sph = cfg.spherical != 0;
+  const Recipe R = resolve(n, k, d, cfg);
+  const size_t bsz = R.batch_size, chunk = std::max<size_t>(R.chunk, 1);
+  const size_t n_epochs = R.epoch_rows.size();
+
+  Buf order(c, n * 4), lab(c, n * 4), sco(c, n * 4), pos(c, k * d * 4), mass(c, k * 4),
+      readout(c, (sph ? k * d : k) * 4), sums(c, k * d * 4), counts(c, k * 4),
+      pass(c, k * d * 4);
+  h2d(c, pos.p, init_pos.data(), k * d * 4);
+  std::vector<float> usage0(k, 1.0f / 65536.0f);  // INIT_USAGE (recipe.rs:14)
+  h2d(c, mass.p, usage0.data(), k * 4);
+  launch_fill_u32(c, pass.u(), k * d, 0);
+
+  RandomState split_rng(cfg.seed);
+  size_t n_splits = 0, step = 0;
+  std::vector<EpochResult> results;
+  std::vector<double> pass_counts(k, 0.0);
+  std::vector<int32_t> all_labels;
+  const bool capture = cfg.capture_assignments && out->labels;
+
+  // The next epoch's permutation, drawn one epoch ahead on a helper thread.
+  std::future<std::vector<uint32_t>> next = std::move(first_order);
+  std::future<EpochResult> pending;
+  std::vector<uint32_t> order_host;
+  std::vector<float> usage_host(k);
+  for (size_t epoch = 0; epoch < n_epochs; epoch++) {
+    const size_t rows = R.epoch_rows[epoch];
+    const bool last = epoch + 1 == n_epochs;
+    order_host = next.get();
+    if (epoch + 1 < n_epochs) {
+      const uint32_t s = epoch_seed(cfg.seed, epoch + 1);
+      next = std::async(std::launch::async, [s, n] { return RandomState(s).permutation(n); });
+    }
+    h2d(c, order.p, order_host.data(), rows * 4);
+    const size_t splits_before = n_splits;
+    for (size_t b = 0; b < rows; b += bsz) {
+      const size_t e = std::min(b + bsz, rows);
+      if (sph)
+        launch_normalize_rows(c, pos.f(), k, d, readout.f());
+      else
+        launch_row_norms(c, pos.f(), k, d, readout.f());
+      const float* cents = sph ? readout.f() : pos.f();
+      const float* cn = sph ? nullptr : readout.f();
+      for (size_t c0 = b; c0 < e; c0 += chunk) {
+        const size_t c1 = std::min(c0 + chunk, e);
+        launch_top1(c, x, n, d, order.u(), c0, c1, cents, cn, k, sph, lab.u(), sco.f());
+      }
+      launch_scatter(c, x, n, d, order.u(), b, e, lab.u(), k, sums.f(), counts.u(),
+                     last ? pass.f() : nullptr);
+      const double alpha = scheduled_alpha(R.alpha0, step, R.total_steps);
+      launch_ema(c, pos.f(), mass.f(), sums.f(), counts.u(), k, d, (float)alpha,
+                 (float)(1.0 - alpha), alpha == 1.0);
+      if ((step + 1) % 5 == 0) {  // CHECK_UNUSED_EVERY (recipe.rs:12)
+        d2h(c, usage_host.data(), mass.p, k * 4);
+        std::vector<uint32_t> plan = plan_revival(usage_host, R.tau, split_rng);
+        if (!plan.empty()) {
+          const size_t np = plan.size() / 2;
+          uint32_t* pd = (uint32_t*)c->misc.get(plan.size() * 4);
+          h2d(c, pd, plan.data(), plan.size() * 4);
+          launch_split(c, pos.f(), mass.f(), pd, np, d, true);  // donors and dead are disjoint
+          n_splits += np;
+        }
+      }
+      step++;
+    }
+    // Epoch end: labels and scores come down; statistics on a helper thread.
+    auto labels_h = std::make_shared<std::vector<uint32_t>>(rows);
+    auto scores_h = std::make_shared<std::vector<float>>(rows);
+    d2h(c, labels_h->data(), lab.p, rows * 4);
+    d2h(c, scores_h->data(), sco.p, rows * 4);
+    check_flags(c);
+    const double t = std::chrono::duration<double>(std::chrono::steady_clock::now() - t_start).count();
+    if (pending.valid()) results.push_back(pending.get());
+    const size_t nsplit = n_splits - splits_before;
+    if (last && capture) {
+      all_labels.assign(n, -1);
+      for (size_t p = 0; p < rows; p++) all_labels[order_host[p]] = (int32_t)(*labels_h)[p];
+    }
+    pending = std::async(std::launch::async, [=]() {  // train.rs:224-279
+      EpochResult er;
+      double obj_epoch = 0.0;
+      for (size_t b = 0; b < rows; b += bsz) {
+        const size_t e = std::min(b + bsz, rows);
+        double obj_batch = 0.0;
+        for (size_t c0 = b; c0 < e; c0 += chunk) {
+          const size_t c1 = std::min(c0 + chunk, e);
+          double obj = 0.0;
+          if (sph) {
+            obj += 2.0 * (double)(c1 - c0);
+            for (size_t p = c0; p < c1; p++) obj += (double)(-2.0f * (*scores_h)[p]);
+          } else {
+            for (size_t p = c0; p < c1; p++) obj += (double)(*scores_h)[p];
+          }
+          obj_batch += obj;
+        }
+        obj_epoch += obj_batch;
+      }
+      er.hist.assign(k, 0);
+      for (uint32_t l : *labels_h)
+        if (l < k) er.hist[l]++;
+      double sq = 0.0;
+      for (size_t j = 0; j < k; j++) sq += (double)er.hist[j] * (double)er.hist[j];
+      er.st.obj = obj_epoch;
+      er.st.time = t;
+      er.st.imbalance_factor = (double)k * sq / ((double)rows * (double)rows);
+      er.st.nsplit = nsplit;
+      if (cfg.verbose)
+        fprintf(stderr, "  Epoch %zu / %zu (%zu rows), iteration %zu (%.2f s): objective=%.17g\n",
+                epoch + 1, n_epochs, rows, step, t, obj_epoch);
+      return er;
+    });
+  }
+  std::vector<float> P(k * d), U(k), S(k * d);
+  d2h(c, P.data(), pos.p, k * d * 4);
+  d2h(c, U.data(), mass.p, k * 4);
+  d2h(c, S.data(), pass.p, k * d * 4);
+  if (pending.valid()) results.push_back(pending.get());
+  for (size_t j = 0; j < k; j++) pass_counts[j] = (double)results.back().hist[j];
+  // Closing means (core/mod.rs:404-429).
+  std::vector<float> C(P);
+  for (size_t j = 0; j < k; j++) {
+    float* cj = &C[j * d];
+    if (pass_counts[j] > 0.0) {
+      const float nf = (float)pass_counts[j];
+      for (size_t t = 0; t < d; t++) cj[t] = S[j * d + t] / nf;
+    }
+    if (sph) normalize_row(cj, d);
+  }
+  std::memcpy(out->centroids, C.data(), k * d * 4);
+  if (out->positions) std::memcpy(out->positions, P.data(), k * d * 4);
+  if (out->usage) std::memcpy(out->usage, U.data(), k * 4);
+  if (out->labels) {
+    if (capture)
+      std::memcpy(out->labels, all_labels.data(), n * 4);
+    else
+      std::fill(out->labels, out->labels + n, -1);
+  }
+  out->n_epochs = n_epochs;
+  for (size_t e = 0; e < n_epochs && e < out->max_epochs; e++)
+    if (out->stats) out->stats[e] = results[e].st;
+  out->n_splits = n_splits;
+  out->batch_size = bsz;
+  out->alpha0 = R.alpha0;
+  out->total_steps = R.total_steps;
+}
+
+void check_cfg(size_t n, const emh_config* cfg, const emh_train_out* out) {
+  EMH_ENSURE(cfg && out && out->centroids, "null argument");
+  EMH_ENSURE(cfg->d > 0 && cfg->k > 0, "d and k must be positive");
+  EMH_ENSURE(std::isfinite(cfg->nepochs) && cfg->nepochs > 0.0, "nepochs must be positive");
+  EMH_ENSURE(!cfg->has_unused_threshold || cfg->unused_threshold >= 0.0,
+             "unused_threshold must be >= 0 (0 disables revival)");
+  EMH_ENSURE(cfg->batch_law >= 0 && cfg->batch_law <= 2, "unknown batch law");
+  EMH_ENSURE(n >= cfg->k, "need at least k = %llu rows, got %zu", (unsigned long long)cfg->k, n);
+  const Recipe r = resolve(n, cfg->k, cfg->d, *cfg);
+  for (size_t e : r.epoch_rows) EMH_ENSURE(e > 0, "nepochs gives an empty epoch for n = %zu", n);
+}
+
+// Emeans::train_rows (model.rs:772-811) with the data on the device.
+void train_dev(emh_ctx* c, const float* xd, size_t n, const emh_config& cfg, emh_train_out* out,
+               const float* x_host) {
+  const auto t0 = std::chrono::steady_clock::now();
+  const size_t k = cfg.k, d = cfg.d;
+  const uint32_t s0 = epoch_seed(cfg.seed, 0);
+  auto first = std::async(std::launch::async, [s0, n] { return RandomState(s0).permutation(n); });
+  std::vector<float> init(k * d);
+  if (n == k) {
+    if (x_host)
+      std::memcpy(init.data(), x_host, k * d * 4);
+    else
+      d2h(c, init.data(), xd, k * d * 4);
+  } else {
+    std::vector<uint32_t> perm = RandomState(cfg.seed).permutation(n);
+    if (x_host) {
+      for (size_t j = 0; j < k; j++)
+        std::memcpy(&init[j * d], x_host + (size_t)perm[j] * d, d * 4);
+    } else {
+      Buf ids(c, k * 4), rows(c, k * d * 4);
+      h2d(c, ids.p, perm.data(), k * 4);
+      launch_gather_rows(c, xd, n, d, ids.u(), k, rows.f());
+      d2h(c, init.data(), rows.p, k * d * 4);
+    }
+  }
+  if (cfg.spherical)  // begin (model.rs:306-315)
+    for (size_t j = 0; j < k; j++) normalize_row(&init[j * d], d);
+  for (float v : init) EMH_ENSURE(std::isfinite(v), "initial centroids must be finite");
+  if (cfg.verbose) {
+    Recipe r = resolve(n, k, d, cfg);
+    fprintf(stderr, "Clustering %zu points in %zuD to %zu clusters, %g epochs (batch %zu, alpha0 %.3f%s)\n",
+            n, d, k, cfg.nepochs, r.batch_size, r.alpha0, cfg.spherical ? ", spherical" : "");
+  }
+  uint32_t fb0 = 0;
+  d2h(c, &fb0, c->small + SW_FALLBACK_TOTAL, 4);
+  train_run(c, xd, n, cfg, init, out, std::move(first), t0);
+  uint32_t fb1 = 0;
+  d2h(c, &fb1, c->small + SW_FALLBACK_TOTAL, 4);
+  out->fallback_rows = (uint32_t)(fb1 - fb0);
+}
+
+// dedup_with_neighbors (dedup.rs:186-358) for rows without timestamps or bursts.
+float dot_seq(const float* a, const float* b, size_t d) {  // dedup.rs:158-160
+  float s = 0.0f;
+  for (size_t t = 0; t < d; t++) {
+    float p = a[t] * b[t];
+    s = s + p;
+  }
+  return s;
+}
+
+size_t dedup_groups(const float* x, size_t n, size_t d, const uint32_t* nb_ids,
+                    const float* nb_sims, size_t kk, float sim_t, float rep_t,
+                    const float* priority, uint32_t* group_of, uint32_t* reps, uint32_t* anchors,
+                    uint32_t* sizes, size_t* linked, size_t* split_components) {
+  std::vector<uint32_t> parent(n);
+  for (size_t i = 0; i < n; i++) parent[i] = (uint32_t)i;
+  auto find = [&](uint32_t i) {
+    while (parent[i] != i) {
+      uint32_t p = parent[i];
+      parent[i] = parent[p];
+      i = p;
+    }
+    return i;
+  };
+  std::vector<uint32_t> degree(n, 0);
+  std::set<std::pair<uint32_t, uint32_t>> pairs;
+  for (size_t i = 0; i < n; i++)
+    for (size_t t = 0; t < kk; t++) {
+      const uint32_t j = nb_ids[i * kk + t];
+      if (j == 0xffffffffu || j >= n || nb_sims[i * kk + t] < sim_t) continue;
+      uint32_t a = find((uint32_t)i), b = find(j);
+      if (a != b) parent[std::max(a, b)] = std::min(a, b);  // lower root wins
+      auto key = std::make_pair(std::min<uint32_t>((uint32_t)i, j), std::max<uint32_t>((uint32_t)i, j));
+      if (pairs.insert(key).second) {
+        degree[i]++;
+        degree[j]++;
+      }
+    }
+  std::map<uint32_t, std::vector<uint32_t>> members;
+  for (uint32_t i = 0; i < n; i++) members[find(i)].push_back(i);
+  std::vector<std::pair<std::vector<uint32_t>, uint32_t>> groups;
+  size_t split = 0;
+  std::vector<char> taken(n, 0);
+  for (auto& kv : members) {
+    const auto& rows = kv.second;
+    if (rows.size() == 1) {
+      groups.push_back({rows, rows[0]});
+      continue;
+    }
+    std::vector<uint32_t> ord(rows);
+    std::sort(ord.begin(), ord.end(), [&](uint32_t a, uint32_t b) {
+      return degree[a] != degree[b] ? degree[a] > degree[b] : a < b;
+    });
+    const size_t before = groups.size();
+    for (uint32_t a : ord) {
+      if (taken[a]) continue;
+      taken[a] = 1;
+      std::vector<uint32_t> g{a};
+      for (uint32_t r : rows) {
+        if (taken[r]) continue;
+        if (dot_seq(x + (size_t)r * d, x + (size_t)a * d, d) >= rep_t) {
+          taken[r] = 1;
+          g.push_back(r);
+        }
+      }
+      std::sort(g.begin(), g.end());
+      groups.push_back({std::move(g), a});
+    }
+    if (groups.size() - before > 1) split++;
+  }
+  std::sort(groups.begin(), groups.end(),
+            [](const auto& a, const auto& b) { return a.first[0] < b.first[0]; });
+  for (size_t gi = 0; gi < groups.size(); gi++) {
+    const auto& g = groups[gi].first;
+    anchors[gi] = groups[gi].second;
+    sizes[gi] = (uint32_t)g.size();
+    uint32_t rep = g[0];
+    if (g.size() > 1) {  // priority, then mean similarity, then lowest id
+      float bp = -INFINITY;
+      double bm = -INFINITY;
+      for (uint32_t a : g) {
+        double s = 0.0;
+        for (uint32_t b : g)
+          if (b != a) s += (double)dot_seq(x + (size_t)a * d, x + (size_t)b * d, d);
+        const double mean = s / (double)(g.size() - 1);
+        const float p = priority ? priority[a] : 0.0f;
+        if (p > bp || (p == bp && mean > bm)) {
+          bp = p;
+          bm = mean;
+          rep = a;
+        }
+      }
+    }
+    reps[gi] = rep;
+    for (uint32_t r : g) group_of[r] = (uint32_t)gi;
+  }
+  *linked = pairs.size();
+  *split_components = split;
+  return groups.size();
+}
+
+}  // namespace host
+}  // namespace emh
+
+namespace {
+template <class F>
+int guard2(F&& f) {
+  try {
+    f();
+    return EMH_OK;
+  } catch (const emh::Invalid& e) {
+    emh::set_last_error(e.what());
+    return EMH_INVALID;
+  } catch (const std::exception& e) {
+    emh::set_last_error(e.what());
+    return EMH_ERROR;
+  } catch (...) {
+    emh::set_last_error("unknown error");
+    return EMH_ERROR;
+  }
+}
+}  // namespace
+
+using namespace emh::host;
+
+extern "C" {
+
+int emh_train_dev(emh_ctx* c, const emh_buf* x, size_t n, const emh_config* cfg,
+                  emh_train_out* out) {
+  return guard2([&] {
+    EMH_ENSURE(c && x && x->kind == 0, "x must be an f32 buffer");
+    check_cfg(n, cfg, out);
+    EMH_ENSURE(x->len == n * cfg->d, "x must be n x d");
+    EMH_HIP(hipSetDevice(c->device));
+    train_dev(c, (const float*)x->ptr, n, *cfg, out, nullptr);
+  });
+}
+
+int emh_train(emh_ctx* c, const float* x, size_t n, const emh_config* cfg, emh_train_out* out) {
+  return guard2([&] {
+    EMH_ENSURE(c && x, "null argument");
+    check_cfg(n, cfg, out);
+    EMH_HIP(hipSetDevice(c->device));
+    Buf xd(c, n * cfg->d * 4);  // Device::bind: the data set goes to the device once
+    h2d(c, xd.p, x, n * cfg->d * 4);
+    train_dev(c, xd.f(), n, *cfg, out, x);
+  });
+}
+
+int emh_assign(emh_ctx* c, const float* x, size_t n, size_t d, const float* cents, size_t k,
+               int metric, size_t chunk, uint32_t* labels, float* scores) {
+  return guard2([&] {
+    EMH_ENSURE(c && d > 0 && k > 0 && cents, "bad arguments");
+    EMH_ENSURE(metric == EMH_L2 || metric == EMH_IP, "unknown metric");
+    if (n == 0) return;
+    EMH_ENSURE(x && labels && scores, "null argument");
+    EMH_HIP(hipSetDevice(c->device));
+    chunk = chunk ? chunk : 65536;
+    // Centroids and their norms go up once for all chunks.
+    Buf cb(c, k * d * 4), cn(c, k * 4);
+    h2d(c, cb.p, cents, k * d * 4);
+    if (metric == EMH_L2) emh::launch_row_norms(c, cb.f(), k, d, cn.f());
+    const size_t m = std::min(chunk, n);
+    Buf xb(c, m * d * 4), lb(c, m * 4), sb(c, m * 4);
+    for (size_t b = 0; b < n; b += chunk) {
+      const size_t e = std::min(b + chunk, n);
+      h2d(c, xb.p, x + b * d, (e - b) * d * 4);
+      emh::launch_top1(c, xb.f(), e - b, d, nullptr, 0, e - b, cb.f(),
+                       metric == EMH_L2 ? cn.f() : nullptr, k, metric == EMH_IP, lb.u(), sb.f());
+      d2h(c, labels + b, lb.p, (e - b) * 4);
+      d2h(c, scores + b, sb.p, (e - b) * 4);
+    }
+    check_flags(c);
+  });
+}
+
+int emh_knn(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,
+            size_t kk, int exclude_self, uint32_t* ids, float* sims) {
+  return emh_topk(c, q, m, data, n, d, kk, exclude_self, ids, sims);
+}
+
+int emh_dedup_neighbors(const float* x, size_t n, size_t d, const uint32_t* nb_ids,
+                        const float* nb_sims, size_t kk, float sim_t, float rep_t,
+                        const float* priority, uint32_t* group_of, uint32_t* reps,
+                        uint32_t* anchors, uint32_t* sizes, size_t* n_groups, size_t* linked,
+                        size_t* split) {
+  return guard2([&] {
+    EMH_ENSURE(d > 0, "x must be n x d");
+    EMH_ENSURE(sim_t >= -1.0f && sim_t <= 1.0f, "sim_threshold must be in [-1, 1]");
+    if (priority)
+      for (size_t i = 0; i < n; i++) EMH_ENSURE(!std::isnan(priority[i]), "priority must not be NaN");
+    EMH_ENSURE(n == 0 || (x && nb_ids && nb_sims && group_of && reps && anchors && sizes),
+               "null argument");
+    size_t lp = 0, sc = 0;
+    *n_groups = dedup_groups(x, n, d, nb_ids, nb_sims, kk, sim_t, rep_t, priority, group_of, reps,
+                             anchors, sizes, &lp, &sc);
+    *linked = lp;
+    *split = sc;
+  });
+}
+
+int emh_dedup(emh_ctx* c, const float* x, size_t n, size_t d, size_t kk, float sim_t, float rep_t,
+              const float* priority, uint32_t* group_of, uint32_t* reps, uint32_t* anchors,
+              uint32_t* sizes, float* nn_sim, size_t* n_groups, size_t* linked, size_t* split) {
+  return guard2([&] {
+    EMH_ENSURE(c && d > 0, "bad arguments");
+    size_t k = std::max<size_t>(std::min(kk, n > 0 ? n - 1 : 0), 1);  // dedup.rs:172
+    std::vector<uint32_t> ids(n * k, 0xffffffffu);
+    std::vector<float> sims(n * k, -INFINITY);
+    if (n > 1) {
+      EMH_ENSURE(k <= 16, "dedup on the GPU searches at most 16 neighbours");
+      if (emh_topk(c, x, n, x, n, d, k, 1, ids.data(), sims.data()) != EMH_OK)
+        throw emh::Failure(emh_last_error());
+    }
+    if (emh_dedup_neighbors(x, n, d, ids.data(), sims.data(), k, sim_t, rep_t, priority, group_of,
+                            reps, anchors, sizes, n_groups, linked, split) != EMH_OK)
+      throw emh::Failure(emh_last_error());
+    if (nn_sim)
+      for (size_t i = 0; i < n; i++) nn_sim[i] = sims[i * k];
+  });
+}
+
+// Host-side pieces of the loop, exported for checks that need no device.
+void emh_host_permutation(uint32_t seed, uint64_t n, uint32_t* out) {
+  std::vector<uint32_t> p = RandomState(seed).permutation(n);
+  std::memcpy(out, p.data(), n * 4);
+}
+double emh_host_random_sample(uint32_t seed, uint64_t skip) {
+  RandomState r(seed);
+  for (uint64_t i = 0; i < skip; i++) r.random_sample();
+  return r.random_sample();
+}
+int emh_host_recipe(uint64_t n, const emh_config* cfg, uint64_t* batch_size, double* alpha0,
+                    uint64_t* epoch_rows, uint64_t cap, uint64_t* n_epochs, uint64_t* total) {
+  return guard2([&] {
+    EMH_ENSURE(cfg && batch_size && alpha0 && n_epochs && total, "null argument");
+    Recipe r = resolve(n, cfg->k, cfg->d, *cfg);
+    *batch_size = r.batch_size;
+    *alpha0 = r.alpha0;
+    *n_epochs = r.epoch_rows.size();
+    for (size_t e = 0; e < r.epoch_rows.size() && e < cap; e++) epoch_rows[e] = r.epoch_rows[e];
+    *total = r.total_steps;
+  });
+}
+double emh_host_scheduled_alpha(double alpha0, uint64_t step, uint64_t total) {
+  return scheduled_alpha(alpha0, step, total);
+}
+// Revival plan from a fresh RandomState(seed) after `skip` samples; returns pairs written.
+uint64_t emh_host_plan_revival(const float* usage, uint64_t k, double tau, uint32_t seed,
+                               uint32_t* pairs) {
+  RandomState r(seed);
+  std::vector<float> u(usage, usage + k);
+  std::vector<uint32_t> p = plan_revival(u, tau, r);
+  std::memcpy(pairs, p.data(), p.size() * 4);
+  return p.size() / 2;
+}
+float emh_host_numpy_sum_f32(const float* a, uint64_t n) { return np_sum(a, n); }
+
+}  // extern "C"

@@ -1,0 +1,132 @@
+// Internal declarations of the gfx950 backend: the context, buffers, error
+// plumbing and the kernel launchers each .hip file provides.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/emeans_hip.h"
+
+namespace emh {
+
+// A failed check inside the library; turned into EMH_INVALID / EMH_ERROR at the ABI.
+struct Invalid : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+struct Failure : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+
+#define EMH_ENSURE(cond, ...)                                  \
+  do {                                                         \
+    if (!(cond)) {                                             \
+      char _m[512];                                            \
+      snprintf(_m, sizeof _m, __VA_ARGS__);                    \
+      throw ::emh::Invalid(_m);                                \
+    }                                                          \
+  } while (0)
+
+#define EMH_HIP(call)                                                               \
+  do {                                                                              \
+    hipError_t _e = (call);                                                         \
+    if (_e != hipSuccess) {                                                         \
+      char _m[512];                                                                 \
+      snprintf(_m, sizeof _m, "%s failed: %s (%s:%d)", #call, hipGetErrorString(_e), \
+               __FILE__, __LINE__);                                                 \
+      throw ::emh::Failure(_m);                                                     \
+    }                                                                               \
+  } while (0)
+
+void set_last_error(const std::string& m);
+
+// Device scratch that grows on demand and is reused by later calls.
+struct Scratch {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  void* get(size_t need) {
+    if (need > bytes) {
+      // Queued kernels may still read the old block: wait before freeing it.
+      if (ptr) {
+        EMH_HIP(hipDeviceSynchronize());
+        EMH_HIP(hipFree(ptr));
+      }
+      ptr = nullptr;
+      size_t b = need + need / 4 + 4096;
+      EMH_HIP(hipMalloc(&ptr, b));
+      bytes = b;
+    }
+    return ptr;
+  }
+  void release() {
+    if (ptr) (void)hipFree(ptr);
+    ptr = nullptr;
+    bytes = 0;
+  }
+};
+
+// Words of the context's small device block.
+enum SmallWord : int {
+  SW_FALLBACK_COUNT = 0,  // rows appended to the exact kernel's list by the current call
+  SW_CMAX2 = 1,           // max over centroids of |c|^2 (f32 bits)
+  SW_CNMAX = 2,           // max over centroids of the given cnorm (f32 bits)
+  SW_BAD_LABEL = 3,       // set when scatter_add saw a label >= k
+  SW_FALLBACK_TOTAL = 4,  // running total of rescanned rows (u32, wraps)
+  SW_BAD_ID = 5,          // set when a selection named a row id >= n
+  SW_WORDS = 16,
+};
+
+}  // namespace emh
+
+struct emh_buf {
+  void* ptr = nullptr;
+  size_t len = 0;   // elements
+  int kind = 0;     // 0 f32, 1 u32
+  bool owned = true;
+};
+
+struct emh_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  int cus = 256;
+  int screen = 1;
+  uint32_t* small = nullptr;  // SW_WORDS u32 on the device
+  uint64_t fallback_total = 0;
+  emh::Scratch cand, fblist, order, start, misc, knn_tmp;
+  std::string name = "hip-gfx950";
+};
+
+namespace emh {
+
+inline dim3 grid1(size_t n, int per) { return dim3((unsigned)((n + per - 1) / per)); }
+
+// ---- launchers (emh_ops.hip)
+void launch_fill_u32(emh_ctx* c, uint32_t* p, size_t n, uint32_t v);
+void launch_row_norms(emh_ctx* c, const float* m, size_t rows, size_t d, float* out);
+void launch_normalize_rows(emh_ctx* c, const float* src, size_t rows, size_t d, float* dst);
+void launch_ema(emh_ctx* c, float* pos, float* usage, const float* sums, const uint32_t* counts,
+                size_t k, size_t d, float alpha, float decay, int replace);
+void launch_split(emh_ctx* c, float* pos, float* usage, const uint32_t* pairs_dev, size_t npairs,
+                  size_t d, bool independent);
+void launch_gather_rows(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
+                        size_t m, float* out);
+
+// ---- emh_scatter.hip
+void launch_scatter(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids, size_t lo,
+                    size_t hi, const uint32_t* labels, size_t k, float* sums, uint32_t* counts,
+                    float* acc);
+
+// ---- emh_top1.hip
+void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids, size_t lo, size_t hi,
+                 const float* cents, const float* cnorm, size_t k, bool ip, uint32_t* labels,
+                 float* scores);
+
+// ---- emh_topk.hip
+void launch_topk(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,
+                 size_t kk, bool exclude_self, uint32_t* ids, float* sims);
+
+}  // namespace emh

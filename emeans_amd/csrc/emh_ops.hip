@@ -1,0 +1,277 @@
+// Exact per-batch ops of the device loop: row norms, faiss normalize_into,
+// the EMA step and the revival split. Each follows the reference CPU backend's
+// f32 operation order (crates/emeans-core/src/core/cpu.rs) so results are
+// bit-equal; the library is built with -ffp-contract=off so that no multiply
+// and add the reference keeps separate is fused, and with IEEE f32 divide and
+// sqrt and f32 denormals kept.
+//
+// These ops are HBM/latency-bound: they touch k x d floats once. A row's
+// squared norm is a sequential chain of d adds (the reference sums in order),
+// so one wave owns a row: its lanes square the elements in parallel into LDS
+// and one lane adds them in order.
+
+#include "emh_internal.h"
+
+namespace emh {
+namespace {
+
+constexpr int WAVE = 64;
+constexpr int WAVES = 4;   // waves per workgroup
+constexpr int CH = 1024;   // elements per LDS chunk of one row
+
+__global__ __launch_bounds__(256) void k_fill_u32(uint32_t* p, size_t n, uint32_t v) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+// Sequential sum of rounded squares of row r (assign.rs:150-155): the lanes of
+// wave w square one chunk into sq[w]; lane 0 adds the chunk in column order.
+__device__ float seq_sq_sum(const float* row, size_t d, float* sq, int lane) {
+  float s = 0.0f;
+  for (size_t c0 = 0; c0 < d; c0 += CH) {
+    int len = (int)min((size_t)CH, d - c0);
+    for (int t = lane; t < len; t += WAVE) {
+      float v = row[c0 + t];
+      sq[t] = v * v;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane == 0) {
+      int t = 0;
+      for (; t + 4 <= len; t += 4) {
+        float4 q = *reinterpret_cast<const float4*>(sq + t);
+        s = s + q.x;
+        s = s + q.y;
+        s = s + q.z;
+        s = s + q.w;
+      }
+      for (; t < len; t++) s = s + sq[t];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  return s;  // valid in lane 0
+}
+
+__global__ __launch_bounds__(256) void k_row_norms(const float* __restrict__ m, size_t rows,
+                                                   size_t d, float* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) float sq[WAVES][CH];
+  int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+  size_t r = (size_t)blockIdx.x * WAVES + w;
+  if (r >= rows) return;  // whole wave; no workgroup barrier below
+  float s = seq_sq_sum(m + r * d, d, sq[w], lane);
+  if (lane == 0) out[r] = s;
+}
+
+__device__ inline float wave_max(float v) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
+  return v;
+}
+
+// faiss normalize_into (core/cpu.rs:219-230): divide by max |v| (if > 0), then
+// by sqrt of the sequential sum of squares of the divided row (if > 0).
+__global__ __launch_bounds__(256) void k_normalize_rows(const float* __restrict__ src,
+                                                        size_t rows, size_t d,
+                                                        float* __restrict__ dst) {
+  __shared__ __attribute__((aligned(16))) float sq[WAVES][CH];
+  int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+  size_t r = (size_t)blockIdx.x * WAVES + w;
+  if (r >= rows) return;
+  const float* row = src + r * d;
+  float mx = 0.0f;  // fold from 0 with max(|v|): NaN never wins (fmaxf)
+  for (size_t t = lane; t < d; t += WAVE) mx = fmaxf(mx, fabsf(row[t]));
+  mx = wave_max(mx);
+  const float s1 = mx > 0.0f ? mx : 1.0f;
+  float s = 0.0f;
+  for (size_t c0 = 0; c0 < d; c0 += CH) {
+    int len = (int)min((size_t)CH, d - c0);
+    for (int t = lane; t < len; t += WAVE) {
+      float v = row[c0 + t] / s1;
+      sq[w][t] = v * v;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane == 0) {
+      int t = 0;
+      for (; t + 4 <= len; t += 4) {
+        float4 q = *reinterpret_cast<const float4*>(&sq[w][t]);
+        s = s + q.x;
+        s = s + q.y;
+        s = s + q.z;
+        s = s + q.w;
+      }
+      for (; t < len; t++) s = s + sq[w][t];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  s = __shfl(s, 0, WAVE);
+  float norm = sqrtf(s);
+  const float s2 = norm > 0.0f ? norm : 1.0f;
+  float* out = dst + r * d;
+  for (size_t t = lane; t < d; t += WAVE) {
+    float v = row[t] / s1;
+    out[t] = v / s2;
+  }
+}
+
+// EMA step (core/cpu.rs:389-432): all masses decay unless replace; each cluster
+// with rows gets mass = retained + alpha n, w = alpha n / mass and
+// c = (w == 1) ? s / n : c + w (s / n - c), two roundings, no FMA.
+__global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __restrict__ usage,
+                                             const float* __restrict__ sums,
+                                             const uint32_t* __restrict__ counts, size_t k,
+                                             size_t d, float alpha, float decay, int replace) {
+  int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+  size_t j = (size_t)blockIdx.x * WAVES + w;
+  if (j >= k) return;
+  float u = usage[j];
+  if (!replace) u = u * decay;
+  uint32_t cnt = counts[j];
+  if (cnt > 0) {
+    float count = (float)cnt;
+    float retained = replace ? 0.0f : u;
+    float step = alpha * count;
+    float mass = retained + step;
+    float weight = step / mass;
+    float* p = pos + j * d;
+    const float* s = sums + j * d;
+    if (weight == 1.0f) {
+      for (size_t t = lane; t < d; t += WAVE) p[t] = s[t] / count;
+    } else {
+      for (size_t t = lane; t < d; t += WAVE) {
+        float mean = s[t] / count;
+        float c = p[t];
+        float diff = mean - c;
+        float inc = weight * diff;
+        p[t] = c + inc;
+      }
+    }
+    u = mass;
+  }
+  if (lane == 0) usage[j] = u;
+}
+
+__device__ inline float next_up(float x) {  // f32::next_up
+  if (x != x || x == INFINITY) return x;
+  uint32_t b = __float_as_uint(x);
+  if ((b & 0x7fffffffu) == 0) return __uint_as_float(1u);
+  return __uint_as_float(x > 0.0f ? b + 1 : b - 1);
+}
+__device__ inline float next_down(float x) {  // f32::next_down
+  return -next_up(-x);
+}
+
+// Revival split (core/mod.rs:374-399): donor c (1 - off), child c (1 + off),
+// off = +-1e-4 alternating by column parity; if donor == child element-wise the
+// child's first element moves one ulp up (down if that overflows); half of the
+// donor's mass each. One workgroup per pair, or one workgroup walking the plan
+// in order when pairs share a centroid.
+__global__ __launch_bounds__(256) void k_split(float* __restrict__ pos, float* __restrict__ usage,
+                                               const uint32_t* __restrict__ pairs, int npairs,
+                                               size_t d, int sequential) {
+  __shared__ int diff;
+  int q0 = sequential ? 0 : (int)blockIdx.x;
+  int q1 = sequential ? npairs : q0 + 1;
+  const float eps = 1e-4f;
+  for (int q = q0; q < q1; q++) {
+    uint32_t s = pairs[2 * q], t = pairs[2 * q + 1];
+    if (threadIdx.x == 0) diff = 0;
+    __syncthreads();
+    float* cs = pos + (size_t)s * d;
+    float* ct = pos + (size_t)t * d;
+    bool mine = false;
+    for (size_t i = threadIdx.x; i < d; i += blockDim.x) {
+      float off = eps * ((i % 2 == 0) ? 1.0f : -1.0f);
+      float c = cs[i];
+      float lo = 1.0f - off, hi = 1.0f + off;
+      float dn = c * lo, ch = c * hi;
+      mine = mine || !(dn == ch);
+    }
+    if (mine) atomicOr(&diff, 1);
+    __syncthreads();
+    const bool same = diff == 0;
+    float half = usage[s] / 2.0f;
+    __syncthreads();
+    for (size_t i = threadIdx.x; i < d; i += blockDim.x) {
+      float off = eps * ((i % 2 == 0) ? 1.0f : -1.0f);
+      float c = cs[i];
+      float lo = 1.0f - off, hi = 1.0f + off;
+      float dn = c * lo, ch = c * hi;
+      if (i == 0 && same) {
+        float up = next_up(ch);
+        ch = isfinite(up) ? up : next_down(ch);
+      }
+      cs[i] = dn;
+      ct[i] = ch;
+    }
+    if (threadIdx.x == 0) {
+      usage[s] = half;
+      usage[t] = half;
+    }
+    __syncthreads();
+  }
+}
+
+// out[i] = x[ids[i]] (m rows of d); an id >= nx gives a zero row.
+__global__ __launch_bounds__(256) void k_gather_rows(const float* __restrict__ x, size_t nx,
+                                                     size_t d, const uint32_t* __restrict__ ids,
+                                                     size_t m, float* __restrict__ out) {
+  size_t i = blockIdx.y;
+  size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= m || t >= d) return;
+  size_t r = ids[i];
+  out[i * d + t] = r < nx ? x[r * d + t] : 0.0f;
+}
+
+}  // namespace
+
+void launch_gather_rows(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
+                        size_t m, float* out) {
+  if (m == 0) return;
+  dim3 g((unsigned)((d + 255) / 256), (unsigned)m);
+  hipLaunchKernelGGL(k_gather_rows, g, dim3(256), 0, c->stream, x, nx, d, ids, m, out);
+  EMH_HIP(hipGetLastError());
+}
+
+void launch_fill_u32(emh_ctx* c, uint32_t* p, size_t n, uint32_t v) {
+  if (n == 0) return;
+  hipLaunchKernelGGL(k_fill_u32, grid1(n, 256), dim3(256), 0, c->stream, p, n, v);
+  EMH_HIP(hipGetLastError());
+}
+
+void launch_row_norms(emh_ctx* c, const float* m, size_t rows, size_t d, float* out) {
+  if (rows == 0) return;
+  hipLaunchKernelGGL(k_row_norms, grid1(rows, WAVES), dim3(256), 0, c->stream, m, rows, d, out);
+  EMH_HIP(hipGetLastError());
+}
+
+void launch_normalize_rows(emh_ctx* c, const float* src, size_t rows, size_t d, float* dst) {
+  if (rows == 0) return;
+  hipLaunchKernelGGL(k_normalize_rows, grid1(rows, WAVES), dim3(256), 0, c->stream, src, rows, d,
+                     dst);
+  EMH_HIP(hipGetLastError());
+}
+
+void launch_ema(emh_ctx* c, float* pos, float* usage, const float* sums, const uint32_t* counts,
+                size_t k, size_t d, float alpha, float decay, int replace) {
+  if (k == 0) return;
+  hipLaunchKernelGGL(k_ema, grid1(k, WAVES), dim3(256), 0, c->stream, pos, usage, sums, counts, k,
+                     d, alpha, decay, replace);
+  EMH_HIP(hipGetLastError());
+}
+
+void launch_split(emh_ctx* c, float* pos, float* usage, const uint32_t* pairs_dev, size_t npairs,
+                  size_t d, bool independent) {
+  if (npairs == 0) return;
+  dim3 g(independent ? (unsigned)npairs : 1u);
+  hipLaunchKernelGGL(k_split, g, dim3(256), 0, c->stream, pos, usage, pairs_dev, (int)npairs, d,
+                     independent ? 0 : 1);
+  EMH_HIP(hipGetLastError());
+}
+
+}  // namespace emh

@@ -1,0 +1,221 @@
+/* emeans_hip.h -- C ABI of the MI355X (gfx950) backend of emeans.
+ *
+ * Layer 1 of the reference is the `Device` trait
+ * (crates/emeans-core/src/core/mod.rs:71-178): buffers that live on the
+ * backend plus the ops of one e-means batch. Each `emh_*` entry point below
+ * replaces one method of that trait, or one caller that the reference writes
+ * generically over it, and cites the line it replaces. A Rust shim crate binds
+ * these with `extern "C"` and implements `Device` + `Assigner` on top.
+ *
+ * Conventions (the reference's FFI rules, crates/emeans-ffi/src/lib.rs:26-140):
+ *  - every call returns EMH_OK (0), EMH_INVALID (1, bad argument) or EMH_ERROR (2);
+ *  - on failure nothing is written to the out-parameters and a message for the
+ *    calling thread is available from emh_last_error();
+ *  - no C++ exception crosses the ABI.
+ * Threading: one emh_ctx is one HIP stream on one device and is not thread-safe;
+ * the caller serializes calls on a context (the Rust shim holds `&mut`).
+ * Ordering: ops are queued on the context's stream; only emh_read_* and
+ * emh_sync wait for the device (core/mod.rs:70).
+ */
+#ifndef EMEANS_HIP_H
+#define EMEANS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EMH_OK 0
+#define EMH_INVALID 1
+#define EMH_ERROR 2
+
+/* Metric (crates/emeans-core/src/assign.rs:14-21). */
+#define EMH_L2 0
+#define EMH_IP 1
+
+typedef struct emh_ctx emh_ctx;
+/* A device buffer of f32 or u32 (Device::F / Device::U). */
+typedef struct emh_buf emh_buf;
+
+/* Message of the last failed call on this thread (emeans-ffi/src/lib.rs:95-140). */
+const char* emh_last_error(void);
+
+/* ------------------------------------------------------------------ context */
+/* Backend construction: make_assigner(Backend::Custom{"hip"}) -> the engine
+ * (emeans-cluster/src/backend.rs:170-178; the CUDA analogue is CudaCore::new,
+ * emeans-cuda/src/lib.rs:302-503). Fails with EMH_ERROR when there is no
+ * gfx950 device. */
+int emh_create(int device, emh_ctx** out);
+int emh_destroy(emh_ctx* ctx);
+/* Device::name (core/mod.rs:77): "hip-gfx950". */
+const char* emh_name(const emh_ctx* ctx);
+/* Device::flush (core/mod.rs:93). */
+int emh_flush(emh_ctx* ctx);
+/* Wait for all queued work (the wait half of Device::read_*). */
+int emh_sync(emh_ctx* ctx);
+/* The HIP stream the context queues on (hipStream_t), for interop. */
+void* emh_stream(emh_ctx* ctx);
+
+/* ------------------------------------------------------------------ buffers */
+/* Device::bind (core/mod.rs:81): copy the data set x (len floats) to the device.
+ * Always copies (assign.rs:75-83). */
+int emh_bind(emh_ctx* ctx, const float* x, size_t len, emh_buf** out);
+/* Device::upload_f32 / upload_u32 (core/mod.rs:82-83). */
+int emh_upload_f32(emh_ctx* ctx, const float* v, size_t len, emh_buf** out);
+int emh_upload_u32(emh_ctx* ctx, const uint32_t* v, size_t len, emh_buf** out);
+/* Device::zeros_f32 / zeros_u32 (core/mod.rs:84-85). */
+int emh_zeros_f32(emh_ctx* ctx, size_t len, emh_buf** out);
+int emh_zeros_u32(emh_ctx* ctx, size_t len, emh_buf** out);
+/* Device::write_f32 / write_u32 (core/mod.rs:86-88): b[offset..offset+len] = v,
+ * after queued work that uses b. */
+int emh_write_f32(emh_ctx* ctx, emh_buf* b, size_t offset, const float* v, size_t len);
+int emh_write_u32(emh_ctx* ctx, emh_buf* b, size_t offset, const uint32_t* v, size_t len);
+/* Device::read_f32 / read_u32 (core/mod.rs:89-91): wait, then copy b[lo..hi). */
+int emh_read_f32(emh_ctx* ctx, const emh_buf* b, size_t lo, size_t hi, float* dst);
+int emh_read_u32(emh_ctx* ctx, const emh_buf* b, size_t lo, size_t hi, uint32_t* dst);
+/* Drop of the backend's buffer type. Waits for queued work first. */
+int emh_free(emh_ctx* ctx, emh_buf* b);
+/* A non-owning view of caller device memory (for example a torch tensor) as a
+ * buffer; freeing the view does not free the memory. kind: 0 f32, 1 u32. */
+int emh_wrap(emh_ctx* ctx, void* dev_ptr, size_t len, int kind, emh_buf** out);
+void* emh_buf_ptr(const emh_buf* b);
+size_t emh_buf_len(const emh_buf* b);
+
+/* --------------------------------------------------------------------- ops */
+/* Device::top1 (core/mod.rs:97-112): for every selected position p in
+ * [lo, hi), row x[ids[p]] (ids != NULL) or x[p]; labels[p] = nearest of the k
+ * centroids (largest inner product, or smallest squared L2), ties to the lower
+ * id; scores[p] its score. cnorm (squared centroid norms) is required for L2.
+ * Only positions in [lo, hi) are written. Labels and scores equal the
+ * reference CPU backend's (cpu-fused, assign/fused.rs) bit for bit. */
+int emh_top1(emh_ctx* ctx, const emh_buf* x, size_t d, const emh_buf* ids, size_t lo, size_t hi,
+             const emh_buf* centroids, const emh_buf* cnorm, size_t k, int metric,
+             emh_buf* labels, emh_buf* scores);
+
+/* Device::topk (core/mod.rs:114-124): best kk (<= 16) data rows per query by
+ * inner product, best first (larger score, then lower id); with exclude_self
+ * query i is data row i and is skipped; missing: id 0xFFFFFFFF, score -inf.
+ * Host pointers in and out (the reference signature). */
+int emh_topk(emh_ctx* ctx, const float* queries, size_t m, const float* data, size_t n, size_t d,
+             size_t kk, int exclude_self, uint32_t* ids, float* sims);
+/* The same on device buffers (queries/data resident; ids/sims m*kk). */
+int emh_topk_dev(emh_ctx* ctx, const emh_buf* queries, size_t m, const emh_buf* data, size_t n,
+                 size_t d, size_t kk, int exclude_self, emh_buf* ids, emh_buf* sims);
+
+/* Device::scatter_add (core/mod.rs:126-139): counts[j] = selected rows with
+ * label j, sums[j] = those rows added in selection order in f32 (bit-equal to
+ * the CPU's row-order sums); both overwritten; acc += sums when acc != NULL.
+ * labels are read at the selection positions. */
+int emh_scatter_add(emh_ctx* ctx, const emh_buf* x, size_t d, const emh_buf* ids, size_t lo,
+                    size_t hi, const emh_buf* labels, size_t k, emh_buf* sums, emh_buf* counts,
+                    emh_buf* acc);
+
+/* Device::row_norms (core/mod.rs:141-142): sequential f32 sum of squares. */
+int emh_row_norms(emh_ctx* ctx, const emh_buf* m, size_t rows, size_t d, emh_buf* out);
+
+/* Device::normalize_rows (core/mod.rs:144-151): faiss normalize_into. */
+int emh_normalize_rows(emh_ctx* ctx, const emh_buf* src, size_t rows, size_t d, emh_buf* dst);
+
+/* Device::split (core/mod.rs:153-162): apply a revival plan of npairs
+ * (donor, dead) pairs given as 2*npairs u32 (host memory); bit-equal to
+ * apply_splits (core/mod.rs:374-399). usage has k = emh_buf_len(usage) floats. */
+int emh_split(emh_ctx* ctx, emh_buf* positions, emh_buf* usage, const uint32_t* pairs,
+              size_t npairs, size_t d);
+
+/* Device::ema_update (core/mod.rs:164-177) with EmaStep (core/mod.rs:182-197):
+ * alpha = (float)alpha64, decay = (float)(1 - alpha64), replace = alpha64 == 1. */
+int emh_ema_update(emh_ctx* ctx, emh_buf* positions, emh_buf* usage, const emh_buf* sums,
+                   const emh_buf* counts, size_t k, size_t d, float alpha, float decay,
+                   int replace);
+
+/* ----------------------------------------------- layer 2 and its callers */
+/* Config (crates/emeans-core/src/model.rs:24-76). Zero/negative "has_*" means None. */
+typedef struct emh_config {
+  uint64_t k, d;
+  double nepochs;               /* 5.0 */
+  uint64_t batch_size;          /* 0 = batch law */
+  int has_alpha0;
+  double alpha0;
+  int batch_law;                /* 0 auto, 1 throughput, 2 quality */
+  uint32_t seed;                /* 1234 */
+  int spherical;
+  int has_unused_threshold;
+  double unused_threshold;
+  uint64_t assignment_chunk_size; /* 0 = 65536 */
+  int capture_assignments;
+  int verbose;
+} emh_config;
+
+/* Per-epoch statistics (EpochStats, model.rs:80-89). */
+typedef struct emh_epoch_stats {
+  double obj;
+  double time;
+  double imbalance_factor;
+  uint64_t nsplit;
+} emh_epoch_stats;
+
+/* Results of one training run; arrays are caller-allocated: centroids,
+ * positions k*d, usage k, labels n (may be NULL), stats capacity max_epochs. */
+typedef struct emh_train_out {
+  float* centroids;
+  float* positions;
+  float* usage;
+  int32_t* labels;
+  emh_epoch_stats* stats;
+  uint64_t max_epochs;
+  uint64_t n_epochs;
+  uint64_t n_splits;
+  uint64_t batch_size;
+  double alpha0;
+  uint64_t total_steps;
+  uint64_t fallback_rows; /* rows the exact top-1 kernel rescanned (screen misses) */
+} emh_train_out;
+
+/* Emeans::train (model.rs:700-811) driving the device loop core::train::run
+ * (core/train.rs:60-303) on this context: sampled initial centroids, the
+ * seeded epoch permutations and revival draws on the host, every batch op on
+ * the device. x is n*d host floats, copied to the device once. */
+int emh_train(emh_ctx* ctx, const float* x, size_t n, const emh_config* cfg, emh_train_out* out);
+/* The same with the data already on the device (x: n*d f32 buffer). */
+int emh_train_dev(emh_ctx* ctx, const emh_buf* x, size_t n, const emh_config* cfg,
+                  emh_train_out* out);
+
+/* Emeans::assign (model.rs:898-919) -> assign_all (assign.rs:785-809) ->
+ * assign_on (core/mod.rs:249-330) on this context: labels/scores of every row
+ * of x (n*d host floats) against k centroids. chunk = rows per call (0 = 65536). */
+int emh_assign(emh_ctx* ctx, const float* x, size_t n, size_t d, const float* centroids,
+               size_t k, int metric, size_t chunk, uint32_t* labels, float* scores);
+
+/* knn_self / knn (emeans-cluster/src/knn.rs:17-64) on this context. */
+int emh_knn(emh_ctx* ctx, const float* queries, size_t m, const float* data, size_t n, size_t d,
+            size_t kk, int exclude_self, uint32_t* ids, float* sims);
+
+/* dedup_with_neighbors (emeans-cluster/src/dedup.rs:186-358) on the host, for
+ * rows without timestamps or burst ids. Outputs: group_of[n]; representatives,
+ * anchors, sizes (capacity n, *n_groups used); linked pairs; split components. */
+int emh_dedup_neighbors(const float* x, size_t n, size_t d, const uint32_t* nb_ids,
+                        const float* nb_sims, size_t kk, float sim_threshold,
+                        float rep_threshold, const float* priority, uint32_t* group_of,
+                        uint32_t* representatives, uint32_t* anchors, uint32_t* sizes,
+                        size_t* n_groups, size_t* linked_pairs, size_t* split_components);
+
+/* dedup (dedup.rs:163-183): knn_self on this context, then the host groups. */
+int emh_dedup(emh_ctx* ctx, const float* x, size_t n, size_t d, size_t kk, float sim_threshold,
+              float rep_threshold, const float* priority, uint32_t* group_of,
+              uint32_t* representatives, uint32_t* anchors, uint32_t* sizes, float* nn_sim,
+              size_t* n_groups, size_t* linked_pairs, size_t* split_components);
+
+/* ------------------------------------------------------------ diagnostics */
+/* Rows the exact top-1 / top-k kernels rescanned since the context was made
+ * (the screen's misses; EMEANS_CUDA_SCREEN_STATS analogue, emeans-cuda lib.rs:278-287). */
+uint64_t emh_fallback_rows(emh_ctx* ctx);
+/* Select the top-1 path: 1 = MFMA screen + exact check (default), 0 = exact
+ * kernel only (the reference "FP32 kernel alone", emeans-cuda tests/contract.rs:27-37). */
+int emh_set_screen(emh_ctx* ctx, int on);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* EMEANS_HIP_H */

@@ -1,0 +1,255 @@
+"""Layer-1 parity on the GPU: every Device op against the oracle, bit for bit.
+
+The shapes and inputs are the reference contract's (core/contract.rs:75-161,
+355-554) and the CUDA backend's adversarial near-tie set
+(emeans-cuda/tests/contract.rs:44-152). The bar is the reference CPU
+backend's exact output: labels, scores, sums, EMA, splits and norms
+bit-equal; kNN ids and sims bit-equal to the oracle's fma-chain order.
+"""
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    from emeans_amd import HipDevice
+    d = HipDevice()
+    yield d
+    d.close()
+
+
+def _mix(n, d, centers, sigma, unit, seed):
+    return O.contract_mixture(n, d, centers, sigma, unit, seed).reshape(n, d)
+
+
+def _gpu_top1(dev, x, c, metric, ids=None, rows=None, fill=True):
+    from emeans_amd import Mat, Select
+    n, d = x.shape
+    k = c.shape[0]
+    xb = dev.bind(x)
+    cb = dev.upload_f32(c)
+    cn = None
+    if metric == "l2":
+        cn = dev.zeros_f32(k)
+        dev.row_norms(cb, k, d, cn)
+    n_sel = len(ids) if ids is not None else n
+    lo, hi = rows if rows is not None else (0, n_sel)
+    lab = dev.upload_u32(np.full(n_sel, 0xFFFFFFFF, np.uint32))
+    sco = dev.upload_f32(np.full(n_sel, np.nan, np.float32))
+    idb = dev.upload_u32(ids) if ids is not None else None
+    dev.top1(Mat(xb, d), Select(idb, (lo, hi)), cb, cn, k, metric, lab, sco)
+    return dev.read_u32(lab), dev.read_f32(sco)
+
+
+def _check_top1(dev, x, c, metric, tag):
+    n, d = x.shape
+    perm = ((np.arange(n, dtype=np.uint64) * 7919 + 13) % n).astype(np.uint32)
+    lo, hi = n // 7, n - n // 9
+    for ids in (perm, None):
+        gl, gs = _gpu_top1(dev, x, c, metric, ids=ids, rows=(lo, hi))
+        ol = np.full(n, 0xFFFFFFFF, np.uint32)
+        osc = np.full(n, np.nan, np.float32)
+        O.top1(x, d, c, metric, ids=ids, rows=(lo, hi), labels=ol, scores=osc)
+        # Only the selection is written (contract.rs:225-231).
+        assert np.all(gl[:lo] == 0xFFFFFFFF) and np.all(gl[hi:] == 0xFFFFFFFF), tag
+        assert np.all(np.isnan(gs[:lo])) and np.all(np.isnan(gs[hi:])), tag
+        bad = np.nonzero(gl[lo:hi] != ol[lo:hi])[0]
+        assert bad.size == 0, f"{tag}: {bad.size} labels differ, first at {lo + bad[0]}"
+        assert gs[lo:hi].tobytes() == osc[lo:hi].tobytes(), f"{tag}: scores not bit-equal"
+
+
+CONTRACT_SHAPES = [(1000, 768, 64), (777, 768, 100), (513, 13, 70), (2000, 20, 300),
+                   (300, 64, 1), (600, 768, 1024)]
+
+
+@pytest.mark.parametrize("n,d,k", CONTRACT_SHAPES)
+@pytest.mark.parametrize("metric", ["ip", "l2"])
+def test_top1_contract_shapes(dev, n, d, k, metric):
+    x = _mix(n, d, 11, 0.6, metric == "ip", 3 * n + k)
+    c = (np.resize(x[: min(k, n)].reshape(-1), k * d) * np.float32(0.95)).reshape(k, d)
+    _check_top1(dev, x, c, metric, f"n={n} d={d} k={k} {metric}")
+
+
+@pytest.mark.parametrize("k", [1024, 1000])
+@pytest.mark.parametrize("metric", ["ip", "l2"])
+def test_top1_production_shape_with_duplicates(dev, k, metric):
+    """contract.rs:120-146: 16,384 x 768; the last 256 centroids copy earlier ones."""
+    n, d = 16384, 768
+    x = _mix(n, d, 64, 0.6, metric == "ip", 5 * n + k)
+    base = k - 256
+    c = np.zeros((k, d), np.float32)
+    for j in range(k):
+        c[j] = x[(j * 37) % n] * np.float32(0.95) if j < base else c[(j * 7) % base]
+    gl, gs = _gpu_top1(dev, x, c, metric)
+    ol, osc = O.top1(x, d, c, metric)
+    assert np.array_equal(gl, ol)
+    assert gs.tobytes() == osc.tobytes()
+    # Exact duplicates: the lower id wins (contract.rs:237-243).
+    assert np.all(gl < base)
+
+
+def _noise(i):
+    i = np.asarray(i, np.uint64)
+    with np.errstate(over="ignore"):
+        h = i * np.uint64(0x9E3779B97F4A7C15)
+        h = ((h << np.uint64(29)) | (h >> np.uint64(35))) ^ np.uint64(0xD1B54A32D192ED03)
+        h = h * np.uint64(0x94D049BB133111EB)
+    return (h >> np.uint64(11)).astype(np.float64) / float(1 << 52) - 1.0
+
+
+@pytest.mark.parametrize("n,d,k", [(4000, 768, 512), (3000, 72, 256)])
+@pytest.mark.parametrize("metric", ["ip", "l2"])
+def test_screen_bit_equal_on_near_ties(dev, n, d, k, metric):
+    """emeans-cuda/tests/contract.rs:44-152: crowds of 32 centroids within 1e-6,
+    pairs within 1e-6, exact duplicates, rows scaled 1, 1e3, 1e-3, 1e-15."""
+    crowds, pairs = k // 2 // 32, k // 2 // 2
+    groups = crowds + pairs
+    bases = _mix(groups, d, groups, 0.0, True, 21)
+    c = np.zeros((k, d), np.float32)
+    for j in range(k):
+        if j < k // 2:
+            g, first, dup = j // 32, j % 32 == 0, j % 32 == 31
+        else:
+            q = (j - k // 2) // 2
+            g, first, dup = crowds + q, j % 2 == 0, j % 2 == 1 and q % 2 == 1
+        if dup:
+            c[j] = c[j - 31 if j < k // 2 else j - 1]
+        elif first:
+            c[j] = bases[g]
+        else:
+            t = np.arange(d)
+            c[j] = (bases[g].astype(np.float64) * (1.0 + 1e-6 * _noise(j * d + t))).astype(np.float32)
+    rows = _mix(n, d, groups, 0.05, True, 21)
+    scale = np.array([1.0, 1e3, 1e-3, 1e-15], np.float32)[np.arange(n) % 4]
+    x = (rows * scale[:, None]).astype(np.float32)
+    perm = ((np.arange(n, dtype=np.uint64) * 7919 + 5) % n).astype(np.uint32)
+    outs = []
+    for screen in (True, False):
+        dev.set_screen(screen)
+        outs.append(_gpu_top1(dev, x, c, metric, ids=perm))
+    dev.set_screen(True)
+    assert np.array_equal(outs[0][0], outs[1][0]), "screen vs exact kernel labels"
+    assert outs[0][1].tobytes() == outs[1][1].tobytes(), "screen vs exact kernel scores"
+    ol, osc = O.top1(x, d, c, metric, ids=perm)
+    assert np.array_equal(outs[0][0], ol)
+    assert outs[0][1].tobytes() == osc.tobytes()
+
+
+def test_screen_fallback_is_rare_on_separated_data(dev):
+    """On data without near-ties the exact kernel rescans few rows."""
+    n, d, k = 16384, 768, 1024
+    x = _mix(n, d, 64, 0.6, False, 99)
+    c = x[(np.arange(k) * 13) % n] * np.float32(0.95)
+    before = dev.fallback_rows()
+    gl, gs = _gpu_top1(dev, x, c, "l2")
+    rescanned = dev.fallback_rows() - before
+    ol, osc = O.top1(x, d, c, "l2")
+    assert np.array_equal(gl, ol) and gs.tobytes() == osc.tobytes()
+    assert rescanned <= n // 20, rescanned
+
+
+@pytest.mark.parametrize("n,d,k", CONTRACT_SHAPES)
+def test_scatter_ema_split(dev, n, d, k):
+    """contract.rs:355-497 on the contract's shapes, bit-equal to the CPU order."""
+    from emeans_amd import EmaStep, Mat, Select
+    k = min(k, n)
+    x = _mix(n, d, 7, 0.5, False, n + d)
+    live = max(k - k // 5, 1)
+    labels = (((np.arange(n, dtype=np.uint64) * 2654435761) % 2**32 >> 7) % live).astype(np.uint32)
+    perm = ((np.arange(n, dtype=np.uint64) * 31 + 5) % n).astype(np.uint32)
+    lo, hi = n // 5, n
+    acc0 = ((np.arange(k * d) % 13) * 0.25).astype(np.float32)
+    xb, idb, lb = dev.bind(x), dev.upload_u32(perm), dev.upload_u32(labels)
+    sums = dev.upload_f32(np.full(k * d, 7.0, np.float32))
+    counts = dev.upload_u32(np.full(k, 3, np.uint32))
+    acc = dev.upload_f32(acc0)
+    dev.scatter_add(Mat(xb, d), Select(idb, (lo, hi)), lb, k, sums, counts, acc)
+    gs, gc, ga = dev.read_f32(sums), dev.read_u32(counts), dev.read_f32(acc)
+    oacc = acc0.copy()
+    os_, oc = O.scatter_add(x, d, labels, k, ids=perm, rows=(lo, hi), acc=oacc)
+    assert np.array_equal(gc, oc)
+    assert gs.tobytes() == os_.tobytes()
+    assert ga.tobytes() == oacc.tobytes()
+    pos0 = x.reshape(-1)[: k * d].copy()
+    for alpha, u0 in [(0.37, 0.8), (1.0, 0.5), (0.9, 0.0)]:
+        usage0 = (u0 + (np.arange(k) % 5) * 0.125).astype(np.float32)
+        p, u = dev.upload_f32(pos0), dev.upload_f32(usage0)
+        dev.ema_update(p, u, sums, counts, k, d, EmaStep.new(alpha))
+        wp, wu = pos0.copy(), usage0.copy()
+        O.ema_update(wp, wu, gs, gc, k, d, alpha)
+        assert dev.read_f32(p).tobytes() == wp.tobytes(), alpha
+        assert dev.read_f32(u).tobytes() == wu.tobytes(), alpha
+    pos1 = pos0.copy()
+    if k >= 4:
+        pos1[d:2 * d] = 0.0
+    usage1 = (1.0 + np.arange(k) * 0.37).astype(np.float32)
+    plan = [(j, k - 1 - j) for j in range(k // 2) if j % 3 != 2 and j != k - 1 - j]
+    p, u = dev.upload_f32(pos1), dev.upload_f32(usage1)
+    dev.split(p, u, plan, d)
+    wp, wu = pos1.copy(), usage1.copy()
+    O.apply_splits(wp, wu, d, plan)
+    assert dev.read_f32(p).tobytes() == wp.tobytes()
+    assert dev.read_f32(u).tobytes() == wu.tobytes()
+
+
+@pytest.mark.parametrize("d", [768, 20, 13, 64, 2500])
+def test_norms_and_normalize(dev, d):
+    """contract.rs:500-554: a zero row and a 1e30-scaled row (the max-prescale path)."""
+    rows = 300
+    m = _mix(rows, d, 7, 0.5, False, 1000 + d)
+    m[0] = 0.0
+    m[1] *= np.float32(1e30)
+    mb = dev.upload_f32(m)
+    nb = dev.zeros_f32(rows)
+    dev.row_norms(mb, rows, d, nb)
+    with np.errstate(over="ignore"):
+        assert dev.read_f32(nb).tobytes() == O.row_norms(m, rows, d).tobytes()
+    ub = dev.zeros_f32(rows * d)
+    dev.normalize_rows(mb, rows, d, ub)
+    assert dev.read_f32(ub).tobytes() == O.normalize_rows(m, rows, d).tobytes()
+
+
+def test_split_zero_row_nudge_and_sequential_plan(dev):
+    """The child-nudge path on an all-zero donor, and a plan that reuses a centroid."""
+    k, d = 8, 5
+    pos = np.arange(k * d, dtype=np.float32) * 0.5
+    pos[:d] = 0.0
+    usage = np.arange(1, k + 1, dtype=np.float32)
+    for plan in ([(0, 7), (1, 6)], [(1, 2), (2, 3), (3, 1)]):
+        p, u = dev.upload_f32(pos), dev.upload_f32(usage)
+        dev.split(p, u, plan, d)
+        wp, wu = pos.copy(), usage.copy()
+        O.apply_splits(wp, wu, d, plan)
+        assert dev.read_f32(p).tobytes() == wp.tobytes(), plan
+        assert dev.read_f32(u).tobytes() == wu.tobytes(), plan
+
+
+@pytest.mark.parametrize("m,n,d,kk", [(300, 300, 768, 16), (200, 900, 20, 5), (130, 7, 33, 10)])
+def test_topk_contract_shapes(dev, m, n, d, kk):
+    """contract.rs:103-110 shapes: ids and sims bit-equal to the oracle (fma-chain dots)."""
+    data = _mix(n, d, 9, 0.3, True, m + n)
+    q = _mix(m, d, 9, 0.3, True, m * 7 + n)
+    gi, gs = dev.topk(q, data, d, kk, False)
+    oi, osims = O.knn(q, data, d, kk, False)
+    assert np.array_equal(gi, oi) and gs.tobytes() == osims.tobytes()
+    if m == n:
+        gi, gs = dev.topk(data, data, d, kk, True)
+        oi, osims = O.knn(data, data, d, kk, True)
+        assert np.array_equal(gi, oi) and gs.tobytes() == osims.tobytes()
+
+
+def test_topk_production_duplicates(dev):
+    """contract.rs:147-159: 64 queries vs 16,384 rows with 512 duplicated rows, k = 16."""
+    n, d = 16384, 768
+    data = _mix(n, d, 9, 0.3, True, 77)
+    for j in range(8192, 8192 + 512):
+        data[j] = data[j - 8000]
+    q = np.stack([data[192 + i] if i % 2 == 0 else data[(i * 61) % n] for i in range(64)])
+    gi, gs = dev.topk(q, data, d, 16, False)
+    oi, osims = O.knn(q, data, d, 16, False)
+    assert np.array_equal(gi, oi) and gs.tobytes() == osims.tobytes()
