@@ -233,6 +233,41 @@ class HipDevice:
                                _p(labels), _p(scores)))
         return labels, scores
 
+    def assign_dev(self, x: DevBuf, n: int, d: int, centroids: DevBuf, k: int, metric,
+                   labels: DevBuf, scores: DevBuf, chunk: int = 65536):
+        """assign_on with rows, centroids and outputs resident on the device."""
+        check(lib().emh_assign_dev(self._ctx, x.h, n, d, centroids.h, k, _metric(metric), chunk,
+                                   labels.h, scores.h))
+
+    def train_dev(self, x: DevBuf, n: int, config: "Config"):
+        """Emeans::train on data already bound to the device; returns (centroids, info)."""
+        k, d = config.k, config.d
+        cent = np.empty(k * d, np.float32)
+        pos = np.empty(k * d, np.float32)
+        usage = np.empty(k, np.float32)
+        labels = np.empty(n, np.int32)
+        stats = (_CEpoch * 64)()
+        out = _CTrainOut(_p(cent), _p(pos), _p(usage), _p(labels), C.addressof(stats), 64)
+        ccfg = config._c()
+        check(lib().emh_train_dev(self._ctx, x.h, n, C.byref(ccfg), C.byref(out)))
+        info = {"stats": [EpochStats(stats[e].obj, stats[e].time, stats[e].imbalance_factor,
+                                     int(stats[e].nsplit)) for e in range(out.n_epochs)],
+                "n_splits": int(out.n_splits), "batch_size": int(out.batch_size),
+                "alpha0": out.alpha0, "total_steps": int(out.total_steps),
+                "fallback_rows": int(out.fallback_rows), "positions": pos, "usage": usage,
+                "labels": labels}
+        return cent, info
+
+    def profile(self, on: bool):
+        """Time each MFMA screen launch with HIP events on the context's stream."""
+        check(lib().emh_profile(self._ctx, int(on)))
+
+    def profile_read(self):
+        """(total ms, launches, algorithmic FLOP) of the timed screen launches; resets."""
+        ms, n, fl = C.c_double(), C.c_uint64(), C.c_double()
+        check(lib().emh_profile_read(self._ctx, C.byref(ms), C.byref(n), C.byref(fl)))
+        return ms.value, n.value, fl.value
+
     def fallback_rows(self) -> int:
         return lib().emh_fallback_rows(self._ctx)
 

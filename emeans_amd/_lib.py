@@ -80,6 +80,9 @@ SIGNATURES = {
     "emh_train": (_i, [_vp, _vp, _sz, _vp, _vp]),
     "emh_train_dev": (_i, [_vp, _vp, _sz, _vp, _vp]),
     "emh_assign": (_i, [_vp, _vp, _sz, _sz, _vp, _sz, _i, _sz, _vp, _vp]),
+    "emh_assign_dev": (_i, [_vp, _vp, _sz, _sz, _vp, _sz, _i, _sz, _vp, _vp]),
+    "emh_profile": (_i, [_vp, _i]),
+    "emh_profile_read": (_i, [_vp, C.POINTER(_d), C.POINTER(_u64), C.POINTER(_d)]),
     "emh_knn": (_i, [_vp, _vp, _sz, _vp, _sz, _sz, _sz, _i, _vp, _vp]),
     "emh_dedup_neighbors": (_i, [_vp, _sz, _sz, _vp, _vp, _sz, _f, _f, _vp, _vp, _vp, _vp, _vp,
                                  C.POINTER(_sz), C.POINTER(_sz), C.POINTER(_sz)]),

@@ -465,4 +465,34 @@ int emh_set_screen(emh_ctx* c, int on) {
   });
 }
 
+int emh_profile(emh_ctx* c, int on) {
+  return guard([&] {
+    EMH_ENSURE(c, "null context");
+    c->prof = on != 0;
+  });
+}
+
+int emh_profile_read(emh_ctx* c, double* ms, uint64_t* launches, double* flop) {
+  return guard([&] {
+    EMH_ENSURE(c && ms && launches && flop, "null argument");
+    use_device(c);
+    EMH_HIP(hipStreamSynchronize(c->stream));
+    double t = 0.0, f = 0.0;
+    for (auto& e : c->timed) {
+      float m = 0.f;
+      EMH_HIP(hipEventElapsedTime(&m, e.a, e.b));
+      t += m;
+      f += e.flop;
+    }
+    *ms = t;
+    *launches = c->timed.size();
+    *flop = f;
+    for (auto& e : c->timed) {
+      (void)hipEventDestroy(e.a);
+      (void)hipEventDestroy(e.b);
+    }
+    c->timed.clear();
+  });
+}
+
 }  // extern "C"

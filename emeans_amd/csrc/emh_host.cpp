@@ -661,6 +661,31 @@ int emh_assign(emh_ctx* c, const float* x, size_t n, size_t d, const float* cent
   });
 }
 
+int emh_assign_dev(emh_ctx* c, const emh_buf* x, size_t n, size_t d, const emh_buf* cents,
+                   size_t k, int metric, size_t chunk, emh_buf* labels, emh_buf* scores) {
+  return guard2([&] {
+    EMH_ENSURE(c && x && cents && labels && scores, "null argument");
+    EMH_ENSURE(d > 0 && k > 0, "d and k must be positive");
+    EMH_ENSURE(metric == EMH_L2 || metric == EMH_IP, "unknown metric");
+    EMH_ENSURE(x->kind == 0 && cents->kind == 0 && scores->kind == 0 && labels->kind == 1,
+               "buffer kinds: x, centroids, scores f32; labels u32");
+    EMH_ENSURE(x->len >= n * d && cents->len >= k * d, "x n x d, centroids k x d");
+    EMH_ENSURE(labels->len >= n && scores->len >= n, "outputs too short");
+    if (n == 0) return;
+    EMH_HIP(hipSetDevice(c->device));
+    chunk = chunk ? chunk : 65536;
+    Buf cn(c, metric == EMH_L2 ? k * 4 : 0);
+    if (metric == EMH_L2) emh::launch_row_norms(c, (const float*)cents->ptr, k, d, cn.f());
+    for (size_t b = 0; b < n; b += chunk) {
+      const size_t e = std::min(b + chunk, n);
+      emh::launch_top1(c, (const float*)x->ptr, n, d, nullptr, b, e, (const float*)cents->ptr,
+                       metric == EMH_L2 ? cn.f() : nullptr, k, metric == EMH_IP,
+                       (uint32_t*)labels->ptr, (float*)scores->ptr);
+    }
+    EMH_HIP(hipStreamSynchronize(c->stream));  // cn is freed on return
+  });
+}
+
 int emh_knn(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,
             size_t kk, int exclude_self, uint32_t* ids, float* sims) {
   return emh_topk(c, q, m, data, n, d, kk, exclude_self, ids, sims);

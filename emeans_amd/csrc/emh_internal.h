@@ -98,11 +98,35 @@ struct emh_ctx {
   uint64_t fallback_total = 0;
   emh::Scratch cand, fblist, order, start, misc, knn_tmp;
   std::string name = "hip-gfx950";
+  // Screen-kernel timing (emh_profile): event pairs and the FLOP each covers.
+  bool prof = false;
+  struct Timed {
+    hipEvent_t a, b;
+    double flop;
+  };
+  std::vector<Timed> timed;
 };
 
 namespace emh {
 
 inline dim3 grid1(size_t n, int per) { return dim3((unsigned)((n + per - 1) / per)); }
+
+// Brackets one kernel launch with events when profiling is on.
+struct ProfScope {
+  emh_ctx* c;
+  hipEvent_t a = nullptr, b = nullptr;
+  double flop;
+  ProfScope(emh_ctx* ctx, double f) : c(ctx), flop(f) {
+    if (!c->prof) return;
+    EMH_HIP(hipEventCreate(&a));
+    EMH_HIP(hipEventCreate(&b));
+    EMH_HIP(hipEventRecord(a, c->stream));
+  }
+  ~ProfScope() {
+    if (!c->prof || !a) return;
+    if (hipEventRecord(b, c->stream) == hipSuccess) c->timed.push_back({a, b, flop});
+  }
+};
 
 // ---- launchers (emh_ops.hip)
 void launch_fill_u32(emh_ctx* c, uint32_t* p, size_t n, uint32_t v);

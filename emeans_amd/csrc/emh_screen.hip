@@ -758,6 +758,7 @@ void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t
                      ip ? nullptr : cnorm, c->small);
   EMH_HIP(hipGetLastError());
   const unsigned blocks = (unsigned)(row_tiles * parts);
+  ProfScope prof(c, 2.0 * (double)n * (double)k * (double)d);
   if (ip)
     hipLaunchKernelGGL((k_screen<2, L1, false, false>), dim3(blocks), dim3(256), 0, c->stream, x,
                        nx, (int)d, ids, lo, (int)n, cents, cnorm, (int)k, tpp, parts, ntiles, vec4,
@@ -796,6 +797,7 @@ void launch_topk(emh_ctx* c, const float* q, size_t m, const float* data, size_t
     hipLaunchKernelGGL(k_prep, grid1(n, 4), dim3(256), 0, c->stream, data, (int)n, (int)d,
                        nullptr, c->small);
     EMH_HIP(hipGetLastError());
+    ProfScope prof(c, 2.0 * (double)m * (double)n * (double)d);
     if (exclude_self)
       hipLaunchKernelGGL((k_screen<1, LK, false, true>), dim3((unsigned)(row_tiles * parts)),
                          dim3(256), 0, c->stream, q, m, (int)d, nullptr, (size_t)0, (int)m, data,

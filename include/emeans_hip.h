@@ -188,6 +188,13 @@ int emh_train_dev(emh_ctx* ctx, const emh_buf* x, size_t n, const emh_config* cf
 int emh_assign(emh_ctx* ctx, const float* x, size_t n, size_t d, const float* centroids,
                size_t k, int metric, size_t chunk, uint32_t* labels, float* scores);
 
+/* assign_on with everything resident on the device: labels/scores (n entries)
+ * of the n rows of x against k centroids (k*d f32 buffer), in chunks of
+ * `chunk` rows (0 = 65536); L2 centroid norms are computed on the device
+ * (row_norms, as assign_on does, core/mod.rs:265-272). */
+int emh_assign_dev(emh_ctx* ctx, const emh_buf* x, size_t n, size_t d, const emh_buf* centroids,
+                   size_t k, int metric, size_t chunk, emh_buf* labels, emh_buf* scores);
+
 /* knn_self / knn (emeans-cluster/src/knn.rs:17-64) on this context. */
 int emh_knn(emh_ctx* ctx, const float* queries, size_t m, const float* data, size_t n, size_t d,
             size_t kk, int exclude_self, uint32_t* ids, float* sims);
@@ -214,6 +221,11 @@ uint64_t emh_fallback_rows(emh_ctx* ctx);
 /* Select the top-1 path: 1 = MFMA screen + exact check (default), 0 = exact
  * kernel only (the reference "FP32 kernel alone", emeans-cuda tests/contract.rs:27-37). */
 int emh_set_screen(emh_ctx* ctx, int on);
+/* Time every launch of the MFMA screen kernel (top-1 and top-k) with HIP events
+ * on the context's stream while on; emh_profile_read waits, sums and resets:
+ * total milliseconds, launches, and algorithmic FLOP (2 rows k d per launch). */
+int emh_profile(emh_ctx* ctx, int on);
+int emh_profile_read(emh_ctx* ctx, double* ms, uint64_t* launches, double* flop);
 
 #ifdef __cplusplus
 }
