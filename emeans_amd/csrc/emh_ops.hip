@@ -24,6 +24,25 @@ __global__ __launch_bounds__(256) void k_fill_u32(uint32_t* p, size_t n, uint32_
   if (i < n) p[i] = v;
 }
 
+// s + v[0] + v[1] + ... in order (one lane), with 8 LDS reads in flight.
+__device__ __forceinline__ float seq_add(const float* v, int len, float s) {
+  int t = 0;
+  for (; t + 32 <= len; t += 32) {
+    float4 q[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) q[u] = *reinterpret_cast<const float4*>(v + t + 4 * u);
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      s = s + q[u].x;
+      s = s + q[u].y;
+      s = s + q[u].z;
+      s = s + q[u].w;
+    }
+  }
+  for (; t < len; t++) s = s + v[t];
+  return s;
+}
+
 // Sequential sum of rounded squares of row r (assign.rs:150-155): the lanes of
 // wave w square one chunk into sq[w]; lane 0 adds the chunk in column order.
 __device__ float seq_sq_sum(const float* row, size_t d, float* sq, int lane) {
@@ -37,17 +56,7 @@ __device__ float seq_sq_sum(const float* row, size_t d, float* sq, int lane) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (lane == 0) {
-      int t = 0;
-      for (; t + 4 <= len; t += 4) {
-        float4 q = *reinterpret_cast<const float4*>(sq + t);
-        s = s + q.x;
-        s = s + q.y;
-        s = s + q.z;
-        s = s + q.w;
-      }
-      for (; t < len; t++) s = s + sq[t];
-    }
+    if (lane == 0) s = seq_add(sq, len, s);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -94,17 +103,7 @@ __global__ __launch_bounds__(256) void k_normalize_rows(const float* __restrict_
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (lane == 0) {
-      int t = 0;
-      for (; t + 4 <= len; t += 4) {
-        float4 q = *reinterpret_cast<const float4*>(&sq[w][t]);
-        s = s + q.x;
-        s = s + q.y;
-        s = s + q.z;
-        s = s + q.w;
-      }
-      for (; t < len; t++) s = s + sq[w][t];
-    }
+    if (lane == 0) s = seq_add(sq[w], len, s);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");

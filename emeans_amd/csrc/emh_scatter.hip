@@ -59,33 +59,66 @@ __global__ __launch_bounds__(1024) void k_scan(const uint32_t* __restrict__ coun
 }
 
 // Stable placement: wave j walks positions lo..hi in order; rows with label j
-// go to rid[start[j] + rank], rank = number of earlier such rows.
-__global__ __launch_bounds__(256) void k_place(const uint32_t* __restrict__ labels,
-                                               const uint32_t* __restrict__ ids, size_t nx,
-                                               size_t lo, size_t hi, size_t k,
-                                               const uint32_t* __restrict__ start,
-                                               uint32_t* __restrict__ rid,
-                                               uint32_t* __restrict__ small) {
-  int lane = threadIdx.x % WAVE;
-  size_t j = (size_t)blockIdx.x * 4 + threadIdx.x / WAVE;
-  if (j >= k) return;
-  uint32_t base = start[j];
-  const uint32_t end = start[j + 1];
-  for (size_t p0 = lo; p0 < hi && base < end; p0 += WAVE) {
-    size_t p = p0 + lane;
-    bool mine = p < hi && labels[p] == (uint32_t)j;
-    uint64_t m = __ballot(mine);
-    if (mine) {
-      uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
-                                                __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-      uint32_t r = ids ? ids[p] : (uint32_t)p;
-      if (r >= nx) {  // a bad id adds nothing; reported at the next read
-        small[SW_BAD_ID] = 1;
-        r = 0xffffffffu;
+// go to rid[start[j] + rank], rank = number of earlier such rows. The block's
+// waves share the labels, staged in LDS a segment of SEG at a time.
+constexpr int SEG = 16384;
+constexpr int PW = 4;  // waves (clusters) per block: k / 4 blocks spread over the CUs
+__global__ __launch_bounds__(64 * PW) void k_place(const uint32_t* __restrict__ labels,
+                                                const uint32_t* __restrict__ ids, size_t nx,
+                                                size_t lo, size_t hi, size_t k,
+                                                const uint32_t* __restrict__ start,
+                                                uint32_t* __restrict__ rid,
+                                                uint32_t* __restrict__ small) {
+  __shared__ uint32_t lab[SEG];
+  const int lane = threadIdx.x % WAVE;
+  const size_t j = (size_t)blockIdx.x * PW + threadIdx.x / WAVE;
+  uint32_t base = 0, end = 0;
+  if (j < k) {
+    base = start[j];
+    end = start[j + 1];
+  }
+  for (size_t s0 = lo; s0 < hi; s0 += SEG) {
+    const int len = (int)min((size_t)SEG, hi - s0);
+    __syncthreads();
+    for (int i0 = threadIdx.x; i0 < len; i0 += blockDim.x * 8) {  // 8 loads in flight
+      uint32_t v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int i = i0 + (int)blockDim.x * u;
+        v[u] = i < len ? labels[s0 + i] : 0u;
       }
-      rid[base + rank] = r;
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int i = i0 + (int)blockDim.x * u;
+        if (i < len) lab[i] = v[u];
+      }
     }
-    base += (uint32_t)__popcll(m);
+    __syncthreads();
+    for (int p0 = 0; p0 < len && base < end; p0 += 4 * WAVE) {
+      uint32_t l[4];
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const int i = p0 + u * WAVE + lane;
+        l[u] = i < len ? lab[i] : 0xffffffffu;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const bool mine = l[u] == (uint32_t)j;
+        const uint64_t m = __ballot(mine);
+        if (mine) {
+          const uint32_t rank = __builtin_amdgcn_mbcnt_hi(
+              (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+          const size_t p = s0 + p0 + u * WAVE + lane;
+          uint32_t r = ids ? ids[p] : (uint32_t)p;
+          if (r >= nx) {  // a bad id adds nothing; reported at the next read
+            small[SW_BAD_ID] = 1;
+            r = 0xffffffffu;
+          }
+          rid[base + rank] = r;
+        }
+        base += (uint32_t)__popcll(m);
+      }
+    }
   }
 }
 
@@ -136,8 +169,8 @@ void launch_scatter(emh_ctx* c, const float* x, size_t nx, size_t d, const uint3
   hipLaunchKernelGGL(k_scan, dim3(1), dim3(1024), 0, c->stream, counts, k, start);
   EMH_HIP(hipGetLastError());
   if (n > 0) {
-    hipLaunchKernelGGL(k_place, grid1(k, 4), dim3(256), 0, c->stream, labels, ids, nx, lo, hi, k,
-                       start, rid, c->small);
+    hipLaunchKernelGGL(k_place, grid1(k, PW), dim3(64 * PW), 0, c->stream, labels, ids, nx, lo,
+                       hi, k, start, rid, c->small);
     EMH_HIP(hipGetLastError());
   }
   dim3 g((unsigned)k, (unsigned)((d + 255) / 256));

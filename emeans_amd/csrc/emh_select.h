@@ -1,0 +1,88 @@
+// Device helpers shared by the MFMA screen (emh_screen.hip) and the exact
+// check kernels (emh_verify.hip) of top-1 and top-k, and their launchers.
+#pragma once
+
+#include "emh_internal.h"
+
+namespace emh {
+
+constexpr uint32_t NONE = 0xffffffffu;
+constexpr int L1 = 9;    // top-1 list: 8 candidates + the bound
+constexpr int LK = 24;   // top-k list: kk <= 16 plus 7 spare + the bound
+constexpr int KMAX = 16;  // largest kk (emeans-core/src/knn.rs:16)
+constexpr int MAX_PARTS = 8;  // centroid parts per row tile: lists per row the verify merges
+
+// A screen candidate: key (smaller is better: -dot for IP, |c|^2 - 2 dot for L2) and id.
+struct Cand {
+  float key;
+  uint32_t id;
+};
+
+// Insert (v, j) into an ascending list of L keys that keeps the L smallest.
+template <int L>
+__device__ __forceinline__ void insert(float (&key)[L], uint32_t (&id)[L], float v, uint32_t j) {
+  if (!(v < key[L - 1])) return;
+  key[L - 1] = v;
+  id[L - 1] = j;
+#pragma unroll
+  for (int e = L - 1; e > 0; e--) {
+    bool sw = key[e] < key[e - 1];
+    float a = key[e - 1], b = key[e];
+    uint32_t ia = id[e - 1], ib = id[e];
+    key[e - 1] = sw ? b : a;
+    key[e] = sw ? a : b;
+    id[e - 1] = sw ? ib : ia;
+    id[e] = sw ? ia : ib;
+  }
+}
+
+// Screen error bound E on |key' - key| for one row (see emh_screen.hip):
+// xn and cmax2 are squared norms summed in any order (relative error <= gamma_d,
+// absorbed by the (1 + g) factors); cnmax bounds the given centroid norms.
+__device__ __forceinline__ float screen_bound(float xn, float cmax2, float cnmax, int d, bool l2) {
+  const float u = 5.9604645e-08f;  // 2^-24
+  const float du = (float)d * u;
+  const float g = du / (1.0f - du);
+  const float S = (sqrtf(xn) * (1.0f + g)) * (sqrtf(cmax2) * (1.0f + g));
+  const float edot = 3.0f * g * S + (float)d * 4.7019774e-38f;  // + d 2^-124
+  float e = l2 ? 2.0f * edot + 2.0f * u * (cnmax + 2.0f * S) : edot;
+  return e * 1.125f;
+}
+
+// IEEE total order of f32 as a signed integer (f32::total_cmp).
+__device__ __forceinline__ int32_t total_key(float v) {
+  int32_t b = __float_as_int(v);
+  return b ^ (int32_t)(((uint32_t)(b >> 31)) >> 1);
+}
+
+// Merge a row's parts' lists (parts x L entries, laid out [part][L]) into one
+// ascending list of L.
+template <int L>
+__device__ __forceinline__ void merge_parts(const Cand* c, int parts, float (&key)[L],
+                                            uint32_t (&id)[L]) {
+#pragma unroll
+  for (int e = 0; e < L; e++) {
+    key[e] = INFINITY;
+    id[e] = NONE;
+  }
+  for (int q = 0; q < parts * L; q++) {
+    const Cand v = c[q];
+    if (v.id != NONE) insert<L>(key, id, v.key, v.id);
+  }
+}
+
+// ---- launchers of emh_verify.hip
+void launch_verify1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
+                    size_t lo, size_t n, const float* cents, const float* cnorm, size_t k, bool ip,
+                    const Cand* cand, int parts, uint32_t* labels, float* scores, uint32_t* fb);
+// Exact scan of rows `list[0..*count)` (list != nullptr) or positions lo..lo+n.
+void launch_exact1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
+                   size_t lo, size_t n, const uint32_t* list, const float* cents,
+                   const float* cnorm, size_t k, bool ip, uint32_t* labels, float* scores);
+void launch_verifyk(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,
+                    size_t kk, const Cand* cand, int parts, uint32_t* ids, float* sims,
+                    uint32_t* fb);
+void launch_exactk(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,
+                   size_t kk, bool exclude_self, const uint32_t* fb, uint32_t* ids, float* sims);
+
+}  // namespace emh
