@@ -18,7 +18,7 @@ CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libemeans_hip.so")
 OBJ = os.path.join(HERE, "_obj")
 SOURCES = ["emh_api.cpp", "emh_host.cpp", "emh_ops.hip", "emh_scatter.hip", "emh_screen.hip",
-           "emh_verify.hip"]
+           "emh_rescore.hip", "emh_verify.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = [

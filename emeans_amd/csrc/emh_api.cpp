@@ -136,7 +136,8 @@ int emh_destroy(emh_ctx* c) {
     if (!c) return;
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
-    for (emh::Scratch* s : {&c->cand, &c->fblist, &c->order, &c->start, &c->misc, &c->knn_tmp})
+    for (emh::Scratch* s : {&c->cand, &c->fblist, &c->order, &c->start, &c->misc, &c->knn_tmp,
+                            &c->xnorm})
       s->release();
     if (c->small) (void)hipFree(c->small);
     (void)hipStreamDestroy(c->stream);

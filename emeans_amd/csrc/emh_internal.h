@@ -96,7 +96,7 @@ struct emh_ctx {
   int screen = 1;
   uint32_t* small = nullptr;  // SW_WORDS u32 on the device
   uint64_t fallback_total = 0;
-  emh::Scratch cand, fblist, order, start, misc, knn_tmp;
+  emh::Scratch cand, fblist, order, start, misc, knn_tmp, xnorm;
   std::string name = "hip-gfx950";
   // Screen-kernel timing (emh_profile): event pairs and the FLOP each covers.
   bool prof = false;
@@ -144,12 +144,11 @@ void launch_scatter(emh_ctx* c, const float* x, size_t nx, size_t d, const uint3
                     size_t hi, const uint32_t* labels, size_t k, float* sums, uint32_t* counts,
                     float* acc);
 
-// ---- emh_top1.hip
+// ---- emh_screen.hip (top-1 and top-k orchestration)
 void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids, size_t lo, size_t hi,
                  const float* cents, const float* cnorm, size_t k, bool ip, uint32_t* labels,
                  float* scores);
 
-// ---- emh_topk.hip
 void launch_topk(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,
                  size_t kk, bool exclude_self, uint32_t* ids, float* sims);
 

@@ -1,6 +1,6 @@
 // Fused top-1 (Device::top1, core/mod.rs:97-112) and exact top-k
 // (Device::topk, core/mod.rs:114-124) for gfx950: the MFMA screen and the
-// orchestration of the exact stages (emh_verify.hip).
+// orchestration of the check (emh_rescore.hip) and exact scans (emh_verify.hip).
 //
 // Exactness: the reference CPU backend (cpu-fused, assign/fused.rs) scores
 // every (row, centroid) pair with one sequential f32 fma chain over the d
@@ -78,7 +78,7 @@ __global__ __launch_bounds__(256, 2) void k_screen(
     const float* __restrict__ x, size_t nx, int d, const uint32_t* __restrict__ ids, size_t lo,
     int nrows, const float* __restrict__ cents, const float* __restrict__ cnorm, int k,
     int tiles_per_part, int parts, int ntiles, Cand* __restrict__ cand,
-    uint32_t* __restrict__ small) {
+    uint32_t* __restrict__ small, float* __restrict__ xnorm) {
   constexpr int TR = 64 * WN;
   constexpr int XL = TR * BK / 4 / 256;  // float4 loads per thread per slab (rows)
   constexpr int CL = TC * BK / 4 / 256;  // float4 loads per thread per slab (centroids)
@@ -162,6 +162,11 @@ __global__ __launch_bounds__(256, 2) void k_screen(
 #pragma unroll
   for (int u = 0; u < CL; u++) csq[u] = 0.f;
   uint32_t cmax_bits = 0, cnmax_bits = 0;
+  // Each row's |x|^2 in any order (for the verify's bound), summed while the
+  // first tile streams the rows through; written by the blocks of part 0.
+  float xsq[XL];
+#pragma unroll
+  for (int u = 0; u < XL; u++) xsq[u] = 0.f;
   auto gload = [&]() {
     const int col = ls * BK + c4;
 #pragma unroll
@@ -180,9 +185,11 @@ __global__ __launch_bounds__(256, 2) void k_screen(
     const int col = ls * BK + c4;
     const bool tail = col + 4 > d;
 #pragma unroll
-    for (int u = 0; u < XL; u++)
-      *reinterpret_cast<float4*>(&Xs[buf][((tid >> 3) + 32 * u) * LDK + c4]) =
-          tail ? mask4(xr[u], col, d) : xr[u];
+    for (int u = 0; u < XL; u++) {
+      const float4 v = tail ? mask4(xr[u], col, d) : xr[u];
+      *reinterpret_cast<float4*>(&Xs[buf][((tid >> 3) + 32 * u) * LDK + c4]) = v;
+      if (lt == t0) xsq[u] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
 #pragma unroll
     for (int u = 0; u < CL; u++) {
       const float4 v = tail ? mask4(cr[u], col, d) : cr[u];
@@ -205,6 +212,17 @@ __global__ __launch_bounds__(256, 2) void k_screen(
         s += __shfl_xor(s, 4, 64);
         cmax_bits = max(cmax_bits, __float_as_uint(s));
         csq[u] = 0.f;
+      }
+      if (lt == t0) {
+#pragma unroll
+        for (int u = 0; u < XL; u++) {
+          float s = xsq[u];
+          s += __shfl_xor(s, 1, 64);
+          s += __shfl_xor(s, 2, 64);
+          s += __shfl_xor(s, 4, 64);
+          const int r = row0 + (tid >> 3) + 32 * u;
+          if (part == 0 && (tid & 7) == 0 && r < nrows) xnorm[r] = s;
+        }
       }
       ls = 0;
       ++lt;
@@ -347,15 +365,16 @@ int choose_parts(int row_tiles, int ntiles, int cus) {
 template <int WN, int L, bool L2, bool KNN>
 void launch_screen(emh_ctx* c, unsigned blocks, const float* x, size_t nx, size_t d,
                    const uint32_t* ids, size_t lo, size_t n, const float* cents,
-                   const float* cnorm, size_t k, int tpp, int parts, int ntiles, Cand* cand) {
+                   const float* cnorm, size_t k, int tpp, int parts, int ntiles, Cand* cand,
+                   float* xnorm) {
   if (d % 4 == 0)
     hipLaunchKernelGGL((k_screen<WN, L, L2, KNN, true>), dim3(blocks), dim3(256), 0, c->stream,
                        x, nx, (int)d, ids, lo, (int)n, cents, cnorm, (int)k, tpp, parts, ntiles,
-                       cand, c->small);
+                       cand, c->small, xnorm);
   else
     hipLaunchKernelGGL((k_screen<WN, L, L2, KNN, false>), dim3(blocks), dim3(256), 0, c->stream,
                        x, nx, (int)d, ids, lo, (int)n, cents, cnorm, (int)k, tpp, parts, ntiles,
-                       cand, c->small);
+                       cand, c->small, xnorm);
   EMH_HIP(hipGetLastError());
 }
 
@@ -381,18 +400,20 @@ void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t
   parts = (ntiles + tpp - 1) / tpp;
   Cand* cand = (Cand*)c->cand.get((size_t)parts * n * L1 * sizeof(Cand));
   uint32_t* fb = (uint32_t*)c->fblist.get(n * 4);
+  float* xnorm = (float*)c->xnorm.get(n * 4);
   launch_fill_u32(c, c->small, 3, 0);  // fallback count, cmax2, cnmax (the screen fills the maxima)
   const unsigned blocks = (unsigned)(row_tiles * parts);
   {
     ProfScope prof(c, 2.0 * (double)n * (double)k * (double)d);
     if (ip)
       launch_screen<2, L1, false, false>(c, blocks, x, nx, d, ids, lo, n, cents, cnorm, k, tpp,
-                                         parts, ntiles, cand);
+                                         parts, ntiles, cand, xnorm);
     else
       launch_screen<2, L1, true, false>(c, blocks, x, nx, d, ids, lo, n, cents, cnorm, k, tpp,
-                                        parts, ntiles, cand);
+                                        parts, ntiles, cand, xnorm);
   }
-  launch_verify1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, cand, parts, labels, scores, fb);
+  launch_verify1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, cand, parts, xnorm, labels, scores,
+                 fb);
   launch_exact1(c, x, nx, d, ids, lo, n, fb, cents, cnorm, k, ip, labels, scores);
 }
 
@@ -410,21 +431,23 @@ void launch_topk(emh_ctx* c, const float* q, size_t m, const float* data, size_t
   parts = (std::max(ntiles, 1) + tpp - 1) / tpp;
   Cand* cand = (Cand*)c->cand.get((size_t)parts * m * LK * sizeof(Cand));
   uint32_t* fb = (uint32_t*)c->fblist.get(m * 4);
+  float* xnorm = (float*)c->xnorm.get(m * 4);
   launch_fill_u32(c, c->small, 3, 0);
   if (n > 0) {
     ProfScope prof(c, 2.0 * (double)m * (double)n * (double)d);
     const unsigned blocks = (unsigned)(row_tiles * parts);
     if (exclude_self)
       launch_screen<1, LK, false, true>(c, blocks, q, m, d, nullptr, 0, m, data, nullptr, n, tpp,
-                                        parts, ntiles, cand);
+                                        parts, ntiles, cand, xnorm);
     else
       launch_screen<1, LK, false, false>(c, blocks, q, m, d, nullptr, 0, m, data, nullptr, n,
-                                         tpp, parts, ntiles, cand);
+                                         tpp, parts, ntiles, cand, xnorm);
   } else {
     parts = 1;
     launch_fill_u32(c, (uint32_t*)cand, m * LK * 2, NONE);  // empty lists
+    launch_fill_u32(c, (uint32_t*)xnorm, m, 0);
   }
-  launch_verifyk(c, q, m, data, n, d, kk, cand, parts, ids, sims, fb);
+  launch_verifyk(c, q, m, data, n, d, kk, cand, parts, xnorm, ids, sims, fb);
   launch_exactk(c, q, m, data, n, d, kk, exclude_self, fb, ids, sims);
 }
 

@@ -1,5 +1,6 @@
-// Device helpers shared by the MFMA screen (emh_screen.hip) and the exact
-// check kernels (emh_verify.hip) of top-1 and top-k, and their launchers.
+// Device helpers shared by the MFMA screen (emh_screen.hip), its check
+// (emh_rescore.hip) and the exact scans (emh_verify.hip) of top-1 and top-k,
+// and their launchers.
 #pragma once
 
 #include "emh_internal.h"
@@ -71,17 +72,20 @@ __device__ __forceinline__ void merge_parts(const Cand* c, int parts, float (&ke
   }
 }
 
-// ---- launchers of emh_verify.hip
+// ---- emh_rescore.hip: merge, bound and re-score the screen's lists; xnorm[r]
+// is row lo + r's |x|^2 summed in any order (the bound's input).
 void launch_verify1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
                     size_t lo, size_t n, const float* cents, const float* cnorm, size_t k, bool ip,
-                    const Cand* cand, int parts, uint32_t* labels, float* scores, uint32_t* fb);
+                    const Cand* cand, int parts, const float* xnorm, uint32_t* labels,
+                    float* scores, uint32_t* fb);
+void launch_verifyk(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,
+                    size_t kk, const Cand* cand, int parts, const float* xnorm, uint32_t* ids,
+                    float* sims, uint32_t* fb);
+// ---- emh_verify.hip: the exact scans
 // Exact scan of rows `list[0..*count)` (list != nullptr) or positions lo..lo+n.
 void launch_exact1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
                    size_t lo, size_t n, const uint32_t* list, const float* cents,
                    const float* cnorm, size_t k, bool ip, uint32_t* labels, float* scores);
-void launch_verifyk(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,
-                    size_t kk, const Cand* cand, int parts, uint32_t* ids, float* sims,
-                    uint32_t* fb);
 void launch_exactk(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,
                    size_t kk, bool exclude_self, const uint32_t* fb, uint32_t* ids, float* sims);
 
