@@ -31,6 +31,11 @@ sys.path.insert(0, ROOT)
 FP32_MFMA_PEAK = 157.3  # TFLOP/s, MI355X dense
 HBM_PEAK = 8000.0       # GB/s
 METRIC = "train s & assign Mrows/s at 200k×768 k=1024 FP32; % of FP32 MFMA peak"
+# HBM bytes per k_screen launch over this workload's launch mix (calibrated
+# FETCH_SIZE + WRITE_SIZE from two rocprofv3 --pmc passes of this script, with
+# a plain copy kernel of known size as the scale;
+# profiles/k_screen_train_assign_200kx768_k1024_hbm_traffic.md).
+SCREEN_TRAFFIC_BYTES = 189.8e6
 
 
 def log(*a):
@@ -107,12 +112,12 @@ def headline(args):
         "fallback_rows_per_run": info["fallback_rows"],
         "roofline": {
             "bound": "mfma",
-            "kernel": "k_screen (FP32 MFMA x.C^T + per-row top-5)",
+            "kernel": "k_screen (FP32 MFMA x.C^T + per-row 9-entry candidate list)",
             "achieved": achieved,
             "peak": FP32_MFMA_PEAK,
             "unit": "TFLOP/s",
             "frac": achieved / FP32_MFMA_PEAK,
-            "traffic": None,
+            "traffic": SCREEN_TRAFFIC_BYTES,
             "launches": launches,
             "avg_launch_ms": ms / max(launches, 1),
             "flop_per_launch": flop / max(launches, 1),
@@ -160,6 +165,21 @@ def cpu_baseline(x, cfg, gpu_cent, info, gpu_labels, gpu_scores, args):
     return base, parity
 
 
+def copy_probe(mib):
+    """A plain device-to-device copy of `mib` MiB, three times: the known-size
+    kernel that calibrates the HBM byte counters (FETCH_SIZE, WRITE_SIZE)."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copy probe: 3 copies of {mib} MiB ({n * 4} bytes each)")
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -167,6 +187,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and parity")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="first run a plain device copy of MIB MiB (HBM counter calibration)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -175,6 +197,8 @@ def main():
         sys.exit(2)
     if args.steps < 1:
         sys.exit("--steps must be >= 1")
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
     out = headline(args)
     print(json.dumps(out), flush=True)
 

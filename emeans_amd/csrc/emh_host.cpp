@@ -757,7 +757,7 @@ int emh_host_recipe(uint64_t n, const emh_config* cfg, uint64_t* batch_size, dou
 double emh_host_scheduled_alpha(double alpha0, uint64_t step, uint64_t total) {
   return scheduled_alpha(alpha0, step, total);
 }
-// Revival plan from a fresh RandomState(seed) after `skip` samples; returns pairs written.
+// Revival plan from a fresh RandomState(seed); returns the number of pairs written.
 uint64_t emh_host_plan_revival(const float* usage, uint64_t k, double tau, uint32_t seed,
                                uint32_t* pairs) {
   RandomState r(seed);

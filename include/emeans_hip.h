@@ -214,6 +214,28 @@ int emh_dedup(emh_ctx* ctx, const float* x, size_t n, size_t d, size_t kk, float
               uint32_t* representatives, uint32_t* anchors, uint32_t* sizes, float* nn_sim,
               size_t* n_groups, size_t* linked_pairs, size_t* split_components);
 
+/* ------------------------------------------------- host replay (no device) */
+/* The seeded host-side pieces of the device loop, exported so that callers and
+ * tests can check them without a GPU. They never touch the device. */
+/* RandomState::new(seed).permutation(n) (crates/emeans-core/src/rng.rs:19,95):
+ * numpy-legacy MT19937 shuffle; out has n entries. */
+void emh_host_permutation(uint32_t seed, uint64_t n, uint32_t* out);
+/* The (skip+1)-th RandomState::random_sample() of a fresh RandomState::new(seed)
+ * (rng.rs:63). */
+double emh_host_random_sample(uint32_t seed, uint64_t skip);
+/* Recipe::resolve (recipe.rs:200-254) for n rows: batch size, alpha0, rows of
+ * each epoch (first `cap` written to epoch_rows), epoch count, total steps. */
+int emh_host_recipe(uint64_t n, const emh_config* cfg, uint64_t* batch_size, double* alpha0,
+                    uint64_t* epoch_rows, uint64_t cap, uint64_t* n_epochs, uint64_t* total);
+/* scheduled_alpha (recipe.rs:148-152): the cosine schedule in f64. */
+double emh_host_scheduled_alpha(double alpha0, uint64_t step, uint64_t total);
+/* plan_revival (core/mod.rs:339-370) with a fresh RandomState::new(seed):
+ * (donor, dead) pairs written to pairs (capacity 2k); returns the pair count. */
+uint64_t emh_host_plan_revival(const float* usage, uint64_t k, double tau, uint32_t seed,
+                               uint32_t* pairs);
+/* numpy_sum_f32 (model.rs:970-1002): numpy's pairwise f32 sum. */
+float emh_host_numpy_sum_f32(const float* a, uint64_t n);
+
 /* ------------------------------------------------------------ diagnostics */
 /* Rows the exact top-1 / top-k kernels rescanned since the context was made
  * (the screen's misses; EMEANS_CUDA_SCREEN_STATS analogue, emeans-cuda lib.rs:278-287). */
