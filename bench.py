@@ -54,14 +54,12 @@ def headline(args):
     labels = dev.zeros_u32(n)
     scores = dev.zeros_f32(n)
     cfg = Config(d=d, k=k, seed=0)
-    cb = None
+    cb = dev.zeros_f32(k * d)  # the trained centroids stay on the device for the assignment
 
     def step():
-        nonlocal cb
         t0 = time.perf_counter()
-        cent, info = dev.train_dev(xb, n, cfg)
+        cent, info = dev.train_dev(xb, n, cfg, centroids_out=cb)
         t1 = time.perf_counter()
-        cb = dev.upload_f32(cent)
         dev.assign_dev(xb, n, d, cb, k, "l2", labels, scores)
         dev.sync()
         t2 = time.perf_counter()

@@ -239,8 +239,9 @@ class HipDevice:
         check(lib().emh_assign_dev(self._ctx, x.h, n, d, centroids.h, k, _metric(metric), chunk,
                                    labels.h, scores.h))
 
-    def train_dev(self, x: DevBuf, n: int, config: "Config"):
-        """Emeans::train on data already bound to the device; returns (centroids, info)."""
+    def train_dev(self, x: DevBuf, n: int, config: "Config", centroids_out: Optional[DevBuf] = None):
+        """Emeans::train on data already bound to the device; returns (centroids, info).
+        With centroids_out (a k*d f32 buffer) the centroids also stay on the device."""
         k, d = config.k, config.d
         cent = np.empty(k * d, np.float32)
         pos = np.empty(k * d, np.float32)
@@ -248,6 +249,7 @@ class HipDevice:
         labels = np.empty(n, np.int32)
         stats = (_CEpoch * 64)()
         out = _CTrainOut(_p(cent), _p(pos), _p(usage), _p(labels), C.addressof(stats), 64)
+        out.centroids_dev = centroids_out.h if centroids_out is not None else None
         ccfg = config._c()
         check(lib().emh_train_dev(self._ctx, x.h, n, C.byref(ccfg), C.byref(out)))
         info = {"stats": [EpochStats(stats[e].obj, stats[e].time, stats[e].imbalance_factor,

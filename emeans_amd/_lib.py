@@ -41,7 +41,7 @@ class TrainOut(C.Structure):
                 ("labels", C.c_void_p), ("stats", C.c_void_p), ("max_epochs", C.c_uint64),
                 ("n_epochs", C.c_uint64), ("n_splits", C.c_uint64), ("batch_size", C.c_uint64),
                 ("alpha0", C.c_double), ("total_steps", C.c_uint64),
-                ("fallback_rows", C.c_uint64)]
+                ("fallback_rows", C.c_uint64), ("centroids_dev", C.c_void_p)]
 
 
 # name: (restype, argtypes). Every function is declared in include/emeans_hip.h.

@@ -118,12 +118,14 @@ int emh_create(int device, emh_ctx** out) {
     if (const char* s = getenv("EMEANS_HIP_SCREEN")) c->screen = atoi(s) != 0;
     try {
       EMH_HIP(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+      EMH_HIP(hipStreamCreateWithFlags(&c->copy_stream, hipStreamNonBlocking));
       EMH_HIP(hipMalloc(&c->small, emh::SW_WORDS * 4));
       EMH_HIP(hipMemsetAsync(c->small, 0, emh::SW_WORDS * 4, c->stream));
       EMH_HIP(hipStreamSynchronize(c->stream));
     } catch (...) {
       if (c->small) (void)hipFree(c->small);
       if (c->stream) (void)hipStreamDestroy(c->stream);
+      if (c->copy_stream) (void)hipStreamDestroy(c->copy_stream);
       delete c;
       throw;
     }
@@ -137,10 +139,17 @@ int emh_destroy(emh_ctx* c) {
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
     for (emh::Scratch* s : {&c->cand, &c->fblist, &c->order, &c->start, &c->misc, &c->knn_tmp,
-                            &c->xnorm})
+                            &c->xnorm, &c->bigj})
+      s->release();
+    for (emh::Pinned* s : {&c->pin_usage, &c->pin_plan, &c->pin_small, &c->pin_order[0],
+                           &c->pin_order[1], &c->pin_lab[0], &c->pin_lab[1], &c->pin_sco[0],
+                           &c->pin_sco[1], &c->pin_out})
       s->release();
     if (c->small) (void)hipFree(c->small);
+    (void)hipStreamSynchronize(c->copy_stream);
+    for (hipEvent_t e : c->ev_pool) (void)hipEventDestroy(e);
     (void)hipStreamDestroy(c->stream);
+    (void)hipStreamDestroy(c->copy_stream);
     delete c;
   });
 }
@@ -488,11 +497,8 @@ int emh_profile_read(emh_ctx* c, double* ms, uint64_t* launches, double* flop) {
     *ms = t;
     *launches = c->timed.size();
     *flop = f;
-    for (auto& e : c->timed) {
-      (void)hipEventDestroy(e.a);
-      (void)hipEventDestroy(e.b);
-    }
     c->timed.clear();
+    c->ev_used = 0;  // the events go back to the pool
   });
 }
 

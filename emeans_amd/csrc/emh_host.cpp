@@ -71,20 +71,47 @@ class RandomState {  // rng.rs:13-102
       if (v <= max) return v;
     }
   }
+  // numpy's legacy shuffle: for i = n-1 down to 1, swap p[i] with p[interval(i)].
+  // The draws do not depend on p, so they are taken AHEAD swaps early and the
+  // element each will touch is prefetched; the swaps stay in the same order.
   std::vector<uint32_t> permutation(size_t n) {
     std::vector<uint32_t> p(n);
-    for (size_t i = 0; i < n; i++) p[i] = (uint32_t)i;
-    for (size_t i = n; i > 1; i--) std::swap(p[i - 1], p[interval(i - 1)]);
+    permutation_into(n, p.data());
     return p;
+  }
+  void permutation_into(size_t n, uint32_t* p) {
+    for (size_t i = 0; i < n; i++) p[i] = (uint32_t)i;
+    constexpr size_t AHEAD = 32;
+    uint64_t js[AHEAD];
+    size_t m = n;  // next i whose draw is taken: interval(m - 1)
+    for (size_t q = 0; q < AHEAD && m > 1; q++, m--) {
+      js[q] = interval(m - 1);
+      __builtin_prefetch(&p[js[q]], 1);
+    }
+    size_t q = 0;
+    for (size_t i = n; i > 1; i--) {
+      const uint64_t j = js[q];
+      if (m > 1) {
+        js[q] = interval(m - 1);
+        __builtin_prefetch(&p[js[q]], 1);
+        m--;
+      }
+      q = q + 1 == AHEAD ? 0 : q + 1;
+      std::swap(p[i - 1], p[j]);
+    }
   }
 
  private:
   static constexpr int N = 624, M = 397;
+  static uint32_t twist(uint32_t a, uint32_t b, uint32_t c) {  // MT19937 recurrence
+    const uint32_t y = (a & 0x80000000u) | (b & 0x7fffffffu);
+    return c ^ (y >> 1) ^ ((0u - (y & 1u)) & 0x9908b0dfu);
+  }
   void refill() {
-    for (int i = 0; i < N; i++) {
-      uint32_t y = (mt_[i] & 0x80000000u) | (mt_[(i + 1) % N] & 0x7fffffffu);
-      mt_[i] = mt_[(i + M) % N] ^ (y >> 1) ^ ((y & 1u) ? 0x9908b0dfu : 0u);
-    }
+    int i = 0;
+    for (; i < N - M; i++) mt_[i] = twist(mt_[i], mt_[i + 1], mt_[i + M]);
+    for (; i < N - 1; i++) mt_[i] = twist(mt_[i], mt_[i + 1], mt_[i + M - N]);
+    mt_[N - 1] = twist(mt_[N - 1], mt_[0], mt_[M - 1]);
     pos_ = 0;
   }
   uint32_t mt_[N];
@@ -181,9 +208,20 @@ float np_sum(const float* a, size_t n) {
   return np_sum(a, h) + np_sum(a + h, n - h);
 }
 
+// The Gumbel terms ln(-ln u) of the next k uniforms of a revival stream
+// (u = random_sample() floored at the smallest normal f64, core/mod.rs:355-357).
+std::vector<double> gumbel_terms(RandomState& rng, size_t k) {
+  std::vector<double> g(k);
+  for (size_t j = 0; j < k; j++)
+    g[j] = std::log(-std::log(std::max(rng.random_sample(), 2.2250738585072014e-308)));
+  return g;
+}
+
 // Revival plan (core/mod.rs:339-370): clusters under tau * mean mass take a
-// donor drawn by Gumbel top-k on ln N; k uniforms drawn only if a split happens.
-std::vector<uint32_t> plan_revival(const std::vector<float>& usage, double tau, RandomState& rng) {
+// donor drawn by Gumbel top-k on ln N. The k uniforms are drawn only if a split
+// happens: `draw` returns their Gumbel terms (gumbel_terms of the stream).
+template <class Draw>
+std::vector<uint32_t> plan_revival(const std::vector<float>& usage, double tau, Draw&& draw) {
   const size_t k = usage.size();
   const float thr = (np_sum(usage.data(), k) * (float)tau) / (float)k;
   std::vector<uint32_t> dead;
@@ -198,24 +236,27 @@ std::vector<uint32_t> plan_revival(const std::vector<float>& usage, double tau, 
   const size_t nsplit = std::min(dead.size(), ndonor);
   std::vector<uint32_t> pairs;
   if (nsplit == 0) return pairs;
-  std::vector<double> g(k);
-  for (size_t j = 0; j < k; j++) g[j] = std::max(rng.random_sample(), 2.2250738585072014e-308);
+  const std::vector<double> g = draw();
   struct Key {
     int64_t ord;
     uint32_t j;
   };
   std::vector<Key> keys;
+  keys.reserve(ndonor);
   for (size_t j = 0; j < k; j++) {
     if (!donor[j]) continue;
-    double v = (double)std::log(usage[j]) - std::log(-std::log(g[j]));
+    double v = (double)std::log(usage[j]) - g[j];  // f32 ln, then f64
     int64_t b;
     std::memcpy(&b, &v, 8);
     b ^= (int64_t)(((uint64_t)(b >> 63)) >> 1);  // IEEE total order as an integer
     keys.push_back({b, (uint32_t)j});
   }
-  std::sort(keys.begin(), keys.end(), [](const Key& a, const Key& b) {
-    return a.ord != b.ord ? a.ord > b.ord : a.j > b.j;
-  });
+  // Larger key first, equal keys: higher index first. The order is total, so
+  // the first nsplit of a partial sort are those of a full sort.
+  std::partial_sort(keys.begin(), keys.begin() + nsplit, keys.end(),
+                    [](const Key& a, const Key& b) {
+                      return a.ord != b.ord ? a.ord > b.ord : a.j > b.j;
+                    });
   for (size_t q = 0; q < nsplit; q++) {
     pairs.push_back(keys[q].j);
     pairs.push_back(dead[q]);
@@ -275,165 +316,37 @@ void check_flags(emh_ctx* c) {
   }
 }
 
-struct EpochResult {
-  emh_epoch_stats st;
-  std::vector<uint64_t> hist;  // last epoch only
+// A HIP event without timing.
+struct Event {
+  hipEvent_t e = nullptr;
+  Event() { EMH_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming)); }
+  ~Event() {
+    if (e) (void)hipEventDestroy(e);
+  }
+  Event(const Event&) = delete;
+  Event& operator=(const Event&) = delete;
+  void record(hipStream_t s) { EMH_HIP(hipEventRecord(e, s)); }
+  void wait() { EMH_HIP(hipEventSynchronize(e)); }  // returns at once if never recorded
 };
 
-// core/train.rs:60-303 on the context, then closing means.
-void train_run(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
-               const std::vector<float>& init_pos, emh_train_out* out,
-               std::future<std::vector<uint32_t>> first_order,
-               std::chrono::steady_clock::time_point t_start) {
-  const size_t k = cfg.k, d = cfg.d;
-  const bool sph = cfg.spherical != 0;
-  const Recipe R = resolve(n, k, d, cfg);
-  const size_t bsz = R.batch_size, chunk = std::max<size_t>(R.chunk, 1);
-  const size_t n_epochs = R.epoch_rows.size();
+// Errors the kernels flagged in the small block (a copy of it in w).
+void raise_flags(emh_ctx* c, const uint32_t* w) {
+  if (!(w[SW_BAD_LABEL] || w[SW_BAD_ID] || w[SW_BAD_INIT])) return;
+  for (int s : {SW_BAD_LABEL, SW_BAD_ID, SW_BAD_INIT}) launch_fill_u32(c, c->small + s, 1, 0);
+  EMH_HIP(hipStreamSynchronize(c->stream));
+  if (w[SW_BAD_INIT]) throw Invalid("initial centroids must be finite");
+  throw Failure(w[SW_BAD_LABEL] ? "label out of range" : "row id out of range");
+}
 
-  Buf order(c, n * 4), lab(c, n * 4), sco(c, n * 4), pos(c, k * d * 4), mass(c, k * 4),
-      readout(c, (sph ? k * d : k) * 4), sums(c, k * d * 4), counts(c, k * 4),
-      pass(c, k * d * 4);
-  h2d(c, pos.p, init_pos.data(), k * d * 4);
-  std::vector<float> usage0(k, 1.0f / 65536.0f);  // INIT_USAGE (recipe.rs:14)
-  h2d(c, mass.p, usage0.data(), k * 4);
-  launch_fill_u32(c, pass.u(), k * d, 0);
-
-  RandomState split_rng(cfg.seed);
-  size_t n_splits = 0, step = 0;
-  std::vector<EpochResult> results;
-  std::vector<double> pass_counts(k, 0.0);
-  std::vector<int32_t> all_labels;
-  const bool capture = cfg.capture_assignments && out->labels;
-
-  // The next epoch's permutation, drawn one epoch ahead on a helper thread.
-  std::future<std::vector<uint32_t>> next = std::move(first_order);
-  std::future<EpochResult> pending;
-  std::vector<uint32_t> order_host;
-  std::vector<float> usage_host(k);
-  for (size_t epoch = 0; epoch < n_epochs; epoch++) {
-    const size_t rows = R.epoch_rows[epoch];
-    const bool last = epoch + 1 == n_epochs;
-    order_host = next.get();
-    if (epoch + 1 < n_epochs) {
-      const uint32_t s = epoch_seed(cfg.seed, epoch + 1);
-      next = std::async(std::launch::async, [s, n] { return RandomState(s).permutation(n); });
-    }
-    h2d(c, order.p, order_host.data(), rows * 4);
-    const size_t splits_before = n_splits;
-    for (size_t b = 0; b < rows; b += bsz) {
-      const size_t e = std::min(b + bsz, rows);
-      if (sph)
-        launch_normalize_rows(c, pos.f(), k, d, readout.f());
-      else
-        launch_row_norms(c, pos.f(), k, d, readout.f());
-      const float* cents = sph ? readout.f() : pos.f();
-      const float* cn = sph ? nullptr : readout.f();
-      for (size_t c0 = b; c0 < e; c0 += chunk) {
-        const size_t c1 = std::min(c0 + chunk, e);
-        launch_top1(c, x, n, d, order.u(), c0, c1, cents, cn, k, sph, lab.u(), sco.f());
-      }
-      launch_scatter(c, x, n, d, order.u(), b, e, lab.u(), k, sums.f(), counts.u(),
-                     last ? pass.f() : nullptr);
-      const double alpha = scheduled_alpha(R.alpha0, step, R.total_steps);
-      launch_ema(c, pos.f(), mass.f(), sums.f(), counts.u(), k, d, (float)alpha,
-                 (float)(1.0 - alpha), alpha == 1.0);
-      if ((step + 1) % 5 == 0) {  // CHECK_UNUSED_EVERY (recipe.rs:12)
-        d2h(c, usage_host.data(), mass.p, k * 4);
-        std::vector<uint32_t> plan = plan_revival(usage_host, R.tau, split_rng);
-        if (!plan.empty()) {
-          const size_t np = plan.size() / 2;
-          uint32_t* pd = (uint32_t*)c->misc.get(plan.size() * 4);
-          h2d(c, pd, plan.data(), plan.size() * 4);
-          launch_split(c, pos.f(), mass.f(), pd, np, d, true);  // donors and dead are disjoint
-          n_splits += np;
-        }
-      }
-      step++;
-    }
-    // Epoch end: labels and scores come down; statistics on a helper thread.
-    auto labels_h = std::make_shared<std::vector<uint32_t>>(rows);
-    auto scores_h = std::make_shared<std::vector<float>>(rows);
-    d2h(c, labels_h->data(), lab.p, rows * 4);
-    d2h(c, scores_h->data(), sco.p, rows * 4);
-    check_flags(c);
-    const double t = std::chrono::duration<double>(std::chrono::steady_clock::now() - t_start).count();
-    if (pending.valid()) results.push_back(pending.get());
-    const size_t nsplit = n_splits - splits_before;
-    if (last && capture) {
-      all_labels.assign(n, -1);
-      for (size_t p = 0; p < rows; p++) all_labels[order_host[p]] = (int32_t)(*labels_h)[p];
-    }
-    pending = std::async(std::launch::async, [=]() {  // train.rs:224-279
-      EpochResult er;
-      double obj_epoch = 0.0;
-      for (size_t b = 0; b < rows; b += bsz) {
-        const size_t e = std::min(b + bsz, rows);
-        double obj_batch = 0.0;
-        for (size_t c0 = b; c0 < e; c0 += chunk) {
-          const size_t c1 = std::min(c0 + chunk, e);
-          double obj = 0.0;
-          if (sph) {
-            obj += 2.0 * (double)(c1 - c0);
-            for (size_t p = c0; p < c1; p++) obj += (double)(-2.0f * (*scores_h)[p]);
-          } else {
-            for (size_t p = c0; p < c1; p++) obj += (double)(*scores_h)[p];
-          }
-          obj_batch += obj;
-        }
-        obj_epoch += obj_batch;
-      }
-      er.hist.assign(k, 0);
-      for (uint32_t l : *labels_h)
-        if (l < k) er.hist[l]++;
-      double sq = 0.0;
-      for (size_t j = 0; j < k; j++) sq += (double)er.hist[j] * (double)er.hist[j];
-      er.st.obj = obj_epoch;
-      er.st.time = t;
-      er.st.imbalance_factor = (double)k * sq / ((double)rows * (double)rows);
-      er.st.nsplit = nsplit;
-      if (cfg.verbose)
-        fprintf(stderr, "  Epoch %zu / %zu (%zu rows), iteration %zu (%.2f s): objective=%.17g\n",
-                epoch + 1, n_epochs, rows, step, t, obj_epoch);
-      return er;
-    });
-  }
-  std::vector<float> P(k * d), U(k), S(k * d);
-  d2h(c, P.data(), pos.p, k * d * 4);
-  d2h(c, U.data(), mass.p, k * 4);
-  d2h(c, S.data(), pass.p, k * d * 4);
-  if (pending.valid()) results.push_back(pending.get());
-  for (size_t j = 0; j < k; j++) pass_counts[j] = (double)results.back().hist[j];
-  // Closing means (core/mod.rs:404-429).
-  std::vector<float> C(P);
-  for (size_t j = 0; j < k; j++) {
-    float* cj = &C[j * d];
-    if (pass_counts[j] > 0.0) {
-      const float nf = (float)pass_counts[j];
-      for (size_t t = 0; t < d; t++) cj[t] = S[j * d + t] / nf;
-    }
-    if (sph) normalize_row(cj, d);
-  }
-  std::memcpy(out->centroids, C.data(), k * d * 4);
-  if (out->positions) std::memcpy(out->positions, P.data(), k * d * 4);
-  if (out->usage) std::memcpy(out->usage, U.data(), k * 4);
-  if (out->labels) {
-    if (capture)
-      std::memcpy(out->labels, all_labels.data(), n * 4);
-    else
-      std::fill(out->labels, out->labels + n, -1);
-  }
-  out->n_epochs = n_epochs;
-  for (size_t e = 0; e < n_epochs && e < out->max_epochs; e++)
-    if (out->stats) out->stats[e] = results[e].st;
-  out->n_splits = n_splits;
-  out->batch_size = bsz;
-  out->alpha0 = R.alpha0;
-  out->total_steps = R.total_steps;
+void copy_async(emh_ctx* c, void* dst, const void* src, size_t bytes, hipMemcpyKind kind) {
+  if (bytes) EMH_HIP(hipMemcpyAsync(dst, src, bytes, kind, c->stream));
 }
 
 void check_cfg(size_t n, const emh_config* cfg, const emh_train_out* out) {
   EMH_ENSURE(cfg && out && out->centroids, "null argument");
+  EMH_ENSURE(!out->centroids_dev ||
+                 (out->centroids_dev->kind == 0 && out->centroids_dev->len == cfg->k * cfg->d),
+             "centroids_dev must be a k x d f32 buffer");
   EMH_ENSURE(cfg->d > 0 && cfg->k > 0, "d and k must be positive");
   EMH_ENSURE(std::isfinite(cfg->nepochs) && cfg->nepochs > 0.0, "nepochs must be positive");
   EMH_ENSURE(!cfg->has_unused_threshold || cfg->unused_threshold >= 0.0,
@@ -444,45 +357,263 @@ void check_cfg(size_t n, const emh_config* cfg, const emh_train_out* out) {
   for (size_t e : r.epoch_rows) EMH_ENSURE(e > 0, "nepochs gives an empty epoch for n = %zu", n);
 }
 
-// Emeans::train_rows (model.rs:772-811) with the data on the device.
-void train_dev(emh_ctx* c, const float* xd, size_t n, const emh_config& cfg, emh_train_out* out,
-               const float* x_host) {
-  const auto t0 = std::chrono::steady_clock::now();
+// Emeans::train_rows (model.rs:772-811) with the data on the device, driving
+// core::train::run (core/train.rs:60-303), then the closing means
+// (core/mod.rs:404-429).
+//
+// The host never idles the device for a whole step: host<->device traffic
+// goes through pinned buffers and events. At a revival check (every 5th step)
+// the masses the step's EMA will leave depend only on the step's counts, so
+// they are computed and copied out right after the count kernel; the host
+// plans the revival while the device still runs the step's sums and EMA. The
+// epoch's labels and scores are copied out asynchronously and the statistics
+// wait for them on a helper thread; the next epoch's order is drawn on
+// another and copied in from a pinned buffer.
+void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
+               emh_train_out* out) {
+  const auto t_start = std::chrono::steady_clock::now();
   const size_t k = cfg.k, d = cfg.d;
-  const uint32_t s0 = epoch_seed(cfg.seed, 0);
-  auto first = std::async(std::launch::async, [s0, n] { return RandomState(s0).permutation(n); });
-  std::vector<float> init(k * d);
+  const bool sph = cfg.spherical != 0;
+  const Recipe R = resolve(n, k, d, cfg);
+  const size_t bsz = R.batch_size, chunk = std::max<size_t>(R.chunk, 1);
+  const size_t n_epochs = R.epoch_rows.size();
+  const bool capture = cfg.capture_assignments && out->labels;
+
+  float* h_usage = (float*)c->pin_usage.get(k * 4);
+  uint32_t* h_plan = (uint32_t*)c->pin_plan.get(2 * k * 4);
+  uint32_t* h_small = (uint32_t*)c->pin_small.get(2 * SW_WORDS * 4);
+  uint32_t* h_small0 = h_small + SW_WORDS;
+  uint32_t* h_order[2];
+  uint32_t* h_lab[2];
+  float* h_sco[2];
+  for (int i = 0; i < 2; i++) {
+    h_order[i] = (uint32_t*)c->pin_order[i].get(n * 4);
+    h_lab[i] = (uint32_t*)c->pin_lab[i].get(n * 4);
+    h_sco[i] = (float*)c->pin_sco[i].get(n * 4);
+  }
+  float* h_out = (float*)c->pin_out.get((2 * k * d + k) * 4);
+  // ev_order[b]: epoch order b is on the device and h_order[b] free again (copy
+  // stream); ev_done[b]: the epoch that used order/labels/scores b has run
+  // (main stream); ev_epoch[b]: its labels and scores are on the host.
+  Event ev_init, ev_check, ev_order[2], ev_done[2], ev_epoch[2];
+
+  // Epochs alternate between two sets of order/labels/scores buffers, so the
+  // copies of one epoch's run on the copy stream beside the next epoch's kernels.
+  Buf order0(c, n * 4), order1(c, n * 4), lab0(c, n * 4), lab1(c, n * 4), sco0(c, n * 4),
+      sco1(c, n * 4), pos(c, k * d * 4), mass(c, k * 4), mass_next(c, k * 4),
+      readout(c, (sph ? k * d : k) * 4), sums(c, k * d * 4), counts(c, k * 4),
+      pass(c, k * d * 4), init_ids(c, k * 4);
+  uint32_t* d_order[2] = {order0.u(), order1.u()};
+  uint32_t* d_lab[2] = {lab0.u(), lab1.u()};
+  float* d_sco[2] = {sco0.f(), sco1.f()};
+  struct Drain {  // nothing queued may outlive the buffers, also on an error
+    emh_ctx* c;
+    ~Drain() {
+      (void)hipStreamSynchronize(c->copy_stream);
+      (void)hipStreamSynchronize(c->stream);
+    }
+  } drain{c};
+
+  // Epoch e's order: drawn into h_order[e % 2] once the last copy out of it is
+  // done, then copied (copy stream) into d_order[e % 2] once the epoch that
+  // last used that buffer has run. Runs on a helper thread.
+  auto fill_order = [&](size_t epoch) {
+    const int buf = (int)(epoch & 1);
+    ev_order[buf].wait();
+    RandomState(epoch_seed(cfg.seed, epoch)).permutation_into(n, h_order[buf]);
+    EMH_HIP(hipStreamWaitEvent(c->copy_stream, ev_done[buf].e, 0));
+    EMH_HIP(hipMemcpyAsync(d_order[buf], h_order[buf], R.epoch_rows[epoch] * 4,
+                           hipMemcpyHostToDevice, c->copy_stream));
+    ev_order[buf].record(c->copy_stream);
+  };
+  // The first epoch's order is drawn while the initial centroids are (model.rs:783-784).
+  std::future<void> next = std::async(std::launch::async, [&] { fill_order(0); });
+
+  // Initial centroids: the rows permutation(n)[..k] (model.rs:786-797),
+  // normalized when spherical (model.rs:306-315), masses INIT_USAGE (recipe.rs:14).
   if (n == k) {
-    if (x_host)
-      std::memcpy(init.data(), x_host, k * d * 4);
-    else
-      d2h(c, init.data(), xd, k * d * 4);
+    EMH_HIP(hipMemcpyAsync(pos.p, x, k * d * 4, hipMemcpyDeviceToDevice, c->stream));
   } else {
-    std::vector<uint32_t> perm = RandomState(cfg.seed).permutation(n);
-    if (x_host) {
-      for (size_t j = 0; j < k; j++)
-        std::memcpy(&init[j * d], x_host + (size_t)perm[j] * d, d * 4);
+    RandomState(cfg.seed).permutation_into(n, h_order[1]);  // unused until epoch 1
+    copy_async(c, init_ids.p, h_order[1], k * 4, hipMemcpyHostToDevice);
+    launch_gather_rows(c, x, n, d, init_ids.u(), k, pos.f());
+  }
+  if (sph) {
+    launch_normalize_rows(c, pos.f(), k, d, readout.f());
+    EMH_HIP(hipMemcpyAsync(pos.p, readout.p, k * d * 4, hipMemcpyDeviceToDevice, c->stream));
+  }
+  launch_check_finite(c, pos.f(), k * d, c->small + SW_BAD_INIT);
+  const float init_usage = 1.0f / 65536.0f;
+  uint32_t init_bits;
+  std::memcpy(&init_bits, &init_usage, 4);
+  launch_fill_u32(c, mass.u(), k, init_bits);
+  launch_fill_u32(c, pass.u(), k * d, 0);
+  copy_async(c, h_small0, c->small, SW_WORDS * 4, hipMemcpyDeviceToHost);
+  ev_order[1].record(c->stream);  // the initial ids are out of h_order[1]
+  ev_init.record(c->stream);
+  ev_init.wait();
+  raise_flags(c, h_small0);
+  if (cfg.verbose)
+    fprintf(stderr, "Clustering %zu points in %zuD to %zu clusters, %g epochs (batch %zu, alpha0 %.3f%s)\n",
+            n, d, k, cfg.nepochs, bsz, R.alpha0, sph ? ", spherical" : "");
+
+  // The revival stream (RandomState(seed)) serves only revivals, k uniforms
+  // per revival that splits: the next k Gumbel terms are drawn ahead.
+  RandomState split_rng(cfg.seed);
+  std::future<std::vector<double>> gnext =
+      std::async(std::launch::async, [&] { return gumbel_terms(split_rng, k); });
+  auto take_gumbel = [&] {
+    std::vector<double> g = gnext.get();
+    gnext = std::async(std::launch::async, [&] { return gumbel_terms(split_rng, k); });
+    return g;
+  };
+  size_t n_splits = 0, step = 0;
+  bool norms_stale = true;  // L2 readout: the EMA keeps the norms of the rows it moves
+  std::vector<emh_epoch_stats> stats;
+  std::future<emh_epoch_stats> pending;
+  for (size_t epoch = 0; epoch < n_epochs; epoch++) {
+    const size_t rows = R.epoch_rows[epoch];
+    const bool last = epoch + 1 == n_epochs;
+    const int buf = (int)(epoch & 1);
+    next.get();
+    EMH_HIP(hipStreamWaitEvent(c->stream, ev_order[buf].e, 0));  // this epoch's order is in
+    EMH_HIP(hipStreamWaitEvent(c->stream, ev_epoch[buf].e, 0));  // labels of epoch - 2 are out
+    if (!last) next = std::async(std::launch::async, [&, e1 = epoch + 1] { fill_order(e1); });
+    uint32_t* order = d_order[buf];
+    uint32_t* lab = d_lab[buf];
+    float* sco = d_sco[buf];
+    const size_t splits_before = n_splits;
+    for (size_t b = 0; b < rows; b += bsz) {
+      const size_t e = std::min(b + bsz, rows);
+      if (sph) {
+        launch_normalize_rows(c, pos.f(), k, d, readout.f());
+      } else if (norms_stale) {
+        launch_row_norms(c, pos.f(), k, d, readout.f());
+        norms_stale = false;
+      }
+      const float* cents = sph ? readout.f() : pos.f();
+      const float* cn = sph ? nullptr : readout.f();
+      for (size_t c0 = b; c0 < e; c0 += chunk) {
+        const size_t c1 = std::min(c0 + chunk, e);
+        launch_top1(c, x, n, d, order, c0, c1, cents, cn, k, sph, lab, sco);
+      }
+      const double alpha = scheduled_alpha(R.alpha0, step, R.total_steps);
+      const float af = (float)alpha, df = (float)(1.0 - alpha);
+      const int replace = alpha == 1.0;
+      const bool check = (step + 1) % 5 == 0;  // CHECK_UNUSED_EVERY (recipe.rs:12)
+      launch_scatter_count(c, b, e, lab, k, counts.u());
+      if (check) {
+        launch_mass_preview(c, mass.f(), counts.u(), k, af, df, replace, mass_next.f());
+        copy_async(c, h_usage, mass_next.p, k * 4, hipMemcpyDeviceToHost);
+        copy_async(c, h_small, c->small, SW_WORDS * 4, hipMemcpyDeviceToHost);
+        ev_check.record(c->stream);
+      }
+      launch_scatter_sums(c, x, n, d, order, b, e, lab, k, sums.f(), last ? pass.f() : nullptr);
+      launch_ema(c, pos.f(), mass.f(), sums.f(), counts.u(), k, d, af, df, replace,
+                 sph ? nullptr : readout.f());
+      if (check) {
+        ev_check.wait();
+        raise_flags(c, h_small);
+        std::vector<float> usage(h_usage, h_usage + k);
+        std::vector<uint32_t> plan = plan_revival(usage, R.tau, take_gumbel);
+        if (!plan.empty()) {
+          const size_t np = plan.size() / 2;
+          std::memcpy(h_plan, plan.data(), plan.size() * 4);
+          uint32_t* pd = (uint32_t*)c->misc.get(plan.size() * 4);
+          copy_async(c, pd, h_plan, plan.size() * 4, hipMemcpyHostToDevice);
+          launch_split(c, pos.f(), mass.f(), pd, np, d, true);  // donors and dead are disjoint
+          n_splits += np;
+          norms_stale = true;
+        }
+      }
+      step++;
+    }
+    // Epoch end: labels and scores go out; the statistics (train.rs:224-279)
+    // wait for them on a helper thread.
+    ev_done[buf].record(c->stream);
+    EMH_HIP(hipStreamWaitEvent(c->copy_stream, ev_done[buf].e, 0));
+    EMH_HIP(hipMemcpyAsync(h_lab[buf], lab, rows * 4, hipMemcpyDeviceToHost, c->copy_stream));
+    EMH_HIP(hipMemcpyAsync(h_sco[buf], sco, rows * 4, hipMemcpyDeviceToHost, c->copy_stream));
+    ev_epoch[buf].record(c->copy_stream);
+    if (pending.valid()) stats.push_back(pending.get());  // frees the other buffer pair
+    const size_t nsplit = n_splits - splits_before;
+    pending = std::async(std::launch::async, [&, rows, buf, nsplit, epoch, st = step]() {
+      ev_epoch[buf].wait();
+      const double t =
+          std::chrono::duration<double>(std::chrono::steady_clock::now() - t_start).count();
+      const float* sc = h_sco[buf];
+      double obj_epoch = 0.0;
+      for (size_t b = 0; b < rows; b += bsz) {
+        const size_t e = std::min(b + bsz, rows);
+        double obj_batch = 0.0;
+        for (size_t c0 = b; c0 < e; c0 += chunk) {
+          const size_t c1 = std::min(c0 + chunk, e);
+          double obj = 0.0;
+          if (sph) {
+            obj += 2.0 * (double)(c1 - c0);
+            for (size_t p = c0; p < c1; p++) obj += (double)(-2.0f * sc[p]);
+          } else {
+            for (size_t p = c0; p < c1; p++) obj += (double)sc[p];
+          }
+          obj_batch += obj;
+        }
+        obj_epoch += obj_batch;
+      }
+      std::vector<uint64_t> hist(k, 0);
+      for (size_t p = 0; p < rows; p++)
+        if (h_lab[buf][p] < k) hist[h_lab[buf][p]]++;
+      double sq = 0.0;
+      for (size_t j = 0; j < k; j++) sq += (double)hist[j] * (double)hist[j];
+      emh_epoch_stats es;
+      es.obj = obj_epoch;
+      es.time = t;
+      es.imbalance_factor = (double)k * sq / ((double)rows * (double)rows);
+      es.nsplit = nsplit;
+      if (cfg.verbose)
+        fprintf(stderr, "  Epoch %zu / %zu (%zu rows), iteration %zu (%.2f s): objective=%.17g\n",
+                epoch + 1, n_epochs, rows, st, t, obj_epoch);
+      return es;
+    });
+  }
+  // Closing means on the device: the last pass's label counts, sums / count.
+  const size_t rows_last = R.epoch_rows.back();
+  launch_hist(c, d_lab[(n_epochs - 1) & 1], rows_last, k, counts.u());
+  launch_closing(c, pos.f(), pass.f(), counts.u(), k, d, sums.f());
+  const float* C = sums.f();
+  if (sph) {
+    launch_normalize_rows(c, sums.f(), k, d, pass.f());
+    C = pass.f();
+  }
+  if (out->centroids_dev)
+    EMH_HIP(hipMemcpyAsync(out->centroids_dev->ptr, C, k * d * 4, hipMemcpyDeviceToDevice,
+                           c->stream));
+  copy_async(c, h_out, C, k * d * 4, hipMemcpyDeviceToHost);
+  copy_async(c, h_out + k * d, pos.p, k * d * 4, hipMemcpyDeviceToHost);
+  copy_async(c, h_out + 2 * k * d, mass.p, k * 4, hipMemcpyDeviceToHost);
+  copy_async(c, h_small, c->small, SW_WORDS * 4, hipMemcpyDeviceToHost);
+  EMH_HIP(hipStreamSynchronize(c->stream));
+  stats.push_back(pending.get());
+  raise_flags(c, h_small);
+  std::memcpy(out->centroids, h_out, k * d * 4);
+  if (out->positions) std::memcpy(out->positions, h_out + k * d, k * d * 4);
+  if (out->usage) std::memcpy(out->usage, h_out + 2 * k * d, k * 4);
+  if (out->labels) {
+    if (capture) {
+      const int lb = (int)((n_epochs - 1) & 1);
+      std::fill(out->labels, out->labels + n, -1);
+      for (size_t p = 0; p < rows_last; p++) out->labels[h_order[lb][p]] = (int32_t)h_lab[lb][p];
     } else {
-      Buf ids(c, k * 4), rows(c, k * d * 4);
-      h2d(c, ids.p, perm.data(), k * 4);
-      launch_gather_rows(c, xd, n, d, ids.u(), k, rows.f());
-      d2h(c, init.data(), rows.p, k * d * 4);
+      std::fill(out->labels, out->labels + n, -1);
     }
   }
-  if (cfg.spherical)  // begin (model.rs:306-315)
-    for (size_t j = 0; j < k; j++) normalize_row(&init[j * d], d);
-  for (float v : init) EMH_ENSURE(std::isfinite(v), "initial centroids must be finite");
-  if (cfg.verbose) {
-    Recipe r = resolve(n, k, d, cfg);
-    fprintf(stderr, "Clustering %zu points in %zuD to %zu clusters, %g epochs (batch %zu, alpha0 %.3f%s)\n",
-            n, d, k, cfg.nepochs, r.batch_size, r.alpha0, cfg.spherical ? ", spherical" : "");
-  }
-  uint32_t fb0 = 0;
-  d2h(c, &fb0, c->small + SW_FALLBACK_TOTAL, 4);
-  train_run(c, xd, n, cfg, init, out, std::move(first), t0);
-  uint32_t fb1 = 0;
-  d2h(c, &fb1, c->small + SW_FALLBACK_TOTAL, 4);
-  out->fallback_rows = (uint32_t)(fb1 - fb0);
+  out->n_epochs = n_epochs;
+  for (size_t e = 0; e < n_epochs && e < out->max_epochs; e++)
+    if (out->stats) out->stats[e] = stats[e];
+  out->n_splits = n_splits;
+  out->batch_size = bsz;
+  out->alpha0 = R.alpha0;
+  out->total_steps = R.total_steps;
+  out->fallback_rows = (uint32_t)(h_small[SW_FALLBACK_TOTAL] - h_small0[SW_FALLBACK_TOTAL]);
 }
 
 // dedup_with_neighbors (dedup.rs:186-358) for rows without timestamps or bursts.
@@ -619,7 +750,7 @@ int emh_train_dev(emh_ctx* c, const emh_buf* x, size_t n, const emh_config* cfg,
     check_cfg(n, cfg, out);
     EMH_ENSURE(x->len == n * cfg->d, "x must be n x d");
     EMH_HIP(hipSetDevice(c->device));
-    train_dev(c, (const float*)x->ptr, n, *cfg, out, nullptr);
+    train_dev(c, (const float*)x->ptr, n, *cfg, out);
   });
 }
 
@@ -630,7 +761,7 @@ int emh_train(emh_ctx* c, const float* x, size_t n, const emh_config* cfg, emh_t
     EMH_HIP(hipSetDevice(c->device));
     Buf xd(c, n * cfg->d * 4);  // Device::bind: the data set goes to the device once
     h2d(c, xd.p, x, n * cfg->d * 4);
-    train_dev(c, xd.f(), n, *cfg, out, x);
+    train_dev(c, xd.f(), n, *cfg, out);
   });
 }
 
@@ -762,7 +893,7 @@ uint64_t emh_host_plan_revival(const float* usage, uint64_t k, double tau, uint3
                                uint32_t* pairs) {
   RandomState r(seed);
   std::vector<float> u(usage, usage + k);
-  std::vector<uint32_t> p = plan_revival(u, tau, r);
+  std::vector<uint32_t> p = plan_revival(u, tau, [&] { return gumbel_terms(r, k); });
   std::memcpy(pairs, p.data(), p.size() * 4);
   return p.size() / 2;
 }

@@ -69,6 +69,30 @@ struct Scratch {
   }
 };
 
+// Pinned host memory that grows on demand and is reused by later calls.
+struct Pinned {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  void* get(size_t need) {
+    if (need > bytes) {
+      if (ptr) {
+        EMH_HIP(hipDeviceSynchronize());  // queued copies may still use it
+        EMH_HIP(hipHostFree(ptr));
+      }
+      ptr = nullptr;
+      size_t b = need + need / 4 + 4096;
+      EMH_HIP(hipHostMalloc(&ptr, b, hipHostMallocDefault));
+      bytes = b;
+    }
+    return ptr;
+  }
+  void release() {
+    if (ptr) (void)hipHostFree(ptr);
+    ptr = nullptr;
+    bytes = 0;
+  }
+};
+
 // Words of the context's small device block.
 enum SmallWord : int {
   SW_FALLBACK_COUNT = 0,  // rows appended to the exact kernel's list by the current call
@@ -77,6 +101,9 @@ enum SmallWord : int {
   SW_BAD_LABEL = 3,       // set when scatter_add saw a label >= k
   SW_FALLBACK_TOTAL = 4,  // running total of rescanned rows (u32, wraps)
   SW_BAD_ID = 5,          // set when a selection named a row id >= n
+  SW_TICKET = 6,          // blocks of the scatter count kernel that have finished (reset by the last)
+  SW_NBIG = 7,            // clusters of the current scatter with more rows than the per-column path takes
+  SW_BAD_INIT = 8,        // set when a training run's initial centroids are not finite
   SW_WORDS = 16,
 };
 
@@ -92,11 +119,15 @@ struct emh_buf {
 struct emh_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
+  hipStream_t copy_stream = nullptr;  // host<->device staging that overlaps the kernels
   int cus = 256;
   int screen = 1;
   uint32_t* small = nullptr;  // SW_WORDS u32 on the device
   uint64_t fallback_total = 0;
-  emh::Scratch cand, fblist, order, start, misc, knn_tmp, xnorm;
+  emh::Scratch cand, fblist, order, start, misc, knn_tmp, xnorm, bigj;
+  // Host staging of the device loop: masses, plan, flags, epoch orders and
+  // epoch labels/scores (double-buffered), results.
+  emh::Pinned pin_usage, pin_plan, pin_small, pin_order[2], pin_lab[2], pin_sco[2], pin_out;
   std::string name = "hip-gfx950";
   // Screen-kernel timing (emh_profile): event pairs and the FLOP each covers.
   bool prof = false;
@@ -105,6 +136,16 @@ struct emh_ctx {
     double flop;
   };
   std::vector<Timed> timed;
+  std::vector<hipEvent_t> ev_pool;  // events for the timing, reused across reads
+  size_t ev_used = 0;
+  hipEvent_t pool_event() {
+    if (ev_used == ev_pool.size()) {
+      hipEvent_t e;
+      EMH_HIP(hipEventCreate(&e));
+      ev_pool.push_back(e);
+    }
+    return ev_pool[ev_used++];
+  }
 };
 
 namespace emh {
@@ -118,8 +159,8 @@ struct ProfScope {
   double flop;
   ProfScope(emh_ctx* ctx, double f) : c(ctx), flop(f) {
     if (!c->prof) return;
-    EMH_HIP(hipEventCreate(&a));
-    EMH_HIP(hipEventCreate(&b));
+    a = c->pool_event();
+    b = c->pool_event();
     EMH_HIP(hipEventRecord(a, c->stream));
   }
   ~ProfScope() {
@@ -133,7 +174,17 @@ void launch_fill_u32(emh_ctx* c, uint32_t* p, size_t n, uint32_t v);
 void launch_row_norms(emh_ctx* c, const float* m, size_t rows, size_t d, float* out);
 void launch_normalize_rows(emh_ctx* c, const float* src, size_t rows, size_t d, float* dst);
 void launch_ema(emh_ctx* c, float* pos, float* usage, const float* sums, const uint32_t* counts,
-                size_t k, size_t d, float alpha, float decay, int replace);
+                size_t k, size_t d, float alpha, float decay, int replace, float* norms = nullptr);
+// The masses launch_ema will leave, into out (usage untouched).
+void launch_mass_preview(emh_ctx* c, const float* usage, const uint32_t* counts, size_t k,
+                         float alpha, float decay, int replace, float* out);
+// counts = histogram of labels[0..n) (labels >= k skipped).
+void launch_hist(emh_ctx* c, const uint32_t* labels, size_t n, size_t k, uint32_t* counts);
+// Closing means: out[j] = sums[j] / counts[j] where counts[j] > 0, else pos[j].
+void launch_closing(emh_ctx* c, const float* pos, const float* sums, const uint32_t* counts,
+                    size_t k, size_t d, float* out);
+// *flag = 1 when any of v[0..n) is not finite.
+void launch_check_finite(emh_ctx* c, const float* v, size_t n, uint32_t* flag);
 void launch_split(emh_ctx* c, float* pos, float* usage, const uint32_t* pairs_dev, size_t npairs,
                   size_t d, bool independent);
 void launch_gather_rows(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
@@ -143,6 +194,13 @@ void launch_gather_rows(emh_ctx* c, const float* x, size_t nx, size_t d, const u
 void launch_scatter(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids, size_t lo,
                     size_t hi, const uint32_t* labels, size_t k, float* sums, uint32_t* counts,
                     float* acc);
+// The same in two halves: counts (and the cluster offsets), then the ordered
+// sums; the caller may queue work that needs only the counts in between.
+void launch_scatter_count(emh_ctx* c, size_t lo, size_t hi, const uint32_t* labels, size_t k,
+                          uint32_t* counts);
+void launch_scatter_sums(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
+                         size_t lo, size_t hi, const uint32_t* labels, size_t k, float* sums,
+                         float* acc);
 
 // ---- emh_screen.hip (top-1 and top-k orchestration)
 void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids, size_t lo, size_t hi,

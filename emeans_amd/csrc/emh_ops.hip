@@ -121,38 +121,113 @@ __global__ __launch_bounds__(256) void k_normalize_rows(const float* __restrict_
 // EMA step (core/cpu.rs:389-432): all masses decay unless replace; each cluster
 // with rows gets mass = retained + alpha n, w = alpha n / mass and
 // c = (w == 1) ? s / n : c + w (s / n - c), two roundings, no FMA.
+// The mass half of the EMA step; *weight = alpha n / mass for a cluster with
+// rows (0 otherwise). One function for the EMA kernel and the mass preview, so
+// both compute the same bits.
+__device__ __forceinline__ float ema_mass(float u, uint32_t cnt, float alpha, float decay,
+                                          int replace, float* weight) {
+  if (!replace) u = u * decay;
+  *weight = 0.0f;
+  if (cnt > 0) {
+    const float count = (float)cnt;
+    const float retained = replace ? 0.0f : u;
+    const float step = alpha * count;
+    const float mass = retained + step;
+    *weight = step / mass;
+    u = mass;
+  }
+  return u;
+}
+
+// With norms != nullptr, also the squared norm of every updated row (the next
+// batch's L2 readout, assign.rs:150-155); rows without members keep theirs.
 __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __restrict__ usage,
                                              const float* __restrict__ sums,
                                              const uint32_t* __restrict__ counts, size_t k,
-                                             size_t d, float alpha, float decay, int replace) {
+                                             size_t d, float alpha, float decay, int replace,
+                                             float* __restrict__ norms) {
+  __shared__ __attribute__((aligned(16))) float sq[WAVES][CH];
   int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
   size_t j = (size_t)blockIdx.x * WAVES + w;
-  if (j >= k) return;
-  float u = usage[j];
-  if (!replace) u = u * decay;
-  uint32_t cnt = counts[j];
+  if (j >= k) return;  // whole wave; no workgroup barrier below
+  const uint32_t cnt = counts[j];
+  float weight;
+  const float u = ema_mass(usage[j], cnt, alpha, decay, replace, &weight);
   if (cnt > 0) {
-    float count = (float)cnt;
-    float retained = replace ? 0.0f : u;
-    float step = alpha * count;
-    float mass = retained + step;
-    float weight = step / mass;
+    const float count = (float)cnt;
     float* p = pos + j * d;
     const float* s = sums + j * d;
-    if (weight == 1.0f) {
-      for (size_t t = lane; t < d; t += WAVE) p[t] = s[t] / count;
-    } else {
-      for (size_t t = lane; t < d; t += WAVE) {
-        float mean = s[t] / count;
-        float c = p[t];
-        float diff = mean - c;
-        float inc = weight * diff;
-        p[t] = c + inc;
+    float nrm = 0.0f;
+    for (size_t c0 = 0; c0 < d; c0 += CH) {
+      const int len = (int)min((size_t)CH, d - c0);
+      for (int t = lane; t < len; t += WAVE) {
+        const float mean = s[c0 + t] / count;
+        float v;
+        if (weight == 1.0f) {
+          v = mean;
+        } else {
+          const float c = p[c0 + t];
+          const float diff = mean - c;
+          const float inc = weight * diff;
+          v = c + inc;
+        }
+        p[c0 + t] = v;
+        sq[w][t] = v * v;
+      }
+      if (norms) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane == 0) nrm = seq_add(sq[w], len, nrm);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       }
     }
-    u = mass;
+    if (norms && lane == 0) norms[j] = nrm;
   }
   if (lane == 0) usage[j] = u;
+}
+
+// The masses the EMA step will leave (for the host's revival check), without
+// touching the state.
+__global__ __launch_bounds__(256) void k_mass_preview(const float* __restrict__ usage,
+                                                      const uint32_t* __restrict__ counts,
+                                                      size_t k, float alpha, float decay,
+                                                      int replace, float* __restrict__ out) {
+  const size_t j = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= k) return;
+  float weight;
+  out[j] = ema_mass(usage[j], counts[j], alpha, decay, replace, &weight);
+}
+
+// Label histogram of positions [0, n) (labels >= k are not counted).
+__global__ __launch_bounds__(256) void k_hist(const uint32_t* __restrict__ labels, size_t n,
+                                              size_t k, uint32_t* __restrict__ counts) {
+  const size_t p = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= n) return;
+  const uint32_t l = labels[p];
+  if (l < k) atomicAdd(&counts[l], 1u);
+}
+
+// Closing means (core/mod.rs:404-429): sums / (f32)count where the last pass
+// gave the cluster rows, else the position.
+__global__ __launch_bounds__(256) void k_closing(const float* __restrict__ pos,
+                                                 const float* __restrict__ sums,
+                                                 const uint32_t* __restrict__ counts, size_t d,
+                                                 float* __restrict__ out) {
+  const size_t j = blockIdx.y;
+  const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= d) return;
+  const uint32_t cnt = counts[j];
+  out[j * d + t] = cnt > 0 ? sums[j * d + t] / (float)cnt : pos[j * d + t];
+}
+
+// flag = 1 when any of v[0..n) is NaN or infinite.
+__global__ __launch_bounds__(256) void k_check_finite(const float* __restrict__ v, size_t n,
+                                                      uint32_t* __restrict__ flag) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n && !isfinite(v[i])) *flag = 1;
 }
 
 __device__ inline float next_up(float x) {  // f32::next_up
@@ -257,10 +332,39 @@ void launch_normalize_rows(emh_ctx* c, const float* src, size_t rows, size_t d, 
 }
 
 void launch_ema(emh_ctx* c, float* pos, float* usage, const float* sums, const uint32_t* counts,
-                size_t k, size_t d, float alpha, float decay, int replace) {
+                size_t k, size_t d, float alpha, float decay, int replace, float* norms) {
   if (k == 0) return;
   hipLaunchKernelGGL(k_ema, grid1(k, WAVES), dim3(256), 0, c->stream, pos, usage, sums, counts, k,
-                     d, alpha, decay, replace);
+                     d, alpha, decay, replace, norms);
+  EMH_HIP(hipGetLastError());
+}
+
+void launch_mass_preview(emh_ctx* c, const float* usage, const uint32_t* counts, size_t k,
+                         float alpha, float decay, int replace, float* out) {
+  if (k == 0) return;
+  hipLaunchKernelGGL(k_mass_preview, grid1(k, 256), dim3(256), 0, c->stream, usage, counts, k,
+                     alpha, decay, replace, out);
+  EMH_HIP(hipGetLastError());
+}
+
+void launch_hist(emh_ctx* c, const uint32_t* labels, size_t n, size_t k, uint32_t* counts) {
+  launch_fill_u32(c, counts, k, 0);
+  if (n == 0) return;
+  hipLaunchKernelGGL(k_hist, grid1(n, 256), dim3(256), 0, c->stream, labels, n, k, counts);
+  EMH_HIP(hipGetLastError());
+}
+
+void launch_closing(emh_ctx* c, const float* pos, const float* sums, const uint32_t* counts,
+                    size_t k, size_t d, float* out) {
+  if (k == 0) return;
+  dim3 g((unsigned)((d + 255) / 256), (unsigned)k);
+  hipLaunchKernelGGL(k_closing, g, dim3(256), 0, c->stream, pos, sums, counts, d, out);
+  EMH_HIP(hipGetLastError());
+}
+
+void launch_check_finite(emh_ctx* c, const float* v, size_t n, uint32_t* flag) {
+  if (n == 0) return;
+  hipLaunchKernelGGL(k_check_finite, grid1(n, 256), dim3(256), 0, c->stream, v, n, flag);
   EMH_HIP(hipGetLastError());
 }
 

@@ -1,15 +1,19 @@
 // scatter_add (core/cpu.rs:118-143, scatter_rows 337-375): per-label counts and
 // sums of the selected rows, each sum added in selection order in f32 so the
 // bits equal the CPU's. The order is a dependency chain per (cluster, column),
-// so the work is split three ways:
-//   1. count:  labels -> counts (integer atomics; exact in any order);
-//   2. scan:   counts -> start offsets (one workgroup);
-//   3. place:  a stable counting sort: one wave per cluster walks the labels in
-//              selection order with wave ballots and writes the cluster's data
-//              row ids, in order, at its start offset;
-//   4. sum:    per (cluster, column strip), rows added in that order; the loads
-//              of a run of rows are issued together so the chain waits on adds,
-//              not on memory.
+// so the work is split into a stable counting sort and ordered sums:
+//   1. count:  labels -> counts (integer atomics; exact in any order); the
+//              last workgroup to finish scans the counts into start offsets
+//              and lists the clusters too large for the per-column path;
+//   2. place:  one wave per cluster walks the labels in selection order with
+//              wave ballots and writes the cluster's positions, in order, at
+//              its start offset;
+//   3. sum:    clusters of up to SMALL rows: a thread per (cluster, column)
+//              adds the rows in order with SU row loads in flight;
+//   4. sum_big larger clusters: a workgroup per (cluster, 32-column strip);
+//              eight threads per column load the next 256 rows into LDS while
+//              one lane per column adds the current 256 in order, so a long
+//              chain waits on adds, not on memory.
 // HBM-bound: reads rows*d*4 bytes of rows (gathered by id) plus labels/ids,
 // writes k*d*4 of sums (+ k*d*4 read/write of acc).
 
@@ -19,56 +23,80 @@ namespace emh {
 namespace {
 
 constexpr int WAVE = 64;
+constexpr uint32_t NOROW = 0xffffffffu;
+constexpr int SMALL = 128;  // largest cluster the per-column path takes
+constexpr int SU = 32;      // row loads in flight per thread on that path
+constexpr int BR = 256;     // rows per chunk on the large-cluster path
+constexpr int BC = 32;      // columns per large-cluster workgroup
+constexpr int BT = 256;     // threads per large-cluster workgroup (BT / BC per column)
 
+// Counts, then (last workgroup) exclusive scan into start[0..k] and the list
+// of clusters with more than SMALL rows.
 __global__ __launch_bounds__(256) void k_count(const uint32_t* __restrict__ labels, size_t lo,
                                                size_t hi, size_t k, uint32_t* __restrict__ counts,
+                                               uint32_t* __restrict__ start,
+                                               uint32_t* __restrict__ bigj,
                                                uint32_t* __restrict__ small) {
-  size_t p = lo + (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (p >= hi) return;
-  uint32_t l = labels[p];
-  if (l < k)
-    atomicAdd(&counts[l], 1u);
-  else
-    small[SW_BAD_LABEL] = 1;
-}
-
-// Exclusive scan of counts[0..k) into start[0..k]; start[k] = total. One workgroup.
-__global__ __launch_bounds__(1024) void k_scan(const uint32_t* __restrict__ counts, size_t k,
-                                               uint32_t* __restrict__ start) {
-  __shared__ uint32_t part[1024];
-  __shared__ uint32_t carry;
-  if (threadIdx.x == 0) carry = 0;
+  __shared__ uint32_t part[256];
+  __shared__ uint32_t nbig;
+  __shared__ int last;
+  const int tid = threadIdx.x;
+  const size_t p = lo + (size_t)blockIdx.x * blockDim.x + tid;
+  if (p < hi) {
+    const uint32_t l = labels[p];
+    if (l < k)
+      atomicAdd(&counts[l], 1u);
+    else
+      small[SW_BAD_LABEL] = 1;
+  }
+  __threadfence();  // this workgroup's counts are visible before its ticket
   __syncthreads();
-  for (size_t b = 0; b < k; b += 1024) {
-    size_t j = b + threadIdx.x;
-    uint32_t v = j < k ? counts[j] : 0;
-    part[threadIdx.x] = v;
+  if (tid == 0) {
+    const uint32_t t = atomicAdd(&small[SW_TICKET], 1u);
+    last = t == gridDim.x - 1;
+    nbig = 0;
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  // Thread t scans the run [t*per, (t+1)*per) of the counts.
+  const size_t per = (k + 255) / 256;
+  const size_t a = min(k, (size_t)tid * per), b = min(k, a + per);
+  uint32_t s = 0;
+  for (size_t j = a; j < b; j++)
+    s += __hip_atomic_load(&counts[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  part[tid] = s;
+  __syncthreads();
+  for (int o = 1; o < 256; o <<= 1) {  // Hillis-Steele inclusive scan of the run totals
+    const uint32_t add = tid >= o ? part[tid - o] : 0u;
     __syncthreads();
-    for (int o = 1; o < 1024; o <<= 1) {  // Hillis-Steele inclusive scan
-      uint32_t add = threadIdx.x >= (unsigned)o ? part[threadIdx.x - o] : 0;
-      __syncthreads();
-      part[threadIdx.x] += add;
-      __syncthreads();
-    }
-    if (j < k) start[j] = carry + part[threadIdx.x] - v;
-    __syncthreads();
-    if (threadIdx.x == 1023) carry += part[1023];
+    part[tid] += add;
     __syncthreads();
   }
-  if (threadIdx.x == 0) start[k] = carry;
+  uint32_t run = part[tid] - s;
+  for (size_t j = a; j < b; j++) {
+    const uint32_t cj = __hip_atomic_load(&counts[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    start[j] = run;
+    run += cj;
+    if (cj > (uint32_t)SMALL) bigj[atomicAdd(&nbig, 1u)] = (uint32_t)j;
+  }
+  if (tid == 255) start[k] = part[255];
+  __syncthreads();
+  if (tid == 0) {
+    small[SW_NBIG] = nbig;
+    small[SW_TICKET] = 0;  // ready for the next call
+  }
 }
 
-// Stable placement: wave j walks positions lo..hi in order; rows with label j
-// go to rid[start[j] + rank], rank = number of earlier such rows. The block's
-// waves share the labels, staged in LDS a segment of SEG at a time.
+// Stable placement: wave j walks positions lo..hi in order; positions with
+// label j go to rid[start[j] + rank], rank = number of earlier such positions.
+// The block's waves share the labels, staged in LDS a segment at a time.
 constexpr int SEG = 16384;
 constexpr int PW = 4;  // waves (clusters) per block: k / 4 blocks spread over the CUs
-__global__ __launch_bounds__(64 * PW) void k_place(const uint32_t* __restrict__ labels,
-                                                const uint32_t* __restrict__ ids, size_t nx,
-                                                size_t lo, size_t hi, size_t k,
+__global__ __launch_bounds__(64 * PW) void k_place(const uint32_t* __restrict__ labels, size_t lo,
+                                                size_t hi, size_t k,
                                                 const uint32_t* __restrict__ start,
-                                                uint32_t* __restrict__ rid,
-                                                uint32_t* __restrict__ small) {
+                                                uint32_t* __restrict__ rid) {
   __shared__ uint32_t lab[SEG];
   const int lane = threadIdx.x % WAVE;
   const size_t j = (size_t)blockIdx.x * PW + threadIdx.x / WAVE;
@@ -108,13 +136,7 @@ __global__ __launch_bounds__(64 * PW) void k_place(const uint32_t* __restrict__ 
         if (mine) {
           const uint32_t rank = __builtin_amdgcn_mbcnt_hi(
               (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-          const size_t p = s0 + p0 + u * WAVE + lane;
-          uint32_t r = ids ? ids[p] : (uint32_t)p;
-          if (r >= nx) {  // a bad id adds nothing; reported at the next read
-            small[SW_BAD_ID] = 1;
-            r = 0xffffffffu;
-          }
-          rid[base + rank] = r;
+          rid[base + rank] = (uint32_t)(s0 + p0 + u * WAVE + lane);
         }
         base += (uint32_t)__popcll(m);
       }
@@ -122,60 +144,162 @@ __global__ __launch_bounds__(64 * PW) void k_place(const uint32_t* __restrict__ 
   }
 }
 
-// Ordered sums: thread = column of cluster blockIdx.x; rows in rid order.
-constexpr int U = 16;  // rows whose loads are in flight together
-__global__ __launch_bounds__(256) void k_sum(const float* __restrict__ x, size_t d,
+// Data row of position pos (NOROW, and the bad-id flag, when out of range).
+__device__ __forceinline__ uint32_t row_of(const uint32_t* __restrict__ ids, size_t nx,
+                                           uint32_t pos, uint32_t* __restrict__ small) {
+  const size_t r = ids ? (size_t)ids[pos] : (size_t)pos;
+  if (r >= nx) {  // a bad id adds nothing; reported at the next read
+    small[SW_BAD_ID] = 1;
+    return NOROW;
+  }
+  return (uint32_t)r;
+}
+
+// Clusters of up to SMALL rows: thread = column of cluster j; rows in order.
+__global__ __launch_bounds__(256) void k_sum(const float* __restrict__ x, size_t nx, size_t d,
+                                             const uint32_t* __restrict__ ids,
                                              const uint32_t* __restrict__ rid,
                                              const uint32_t* __restrict__ start, size_t k,
-                                             float* __restrict__ sums, float* __restrict__ acc) {
-  size_t j = blockIdx.x;
-  size_t col = (size_t)blockIdx.y * blockDim.x + threadIdx.x;
+                                             float* __restrict__ sums, float* __restrict__ acc,
+                                             uint32_t* __restrict__ small) {
+  __shared__ uint32_t rows[SMALL];
+  const size_t j = blockIdx.x;
+  const uint32_t b = start[j], cnt = start[j + 1] - b;
+  if (cnt > (uint32_t)SMALL) return;  // k_sum_big
+  if (threadIdx.x < cnt) rows[threadIdx.x] = row_of(ids, nx, rid[b + threadIdx.x], small);
+  __syncthreads();
+  const size_t col = (size_t)blockIdx.y * blockDim.x + threadIdx.x;
   if (col >= d) return;
-  const uint32_t b = start[j], e = start[j + 1];
   float s = 0.0f;
-  uint32_t q = b;
-  for (; q + U <= e; q += U) {
-    float v[U];
+  for (uint32_t q = 0; q < cnt; q += SU) {
+    float v[SU];
 #pragma unroll
-    for (int u = 0; u < U; u++) {
-      uint32_t r = rid[q + u];
-      v[u] = r != 0xffffffffu ? x[(size_t)r * d + col] : 0.0f;
+    for (int u = 0; u < SU; u++) {
+      const uint32_t r = q + u < cnt ? rows[q + u] : NOROW;
+      v[u] = r != NOROW ? x[(size_t)r * d + col] : 0.0f;
     }
 #pragma unroll
-    for (int u = 0; u < U; u++) s = s + v[u];
-  }
-  for (; q < e; q++) {
-    uint32_t r = rid[q];
-    if (r != 0xffffffffu) s = s + x[(size_t)r * d + col];
+    for (int u = 0; u < SU; u++)
+      if (q + u < cnt) s = s + v[u];  // +0 for a bad row: s is never -0, so this adds nothing
   }
   sums[j * d + col] = s;
   if (acc) acc[j * d + col] = acc[j * d + col] + s;
 }
 
+// Clusters with more than SMALL rows (listed by k_count): workgroup =
+// (listed cluster, strip of BC columns). Chunks of BR rows are double-buffered
+// in LDS; thread t loads column t % BC of rows t / BC + (BT / BC) u.
+__global__ __launch_bounds__(BT) void k_sum_big(const float* __restrict__ x, size_t nx, size_t d,
+                                                const uint32_t* __restrict__ ids,
+                                                const uint32_t* __restrict__ rid,
+                                                const uint32_t* __restrict__ start,
+                                                const uint32_t* __restrict__ bigj, int strips,
+                                                float* __restrict__ sums, float* __restrict__ acc,
+                                                uint32_t* __restrict__ small) {
+  constexpr int RPT = BR * BC / BT;  // rows loaded per thread per chunk
+  constexpr int RS = BT / BC;        // row stride between a thread's loads
+  __shared__ float vals[2][BR * BC];
+  __shared__ uint32_t rows[2][BR];
+  const int bi = blockIdx.x / strips, strip = blockIdx.x % strips;
+  if (bi >= (int)small[SW_NBIG]) return;
+  const uint32_t j = bigj[bi];
+  const uint32_t b = start[j], cnt = start[j + 1] - b;
+  const int tid = threadIdx.x, c = tid % BC, r0 = tid / BC;
+  const size_t col = (size_t)strip * BC + c;
+  const bool colok = col < d;
+  const uint32_t nchunks = (cnt + BR - 1) / BR;
+  auto stage = [&](uint32_t ch, int buf) {  // row ids of chunk ch
+    const uint32_t i = ch * BR + tid;
+    if (tid < BR) rows[buf][tid] = i < cnt ? row_of(ids, nx, rid[b + i], small) : NOROW;
+  };
+  float v[RPT];
+  auto gload = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < RPT; u++) {
+      const uint32_t r = rows[buf][r0 + RS * u];
+      v[u] = (r != NOROW && colok) ? x[(size_t)r * d + col] : 0.0f;
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < RPT; u++) vals[buf][(r0 + RS * u) * BC + c] = v[u];
+  };
+  stage(0, 0);
+  __syncthreads();
+  gload(0);
+  lstore(0);
+  if (nchunks > 1) stage(1, 1);
+  __syncthreads();
+  float s = 0.0f;
+  for (uint32_t ch = 0; ch < nchunks; ch++) {
+    const int cur = ch & 1, nxt = cur ^ 1;
+    if (ch + 1 < nchunks) gload(nxt);  // in flight while the current chunk is added
+    if (tid < BC) {
+      const uint32_t len = min((uint32_t)BR, cnt - ch * BR);
+      const float* vc = vals[cur];
+      for (uint32_t i = 0; i < len; i++) s = s + vc[i * BC + tid];
+    }
+    __syncthreads();  // the current chunk's values and row ids are consumed
+    if (ch + 1 < nchunks) lstore(nxt);
+    if (ch + 2 < nchunks) stage(ch + 2, cur);
+    __syncthreads();
+  }
+  if (tid < BC && colok) {
+    sums[(size_t)j * d + col] = s;
+    if (acc) acc[(size_t)j * d + col] = acc[(size_t)j * d + col] + s;
+  }
+}
+
 }  // namespace
+
+void launch_scatter_count(emh_ctx* c, size_t lo, size_t hi, const uint32_t* labels, size_t k,
+                          uint32_t* counts) {
+  const size_t n = hi > lo ? hi - lo : 0;
+  uint32_t* start = (uint32_t*)c->start.get((k + 1) * 4);
+  // Clusters above SMALL rows: at most n / (SMALL + 1) of them.
+  const size_t maxbig = std::min(k, n / (SMALL + 1) + 1);
+  uint32_t* bigj = (uint32_t*)c->bigj.get(maxbig * 4);
+  launch_fill_u32(c, counts, k, 0);
+  if (n > 0) {
+    hipLaunchKernelGGL(k_count, grid1(n, 256), dim3(256), 0, c->stream, labels, lo, hi, k, counts,
+                       start, bigj, c->small);
+    EMH_HIP(hipGetLastError());
+  } else {
+    launch_fill_u32(c, start, k + 1, 0);
+    launch_fill_u32(c, c->small + SW_NBIG, 1, 0);
+  }
+}
+
+void launch_scatter_sums(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
+                         size_t lo, size_t hi, const uint32_t* labels, size_t k, float* sums,
+                         float* acc) {
+  const size_t n = hi > lo ? hi - lo : 0;
+  uint32_t* start = (uint32_t*)c->start.get((k + 1) * 4);
+  uint32_t* rid = (uint32_t*)c->order.get(std::max<size_t>(n, 1) * 4);
+  const size_t maxbig = std::min(k, n / (SMALL + 1) + 1);
+  uint32_t* bigj = (uint32_t*)c->bigj.get(maxbig * 4);
+  if (n > 0) {
+    hipLaunchKernelGGL(k_place, grid1(k, PW), dim3(64 * PW), 0, c->stream, labels, lo, hi, k,
+                       start, rid);
+    EMH_HIP(hipGetLastError());
+  }
+  dim3 g((unsigned)k, (unsigned)((d + 255) / 256));
+  hipLaunchKernelGGL(k_sum, g, dim3(256), 0, c->stream, x, nx, d, ids, rid, start, k, sums, acc,
+                     c->small);
+  EMH_HIP(hipGetLastError());
+  if (n > (size_t)SMALL) {
+    const int strips = (int)((d + BC - 1) / BC);
+    hipLaunchKernelGGL(k_sum_big, dim3((unsigned)(maxbig * strips)), dim3(BT), 0, c->stream, x,
+                       nx, d, ids, rid, start, bigj, strips, sums, acc, c->small);
+    EMH_HIP(hipGetLastError());
+  }
+}
 
 void launch_scatter(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids, size_t lo,
                     size_t hi, const uint32_t* labels, size_t k, float* sums, uint32_t* counts,
                     float* acc) {
-  size_t n = hi > lo ? hi - lo : 0;
-  uint32_t* start = (uint32_t*)c->start.get((k + 1) * 4);
-  uint32_t* rid = (uint32_t*)c->order.get(std::max<size_t>(n, 1) * 4);
-  launch_fill_u32(c, counts, k, 0);
-  if (n > 0) {
-    hipLaunchKernelGGL(k_count, grid1(n, 256), dim3(256), 0, c->stream, labels, lo, hi, k, counts,
-                       c->small);
-    EMH_HIP(hipGetLastError());
-  }
-  hipLaunchKernelGGL(k_scan, dim3(1), dim3(1024), 0, c->stream, counts, k, start);
-  EMH_HIP(hipGetLastError());
-  if (n > 0) {
-    hipLaunchKernelGGL(k_place, grid1(k, PW), dim3(64 * PW), 0, c->stream, labels, ids, nx, lo,
-                       hi, k, start, rid, c->small);
-    EMH_HIP(hipGetLastError());
-  }
-  dim3 g((unsigned)k, (unsigned)((d + 255) / 256));
-  hipLaunchKernelGGL(k_sum, g, dim3(256), 0, c->stream, x, d, rid, start, k, sums, acc);
-  EMH_HIP(hipGetLastError());
+  launch_scatter_count(c, lo, hi, labels, k, counts);
+  launch_scatter_sums(c, x, nx, d, ids, lo, hi, labels, k, sums, acc);
 }
 
 }  // namespace emh

@@ -2,7 +2,7 @@
 // (emh_rescore.hip), for the rows the check could not settle:
 //
 //  k_exact_*   top-1: the rows' scan over all centroids, split into
-//              (8 rows x 64 centroids) items so that a handful of rows still
+//              (4 rows x 64 centroids) items so that a handful of rows still
 //              spreads over the whole chip, then a per-row reduction;
 //  k_exactk    top-k: one block per queued query over all data rows.
 //
@@ -21,8 +21,19 @@ constexpr int WAVE = 64;
 
 // ------------------------------------------------------------- exact top-1
 // Item = (group of RG rows, chunk of CJ centroids): one wave, lane = centroid,
-// RG chains per lane over d in tiles of TD dimensions staged in LDS.
-constexpr int CJ = 64, RG = 8, TD = 64;
+// RG chains per lane. The dimensions go in tiles of TD: a tile of the chunk's
+// centroids and the group's rows is loaded into registers (every load of the
+// tile in flight at once) while the previous tile is consumed from LDS.
+constexpr int CJ = 64, RG = 4, TD = 128, TDP = TD + 4;
+constexpr int CL4 = CJ * TD / 4 / WAVE;  // float4 loads per lane per tile (centroids)
+constexpr int XL4 = RG * TD / 4 / WAVE;  // float4 loads per lane per tile (rows)
+
+template <bool VEC4>
+__device__ __forceinline__ float4 load_tile4(const float* row, int col, int d) {
+  if (VEC4 && col + 4 <= d) return *reinterpret_cast<const float4*>(row + col);
+  return make_float4(col < d ? row[col] : 0.f, col + 1 < d ? row[col + 1] : 0.f,
+                     col + 2 < d ? row[col + 2] : 0.f, col + 3 < d ? row[col + 3] : 0.f);
+}
 
 template <bool VEC4>
 __global__ __launch_bounds__(64) void k_exact_part(
@@ -30,13 +41,16 @@ __global__ __launch_bounds__(64) void k_exact_part(
     int n_direct, const uint32_t* __restrict__ list, const uint32_t* __restrict__ small,
     const float* __restrict__ cents, const float* __restrict__ cnorm, int k, int ip,
     Cand* __restrict__ partial) {
-  __shared__ float ct[CJ][TD + 1];
-  __shared__ __attribute__((aligned(16))) float xt[RG][TD];
+  __shared__ __attribute__((aligned(16))) float ct[CJ * TDP];
+  __shared__ __attribute__((aligned(16))) float xt[RG * TD];
   __shared__ uint32_t xid_s[RG];
   const int nrows = list ? (int)small[SW_FALLBACK_COUNT] : n_direct;
   const int nch = (k + CJ - 1) / CJ;
   const int ngr = (nrows + RG - 1) / RG;
+  const int ntd = (d + TD - 1) / TD;
   const int lane = threadIdx.x;
+  const int c4 = lane % (TD / 4), r0 = lane / (TD / 4);  // this lane's float4 column, first row
+  constexpr int RSTEP = WAVE / (TD / 4);                  // rows per load instruction
   for (int item = blockIdx.x; item < ngr * nch; item += gridDim.x) {
     const int g = item / nch, q = item - g * nch;
     if (lane < RG) {
@@ -50,44 +64,60 @@ __global__ __launch_bounds__(64) void k_exact_part(
       xid_s[lane] = xid;
     }
     __syncthreads();
-    const int j = q * CJ + lane;
+    const float* xp[XL4];
+    bool xv[XL4];
+#pragma unroll
+    for (int u = 0; u < XL4; u++) {
+      const uint32_t xid = xid_s[r0 + RSTEP * u];
+      xv[u] = xid != NONE;
+      xp[u] = x + (size_t)(xv[u] ? xid : 0) * d;
+    }
+    float4 cr[CL4], xr[XL4];
+    auto gload = [&](int t0) {
+      const int col = t0 + 4 * c4;
+#pragma unroll
+      for (int u = 0; u < CL4; u++)
+        cr[u] = load_tile4<VEC4>(cents + (size_t)min(q * CJ + r0 + RSTEP * u, k - 1) * d, col, d);
+#pragma unroll
+      for (int u = 0; u < XL4; u++)
+        xr[u] = xv[u] ? load_tile4<VEC4>(xp[u], col, d) : make_float4(0.f, 0.f, 0.f, 0.f);
+    };
     float acc[RG];
 #pragma unroll
     for (int r = 0; r < RG; r++) acc[r] = 0.f;
-    for (int t0 = 0; t0 < d; t0 += TD) {
-      const int tl = min(TD, d - t0);
-      for (int i = lane; i < CJ * (TD / 4); i += WAVE) {
-        const int r = i / (TD / 4), c4 = i % (TD / 4);
-        const int jj = min(q * CJ + r, k - 1);
-        const float* cr = cents + (size_t)jj * d;
-        const int col = t0 + 4 * c4;
-        float4 v;
-        if (VEC4 && col + 4 <= d) {
-          v = *reinterpret_cast<const float4*>(cr + col);
-        } else {
-          v.x = col + 0 < d ? cr[col + 0] : 0.f;
-          v.y = col + 1 < d ? cr[col + 1] : 0.f;
-          v.z = col + 2 < d ? cr[col + 2] : 0.f;
-          v.w = col + 3 < d ? cr[col + 3] : 0.f;
-        }
-        ct[r][4 * c4 + 0] = v.x;
-        ct[r][4 * c4 + 1] = v.y;
-        ct[r][4 * c4 + 2] = v.z;
-        ct[r][4 * c4 + 3] = v.w;
-      }
-      for (int i = lane; i < RG * TD; i += WAVE) {
-        const int r = i / TD, c = i % TD;
-        const uint32_t xid = xid_s[r];
-        xt[r][c] = (xid != NONE && t0 + c < d) ? x[(size_t)xid * d + t0 + c] : 0.f;
-      }
-      __syncthreads();
-      for (int tt = 0; tt < tl; tt++) {
-        const float cv = ct[lane][tt];
+    gload(0);
+    for (int tile = 0; tile < ntd; tile++) {
 #pragma unroll
-        for (int r = 0; r < RG; r++) acc[r] = fmaf(xt[r][tt], cv, acc[r]);
+      for (int u = 0; u < CL4; u++)
+        *reinterpret_cast<float4*>(&ct[(r0 + RSTEP * u) * TDP + 4 * c4]) = cr[u];
+#pragma unroll
+      for (int u = 0; u < XL4; u++)
+        *reinterpret_cast<float4*>(&xt[(r0 + RSTEP * u) * TD + 4 * c4]) = xr[u];
+      __syncthreads();
+      const int t0 = tile * TD;
+      if (tile + 1 < ntd) gload(t0 + TD);
+      const int tl = min(TD, d - t0);
+      const float* crow = &ct[lane * TDP];
+      int tt = 0;
+      for (; tt + 4 <= tl; tt += 4) {
+        const float4 cv = *reinterpret_cast<const float4*>(crow + tt);
+#pragma unroll
+        for (int r = 0; r < RG; r++) {
+          const float4 v = *reinterpret_cast<const float4*>(&xt[r * TD + tt]);
+          acc[r] = fmaf(v.x, cv.x, acc[r]);
+          acc[r] = fmaf(v.y, cv.y, acc[r]);
+          acc[r] = fmaf(v.z, cv.z, acc[r]);
+          acc[r] = fmaf(v.w, cv.w, acc[r]);
+        }
+      }
+      for (; tt < tl; tt++) {
+        const float cv = crow[tt];
+#pragma unroll
+        for (int r = 0; r < RG; r++) acc[r] = fmaf(xt[r * TD + tt], cv, acc[r]);
       }
       __syncthreads();
     }
+    const int j = q * CJ + lane;
 #pragma unroll
     for (int r = 0; r < RG; r++) {
       float kx = INFINITY;
@@ -120,44 +150,75 @@ __global__ __launch_bounds__(64) void k_exact_part(
   }
 }
 
-__global__ __launch_bounds__(256) void k_exact_final(
+// One wave per row: the smallest of the row's chunk minima (lower id on ties),
+// and for L2 the row's |x|^2 as a sequential sum of rounded squares: the wave
+// loads 1024 dimensions at a time into LDS and lane 0 adds them in order.
+constexpr int FW = 4;      // rows (waves) per block
+constexpr int FSEG = 1024;  // dimensions staged per pass
+__global__ __launch_bounds__(64 * FW) void k_exact_final(
     const float* __restrict__ x, size_t nx, int d, const uint32_t* __restrict__ ids, size_t lo,
     int n_direct, const uint32_t* __restrict__ list, uint32_t* __restrict__ small, int k, int ip,
     const Cand* __restrict__ partial, uint32_t* __restrict__ labels, float* __restrict__ scores) {
+  __shared__ float sq[FW][FSEG];
+  const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
   const int nrows = list ? (int)small[SW_FALLBACK_COUNT] : n_direct;
   const int nch = (k + CJ - 1) / CJ;
   if (list && blockIdx.x == 0 && threadIdx.x == 0) small[SW_FALLBACK_TOTAL] += (uint32_t)nrows;
-  for (int f = blockIdx.x * blockDim.x + threadIdx.x; f < nrows; f += gridDim.x * blockDim.x) {
+  for (int f = blockIdx.x * FW + w; f < nrows; f += gridDim.x * FW) {  // uniform per wave
     const size_t p = list ? (size_t)list[f] : lo + (size_t)f;
     const size_t xid = ids ? (size_t)ids[p] : p;
     if (xid >= nx) {
-      small[SW_BAD_ID] = 1;
+      if (lane == 0) small[SW_BAD_ID] = 1;
       continue;
     }
     float best = INFINITY;
     uint32_t bid = NONE;
-    for (int q = 0; q < nch; q++) {
+    for (int q = lane; q < nch; q += WAVE) {
       const Cand c = partial[(size_t)f * nch + q];
       if (c.id != NONE && (c.key < best || (c.key == best && c.id < bid))) {
         best = c.key;
         bid = c.id;
       }
     }
+    for (int o = 32; o > 0; o >>= 1) {
+      float b2 = __shfl_xor(best, o, WAVE);
+      uint32_t i2 = __shfl_xor(bid, o, WAVE);
+      if (i2 != NONE && (b2 < best || (b2 == best && i2 < bid))) {
+        best = b2;
+        bid = i2;
+      }
+    }
     if (bid == NONE) {
       bid = 0;
       best = INFINITY;
     }
-    labels[p] = bid;
-    if (ip) {
-      scores[p] = -best;
-    } else {
+    float xn = 0.f;
+    if (!ip) {
       const float* xr = x + xid * (size_t)d;
-      float xn = 0.f;
-      for (int t = 0; t < d; t++) {
-        float q2 = xr[t] * xr[t];
-        xn = xn + q2;
+      for (int t0 = 0; t0 < d; t0 += FSEG) {
+        const int tl = min(FSEG, d - t0);
+        float v[FSEG / WAVE];
+#pragma unroll
+        for (int u = 0; u < FSEG / WAVE; u++) {
+          const int i = lane + WAVE * u;
+          v[u] = i < tl ? xr[t0 + i] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < FSEG / WAVE; u++) {
+          const int i = lane + WAVE * u;
+          if (i < tl) sq[w][i] = v[u] * v[u];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        if (lane == 0)
+          for (int i = 0; i < tl; i++) xn = xn + sq[w][i];
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
       }
-      scores[p] = fmaxf(xn + best, 0.0f);
+    }
+    if (lane == 0) {
+      labels[p] = bid;
+      scores[p] = ip ? -best : fmaxf(xn + best, 0.0f);
     }
   }
 }
@@ -304,8 +365,8 @@ void launch_exact1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32
     hipLaunchKernelGGL(k_exact_part<false>, dim3(g), dim3(64), 0, c->stream, x, nx, (int)d, ids,
                        lo, (int)n, list, c->small, cents, cnorm, (int)k, ip ? 1 : 0, partial);
   EMH_HIP(hipGetLastError());
-  const unsigned g2 = (unsigned)std::min<size_t>((n + 255) / 256, (size_t)4 * c->cus);
-  hipLaunchKernelGGL(k_exact_final, dim3(g2), dim3(256), 0, c->stream, x, nx, (int)d, ids, lo,
+  const unsigned g2 = (unsigned)std::min<size_t>((n + FW - 1) / FW, (size_t)4 * c->cus);
+  hipLaunchKernelGGL(k_exact_final, dim3(g2), dim3(64 * FW), 0, c->stream, x, nx, (int)d, ids, lo,
                      (int)n, list, c->small, (int)k, ip ? 1 : 0, partial, labels, scores);
   EMH_HIP(hipGetLastError());
 }

@@ -171,6 +171,7 @@ typedef struct emh_train_out {
   double alpha0;
   uint64_t total_steps;
   uint64_t fallback_rows; /* rows the exact top-1 kernel rescanned (screen misses) */
+  emh_buf* centroids_dev; /* optional: the centroids also land in this k*d f32 buffer */
 } emh_train_out;
 
 /* Emeans::train (model.rs:700-811) driving the device loop core::train::run

@@ -197,6 +197,40 @@ def test_scatter_ema_split(dev, n, d, k):
     assert dev.read_f32(u).tobytes() == wu.tobytes()
 
 
+@pytest.mark.parametrize("d", [200, 768])
+def test_scatter_skewed_clusters(dev, d):
+    """Skewed cluster sizes (the Zipf case of training): clusters of several
+    thousand rows, sizes at the edges of the per-column path (127..129, 256,
+    257 rows), a single row and empty clusters; rows gathered by id; with acc."""
+    from emeans_amd import Mat, Select
+    n, k = 20000, 96
+    g = np.random.default_rng(d)
+    sizes = [5000, 2049, 257, 256, 129, 128, 127, 1, 0]
+    rest = n - sum(sizes)
+    labels = np.concatenate([np.full(s, j, np.uint32) for j, s in enumerate(sizes)] +
+                            [g.integers(len(sizes), k, rest).astype(np.uint32)])
+    g.shuffle(labels)
+    nx = n + 37
+    x = g.standard_normal((nx, d)).astype(np.float32)
+    perm = g.permutation(nx)[:n].astype(np.uint32)
+    acc0 = g.standard_normal(k * d).astype(np.float32)
+    xb, idb, lb = dev.bind(x), dev.upload_u32(perm), dev.upload_u32(labels)
+    sums, counts, acc = dev.zeros_f32(k * d), dev.zeros_u32(k), dev.upload_f32(acc0)
+    for lo, hi in [(0, n), (3, n - 5)]:
+        dev.scatter_add(Mat(xb, d), Select(idb, (lo, hi)), lb, k, sums, counts, acc)
+        oacc = acc0.copy()
+        os_, oc = O.scatter_add(x, d, labels, k, ids=perm, rows=(lo, hi), acc=oacc)
+        assert np.array_equal(dev.read_u32(counts), oc), (lo, hi)
+        assert dev.read_f32(sums).tobytes() == os_.tobytes(), (lo, hi)
+        assert dev.read_f32(acc).tobytes() == oacc.tobytes(), (lo, hi)
+        acc = dev.upload_f32(acc0)
+    # Without ids (rows are positions) and without acc.
+    dev.scatter_add(Mat(xb, d), Select(None, (0, n)), lb, k, sums, counts, None)
+    os_, oc = O.scatter_add(x[:n], d, labels, k)
+    assert np.array_equal(dev.read_u32(counts), oc)
+    assert dev.read_f32(sums).tobytes() == os_.tobytes()
+
+
 @pytest.mark.parametrize("d", [768, 20, 13, 64, 2500])
 def test_norms_and_normalize(dev, d):
     """contract.rs:500-554: a zero row and a 1e30-scaled row (the max-prescale path)."""
