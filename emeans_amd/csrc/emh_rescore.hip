@@ -8,7 +8,7 @@
 //   score = dot (IP) or max(|x|^2 + key, 0) (L2, assign.rs:497-502);
 //   ties to the lower id.
 // One thread per (row, candidate) pair runs a chain, reading the row and the
-// candidate from global memory (L2/MALL-resident after the screen) with eight
+// candidate from global memory (L2/MALL-resident after the screen) with PF
 // float4 loads of each in flight; the small LDS footprint keeps many blocks
 // per CU so the chains' latency overlaps.
 
@@ -16,6 +16,8 @@
 
 namespace emh {
 namespace {
+
+constexpr int PF = 16;  // float4 loads of each operand in flight per chain
 
 // Exact fma chain of x and c (the cpu-fused dot); acc starts at +0.
 template <bool VEC4>
@@ -27,15 +29,15 @@ __device__ __forceinline__ float chain(const float* __restrict__ xr, const float
     const float4* x4 = reinterpret_cast<const float4*>(xr);
     const int d4 = d >> 2;
     int t = 0;
-    for (; t + 8 <= d4; t += 8) {
-      float4 a[8], b[8];
+    for (; t + PF <= d4; t += PF) {
+      float4 a[PF], b[PF];
 #pragma unroll
-      for (int u = 0; u < 8; u++) {
+      for (int u = 0; u < PF; u++) {
         a[u] = x4[t + u];
         b[u] = c4[t + u];
       }
 #pragma unroll
-      for (int u = 0; u < 8; u++) {
+      for (int u = 0; u < PF; u++) {
         acc = fmaf(a[u].x, b[u].x, acc);
         acc = fmaf(a[u].y, b[u].y, acc);
         acc = fmaf(a[u].z, b[u].z, acc);
@@ -63,12 +65,12 @@ __device__ __forceinline__ float seq_sq(const float* __restrict__ xr, int d) {
     const float4* x4 = reinterpret_cast<const float4*>(xr);
     const int d4 = d >> 2;
     int t = 0;
-    for (; t + 8 <= d4; t += 8) {
-      float4 a[8];
+    for (; t + PF <= d4; t += PF) {
+      float4 a[PF];
 #pragma unroll
-      for (int u = 0; u < 8; u++) a[u] = x4[t + u];
+      for (int u = 0; u < PF; u++) a[u] = x4[t + u];
 #pragma unroll
-      for (int u = 0; u < 8; u++) {
+      for (int u = 0; u < PF; u++) {
         float p0 = a[u].x * a[u].x, p1 = a[u].y * a[u].y, p2 = a[u].z * a[u].z,
               p3 = a[u].w * a[u].w;
         s = s + p0;
@@ -279,7 +281,7 @@ __global__ __launch_bounds__(256) void k_verify(
   }
 }
 
-constexpr int R1 = 32;  // rows per block, top-1
+constexpr int R1 = 16;  // rows per block, top-1
 constexpr int RK = 16;  // rows per block, top-k
 
 }  // namespace

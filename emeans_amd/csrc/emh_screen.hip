@@ -71,8 +71,9 @@ __device__ __forceinline__ float4 mask4(float4 v, int col, int d) {
 // row n = l % 32 of each block, so a row's keys stay in two lanes of a wave.
 // The screen sums the K dimension in any order: lane half h = l / 32 takes
 // dimensions [h*16, h*16 + 16) of each slab, four per b128 LDS read. Slabs
-// are double-buffered in LDS; the global loads of the next slab are in flight
-// while the MFMAs of the current one run.
+// are double-buffered in LDS; the global loads of the next slab are issued
+// before the MFMAs of the current one and stored to the other buffer after
+// them.
 template <int WN, int L, bool L2, bool KNN, bool VEC4>
 __global__ __launch_bounds__(256, 2) void k_screen(
     const float* __restrict__ x, size_t nx, int d, const uint32_t* __restrict__ ids, size_t lo,
@@ -155,9 +156,9 @@ __global__ __launch_bounds__(256, 2) void k_screen(
     }
   };
   // The error bound's inputs, gathered on the way: max |c_j|^2 over the
-  // centroids this block loads (each row's squares summed in any order), and
-  // max cnorm[j]. Compared as f32 bit patterns: a NaN or negative value wins
-  // and sends every row of the call to the exact scan.
+  // centroids (each row's squares summed in any order; by the blocks of row
+  // tile 0), and max cnorm[j]. Compared as f32 bit patterns: a NaN or negative
+  // value wins and sends every row of the call to the exact scan.
   float csq[CL];
 #pragma unroll
   for (int u = 0; u < CL; u++) csq[u] = 0.f;
@@ -180,21 +181,38 @@ __global__ __launch_bounds__(256, 2) void k_screen(
     }
   };
   // Stores the slab loaded by gload (masked past d); the first use of the
-  // loaded registers, so the loads overlap the MFMAs issued in between.
+  // loaded registers, so the loads overlap the MFMAs issued in between. The
+  // mask and the norm sums are block-uniform branches: only a final partial
+  // slab is masked; only part 0 sums its rows' squares (during its first
+  // tile), and only row tile 0 the centroids' (its parts together cover every
+  // centroid tile).
   auto lstore = [&](int buf) {
     const int col = ls * BK + c4;
-    const bool tail = col + 4 > d;
+    if (ls == nslabs - 1 && d % BK != 0) {
 #pragma unroll
-    for (int u = 0; u < XL; u++) {
-      const float4 v = tail ? mask4(xr[u], col, d) : xr[u];
-      *reinterpret_cast<float4*>(&Xs[buf][((tid >> 3) + 32 * u) * LDK + c4]) = v;
-      if (lt == t0) xsq[u] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+      for (int u = 0; u < XL; u++) xr[u] = mask4(xr[u], col, d);
+#pragma unroll
+      for (int u = 0; u < CL; u++) cr[u] = mask4(cr[u], col, d);
     }
 #pragma unroll
-    for (int u = 0; u < CL; u++) {
-      const float4 v = tail ? mask4(cr[u], col, d) : cr[u];
-      *reinterpret_cast<float4*>(&Cs[buf][((tid >> 3) + 32 * u) * LDK + c4]) = v;
-      csq[u] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    for (int u = 0; u < XL; u++)
+      *reinterpret_cast<float4*>(&Xs[buf][((tid >> 3) + 32 * u) * LDK + c4]) = xr[u];
+#pragma unroll
+    for (int u = 0; u < CL; u++)
+      *reinterpret_cast<float4*>(&Cs[buf][((tid >> 3) + 32 * u) * LDK + c4]) = cr[u];
+    if (part == 0 && lt == t0) {
+#pragma unroll
+      for (int u = 0; u < XL; u++) {
+        const float4 v = xr[u];
+        xsq[u] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+      }
+    }
+    if (rt == 0) {
+#pragma unroll
+      for (int u = 0; u < CL; u++) {
+        const float4 v = cr[u];
+        csq[u] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+      }
     }
     if (ls == 0 && tid < TC) {
       Ns[lt & 1][tid] = nvalid ? nreg : INFINITY;
@@ -204,16 +222,18 @@ __global__ __launch_bounds__(256, 2) void k_screen(
   auto advance = [&]() {
     if (++ls == nslabs) {
       // Tile lt fully loaded: its rows' squared norms (8 lanes per row).
+      if (rt == 0) {
 #pragma unroll
-      for (int u = 0; u < CL; u++) {
-        float s = csq[u];
-        s += __shfl_xor(s, 1, 64);
-        s += __shfl_xor(s, 2, 64);
-        s += __shfl_xor(s, 4, 64);
-        cmax_bits = max(cmax_bits, __float_as_uint(s));
-        csq[u] = 0.f;
+        for (int u = 0; u < CL; u++) {
+          float s = csq[u];
+          s += __shfl_xor(s, 1, 64);
+          s += __shfl_xor(s, 2, 64);
+          s += __shfl_xor(s, 4, 64);
+          cmax_bits = max(cmax_bits, __float_as_uint(s));
+          csq[u] = 0.f;
+        }
       }
-      if (lt == t0) {
+      if (part == 0 && lt == t0) {
 #pragma unroll
         for (int u = 0; u < XL; u++) {
           float s = xsq[u];
@@ -221,7 +241,7 @@ __global__ __launch_bounds__(256, 2) void k_screen(
           s += __shfl_xor(s, 2, 64);
           s += __shfl_xor(s, 4, 64);
           const int r = row0 + (tid >> 3) + 32 * u;
-          if (part == 0 && (tid & 7) == 0 && r < nrows) xnorm[r] = s;
+          if ((tid & 7) == 0 && r < nrows) xnorm[r] = s;
         }
       }
       ls = 0;
@@ -290,7 +310,7 @@ __global__ __launch_bounds__(256, 2) void k_screen(
             float v = acc[a][y][r];
             float key = L2 ? nn - 2.0f * v : nn - v;
             if (KNN && gj == qrow[y]) key = INFINITY;
-            insert<L>(lkey[y], lid[y], key, gj);
+            insert_nb<L>(lkey[y], lid[y], key, gj);
             acc[a][y][r] = 0.f;
           }
         }
@@ -301,7 +321,7 @@ __global__ __launch_bounds__(256, 2) void k_screen(
       ++ct;
     }
     if (more) {
-      lstore(buf ^ 1);
+      lstore(buf ^ 1);  // after this slab's MFMAs: the loads had all of them to land
       advance();
     }
     __syncthreads();

@@ -37,6 +37,28 @@ __device__ __forceinline__ void insert(float (&key)[L], uint32_t (&id)[L], float
   }
 }
 
+// The same insertion without a branch: every slot takes its new value at once
+// from the comparisons c[e] = v < key[e] of the old list. For a sorted list,
+// slot e becomes key[e - 1] if v < key[e - 1], else min(v, key[e]), which is
+// med3(key[e - 1], v, key[e]). v is first mapped to +inf when it is NaN or
+// +inf, so such a key leaves the list unchanged; equal keys stay after the
+// ones already in the list.
+template <int L>
+__device__ __forceinline__ void insert_nb(float (&key)[L], uint32_t (&id)[L], float v,
+                                          uint32_t j) {
+  v = fminf(v, INFINITY);  // NaN -> +inf
+  bool c[L];
+#pragma unroll
+  for (int e = 0; e < L; e++) c[e] = v < key[e];
+#pragma unroll
+  for (int e = L - 1; e > 0; e--) {
+    key[e] = __builtin_amdgcn_fmed3f(key[e - 1], v, key[e]);
+    id[e] = c[e - 1] ? id[e - 1] : (c[e] ? j : id[e]);
+  }
+  key[0] = fminf(v, key[0]);
+  id[0] = c[0] ? j : id[0];
+}
+
 // Screen error bound E on |key' - key| for one row (see emh_screen.hip):
 // xn and cmax2 are squared norms summed in any order (relative error <= gamma_d,
 // absorbed by the (1 + g) factors); cnmax bounds the given centroid norms.
