@@ -495,7 +495,9 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
       const float* cn = sph ? nullptr : readout.f();
       for (size_t c0 = b; c0 < e; c0 += chunk) {
         const size_t c1 = std::min(c0 + chunk, e);
-        launch_top1(c, x, n, d, order, c0, c1, cents, cn, k, sph, lab, sco);
+        // After the first step the previous EMA cleared the screen's words.
+        launch_top1(c, x, n, d, order, c0, c1, cents, cn, k, sph, lab, sco,
+                    step > 0 && c0 == b);
       }
       const double alpha = scheduled_alpha(R.alpha0, step, R.total_steps);
       const float af = (float)alpha, df = (float)(1.0 - alpha);
@@ -510,7 +512,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
       }
       launch_scatter_sums(c, x, n, d, order, b, e, lab, k, sums.f(), last ? pass.f() : nullptr);
       launch_ema(c, pos.f(), mass.f(), sums.f(), counts.u(), k, d, af, df, replace,
-                 sph ? nullptr : readout.f());
+                 sph ? nullptr : readout.f(), true);
       if (check) {
         ev_check.wait();
         raise_flags(c, h_small);

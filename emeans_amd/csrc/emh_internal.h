@@ -124,7 +124,7 @@ struct emh_ctx {
   int screen = 1;
   uint32_t* small = nullptr;  // SW_WORDS u32 on the device
   uint64_t fallback_total = 0;
-  emh::Scratch cand, fblist, order, start, misc, knn_tmp, xnorm, bigj;
+  emh::Scratch cand, fblist, order, start, misc, knn_tmp, xnorm, bigj, chunkcnt;
   // Host staging of the device loop: masses, plan, flags, epoch orders and
   // epoch labels/scores (double-buffered), results.
   emh::Pinned pin_usage, pin_plan, pin_small, pin_order[2], pin_lab[2], pin_sco[2], pin_out;
@@ -173,8 +173,12 @@ struct ProfScope {
 void launch_fill_u32(emh_ctx* c, uint32_t* p, size_t n, uint32_t v);
 void launch_row_norms(emh_ctx* c, const float* m, size_t rows, size_t d, float* out);
 void launch_normalize_rows(emh_ctx* c, const float* src, size_t rows, size_t d, float* dst);
+// With clear_screen_words, also zeroes the small-block words launch_top1
+// clears before its screen (the fallback count and the bound maxima), so the
+// next top-1 may skip that fill.
 void launch_ema(emh_ctx* c, float* pos, float* usage, const float* sums, const uint32_t* counts,
-                size_t k, size_t d, float alpha, float decay, int replace, float* norms = nullptr);
+                size_t k, size_t d, float alpha, float decay, int replace, float* norms = nullptr,
+                bool clear_screen_words = false);
 // The masses launch_ema will leave, into out (usage untouched).
 void launch_mass_preview(emh_ctx* c, const float* usage, const uint32_t* counts, size_t k,
                          float alpha, float decay, int replace, float* out);
@@ -203,9 +207,11 @@ void launch_scatter_sums(emh_ctx* c, const float* x, size_t nx, size_t d, const 
                          float* acc);
 
 // ---- emh_screen.hip (top-1 and top-k orchestration)
+// words_clear: the caller zeroed the screen's small-block words since the
+// last top-1 (launch_ema with clear_screen_words), so the fill is skipped.
 void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids, size_t lo, size_t hi,
                  const float* cents, const float* cnorm, size_t k, bool ip, uint32_t* labels,
-                 float* scores);
+                 float* scores, bool words_clear = false);
 
 void launch_topk(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,
                  size_t kk, bool exclude_self, uint32_t* ids, float* sims);

@@ -141,52 +141,88 @@ __device__ __forceinline__ float ema_mass(float u, uint32_t cnt, float alpha, fl
 
 // With norms != nullptr, also the squared norm of every updated row (the next
 // batch's L2 readout, assign.rs:150-155); rows without members keep theirs.
+// Workgroup = EC clusters: the 256 threads update the clusters' positions
+// element by element, then lane c of the first wave adds cluster c's rounded
+// squares in order from LDS (rows padded by one float so the EC lanes read
+// different banks); the chains of EC clusters run side by side.
+constexpr int EC = 16;
+constexpr int ECH = 512;  // dimensions per LDS pass
+constexpr int EU = 16;    // elements per thread whose loads are in flight together
 __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __restrict__ usage,
                                              const float* __restrict__ sums,
                                              const uint32_t* __restrict__ counts, size_t k,
                                              size_t d, float alpha, float decay, int replace,
-                                             float* __restrict__ norms) {
-  __shared__ __attribute__((aligned(16))) float sq[WAVES][CH];
-  int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-  size_t j = (size_t)blockIdx.x * WAVES + w;
-  if (j >= k) return;  // whole wave; no workgroup barrier below
-  const uint32_t cnt = counts[j];
-  float weight;
-  const float u = ema_mass(usage[j], cnt, alpha, decay, replace, &weight);
-  if (cnt > 0) {
-    const float count = (float)cnt;
-    float* p = pos + j * d;
-    const float* s = sums + j * d;
-    float nrm = 0.0f;
-    for (size_t c0 = 0; c0 < d; c0 += CH) {
-      const int len = (int)min((size_t)CH, d - c0);
-      for (int t = lane; t < len; t += WAVE) {
-        const float mean = s[c0 + t] / count;
-        float v;
-        if (weight == 1.0f) {
-          v = mean;
-        } else {
-          const float c = p[c0 + t];
-          const float diff = mean - c;
-          const float inc = weight * diff;
-          v = c + inc;
+                                             float* __restrict__ norms,
+                                             uint32_t* __restrict__ clear3) {
+  extern __shared__ float sq[];  // EC rows of min(d, ECH) + 1 floats (norms only)
+  __shared__ float wgt[EC], cntf[EC];
+  const int tid = threadIdx.x;
+  const size_t j0 = (size_t)blockIdx.x * EC;
+  const int nc = (int)min((size_t)EC, k - j0);
+  if (clear3 && blockIdx.x == 0 && tid < 3) clear3[tid] = 0;
+  if (tid < nc) {
+    const uint32_t cnt = counts[j0 + tid];
+    float weight;
+    usage[j0 + tid] = ema_mass(usage[j0 + tid], cnt, alpha, decay, replace, &weight);
+    wgt[tid] = cnt > 0 ? weight : -1.0f;  // -1: no rows, position unchanged
+    cntf[tid] = (float)cnt;
+  }
+  __syncthreads();
+  const int seg = (int)min(d, (size_t)ECH), row = seg + 1;
+  // Thread layout of the update: 16 threads per cluster, thread q of cluster
+  // c takes dimensions q, q + 16, ...
+  const int c = tid / (256 / EC), q = tid % (256 / EC);
+  const float weight = c < nc ? wgt[c] : -1.0f;
+  const float count = c < nc ? cntf[c] : 1.0f;
+  float nrm = 0.0f;  // lane c < nc of wave 0: cluster c's chain
+  for (size_t c0 = 0; c0 < d; c0 += ECH) {
+    const int len = (int)min((size_t)ECH, d - c0);
+    if (weight >= 0.0f) {
+      float* p = pos + (j0 + c) * d + c0;
+      const float* s = sums + (j0 + c) * d + c0;
+      for (int t0 = q; t0 < len; t0 += 16 * EU) {
+        float sv[EU], pv[EU];
+#pragma unroll
+        for (int u = 0; u < EU; u++) {
+          const int t = t0 + 16 * u;
+          sv[u] = t < len ? s[t] : 0.0f;
+          pv[u] = t < len ? p[t] : 0.0f;
         }
-        p[c0 + t] = v;
-        sq[w][t] = v * v;
-      }
-      if (norms) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        if (lane == 0) nrm = seq_add(sq[w], len, nrm);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int u = 0; u < EU; u++) {
+          const int t = t0 + 16 * u;
+          if (t >= len) continue;
+          const float mean = sv[u] / count;
+          float v;
+          if (weight == 1.0f) {
+            v = mean;
+          } else {
+            const float diff = mean - pv[u];
+            const float inc = weight * diff;
+            v = pv[u] + inc;
+          }
+          p[t] = v;
+          if (norms) sq[c * row + t] = v * v;
+        }
       }
     }
-    if (norms && lane == 0) norms[j] = nrm;
+    if (!norms) continue;
+    __syncthreads();
+    if (tid < nc && wgt[tid] >= 0.0f) {
+      const float* r = sq + tid * row;
+      int t = 0;
+      for (; t + 16 <= len; t += 16) {  // 16 LDS reads in flight, adds in order
+        float v[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) v[u] = r[t + u];
+#pragma unroll
+        for (int u = 0; u < 16; u++) nrm = nrm + v[u];
+      }
+      for (; t < len; t++) nrm = nrm + r[t];
+    }
+    __syncthreads();
   }
-  if (lane == 0) usage[j] = u;
+  if (norms && tid < nc && wgt[tid] >= 0.0f) norms[j0 + tid] = nrm;
 }
 
 // The masses the EMA step will leave (for the host's revival check), without
@@ -332,10 +368,12 @@ void launch_normalize_rows(emh_ctx* c, const float* src, size_t rows, size_t d, 
 }
 
 void launch_ema(emh_ctx* c, float* pos, float* usage, const float* sums, const uint32_t* counts,
-                size_t k, size_t d, float alpha, float decay, int replace, float* norms) {
+                size_t k, size_t d, float alpha, float decay, int replace, float* norms,
+                bool clear_screen_words) {
   if (k == 0) return;
-  hipLaunchKernelGGL(k_ema, grid1(k, WAVES), dim3(256), 0, c->stream, pos, usage, sums, counts, k,
-                     d, alpha, decay, replace, norms);
+  const size_t lds = norms ? (size_t)EC * (std::min(d, (size_t)ECH) + 1) * sizeof(float) : 0;
+  hipLaunchKernelGGL(k_ema, grid1(k, EC), dim3(256), lds, c->stream, pos, usage, sums, counts, k,
+                     d, alpha, decay, replace, norms, clear_screen_words ? c->small : nullptr);
   EMH_HIP(hipGetLastError());
 }
 

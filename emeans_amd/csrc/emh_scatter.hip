@@ -4,10 +4,14 @@
 // so the work is split into a stable counting sort and ordered sums:
 //   1. count:  labels -> counts (integer atomics; exact in any order); the
 //              last workgroup to finish scans the counts into start offsets
-//              and lists the clusters too large for the per-column path;
-//   2. place:  one wave per cluster walks the labels in selection order with
-//              wave ballots and writes the cluster's positions, in order, at
-//              its start offset;
+//              and lists the clusters too large for the per-column path. For
+//              k up to KCH the counts are per-chunk LDS histograms of CP
+//              positions, and that workgroup also prefixes them per label;
+//   2. place:  each position's rank among the earlier positions of its label
+//              (chunked: the earlier chunks' prefix plus a scan of its own
+//              chunk in LDS; else one wave per cluster walking the labels with
+//              ballots), so each cluster's positions land in order at its
+//              start offset;
 //   3. sum:    clusters of up to SMALL rows: a thread per (cluster, column)
 //              adds the rows in order with SU row loads in flight;
 //   4. sum_big larger clusters: a workgroup per (cluster, 32-column strip);
@@ -86,6 +90,139 @@ __global__ __launch_bounds__(256) void k_count(const uint32_t* __restrict__ labe
     small[SW_NBIG] = nbig;
     small[SW_TICKET] = 0;  // ready for the next call
   }
+}
+
+// ---- chunked count and placement (k <= KCH): positions in chunks of CP.
+constexpr int CP = 256;
+constexpr int KCH = 8192;  // LDS histogram of one chunk
+
+// Chunk c's label histogram (LDS atomics) goes to cnt[c][0..k); the last
+// workgroup to finish turns every label's column into its exclusive prefix
+// over the chunks (in place), totals it into counts, and scans the counts
+// into start offsets and the list of clusters above SMALL rows.
+__global__ __launch_bounds__(256) void k_count_chunks(
+    const uint32_t* __restrict__ labels, size_t lo, size_t hi, size_t k,
+    uint32_t* __restrict__ counts, uint32_t* __restrict__ start, uint32_t* __restrict__ bigj,
+    uint32_t* __restrict__ cnt, uint32_t* __restrict__ small) {
+  __shared__ uint32_t h[KCH];
+  __shared__ uint32_t part[256];
+  __shared__ uint32_t nbig;
+  __shared__ int last;
+  const int tid = threadIdx.x;
+  const size_t c = blockIdx.x, nch = gridDim.x;
+  for (size_t j = tid; j < k; j += 256) h[j] = 0;
+  __syncthreads();
+  const size_t p = lo + c * CP + tid;
+  if (p < hi) {
+    const uint32_t l = labels[p];
+    if (l < k)
+      atomicAdd(&h[l], 1u);
+    else
+      small[SW_BAD_LABEL] = 1;
+  }
+  __syncthreads();
+  for (size_t j = tid; j < k; j += 256) cnt[c * k + j] = h[j];
+  __threadfence();  // this chunk's histogram is visible before its ticket
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t tk = atomicAdd(&small[SW_TICKET], 1u);
+    last = tk == nch - 1;
+    nbig = 0;
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  // Each thread takes four labels (256 apart) at a time and the chunks in
+  // batches of PB, all of a batch's loads issued before its stores. The other
+  // workgroups' histograms reached L2 before their tickets, and this one's L1
+  // holds none of their lines, so plain loads see them.
+  constexpr int PQ = 4, PB = 16;
+  for (size_t j0 = tid; j0 < k; j0 += 256 * PQ) {
+    uint32_t s[PQ];
+#pragma unroll
+    for (int q = 0; q < PQ; q++) s[q] = 0;
+    for (size_t cc0 = 0; cc0 < nch; cc0 += PB) {
+      uint32_t v[PQ][PB];
+#pragma unroll
+      for (int q = 0; q < PQ; q++)
+#pragma unroll
+        for (int u = 0; u < PB; u++) {
+          const size_t j = j0 + 256 * q, cc = cc0 + u;
+          v[q][u] = (j < k && cc < nch) ? cnt[cc * k + j] : 0u;
+        }
+#pragma unroll
+      for (int q = 0; q < PQ; q++)
+#pragma unroll
+        for (int u = 0; u < PB; u++) {
+          const size_t j = j0 + 256 * q, cc = cc0 + u;
+          if (j < k && cc < nch) {
+            cnt[cc * k + j] = s[q];
+            s[q] += v[q][u];
+          }
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < PQ; q++) {
+      const size_t j = j0 + 256 * q;
+      if (j < k) {
+        counts[j] = s[q];
+        h[j] = s[q];  // the totals, for the scan below
+      }
+    }
+  }
+  __syncthreads();
+  const size_t per = (k + 255) / 256;
+  const size_t a = min(k, (size_t)tid * per), b = min(k, a + per);
+  uint32_t s = 0;
+  for (size_t j = a; j < b; j++) s += h[j];
+  part[tid] = s;
+  __syncthreads();
+  for (int o = 1; o < 256; o <<= 1) {  // Hillis-Steele inclusive scan of the run totals
+    const uint32_t add = tid >= o ? part[tid - o] : 0u;
+    __syncthreads();
+    part[tid] += add;
+    __syncthreads();
+  }
+  uint32_t run = part[tid] - s;
+  for (size_t j = a; j < b; j++) {
+    const uint32_t cj = h[j];
+    start[j] = run;
+    run += cj;
+    if (cj > (uint32_t)SMALL) bigj[atomicAdd(&nbig, 1u)] = (uint32_t)j;
+  }
+  if (tid == 255) start[k] = part[255];
+  __syncthreads();
+  if (tid == 0) {
+    small[SW_NBIG] = nbig;
+    small[SW_TICKET] = 0;  // ready for the next call
+  }
+}
+
+// Position p of chunk c goes to rid[start[l] + (rows of label l in earlier
+// chunks) + (rows of label l earlier in this chunk)], l = labels[p].
+__global__ __launch_bounds__(256) void k_place_chunks(const uint32_t* __restrict__ labels,
+                                                       size_t lo, size_t hi, size_t k,
+                                                       const uint32_t* __restrict__ start,
+                                                       const uint32_t* __restrict__ cnt,
+                                                       uint32_t* __restrict__ rid) {
+  __shared__ __attribute__((aligned(16))) uint32_t lab[CP];
+  const int tid = threadIdx.x;
+  const size_t c = blockIdx.x;
+  const size_t p = lo + c * CP + tid;
+  const uint32_t l = p < hi ? labels[p] : 0xffffffffu;
+  lab[tid] = l;
+  __syncthreads();
+  if (l >= k) return;
+  uint32_t rank = 0;
+  const uint4* l4 = reinterpret_cast<const uint4*>(lab);
+#pragma unroll 8
+  for (int i4 = 0; i4 < CP / 4; i4++) {
+    const uint4 q = l4[i4];
+    const int i = 4 * i4;
+    rank += (uint32_t)(i < tid && q.x == l) + (uint32_t)(i + 1 < tid && q.y == l) +
+            (uint32_t)(i + 2 < tid && q.z == l) + (uint32_t)(i + 3 < tid && q.w == l);
+  }
+  rid[start[l] + cnt[c * k + l] + rank] = (uint32_t)p;
 }
 
 // Stable placement: wave j walks positions lo..hi in order; positions with
@@ -252,6 +389,13 @@ __global__ __launch_bounds__(BT) void k_sum_big(const float* __restrict__ x, siz
 
 }  // namespace
 
+// The chunked path when the chunk histograms fit LDS and the last
+// workgroup's per-label prefixes stay short; else per-cluster ballot walks.
+static bool chunked(size_t n, size_t k) {
+  const size_t nch = (n + CP - 1) / CP;
+  return n > 0 && k <= (size_t)KCH && nch * ((k + 255) / 256) <= 4096;
+}
+
 void launch_scatter_count(emh_ctx* c, size_t lo, size_t hi, const uint32_t* labels, size_t k,
                           uint32_t* counts) {
   const size_t n = hi > lo ? hi - lo : 0;
@@ -259,6 +403,14 @@ void launch_scatter_count(emh_ctx* c, size_t lo, size_t hi, const uint32_t* labe
   // Clusters above SMALL rows: at most n / (SMALL + 1) of them.
   const size_t maxbig = std::min(k, n / (SMALL + 1) + 1);
   uint32_t* bigj = (uint32_t*)c->bigj.get(maxbig * 4);
+  if (chunked(n, k)) {
+    const size_t nch = (n + CP - 1) / CP;
+    uint32_t* cnt = (uint32_t*)c->chunkcnt.get(nch * k * 4);
+    hipLaunchKernelGGL(k_count_chunks, dim3((unsigned)nch), dim3(256), 0, c->stream, labels, lo,
+                       hi, k, counts, start, bigj, cnt, c->small);
+    EMH_HIP(hipGetLastError());
+    return;
+  }
   launch_fill_u32(c, counts, k, 0);
   if (n > 0) {
     hipLaunchKernelGGL(k_count, grid1(n, 256), dim3(256), 0, c->stream, labels, lo, hi, k, counts,
@@ -278,7 +430,13 @@ void launch_scatter_sums(emh_ctx* c, const float* x, size_t nx, size_t d, const 
   uint32_t* rid = (uint32_t*)c->order.get(std::max<size_t>(n, 1) * 4);
   const size_t maxbig = std::min(k, n / (SMALL + 1) + 1);
   uint32_t* bigj = (uint32_t*)c->bigj.get(maxbig * 4);
-  if (n > 0) {
+  if (chunked(n, k)) {
+    const size_t nch = (n + CP - 1) / CP;
+    const uint32_t* cnt = (const uint32_t*)c->chunkcnt.get(nch * k * 4);
+    hipLaunchKernelGGL(k_place_chunks, dim3((unsigned)nch), dim3(256), 0, c->stream, labels, lo,
+                       hi, k, start, cnt, rid);
+    EMH_HIP(hipGetLastError());
+  } else if (n > 0) {
     hipLaunchKernelGGL(k_place, grid1(k, PW), dim3(64 * PW), 0, c->stream, labels, lo, hi, k,
                        start, rid);
     EMH_HIP(hipGetLastError());

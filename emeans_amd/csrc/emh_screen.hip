@@ -402,7 +402,7 @@ void launch_screen(emh_ctx* c, unsigned blocks, const float* x, size_t nx, size_
 
 void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids, size_t lo,
                  size_t hi, const float* cents, const float* cnorm, size_t k, bool ip,
-                 uint32_t* labels, float* scores) {
+                 uint32_t* labels, float* scores, bool words_clear) {
   if (hi <= lo) return;
   const size_t n = hi - lo;
   EMH_ENSURE(d <= 16384, "top1: d = %zu above the supported 16384", d);
@@ -421,7 +421,8 @@ void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t
   Cand* cand = (Cand*)c->cand.get((size_t)parts * n * L1 * sizeof(Cand));
   uint32_t* fb = (uint32_t*)c->fblist.get(n * 4);
   float* xnorm = (float*)c->xnorm.get(n * 4);
-  launch_fill_u32(c, c->small, 3, 0);  // fallback count, cmax2, cnmax (the screen fills the maxima)
+  if (!words_clear)  // fallback count, cmax2, cnmax (the screen fills the maxima)
+    launch_fill_u32(c, c->small, 3, 0);
   const unsigned blocks = (unsigned)(row_tiles * parts);
   {
     ProfScope prof(c, 2.0 * (double)n * (double)k * (double)d);

@@ -99,6 +99,7 @@ __global__ __launch_bounds__(64) void k_exact_part(
       const int tl = min(TD, d - t0);
       const float* crow = &ct[lane * TDP];
       int tt = 0;
+#pragma unroll 4
       for (; tt + 4 <= tl; tt += 4) {
         const float4 cv = *reinterpret_cast<const float4*>(crow + tt);
 #pragma unroll
@@ -210,8 +211,17 @@ __global__ __launch_bounds__(64 * FW) void k_exact_final(
         }
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         __builtin_amdgcn_wave_barrier();
-        if (lane == 0)
-          for (int i = 0; i < tl; i++) xn = xn + sq[w][i];
+        if (lane == 0) {  // in order, 16 LDS reads in flight
+          int i = 0;
+          for (; i + 16 <= tl; i += 16) {
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) v[u] = sq[w][i + u];
+#pragma unroll
+            for (int u = 0; u < 16; u++) xn = xn + v[u];
+          }
+          for (; i < tl; i++) xn = xn + sq[w][i];
+        }
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         __builtin_amdgcn_wave_barrier();
       }

@@ -197,13 +197,15 @@ def test_scatter_ema_split(dev, n, d, k):
     assert dev.read_f32(u).tobytes() == wu.tobytes()
 
 
-@pytest.mark.parametrize("d", [200, 768])
-def test_scatter_skewed_clusters(dev, d):
+@pytest.mark.parametrize("d,k", [(200, 96), (768, 96), (64, 9000)])
+def test_scatter_skewed_clusters(dev, d, k):
     """Skewed cluster sizes (the Zipf case of training): clusters of several
     thousand rows, sizes at the edges of the per-column path (127..129, 256,
-    257 rows), a single row and empty clusters; rows gathered by id; with acc."""
+    257 rows), a single row and empty clusters; rows gathered by id; with acc.
+    k = 9000 takes the placement path for more clusters than the chunk
+    histograms hold."""
     from emeans_amd import Mat, Select
-    n, k = 20000, 96
+    n = 20000
     g = np.random.default_rng(d)
     sizes = [5000, 2049, 257, 256, 129, 128, 127, 1, 0]
     rest = n - sum(sizes)
