@@ -310,7 +310,9 @@ __global__ __launch_bounds__(256, 2) void k_screen(
             float v = acc[a][y][r];
             float key = L2 ? nn - 2.0f * v : nn - v;
             if (KNN && gj == qrow[y]) key = INFINITY;
-            insert_nb<L>(lkey[y], lid[y], key, gj);
+            // Skipped by the whole wave when no lane's key beats its list's
+            // last entry (the common case once the lists have filled).
+            if (__ballot(key < lkey[y][L - 1]) != 0ull) insert_nb<L>(lkey[y], lid[y], key, gj);
             acc[a][y][r] = 0.f;
           }
         }
