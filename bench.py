@@ -35,7 +35,7 @@ METRIC = "train s & assign Mrows/s at 200k×768 k=1024 FP32; % of FP32 MFMA peak
 # FETCH_SIZE + WRITE_SIZE from two rocprofv3 --pmc passes of this script, with
 # a plain copy kernel of known size as the scale;
 # profiles/k_screen_train_assign_200kx768_k1024_hbm_traffic.md).
-SCREEN_TRAFFIC_BYTES = 189.8e6
+SCREEN_TRAFFIC_BYTES = 190.0e6
 
 
 def log(*a):
@@ -196,7 +196,9 @@ def knn_workload(args):
            "config": {"workload": f"knn_self k=10 {n}x{d} unit rows, 5% near-duplicates, seed 2"},
            "roofline": {"bound": "mfma", "kernel": "k_screen (kNN, 24-entry lists)",
                         "achieved": achieved, "peak": FP32_MFMA_PEAK, "unit": "TFLOP/s",
-                        "frac": achieved / FP32_MFMA_PEAK}}
+                        "frac": achieved / FP32_MFMA_PEAK, "traffic": None, "launches": launches,
+                        "avg_launch_ms": ms / max(launches, 1),
+                        "flop_per_launch": flop / max(launches, 1)}}
     if not args.no_cpu:
         from oracle import oracle as O
         g = np.random.default_rng(0)
@@ -250,7 +252,9 @@ def assign_workload(args):
            "tflops": 2.0 * n * k * d / step_s / 1e12,
            "roofline": {"bound": "mfma", "kernel": "k_screen (FP32 MFMA x.C^T + per-row 9-entry candidate list)",
                         "achieved": achieved, "peak": FP32_MFMA_PEAK, "unit": "TFLOP/s",
-                        "frac": achieved / FP32_MFMA_PEAK}}
+                        "frac": achieved / FP32_MFMA_PEAK, "traffic": None, "launches": launches,
+                        "avg_launch_ms": ms / max(launches, 1),
+                        "flop_per_launch": flop / max(launches, 1)}}
     if not args.no_cpu:
         from oracle import oracle as O
         gl, gsc = dev.read_u32(labels), dev.read_f32(scores)
