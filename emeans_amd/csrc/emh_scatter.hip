@@ -6,7 +6,8 @@
 //              last workgroup to finish scans the counts into start offsets
 //              and lists the clusters too large for the per-column path. For
 //              k up to KCH the counts are per-chunk LDS histograms of CP
-//              positions, and that workgroup also prefixes them per label;
+//              positions, prefixed per label over the chunks by one workgroup
+//              (a thread per label);
 //   2. place:  each position's rank among the earlier positions of its label
 //              (chunked: the earlier chunks' prefix plus a scan of its own
 //              chunk in LDS; else one wave per cluster walking the labels with
@@ -96,20 +97,14 @@ __global__ __launch_bounds__(256) void k_count(const uint32_t* __restrict__ labe
 constexpr int CP = 256;
 constexpr int KCH = 8192;  // LDS histogram of one chunk
 
-// Chunk c's label histogram (LDS atomics) goes to cnt[c][0..k); the last
-// workgroup to finish turns every label's column into its exclusive prefix
-// over the chunks (in place), totals it into counts, and scans the counts
-// into start offsets and the list of clusters above SMALL rows.
-__global__ __launch_bounds__(256) void k_count_chunks(
-    const uint32_t* __restrict__ labels, size_t lo, size_t hi, size_t k,
-    uint32_t* __restrict__ counts, uint32_t* __restrict__ start, uint32_t* __restrict__ bigj,
-    uint32_t* __restrict__ cnt, uint32_t* __restrict__ small) {
+// Chunk c's label histogram (LDS atomics) goes to cnt[c][0..k).
+__global__ __launch_bounds__(256) void k_hist_chunks(const uint32_t* __restrict__ labels,
+                                                      size_t lo, size_t hi, size_t k,
+                                                      uint32_t* __restrict__ cnt,
+                                                      uint32_t* __restrict__ small) {
   __shared__ uint32_t h[KCH];
-  __shared__ uint32_t part[256];
-  __shared__ uint32_t nbig;
-  __shared__ int last;
   const int tid = threadIdx.x;
-  const size_t c = blockIdx.x, nch = gridDim.x;
+  const size_t c = blockIdx.x;
   for (size_t j = tid; j < k; j += 256) h[j] = 0;
   __syncthreads();
   const size_t p = lo + c * CP + tid;
@@ -122,79 +117,72 @@ __global__ __launch_bounds__(256) void k_count_chunks(
   }
   __syncthreads();
   for (size_t j = tid; j < k; j += 256) cnt[c * k + j] = h[j];
-  __threadfence();  // this chunk's histogram is visible before its ticket
-  __syncthreads();
+}
+
+// One workgroup of 1024 threads, 1024 labels at a time: thread j turns label
+// j's column of chunk counts into its exclusive prefix over the chunks (in
+// place; the column's loads all in flight at once) and its total; the totals
+// are scanned (shuffles within each wave, LDS across waves, a running carry
+// across label groups) into start offsets, and the clusters above SMALL rows
+// are listed.
+constexpr int PMC = 32;  // chunk counts per thread in flight
+constexpr int PT = 1024;
+__global__ __launch_bounds__(PT) void k_prefix_chunks(size_t k, size_t nch,
+                                                       uint32_t* __restrict__ cnt,
+                                                       uint32_t* __restrict__ counts,
+                                                       uint32_t* __restrict__ start,
+                                                       uint32_t* __restrict__ bigj,
+                                                       uint32_t* __restrict__ small) {
+  __shared__ uint32_t part[PT / 64];
+  __shared__ uint32_t nbig, carry_s;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   if (tid == 0) {
-    const uint32_t tk = atomicAdd(&small[SW_TICKET], 1u);
-    last = tk == nch - 1;
     nbig = 0;
+    carry_s = 0;
   }
   __syncthreads();
-  if (!last) return;
-  __threadfence();
-  // Each thread takes four labels (256 apart) at a time and the chunks in
-  // batches of PB, all of a batch's loads issued before its stores. The other
-  // workgroups' histograms reached L2 before their tickets, and this one's L1
-  // holds none of their lines, so plain loads see them.
-  constexpr int PQ = 4, PB = 16;
-  for (size_t j0 = tid; j0 < k; j0 += 256 * PQ) {
-    uint32_t s[PQ];
+  for (size_t j0 = 0; j0 < k; j0 += PT) {
+    const size_t j = j0 + tid;
+    uint32_t s = 0;
+    if (j < k) {
+      for (size_t cc0 = 0; cc0 < nch; cc0 += PMC) {
+        uint32_t v[PMC];
 #pragma unroll
-    for (int q = 0; q < PQ; q++) s[q] = 0;
-    for (size_t cc0 = 0; cc0 < nch; cc0 += PB) {
-      uint32_t v[PQ][PB];
+        for (int u = 0; u < PMC; u++) v[u] = cc0 + u < nch ? cnt[(cc0 + u) * k + j] : 0u;
 #pragma unroll
-      for (int q = 0; q < PQ; q++)
-#pragma unroll
-        for (int u = 0; u < PB; u++) {
-          const size_t j = j0 + 256 * q, cc = cc0 + u;
-          v[q][u] = (j < k && cc < nch) ? cnt[cc * k + j] : 0u;
-        }
-#pragma unroll
-      for (int q = 0; q < PQ; q++)
-#pragma unroll
-        for (int u = 0; u < PB; u++) {
-          const size_t j = j0 + 256 * q, cc = cc0 + u;
-          if (j < k && cc < nch) {
-            cnt[cc * k + j] = s[q];
-            s[q] += v[q][u];
+        for (int u = 0; u < PMC; u++)
+          if (cc0 + u < nch) {
+            cnt[(cc0 + u) * k + j] = s;
+            s += v[u];
           }
-        }
-    }
-#pragma unroll
-    for (int q = 0; q < PQ; q++) {
-      const size_t j = j0 + 256 * q;
-      if (j < k) {
-        counts[j] = s[q];
-        h[j] = s[q];  // the totals, for the scan below
       }
+      counts[j] = s;
     }
-  }
-  __syncthreads();
-  const size_t per = (k + 255) / 256;
-  const size_t a = min(k, (size_t)tid * per), b = min(k, a + per);
-  uint32_t s = 0;
-  for (size_t j = a; j < b; j++) s += h[j];
-  part[tid] = s;
-  __syncthreads();
-  for (int o = 1; o < 256; o <<= 1) {  // Hillis-Steele inclusive scan of the run totals
-    const uint32_t add = tid >= o ? part[tid - o] : 0u;
+    uint32_t x = s;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    if (lane == 63) part[w] = x;
     __syncthreads();
-    part[tid] += add;
+    uint32_t run = carry_s + x - s;
+    for (int i = 0; i < w; i++) run += part[i];
+    if (j < k) {
+      start[j] = run;
+      if (s > (uint32_t)SMALL) bigj[atomicAdd(&nbig, 1u)] = (uint32_t)j;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t tot = 0;
+      for (int i = 0; i < PT / 64; i++) tot += part[i];
+      carry_s += tot;
+    }
     __syncthreads();
   }
-  uint32_t run = part[tid] - s;
-  for (size_t j = a; j < b; j++) {
-    const uint32_t cj = h[j];
-    start[j] = run;
-    run += cj;
-    if (cj > (uint32_t)SMALL) bigj[atomicAdd(&nbig, 1u)] = (uint32_t)j;
-  }
-  if (tid == 255) start[k] = part[255];
-  __syncthreads();
   if (tid == 0) {
+    start[k] = carry_s;
     small[SW_NBIG] = nbig;
-    small[SW_TICKET] = 0;  // ready for the next call
   }
 }
 
@@ -393,7 +381,7 @@ __global__ __launch_bounds__(BT) void k_sum_big(const float* __restrict__ x, siz
 // workgroup's per-label prefixes stay short; else per-cluster ballot walks.
 static bool chunked(size_t n, size_t k) {
   const size_t nch = (n + CP - 1) / CP;
-  return n > 0 && k <= (size_t)KCH && nch * ((k + 255) / 256) <= 4096;
+  return n > 0 && k <= (size_t)KCH && nch <= 256;
 }
 
 void launch_scatter_count(emh_ctx* c, size_t lo, size_t hi, const uint32_t* labels, size_t k,
@@ -406,8 +394,11 @@ void launch_scatter_count(emh_ctx* c, size_t lo, size_t hi, const uint32_t* labe
   if (chunked(n, k)) {
     const size_t nch = (n + CP - 1) / CP;
     uint32_t* cnt = (uint32_t*)c->chunkcnt.get(nch * k * 4);
-    hipLaunchKernelGGL(k_count_chunks, dim3((unsigned)nch), dim3(256), 0, c->stream, labels, lo,
-                       hi, k, counts, start, bigj, cnt, c->small);
+    hipLaunchKernelGGL(k_hist_chunks, dim3((unsigned)nch), dim3(256), 0, c->stream, labels, lo,
+                       hi, k, cnt, c->small);
+    EMH_HIP(hipGetLastError());
+    hipLaunchKernelGGL(k_prefix_chunks, dim3(1), dim3(PT), 0, c->stream, k, nch, cnt, counts,
+                       start, bigj, c->small);
     EMH_HIP(hipGetLastError());
     return;
   }
