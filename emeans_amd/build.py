@@ -18,8 +18,11 @@ CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libemeans_hip.so")
 OBJ = os.path.join(HERE, "_obj")
 SOURCES = ["emh_api.cpp", "emh_host.cpp", "emh_ops.hip", "emh_scatter.hip", "emh_screen.hip",
-           "emh_rescore.hip", "emh_verify.hip"]
+           "emh_rescore.hip", "emh_verify.hip", "emh_perm.cpp"]
+# Plain host C++ (no HIP), built by the system compiler.
+HOST_ONLY = {"emh_perm.cpp"}
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+CXX = os.environ.get("CXX", "g++")
 
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
@@ -32,11 +35,13 @@ FLAGS = [
 
 def _compile(src):
     obj = os.path.join(OBJ, os.path.splitext(src)[0] + ".o")
-    lang = ["-x", "hip"]
-    cmd = [HIPCC, *FLAGS, *lang, "-c", os.path.join(CSRC, src), "-o", obj]
+    if src in HOST_ONLY:
+        cmd = [CXX, "-O3", "-std=c++17", "-fPIC", "-Wall", "-c", os.path.join(CSRC, src), "-o", obj]
+    else:
+        cmd = [HIPCC, *FLAGS, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed on {src}:\n{r.stderr}")
+        raise RuntimeError(f"{cmd[0]} failed on {src}:\n{r.stderr}")
     err = "\n".join(l for l in r.stderr.splitlines()
                     if "packed-fp32-ops" not in l and "not a recognized feature" not in l
                     and l.strip())

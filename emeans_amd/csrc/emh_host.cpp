@@ -28,6 +28,9 @@ namespace emh {
 namespace host {
 
 // ------------------------------------------------------------------ MT19937
+// RandomState(seed).permutation(n) into p (emh_perm.cpp).
+void mt_permutation(uint32_t seed, size_t n, uint32_t* p);
+
 class RandomState {  // rng.rs:13-102
  public:
   explicit RandomState(uint32_t seed) {
@@ -40,19 +43,34 @@ class RandomState {  // rng.rs:13-102
   }
   uint32_t next_u32() {
     if (pos_ == N) refill();
-    uint32_t y = mt_[pos_++];
-    y ^= y >> 11;
-    y ^= (y << 7) & 0x9d2c5680u;
-    y ^= (y << 15) & 0xefc60000u;
-    return y ^ (y >> 18);
+    return out_[pos_++];
   }
   double random_sample() {
     uint32_t a = next_u32() >> 5, b = next_u32() >> 6;
     return ((double)a * 67108864.0 + (double)b) / 9007199254740992.0;
   }
-  // numpy legacy random_interval: masked rejection in [0, max].
+  // numpy legacy random_interval: masked rejection in [0, max]. For max below
+  // 2^32 two candidate words are tested at once, so the loop branches only
+  // when both are rejected; the words consumed are the same as one at a time.
   uint64_t interval(uint64_t max) {
     if (max == 0) return 0;
+    if (max <= 0xffffffffull) {
+      const uint32_t mx = (uint32_t)max, m = 0xffffffffu >> __builtin_clz(mx);
+      for (;;) {
+        if (pos_ >= N - 1) {
+          const uint32_t v = next_u32() & m;
+          if (v <= mx) return v;
+          continue;
+        }
+        const uint32_t v1 = out_[pos_] & m, v2 = out_[pos_ + 1] & m;
+        const bool a1 = v1 <= mx, a2 = v2 <= mx;
+        if (a1 | a2) {
+          pos_ += a1 ? 1 : 2;
+          return a1 ? v1 : v2;
+        }
+        pos_ += 2;
+      }
+    }
     uint64_t mask = max;
     mask |= mask >> 1;
     mask |= mask >> 2;
@@ -61,45 +79,19 @@ class RandomState {  // rng.rs:13-102
     mask |= mask >> 16;
     mask |= mask >> 32;
     for (;;) {
-      uint64_t v;
-      if (max <= 0xffffffffull) {
-        v = next_u32() & mask;
-      } else {
-        uint64_t hi = next_u32();
-        v = ((hi << 32) | next_u32()) & mask;
-      }
+      const uint64_t hi = next_u32();
+      const uint64_t v = ((hi << 32) | next_u32()) & mask;
       if (v <= max) return v;
     }
   }
   // numpy's legacy shuffle: for i = n-1 down to 1, swap p[i] with p[interval(i)].
-  // The draws do not depend on p, so they are taken AHEAD swaps early and the
-  // element each will touch is prefetched; the swaps stay in the same order.
-  std::vector<uint32_t> permutation(size_t n) {
+  static std::vector<uint32_t> permutation(uint32_t seed, size_t n) {
     std::vector<uint32_t> p(n);
-    permutation_into(n, p.data());
+    mt_permutation(seed, n, p.data());
     return p;
   }
-  void permutation_into(size_t n, uint32_t* p) {
-    for (size_t i = 0; i < n; i++) p[i] = (uint32_t)i;
-    constexpr size_t AHEAD = 32;
-    uint64_t js[AHEAD];
-    size_t m = n;  // next i whose draw is taken: interval(m - 1)
-    for (size_t q = 0; q < AHEAD && m > 1; q++, m--) {
-      js[q] = interval(m - 1);
-      __builtin_prefetch(&p[js[q]], 1);
-    }
-    size_t q = 0;
-    for (size_t i = n; i > 1; i--) {
-      const uint64_t j = js[q];
-      if (m > 1) {
-        js[q] = interval(m - 1);
-        __builtin_prefetch(&p[js[q]], 1);
-        m--;
-      }
-      q = q + 1 == AHEAD ? 0 : q + 1;
-      std::swap(p[i - 1], p[j]);
-    }
-  }
+  // The same draws as interval() from a fresh state (emh_perm.cpp).
+  static void permutation_into(uint32_t seed, size_t n, uint32_t* p) { mt_permutation(seed, n, p); }
 
  private:
   static constexpr int N = 624, M = 397;
@@ -107,14 +99,23 @@ class RandomState {  // rng.rs:13-102
     const uint32_t y = (a & 0x80000000u) | (b & 0x7fffffffu);
     return c ^ (y >> 1) ^ ((0u - (y & 1u)) & 0x9908b0dfu);
   }
+  static uint32_t temper(uint32_t y) {
+    y ^= y >> 11;
+    y ^= (y << 7) & 0x9d2c5680u;
+    y ^= (y << 15) & 0xefc60000u;
+    return y ^ (y >> 18);
+  }
+  // The next N words of the state, tempered into out_.
   void refill() {
     int i = 0;
     for (; i < N - M; i++) mt_[i] = twist(mt_[i], mt_[i + 1], mt_[i + M]);
     for (; i < N - 1; i++) mt_[i] = twist(mt_[i], mt_[i + 1], mt_[i + M - N]);
     mt_[N - 1] = twist(mt_[N - 1], mt_[0], mt_[M - 1]);
+    for (int j = 0; j < N; j++) out_[j] = temper(mt_[j]);
     pos_ = 0;
   }
   uint32_t mt_[N];
+  uint32_t out_[N];
   int pos_;
 };
 
@@ -395,7 +396,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   // ev_order[b]: epoch order b is on the device and h_order[b] free again (copy
   // stream); ev_done[b]: the epoch that used order/labels/scores b has run
   // (main stream); ev_epoch[b]: its labels and scores are on the host.
-  Event ev_init, ev_check, ev_order[2], ev_done[2], ev_epoch[2];
+  Event ev_init, ev_check, ev_order[2], ev_done[2], ev_epoch[2], ev_last, ev_posout;
 
   // Epochs alternate between two sets of order/labels/scores buffers, so the
   // copies of one epoch's run on the copy stream beside the next epoch's kernels.
@@ -420,7 +421,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   auto fill_order = [&](size_t epoch) {
     const int buf = (int)(epoch & 1);
     ev_order[buf].wait();
-    RandomState(epoch_seed(cfg.seed, epoch)).permutation_into(n, h_order[buf]);
+    RandomState::permutation_into(epoch_seed(cfg.seed, epoch), n, h_order[buf]);
     EMH_HIP(hipStreamWaitEvent(c->copy_stream, ev_done[buf].e, 0));
     EMH_HIP(hipMemcpyAsync(d_order[buf], h_order[buf], R.epoch_rows[epoch] * 4,
                            hipMemcpyHostToDevice, c->copy_stream));
@@ -434,7 +435,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   if (n == k) {
     EMH_HIP(hipMemcpyAsync(pos.p, x, k * d * 4, hipMemcpyDeviceToDevice, c->stream));
   } else {
-    RandomState(cfg.seed).permutation_into(n, h_order[1]);  // unused until epoch 1
+    RandomState::permutation_into(cfg.seed, n, h_order[1]);  // unused until epoch 1
     copy_async(c, init_ids.p, h_order[1], k * 4, hipMemcpyHostToDevice);
     launch_gather_rows(c, x, n, d, init_ids.u(), k, pos.f());
   }
@@ -577,9 +578,18 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
       return es;
     });
   }
-  // Closing means on the device: the last pass's label counts, sums / count.
+  // The end: positions and masses are final after the last EMA and go out on
+  // the copy stream while the closing means (core/mod.rs:404-429: the last
+  // pass's label counts, sums / count) and the labels by data row are
+  // computed; the host copies into the caller's arrays run in parallel.
   const size_t rows_last = R.epoch_rows.back();
-  launch_hist(c, d_lab[(n_epochs - 1) & 1], rows_last, k, counts.u());
+  const int lb = (int)((n_epochs - 1) & 1);
+  ev_last.record(c->stream);
+  EMH_HIP(hipStreamWaitEvent(c->copy_stream, ev_last.e, 0));
+  EMH_HIP(hipMemcpyAsync(h_out + k * d, pos.p, k * d * 4, hipMemcpyDeviceToHost, c->copy_stream));
+  EMH_HIP(hipMemcpyAsync(h_out + 2 * k * d, mass.p, k * 4, hipMemcpyDeviceToHost, c->copy_stream));
+  ev_posout.record(c->copy_stream);
+  launch_hist(c, d_lab[lb], rows_last, k, counts.u());
   launch_closing(c, pos.f(), pass.f(), counts.u(), k, d, sums.f());
   const float* C = sums.f();
   if (sph) {
@@ -590,24 +600,28 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
     EMH_HIP(hipMemcpyAsync(out->centroids_dev->ptr, C, k * d * 4, hipMemcpyDeviceToDevice,
                            c->stream));
   copy_async(c, h_out, C, k * d * 4, hipMemcpyDeviceToHost);
-  copy_async(c, h_out + k * d, pos.p, k * d * 4, hipMemcpyDeviceToHost);
-  copy_async(c, h_out + 2 * k * d, mass.p, k * 4, hipMemcpyDeviceToHost);
+  uint32_t* h_rowlab = h_lab[lb ^ 1];  // free: its epoch's statistics are done
+  if (out->labels && capture) {
+    launch_labels_by_row(c, d_order[lb], d_lab[lb], rows_last, n, d_lab[lb ^ 1]);
+    copy_async(c, h_rowlab, d_lab[lb ^ 1], n * 4, hipMemcpyDeviceToHost);
+  }
   copy_async(c, h_small, c->small, SW_WORDS * 4, hipMemcpyDeviceToHost);
+  auto side = std::async(std::launch::async, [&] {
+    ev_posout.wait();
+    if (out->positions) std::memcpy(out->positions, h_out + k * d, k * d * 4);
+    if (out->usage) std::memcpy(out->usage, h_out + 2 * k * d, k * 4);
+  });
   EMH_HIP(hipStreamSynchronize(c->stream));
   stats.push_back(pending.get());
   raise_flags(c, h_small);
   std::memcpy(out->centroids, h_out, k * d * 4);
-  if (out->positions) std::memcpy(out->positions, h_out + k * d, k * d * 4);
-  if (out->usage) std::memcpy(out->usage, h_out + 2 * k * d, k * 4);
   if (out->labels) {
-    if (capture) {
-      const int lb = (int)((n_epochs - 1) & 1);
+    if (capture)
+      std::memcpy(out->labels, h_rowlab, n * 4);
+    else
       std::fill(out->labels, out->labels + n, -1);
-      for (size_t p = 0; p < rows_last; p++) out->labels[h_order[lb][p]] = (int32_t)h_lab[lb][p];
-    } else {
-      std::fill(out->labels, out->labels + n, -1);
-    }
   }
+  side.get();
   out->n_epochs = n_epochs;
   for (size_t e = 0; e < n_epochs && e < out->max_epochs; e++)
     if (out->stats) out->stats[e] = stats[e];
@@ -867,8 +881,7 @@ int emh_dedup(emh_ctx* c, const float* x, size_t n, size_t d, size_t kk, float s
 
 // Host-side pieces of the loop, exported for checks that need no device.
 void emh_host_permutation(uint32_t seed, uint64_t n, uint32_t* out) {
-  std::vector<uint32_t> p = RandomState(seed).permutation(n);
-  std::memcpy(out, p.data(), n * 4);
+  RandomState::permutation_into(seed, n, out);
 }
 double emh_host_random_sample(uint32_t seed, uint64_t skip) {
   RandomState r(seed);

@@ -187,6 +187,9 @@ void launch_hist(emh_ctx* c, const uint32_t* labels, size_t n, size_t k, uint32_
 // Closing means: out[j] = sums[j] / counts[j] where counts[j] > 0, else pos[j].
 void launch_closing(emh_ctx* c, const float* pos, const float* sums, const uint32_t* counts,
                     size_t k, size_t d, float* out);
+// out[0..n) = -1, then out[order[p]] = lab[p] for p < rows.
+void launch_labels_by_row(emh_ctx* c, const uint32_t* order, const uint32_t* lab, size_t rows,
+                          size_t n, uint32_t* out);
 // *flag = 1 when any of v[0..n) is not finite.
 void launch_check_finite(emh_ctx* c, const float* v, size_t n, uint32_t* flag);
 void launch_split(emh_ctx* c, float* pos, float* usage, const uint32_t* pairs_dev, size_t npairs,

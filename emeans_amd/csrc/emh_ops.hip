@@ -259,6 +259,17 @@ __global__ __launch_bounds__(256) void k_closing(const float* __restrict__ pos,
   out[j * d + t] = cnt > 0 ? sums[j * d + t] / (float)cnt : pos[j * d + t];
 }
 
+// out[order[p]] = lab[p] for p < rows: the last pass's labels by data row.
+__global__ __launch_bounds__(256) void k_labels_by_row(const uint32_t* __restrict__ order,
+                                                       const uint32_t* __restrict__ lab,
+                                                       size_t rows, size_t n,
+                                                       uint32_t* __restrict__ out) {
+  const size_t p = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= rows) return;
+  const uint32_t r = order[p];
+  if (r < n) out[r] = lab[p];
+}
+
 // flag = 1 when any of v[0..n) is NaN or infinite.
 __global__ __launch_bounds__(256) void k_check_finite(const float* __restrict__ v, size_t n,
                                                       uint32_t* __restrict__ flag) {
@@ -397,6 +408,15 @@ void launch_closing(emh_ctx* c, const float* pos, const float* sums, const uint3
   if (k == 0) return;
   dim3 g((unsigned)((d + 255) / 256), (unsigned)k);
   hipLaunchKernelGGL(k_closing, g, dim3(256), 0, c->stream, pos, sums, counts, d, out);
+  EMH_HIP(hipGetLastError());
+}
+
+void launch_labels_by_row(emh_ctx* c, const uint32_t* order, const uint32_t* lab, size_t rows,
+                          size_t n, uint32_t* out) {
+  launch_fill_u32(c, out, n, 0xffffffffu);  // -1 for rows the pass did not see
+  if (rows == 0) return;
+  hipLaunchKernelGGL(k_labels_by_row, grid1(rows, 256), dim3(256), 0, c->stream, order, lab, rows,
+                     n, out);
   EMH_HIP(hipGetLastError());
 }
 
