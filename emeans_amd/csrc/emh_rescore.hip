@@ -7,10 +7,11 @@
 //   |x|^2 = sequential sum of rounded squares (assign.rs:150-155);
 //   score = dot (IP) or max(|x|^2 + key, 0) (L2, assign.rs:497-502);
 //   ties to the lower id.
-// One thread per (row, candidate) pair runs a chain, reading the row and the
-// candidate from global memory (L2/MALL-resident after the screen) with PF
-// float4 loads of each in flight; the small LDS footprint keeps many blocks
-// per CU so the chains' latency overlaps.
+// Top-1 with d % 4 == 0 (k_check1): the rows and their candidates are staged
+// through LDS in chunks by loader waves while compute waves run the chains.
+// Top-k and the top-1 case d % 4 != 0 (k_verify): one thread per (row,
+// candidate) pair runs a chain, reading the row and the candidate from global
+// memory with PF float4 loads of each in flight.
 
 #include "emh_select.h"
 
@@ -284,6 +285,297 @@ __global__ __launch_bounds__(256) void k_verify(
 constexpr int R1 = 16;  // rows per block, top-1
 constexpr int RK = 16;  // rows per block, top-k
 
+// ---- Top-1 check with the rows staged through LDS (d % 4 == 0).
+//
+// Decision without a merge. The merged list is the L1 smallest keys of the
+// parts' lists, so with thr = best + 2E and le(key) = key <= thr || thr is NaN,
+// and lists holding only finite keys (the screen never keeps +inf or NaN):
+//   the row is settled  <=>  some entry is valid and at most L1 - 1 valid
+//                            entries satisfy le,
+// and then its candidates are exactly the valid entries satisfying le (all of
+// them are among the merged list's first L1 - 1). Eight threads per row scan
+// one part's list each and combine with lane shuffles.
+//
+// Chains. The block's settled rows (x) and their candidates (centroid rows)
+// are staged in CDC-float chunks into a double-buffered LDS tile by waves 2-3,
+// which keep CNR chunks of loads in flight in registers; waves 0-1 run the
+// chains from LDS: wave 0 one lane per (row, candidate) fma chain, wave 1 one
+// lane per row for the |x|^2 chain (L2). Every chunk costs each wave one
+// barrier. Blocks whose rows have more than CCAP candidates in total take
+// further passes over the chunks.
+constexpr int CR = 32;              // rows per block
+constexpr int CCAP = 48;            // candidate slots per pass
+constexpr int CSLOT = CR + CCAP;    // staged rows per chunk
+constexpr int CDC = 64;             // floats per chunk
+constexpr int CDC4 = CDC / 4;
+constexpr int CDP4 = CDC4 + 1;      // LDS row stride in float4: conflict-free chain reads
+constexpr int CNR = 2;              // chunks in flight per loading thread
+constexpr int CNQ = CSLOT * CDC4 / 128;  // float4 per loading thread per chunk
+static_assert(CSLOT * CDC4 % 128 == 0, "chunk split");
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void k_check1(
+    const float* __restrict__ x, size_t nx, int d, const uint32_t* __restrict__ ids, size_t lo,
+    int nrows, const float* __restrict__ cents, const float* __restrict__ cnorm, int ip,
+    const Cand* __restrict__ cand, int parts, const float* __restrict__ xnorm,
+    uint32_t* __restrict__ labels, float* __restrict__ scores, uint32_t* __restrict__ fb,
+    uint32_t* __restrict__ small) {
+  __shared__ v4f stage[2][CSLOT * CDP4];
+  __shared__ uint32_t xrow[CR];  // x row of each settled row, NONE otherwise
+  __shared__ int rcnt[CR], roff[CR + 1], rset[CR];
+  __shared__ uint32_t prow[CR * (L1 - 1)], pcid[CR * (L1 - 1)];
+  __shared__ float pdot[CR * (L1 - 1)], pcn[CR * (L1 - 1)], rnorm[CR];
+  const int tid = threadIdx.x;
+  const int r0 = blockIdx.x * CR;
+  const int rows = min(CR, nrows - r0);
+  const bool l2 = !ip;
+  {
+    const int r = tid >> 3, j = tid & 7;
+    const bool live = r < rows;
+    float key[L1];
+    uint32_t idv[L1];
+#pragma unroll
+    for (int e = 0; e < L1; e++) {
+      key[e] = INFINITY;
+      idv[e] = NONE;
+    }
+    uint32_t xid = NONE;
+    float xn = 0.f;
+    bool badid = false;
+    if (live) {
+      const size_t p = lo + (size_t)(r0 + r);
+      const size_t xi = ids ? (size_t)ids[p] : p;
+      badid = xi >= nx;
+      xid = badid ? NONE : (uint32_t)xi;
+      xn = xnorm[r0 + r];
+      if (j < parts) {
+        const Cand* c = cand + ((size_t)(r0 + r) * parts + j) * L1;
+#pragma unroll
+        for (int e = 0; e < L1; e++) {
+          const Cand v = c[e];
+          key[e] = v.key;
+          idv[e] = v.id;
+        }
+      }
+    }
+    // Each list is ascending with its valid entries first: the row's best key
+    // is the smallest head.
+    float best = idv[0] != NONE ? key[0] : INFINITY;
+    int anyv = idv[0] != NONE;
+#pragma unroll
+    for (int m = 1; m < 8; m <<= 1) {
+      best = fminf(best, __shfl_xor(best, m));
+      anyv |= __shfl_xor(anyv, m);
+    }
+    const bool vrow = live && !badid;
+    uint32_t inc = 0;
+    int cj = 0;
+    if (vrow) {
+      const float E = screen_bound(xn, __uint_as_float(small[SW_CMAX2]),
+                                   __uint_as_float(small[SW_CNMAX]), d, l2);
+      const float thr = best + 2.0f * E;
+#pragma unroll
+      for (int e = 0; e < L1; e++)
+        if (idv[e] != NONE && (key[e] <= thr || thr != thr)) {
+          inc |= 1u << e;
+          cj++;
+        }
+    }
+    int tot = cj, incl = cj;
+#pragma unroll
+    for (int m = 1; m < 8; m <<= 1) {
+      tot += __shfl_xor(tot, m);
+      const int v = __shfl_up(incl, m, 8);
+      if (j >= m) incl += v;
+    }
+    const bool settled = vrow && anyv && tot <= L1 - 1;
+    if (j == 0) {
+      xrow[r] = settled ? xid : NONE;
+      rcnt[r] = settled ? tot : 0;
+      rset[r] = settled;
+      if (live && badid) small[SW_BAD_ID] = 1;
+      if (vrow && !settled) {
+        const uint32_t f = atomicAdd(&small[SW_FALLBACK_COUNT], 1u);
+        fb[f] = (uint32_t)(lo + r0 + r);
+      }
+    }
+    __syncthreads();
+    if (tid < 64) {
+      int v = tid < CR ? rcnt[tid] : 0;
+#pragma unroll
+      for (int m = 1; m < 64; m <<= 1) {
+        const int u = __shfl_up(v, m);
+        if (tid >= m) v += u;
+      }
+      if (tid < CR) roff[tid + 1] = v;
+      if (tid == 0) roff[0] = 0;
+    }
+    __syncthreads();
+    if (settled) {
+      int o = roff[r] + incl - cj;
+#pragma unroll
+      for (int e = 0; e < L1; e++)
+        if ((inc >> e) & 1u) {
+          prow[o] = (uint32_t)r;
+          pcid[o] = idv[e];
+          o++;
+        }
+    }
+    __syncthreads();
+  }
+  const int npairs = roff[CR];
+  const int d4 = d >> 2;
+  const int nch = (d + CDC - 1) / CDC;
+  const int wave = tid >> 6, lane = tid & 63;
+  for (int pb = 0; pb < npairs; pb += CCAP) {
+    const int np = min(CCAP, npairs - pb);
+    const bool dl = wave == 0 && lane < np;
+    const bool nl = l2 && pb == 0 && wave == 1 && lane < CR && rset[lane];
+    float acc = 0.f, nrm = 0.f, cn = 0.f;
+    if (wave >= 2) {
+      // Loaders. Float4 i of a chunk is slot i / CDC4, column i % CDC4; past
+      // the used slots (and past d in the last chunk) the index is clamped, so
+      // every thread issues the same loads each step and the waits stay exact.
+      const int nlast = (CR + np) * CDC4 - 1;
+      const int lt = tid - 128;
+      const v4f* src[CNQ];
+      int col[CNQ], dst[CNQ];
+#pragma unroll
+      for (int q = 0; q < CNQ; q++) {
+        const int i = min(lt + 128 * q, nlast);
+        const int slot = i / CDC4;
+        const float* base;
+        if (slot < CR) {
+          const uint32_t xr = xrow[slot];
+          base = x + (size_t)(xr == NONE ? 0u : xr) * d;
+        } else {
+          base = cents + (size_t)pcid[pb + slot - CR] * d;
+        }
+        src[q] = reinterpret_cast<const v4f*>(base);
+        col[q] = i % CDC4;
+        dst[q] = slot * CDP4 + col[q];
+      }
+      v4f rb[CNR][CNQ];
+#pragma unroll
+      for (int s = 0; s < CNR; s++)
+#pragma unroll
+        for (int q = 0; q < CNQ; q++) rb[s][q] = src[q][min(min(s, nch - 1) * CDC4 + col[q], d4 - 1)];
+#pragma unroll
+      for (int q = 0; q < CNQ; q++) stage[0][dst[q]] = rb[0][q];
+#pragma unroll
+      for (int q = 0; q < CNQ; q++) rb[0][q] = src[q][min(min(CNR, nch - 1) * CDC4 + col[q], d4 - 1)];
+      __syncthreads();
+      // Step c stores chunk c + 1 (register set (c + 1) % CNR) and refills
+      // that set with chunk c + 1 + CNR; the set index is a constant in each
+      // unrolled step, so the sets stay in registers.
+      auto step = [&](auto U, int c0) __attribute__((always_inline)) {
+        constexpr int s = (decltype(U)::value + 1) % CNR;
+        const int c = c0 + decltype(U)::value;
+#pragma unroll
+        for (int q = 0; q < CNQ; q++) stage[(c + 1) & 1][dst[q]] = rb[s][q];
+        const int cn2 = min(c + 1 + CNR, nch - 1);
+#pragma unroll
+        for (int q = 0; q < CNQ; q++) rb[s][q] = src[q][min(cn2 * CDC4 + col[q], d4 - 1)];
+        __syncthreads();
+      };
+      for (int c0 = 0; c0 < nch; c0 += CNR) {
+        step(std::integral_constant<int, 0>{}, c0);
+        step(std::integral_constant<int, 1>{}, c0);
+      }
+    } else {
+      const int xs = dl ? (int)prow[pb + lane] : (nl ? lane : 0);
+      const int cs = CR + (dl ? lane : 0);
+      if (dl && l2) cn = cnorm[pcid[pb + lane]];
+      __syncthreads();
+      // As many barriers as the loaders: nch rounded up to a multiple of CNR.
+      const int nsteps = (nch + CNR - 1) / CNR * CNR;
+      for (int c = 0; c < nsteps; c++) {
+        if (c < nch) {
+          const int n4 = min(CDC4, d4 - c * CDC4);
+          const v4f* xp = &stage[c & 1][xs * CDP4];
+          if (dl) {
+            const v4f* cp = &stage[c & 1][cs * CDP4];
+            if (n4 == CDC4) {
+#pragma unroll
+              for (int f = 0; f < CDC4; f++) {
+                const v4f a = xp[f], w = cp[f];
+                acc = fmaf(a.x, w.x, acc);
+                acc = fmaf(a.y, w.y, acc);
+                acc = fmaf(a.z, w.z, acc);
+                acc = fmaf(a.w, w.w, acc);
+              }
+            } else {
+              for (int f = 0; f < n4; f++) {
+                const v4f a = xp[f], w = cp[f];
+                acc = fmaf(a.x, w.x, acc);
+                acc = fmaf(a.y, w.y, acc);
+                acc = fmaf(a.z, w.z, acc);
+                acc = fmaf(a.w, w.w, acc);
+              }
+            }
+          } else if (nl) {
+            if (n4 == CDC4) {
+#pragma unroll
+              for (int f = 0; f < CDC4; f++) {
+                const v4f a = xp[f];
+                const float p0 = a.x * a.x, p1 = a.y * a.y, p2 = a.z * a.z, p3 = a.w * a.w;
+                nrm = nrm + p0;
+                nrm = nrm + p1;
+                nrm = nrm + p2;
+                nrm = nrm + p3;
+              }
+            } else {
+              for (int f = 0; f < n4; f++) {
+                const v4f a = xp[f];
+                const float p0 = a.x * a.x, p1 = a.y * a.y, p2 = a.z * a.z, p3 = a.w * a.w;
+                nrm = nrm + p0;
+                nrm = nrm + p1;
+                nrm = nrm + p2;
+                nrm = nrm + p3;
+              }
+            }
+          }
+        }
+        __syncthreads();
+      }
+    }
+    if (dl) {
+      pdot[pb + lane] = acc;
+      pcn[pb + lane] = cn;
+    }
+    if (nl) rnorm[lane] = nrm;
+    __syncthreads();
+  }
+  // One thread per settled row picks the exact best (ties to the lower id).
+  if (tid < rows && rset[tid]) {
+    const int a = roff[tid], b = roff[tid + 1];
+    float bk = INFINITY;
+    uint32_t bid = NONE;
+    for (int s = a; s < b; s++) {
+      const uint32_t cid = pcid[s];
+      float kx;
+      if (ip) {
+        kx = -pdot[s];
+      } else {
+        const float two = 2.0f * pdot[s];
+        kx = pcn[s] - two;
+      }
+      if (kx < bk || (kx == bk && cid < bid)) {
+        bk = kx;
+        bid = cid;
+      }
+    }
+    if (bid == NONE) {
+      bid = 0;
+      bk = INFINITY;
+    }
+    const size_t p = lo + (size_t)(r0 + tid);
+    labels[p] = bid;
+    scores[p] = ip ? -bk : fmaxf(rnorm[tid] + bk, 0.0f);
+  }
+}
+
 }  // namespace
 
 void launch_verify1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
@@ -292,9 +584,9 @@ void launch_verify1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint3
                     float* scores, uint32_t* fb) {
   const dim3 g((unsigned)((n + R1 - 1) / R1));
   if (d % 4 == 0)
-    hipLaunchKernelGGL((k_verify<L1, R1, false, true>), g, dim3(256), 0, c->stream, x, nx,
-                       (int)d, ids, lo, (int)n, cents, cnorm, (int)k, ip ? 1 : 0, 1, cand, parts,
-                       xnorm, labels, scores, fb, c->small);
+    hipLaunchKernelGGL(k_check1, dim3((unsigned)((n + CR - 1) / CR)), dim3(256), 0, c->stream, x,
+                       nx, (int)d, ids, lo, (int)n, cents, cnorm, ip ? 1 : 0, cand, parts, xnorm,
+                       labels, scores, fb, c->small);
   else
     hipLaunchKernelGGL((k_verify<L1, R1, false, false>), g, dim3(256), 0, c->stream, x, nx,
                        (int)d, ids, lo, (int)n, cents, cnorm, (int)k, ip ? 1 : 0, 1, cand, parts,
