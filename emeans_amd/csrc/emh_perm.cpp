@@ -3,9 +3,21 @@
 // rejection random_interval, and the shuffle from the last index down.
 //
 // Every training run draws two of these before its first batch can start
-// (the initial centroids and the first epoch's order), so this file is plain
-// host C++ built by the system C++ compiler, which turns the two-candidate
-// rejection below into branch-free selects.
+// (the initial centroids and the first epoch's order), so the draws are
+// restated for speed, consuming exactly the words numpy consumes:
+//  - random_interval(max) takes the next word w while (w & mask) > max, and
+//    max falls by one per draw: over the word stream that is one pass with a
+//    running max that drops at each taken word. No word position depends on
+//    the previous draw's value;
+//  - in a chunk of S words the max falls by at most S, so a word at or below
+//    max - S is taken and one above max is not, whatever came before it.
+//    Chunks with no word in between and no mask change are decided without
+//    the running max (8 words at a time with AVX2 where the CPU has it); the
+//    rest go word by word;
+//  - the swaps of a block's draws follow its scan, in draw order.
+// Plain host C++, built by the system C++ compiler.
+
+#include <immintrin.h>
 
 #include <cstddef>
 #include <cstdint>
@@ -17,6 +29,49 @@ namespace host {
 namespace {
 
 constexpr int N = 624, M = 397;
+
+// Left-pack tables: for each 8-bit mask, the indices of its set bits in order.
+struct PackLut {
+  uint64_t idx[256];
+  PackLut() {
+    for (int msk = 0; msk < 256; msk++) {
+      uint64_t v = 0;
+      int o = 0;
+      for (int b = 0; b < 8; b++)
+        if (msk >> b & 1) v |= (uint64_t)b << (8 * o++);
+      idx[msk] = v;
+    }
+  }
+};
+const PackLut kLut;
+
+// Words k..e (e - k a multiple of 8) decided against thr: stores the taken
+// (v <= thr) masked words in order at jb + nj and returns the new count;
+// *unc gets whether some word lies in (thr, mx].
+__attribute__((target("avx2"))) int pack_avx2(const uint32_t* out, int k, int e, uint32_t m,
+                                              uint32_t thr, uint32_t mx, uint32_t* jb, int nj,
+                                              uint32_t* unc) {
+  const __m256i vm = _mm256_set1_epi32((int)m);
+  const __m256i bias = _mm256_set1_epi32((int)0x80000000u);
+  const __m256i vthr = _mm256_set1_epi32((int)(thr ^ 0x80000000u));
+  const __m256i vmx = _mm256_set1_epi32((int)(mx ^ 0x80000000u));
+  __m256i u = _mm256_setzero_si256();
+  for (int t = k; t < e; t += 8) {
+    const __m256i v = _mm256_and_si256(_mm256_loadu_si256((const __m256i*)(out + t)), vm);
+    const __m256i vb = _mm256_xor_si256(v, bias);
+    const __m256i gt = _mm256_cmpgt_epi32(vb, vthr);  // v > thr
+    const __m256i gtm = _mm256_cmpgt_epi32(vb, vmx);  // v > mx
+    u = _mm256_or_si256(u, _mm256_andnot_si256(gtm, gt));
+    const int msk = ~_mm256_movemask_ps(_mm256_castsi256_ps(gt)) & 0xff;
+    const __m256i perm = _mm256_cvtepu8_epi32(_mm_loadl_epi64((const __m128i*)&kLut.idx[msk]));
+    _mm256_storeu_si256((__m256i*)(jb + nj), _mm256_permutevar8x32_epi32(v, perm));
+    nj += __builtin_popcount((unsigned)msk);
+  }
+  *unc = !_mm256_testz_si256(u, u);
+  return nj;
+}
+
+const bool kAvx2 = __builtin_cpu_supports("avx2");
 
 struct Words {
   uint32_t mt[N];
@@ -40,7 +95,7 @@ struct Words {
     y ^= (y << 15) & 0xefc60000u;
     return y ^ (y >> 18);
   }
-  void refill() {
+  __attribute__((target_clones("avx2", "default"))) void refill() {
     int i = 0;
     for (; i < N - M; i++) mt[i] = twist(mt[i], mt[i + 1], mt[i + M]);
     for (; i < N - 1; i++) mt[i] = twist(mt[i], mt[i + 1], mt[i + M - N]);
@@ -51,26 +106,6 @@ struct Words {
   uint32_t next() {
     if (pos == N) refill();
     return out[pos++];
-  }
-  // random_interval(max) for 0 < max < 2^32: two candidate words are tested
-  // at once, so the loop branches only when both are rejected; the words
-  // consumed are the same as testing them one at a time.
-  uint32_t interval(uint32_t max) {
-    const uint32_t m = 0xffffffffu >> __builtin_clz(max);
-    for (;;) {
-      if (pos >= N - 1) {
-        const uint32_t v = next() & m;
-        if (v <= max) return v;
-        continue;
-      }
-      const uint32_t v1 = out[pos] & m, v2 = out[pos + 1] & m;
-      const bool a1 = v1 <= max, a2 = v2 <= max;
-      if (a1 | a2) {
-        pos += a1 ? 1 : 2;
-        return a1 ? v1 : v2;
-      }
-      pos += 2;
-    }
   }
   // random_interval(max) for max >= 2^32 (two words per candidate).
   uint64_t interval64(uint64_t max) {
@@ -96,8 +131,69 @@ void mt_permutation(uint32_t seed, size_t n, uint32_t* p) {
   for (size_t i = 0; i < n; i++) p[i] = (uint32_t)i;
   size_t i = n;
   for (; i > 1 && i - 1 > 0xffffffffull; i--) std::swap(p[i - 1], p[w.interval64(i - 1)]);
-  for (; i > 1; i--) std::swap(p[i - 1], p[w.interval((uint32_t)(i - 1))]);
+  if (i <= 1) return;
+  // Draws with max < 2^32: the running max mx, its mask m, and lo = m >> 1,
+  // the max at which the mask halves.
+  uint32_t m = 0xffffffffu >> __builtin_clz((uint32_t)(i - 1));
+  uint32_t lo = m >> 1;
+  uint32_t jb[N + 8];    // a block's draws (slack for 8-wide stores)
+  constexpr int S = 64;  // words decided together
+  while (i > 1) {
+    if (w.pos == N) w.refill();
+    const size_t i0 = i;
+    int k = w.pos, nj = 0;
+    uint32_t mx = (uint32_t)(i - 1);
+    while (k < N) {
+      const int e = k + S < N ? k + S : N;
+      // The max falls by at most e - k within the chunk: a word at or below
+      // mx - S is taken whatever came before it, one above mx is not. With
+      // no word in between and no mask change, the chunk needs no running max.
+      if (mx > lo + (uint32_t)S) {
+        const uint32_t thr = mx - (uint32_t)S;
+        const int nj0 = nj;
+        uint32_t unc = 0;
+        int t = k;
+        if (kAvx2) {
+          const int e8 = k + ((e - k) & ~7);
+          nj = pack_avx2(w.out, k, e8, m, thr, mx, jb, nj, &unc);
+          t = e8;
+        }
+        for (; t < e; t++) {
+          const uint32_t v = w.out[t] & m;
+          jb[nj] = v;
+          nj += (int)(v <= thr);
+          unc |= (uint32_t)(v > thr) & (uint32_t)(v <= mx);
+        }
+        if (!unc) {
+          mx -= (uint32_t)(nj - nj0);
+          k = e;
+          continue;
+        }
+        nj = nj0;
+      }
+      bool done = false;
+      for (; k < e; k++) {
+        const uint32_t v = w.out[k] & m;
+        jb[nj] = v;
+        const uint32_t acc = v <= mx;
+        nj += (int)acc;
+        mx -= acc;
+        if (mx == lo) {
+          if (mx == 0) {
+            k++;
+            done = true;
+            break;
+          }
+          m >>= 1;
+          lo = m >> 1;
+        }
+      }
+      if (done) break;
+    }
+    w.pos = k;
+    i = (size_t)mx + 1;
+    for (int t = 0; t < nj; t++) std::swap(p[i0 - 1 - t], p[jb[t]]);
+  }
 }
-
 }  // namespace host
 }  // namespace emh
