@@ -15,11 +15,17 @@
 #include <algorithm>
 #include <chrono>
 #include <cmath>
+#include <condition_variable>
 #include <cstring>
+#include <deque>
+#include <functional>
 #include <future>
 #include <map>
+#include <memory>
+#include <mutex>
 #include <set>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "emh_internal.h"
@@ -339,6 +345,56 @@ void raise_flags(emh_ctx* c, const uint32_t* w) {
   throw Failure(w[SW_BAD_LABEL] ? "label out of range" : "row id out of range");
 }
 
+// Threads for the host work beside the device loop (the next epoch's order,
+// Gumbel terms, epoch statistics, the final copies). They live as long as the
+// process: starting a thread per task would put its start-up on the loop's
+// path. Tasks only wait on HIP events of work already queued, never on each
+// other, so four threads cannot all block on what a queued task would do.
+class Helpers {
+ public:
+  static Helpers& get() {
+    static Helpers* h = new Helpers(4);  // never destroyed: idle threads end with the process
+    return *h;
+  }
+  template <class F>
+  auto run(F&& f) -> std::future<decltype(f())> {
+    using R = decltype(f());
+    auto task = std::make_shared<std::packaged_task<R()>>(std::forward<F>(f));
+    std::future<R> fut = task->get_future();
+    {
+      std::lock_guard<std::mutex> g(m_);
+      q_.emplace_back([task] { (*task)(); });
+    }
+    cv_.notify_one();
+    return fut;
+  }
+
+ private:
+  explicit Helpers(int n) {
+    for (int i = 0; i < n; i++) std::thread([this] { loop(); }).detach();
+  }
+  void loop() {
+    for (;;) {
+      std::function<void()> f;
+      {
+        std::unique_lock<std::mutex> l(m_);
+        cv_.wait(l, [&] { return !q_.empty(); });
+        f = std::move(q_.front());
+        q_.pop_front();
+      }
+      f();
+    }
+  }
+  std::mutex m_;
+  std::condition_variable cv_;
+  std::deque<std::function<void()>> q_;
+};
+
+template <class F>
+auto beside(F&& f) {
+  return Helpers::get().run(std::forward<F>(f));
+}
+
 void copy_async(emh_ctx* c, void* dst, const void* src, size_t bytes, hipMemcpyKind kind) {
   if (bytes) EMH_HIP(hipMemcpyAsync(dst, src, bytes, kind, c->stream));
 }
@@ -392,6 +448,18 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
     h_lab[i] = (uint32_t*)c->pin_lab[i].get(n * 4);
     h_sco[i] = (float*)c->pin_sco[i].get(n * 4);
   }
+  // The split kernel reads the plan where the host writes it (pinned memory
+  // mapped into the device's address space): no copy between planning and
+  // the split. The next plan is written only after ev_check of the next
+  // revival, which the stream records after this split.
+  uint32_t* d_plan = nullptr;
+  EMH_HIP(hipHostGetDevicePointer((void**)&d_plan, h_plan, 0));
+  // Likewise the revival check's masses and small-block words are written by
+  // the mass preview kernel straight into h_usage and h_small.
+  float* d_usage_h = nullptr;
+  uint32_t* d_small_h = nullptr;
+  EMH_HIP(hipHostGetDevicePointer((void**)&d_usage_h, h_usage, 0));
+  EMH_HIP(hipHostGetDevicePointer((void**)&d_small_h, h_small, 0));
   float* h_out = (float*)c->pin_out.get((2 * k * d + k) * 4);
   // ev_order[b]: epoch order b is on the device and h_order[b] free again (copy
   // stream); ev_done[b]: the epoch that used order/labels/scores b has run
@@ -401,9 +469,9 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   // Epochs alternate between two sets of order/labels/scores buffers, so the
   // copies of one epoch's run on the copy stream beside the next epoch's kernels.
   Buf order0(c, n * 4), order1(c, n * 4), lab0(c, n * 4), lab1(c, n * 4), sco0(c, n * 4),
-      sco1(c, n * 4), pos(c, k * d * 4), mass(c, k * 4), mass_next(c, k * 4),
+      sco1(c, n * 4), pos(c, k * d * 4), mass(c, k * 4),
       readout(c, (sph ? k * d : k) * 4), sums(c, k * d * 4), counts(c, k * 4),
-      pass(c, k * d * 4), init_ids(c, k * 4);
+      pass(c, k * d * 4), passc(c, k * 4), init_ids(c, k * 4);
   uint32_t* d_order[2] = {order0.u(), order1.u()};
   uint32_t* d_lab[2] = {lab0.u(), lab1.u()};
   float* d_sco[2] = {sco0.f(), sco1.f()};
@@ -428,7 +496,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
     ev_order[buf].record(c->copy_stream);
   };
   // The first epoch's order is drawn while the initial centroids are (model.rs:783-784).
-  std::future<void> next = std::async(std::launch::async, [&] { fill_order(0); });
+  std::future<void> next = beside([&] { fill_order(0); });
 
   // Initial centroids: the rows permutation(n)[..k] (model.rs:786-797),
   // normalized when spherical (model.rs:306-315), masses INIT_USAGE (recipe.rs:14).
@@ -449,6 +517,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   std::memcpy(&init_bits, &init_usage, 4);
   launch_fill_u32(c, mass.u(), k, init_bits);
   launch_fill_u32(c, pass.u(), k * d, 0);
+  launch_fill_u32(c, passc.u(), k, 0);
   copy_async(c, h_small0, c->small, SW_WORDS * 4, hipMemcpyDeviceToHost);
   ev_order[1].record(c->stream);  // the initial ids are out of h_order[1]
   ev_init.record(c->stream);
@@ -462,12 +531,9 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   // per revival that splits: the next k Gumbel terms are drawn ahead.
   RandomState split_rng(cfg.seed);
   std::future<std::vector<double>> gnext =
-      std::async(std::launch::async, [&] { return gumbel_terms(split_rng, k); });
-  auto take_gumbel = [&] {
-    std::vector<double> g = gnext.get();
-    gnext = std::async(std::launch::async, [&] { return gumbel_terms(split_rng, k); });
-    return g;
-  };
+      beside([&] { return gumbel_terms(split_rng, k); });
+  // The next block is started once the split is queued, off the GPU's path.
+  auto take_gumbel = [&] { return gnext.get(); };
   size_t n_splits = 0, step = 0;
   bool norms_stale = true;  // L2 readout: the EMA keeps the norms of the rows it moves
   std::vector<emh_epoch_stats> stats;
@@ -479,7 +545,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
     next.get();
     EMH_HIP(hipStreamWaitEvent(c->stream, ev_order[buf].e, 0));  // this epoch's order is in
     EMH_HIP(hipStreamWaitEvent(c->stream, ev_epoch[buf].e, 0));  // labels of epoch - 2 are out
-    if (!last) next = std::async(std::launch::async, [&, e1 = epoch + 1] { fill_order(e1); });
+    if (!last) next = beside([&, e1 = epoch + 1] { fill_order(e1); });
     uint32_t* order = d_order[buf];
     uint32_t* lab = d_lab[buf];
     float* sco = d_sco[buf];
@@ -506,14 +572,12 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
       const bool check = (step + 1) % 5 == 0;  // CHECK_UNUSED_EVERY (recipe.rs:12)
       launch_scatter_count(c, b, e, lab, k, counts.u());
       if (check) {
-        launch_mass_preview(c, mass.f(), counts.u(), k, af, df, replace, mass_next.f());
-        copy_async(c, h_usage, mass_next.p, k * 4, hipMemcpyDeviceToHost);
-        copy_async(c, h_small, c->small, SW_WORDS * 4, hipMemcpyDeviceToHost);
+        launch_mass_preview(c, mass.f(), counts.u(), k, af, df, replace, d_usage_h, d_small_h);
         ev_check.record(c->stream);
       }
       launch_scatter_sums(c, x, n, d, order, b, e, lab, k, sums.f(), last ? pass.f() : nullptr);
       launch_ema(c, pos.f(), mass.f(), sums.f(), counts.u(), k, d, af, df, replace,
-                 sph ? nullptr : readout.f(), true);
+                 sph ? nullptr : readout.f(), true, last ? passc.u() : nullptr);
       if (check) {
         ev_check.wait();
         raise_flags(c, h_small);
@@ -522,12 +586,12 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
         if (!plan.empty()) {
           const size_t np = plan.size() / 2;
           std::memcpy(h_plan, plan.data(), plan.size() * 4);
-          uint32_t* pd = (uint32_t*)c->misc.get(plan.size() * 4);
-          copy_async(c, pd, h_plan, plan.size() * 4, hipMemcpyHostToDevice);
-          launch_split(c, pos.f(), mass.f(), pd, np, d, true);  // donors and dead are disjoint
+          launch_split(c, pos.f(), mass.f(), d_plan, np, d, true);  // donors and dead are disjoint
           n_splits += np;
           norms_stale = true;
         }
+        if (!gnext.valid())
+          gnext = beside([&] { return gumbel_terms(split_rng, k); });
       }
       step++;
     }
@@ -540,7 +604,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
     ev_epoch[buf].record(c->copy_stream);
     if (pending.valid()) stats.push_back(pending.get());  // frees the other buffer pair
     const size_t nsplit = n_splits - splits_before;
-    pending = std::async(std::launch::async, [&, rows, buf, nsplit, epoch, st = step]() {
+    pending = beside([&, rows, buf, nsplit, epoch, st = step]() {
       ev_epoch[buf].wait();
       const double t =
           std::chrono::duration<double>(std::chrono::steady_clock::now() - t_start).count();
@@ -580,8 +644,9 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   }
   // The end: positions and masses are final after the last EMA and go out on
   // the copy stream while the closing means (core/mod.rs:404-429: the last
-  // pass's label counts, sums / count) and the labels by data row are
-  // computed; the host copies into the caller's arrays run in parallel.
+  // pass's label counts, sums / count; the counts were tallied batch by batch
+  // by the last pass's EMA launches) and the labels by data row are computed;
+  // the host copies into the caller's arrays run in parallel.
   const size_t rows_last = R.epoch_rows.back();
   const int lb = (int)((n_epochs - 1) & 1);
   ev_last.record(c->stream);
@@ -589,8 +654,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   EMH_HIP(hipMemcpyAsync(h_out + k * d, pos.p, k * d * 4, hipMemcpyDeviceToHost, c->copy_stream));
   EMH_HIP(hipMemcpyAsync(h_out + 2 * k * d, mass.p, k * 4, hipMemcpyDeviceToHost, c->copy_stream));
   ev_posout.record(c->copy_stream);
-  launch_hist(c, d_lab[lb], rows_last, k, counts.u());
-  launch_closing(c, pos.f(), pass.f(), counts.u(), k, d, sums.f());
+  launch_closing(c, pos.f(), pass.f(), passc.u(), k, d, sums.f());
   const float* C = sums.f();
   if (sph) {
     launch_normalize_rows(c, sums.f(), k, d, pass.f());
@@ -606,7 +670,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
     copy_async(c, h_rowlab, d_lab[lb ^ 1], n * 4, hipMemcpyDeviceToHost);
   }
   copy_async(c, h_small, c->small, SW_WORDS * 4, hipMemcpyDeviceToHost);
-  auto side = std::async(std::launch::async, [&] {
+  auto side = beside([&] {
     ev_posout.wait();
     if (out->positions) std::memcpy(out->positions, h_out + k * d, k * d * 4);
     if (out->usage) std::memcpy(out->usage, h_out + 2 * k * d, k * 4);

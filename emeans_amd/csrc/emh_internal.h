@@ -175,13 +175,16 @@ void launch_row_norms(emh_ctx* c, const float* m, size_t rows, size_t d, float* 
 void launch_normalize_rows(emh_ctx* c, const float* src, size_t rows, size_t d, float* dst);
 // With clear_screen_words, also zeroes the small-block words launch_top1
 // clears before its screen (the fallback count and the bound maxima), so the
-// next top-1 may skip that fill.
+// next top-1 may skip that fill. With tally, also adds counts into it.
 void launch_ema(emh_ctx* c, float* pos, float* usage, const float* sums, const uint32_t* counts,
                 size_t k, size_t d, float alpha, float decay, int replace, float* norms = nullptr,
-                bool clear_screen_words = false);
-// The masses launch_ema will leave, into out (usage untouched).
+                bool clear_screen_words = false, uint32_t* tally = nullptr);
+// The masses launch_ema will leave, into out (usage untouched); with
+// small_out, also a copy of the small block's words. out and small_out may be
+// pinned host memory mapped into the device's address space.
 void launch_mass_preview(emh_ctx* c, const float* usage, const uint32_t* counts, size_t k,
-                         float alpha, float decay, int replace, float* out);
+                         float alpha, float decay, int replace, float* out,
+                         uint32_t* small_out = nullptr);
 // counts = histogram of labels[0..n) (labels >= k skipped).
 void launch_hist(emh_ctx* c, const uint32_t* labels, size_t n, size_t k, uint32_t* counts);
 // Closing means: out[j] = sums[j] / counts[j] where counts[j] > 0, else pos[j].

@@ -153,7 +153,8 @@ __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __r
                                              const uint32_t* __restrict__ counts, size_t k,
                                              size_t d, float alpha, float decay, int replace,
                                              float* __restrict__ norms,
-                                             uint32_t* __restrict__ clear3) {
+                                             uint32_t* __restrict__ clear3,
+                                             uint32_t* __restrict__ tally) {
   extern __shared__ float sq[];  // EC rows of min(d, ECH) + 1 floats (norms only)
   __shared__ float wgt[EC], cntf[EC];
   const int tid = threadIdx.x;
@@ -162,6 +163,7 @@ __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __r
   if (clear3 && blockIdx.x == 0 && tid < 3) clear3[tid] = 0;
   if (tid < nc) {
     const uint32_t cnt = counts[j0 + tid];
+    if (tally) tally[j0 + tid] += cnt;
     float weight;
     usage[j0 + tid] = ema_mass(usage[j0 + tid], cnt, alpha, decay, replace, &weight);
     wgt[tid] = cnt > 0 ? weight : -1.0f;  // -1: no rows, position unchanged
@@ -230,8 +232,11 @@ __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __r
 __global__ __launch_bounds__(256) void k_mass_preview(const float* __restrict__ usage,
                                                       const uint32_t* __restrict__ counts,
                                                       size_t k, float alpha, float decay,
-                                                      int replace, float* __restrict__ out) {
+                                                      int replace, float* __restrict__ out,
+                                                      const uint32_t* __restrict__ small,
+                                                      uint32_t* __restrict__ small_out) {
   const size_t j = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (small_out && j < (size_t)SW_WORDS) small_out[j] = small[j];
   if (j >= k) return;
   float weight;
   out[j] = ema_mass(usage[j], counts[j], alpha, decay, replace, &weight);
@@ -380,19 +385,20 @@ void launch_normalize_rows(emh_ctx* c, const float* src, size_t rows, size_t d, 
 
 void launch_ema(emh_ctx* c, float* pos, float* usage, const float* sums, const uint32_t* counts,
                 size_t k, size_t d, float alpha, float decay, int replace, float* norms,
-                bool clear_screen_words) {
+                bool clear_screen_words, uint32_t* tally) {
   if (k == 0) return;
   const size_t lds = norms ? (size_t)EC * (std::min(d, (size_t)ECH) + 1) * sizeof(float) : 0;
   hipLaunchKernelGGL(k_ema, grid1(k, EC), dim3(256), lds, c->stream, pos, usage, sums, counts, k,
-                     d, alpha, decay, replace, norms, clear_screen_words ? c->small : nullptr);
+                     d, alpha, decay, replace, norms, clear_screen_words ? c->small : nullptr,
+                     tally);
   EMH_HIP(hipGetLastError());
 }
 
 void launch_mass_preview(emh_ctx* c, const float* usage, const uint32_t* counts, size_t k,
-                         float alpha, float decay, int replace, float* out) {
+                         float alpha, float decay, int replace, float* out, uint32_t* small_out) {
   if (k == 0) return;
-  hipLaunchKernelGGL(k_mass_preview, grid1(k, 256), dim3(256), 0, c->stream, usage, counts, k,
-                     alpha, decay, replace, out);
+  hipLaunchKernelGGL(k_mass_preview, grid1(std::max(k, (size_t)SW_WORDS), 256), dim3(256), 0,
+                     c->stream, usage, counts, k, alpha, decay, replace, out, c->small, small_out);
   EMH_HIP(hipGetLastError());
 }
 
