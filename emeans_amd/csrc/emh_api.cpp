@@ -139,7 +139,7 @@ int emh_destroy(emh_ctx* c) {
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
     for (emh::Scratch* s : {&c->cand, &c->fblist, &c->order, &c->start, &c->misc, &c->knn_tmp,
-                            &c->xnorm, &c->bigj, &c->chunkcnt})
+                            &c->xnorm, &c->bigj, &c->chunkcnt, &c->tickets})
       s->release();
     for (emh::Pinned* s : {&c->pin_usage, &c->pin_plan, &c->pin_small, &c->pin_order[0],
                            &c->pin_order[1], &c->pin_lab[0], &c->pin_lab[1], &c->pin_sco[0],

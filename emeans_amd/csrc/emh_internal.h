@@ -62,6 +62,15 @@ struct Scratch {
     }
     return ptr;
   }
+  // The same, with a new block zeroed in stream order (counters that every
+  // use leaves at zero again).
+  void* get_zeroed(size_t need, hipStream_t s) {
+    if (need > bytes) {
+      get(need);
+      EMH_HIP(hipMemsetAsync(ptr, 0, bytes, s));
+    }
+    return ptr;
+  }
   void release() {
     if (ptr) (void)hipFree(ptr);
     ptr = nullptr;
@@ -124,7 +133,7 @@ struct emh_ctx {
   int screen = 1;
   uint32_t* small = nullptr;  // SW_WORDS u32 on the device
   uint64_t fallback_total = 0;
-  emh::Scratch cand, fblist, order, start, misc, knn_tmp, xnorm, bigj, chunkcnt;
+  emh::Scratch cand, fblist, order, start, misc, knn_tmp, xnorm, bigj, chunkcnt, tickets;
   // Host staging of the device loop: masses, plan, flags, epoch orders and
   // epoch labels/scores (double-buffered), results.
   emh::Pinned pin_usage, pin_plan, pin_small, pin_order[2], pin_lab[2], pin_sco[2], pin_out;

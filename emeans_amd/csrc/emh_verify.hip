@@ -1,9 +1,10 @@
 // The exact scans behind the MFMA screen (emh_screen.hip) and its check
 // (emh_rescore.hip), for the rows the check could not settle:
 //
-//  k_exact_*   top-1: the rows' scan over all centroids, split into
+//  k_exact1    top-1: the rows' scan over all centroids, split into
 //              (4 rows x 64 centroids) items so that a handful of rows still
-//              spreads over the whole chip, then a per-row reduction;
+//              spreads over the whole chip; the block that completes a row
+//              group's last item reduces the group's rows (one launch);
 //  k_exactk    top-k: one block per queued query over all data rows.
 //
 // Float order (the reference CPU backend, assign/fused.rs + assign.rs):
@@ -35,16 +36,123 @@ __device__ __forceinline__ float4 load_tile4(const float* row, int col, int d) {
                      col + 2 < d ? row[col + 2] : 0.f, col + 3 < d ? row[col + 3] : 0.f);
 }
 
+// The end of row group g (rows g*RG ...): each row's smallest chunk minimum
+// (lower id on ties; a row where nothing wins gets label 0 and the initial
+// score) and, for L2, its |x|^2 as a sequential sum of rounded squares: the
+// wave stages the group's squares in LDS (sq, RG rows of SEG floats per pass)
+// and lane r adds row r's in order. One wave.
+constexpr int SEG = CJ * TDP / RG;
+__device__ __attribute__((noinline)) void finish_group(const float* __restrict__ x, size_t nx, int d,
+                             const uint32_t* __restrict__ ids, size_t lo,
+                             const uint32_t* __restrict__ list, uint32_t* __restrict__ small,
+                             int nch, int ip, const Cand* __restrict__ partial, int g, int nrows,
+                             float* sq, uint32_t* __restrict__ labels,
+                             float* __restrict__ scores) {
+  const int lane = threadIdx.x;
+  float mybest = INFINITY;  // lane r < RG: row r's best key and id
+  uint32_t mybid = NONE;
+  size_t myp = 0;
+  const float* xr[RG];
+  bool ok[RG];
+#pragma unroll
+  for (int r = 0; r < RG; r++) {
+    const int f = g * RG + r;
+    ok[r] = false;
+    xr[r] = x;
+    if (f >= nrows) continue;  // uniform
+    const size_t p = list ? (size_t)list[f] : lo + (size_t)f;
+    const size_t xid = ids ? (size_t)ids[p] : p;
+    if (xid >= nx) {
+      if (lane == 0) small[SW_BAD_ID] = 1;
+      continue;
+    }
+    ok[r] = true;
+    xr[r] = x + xid * (size_t)d;
+    float best = INFINITY;
+    uint32_t bid = NONE;
+    for (int q = lane; q < nch; q += WAVE) {
+      const Cand c = partial[(size_t)f * nch + q];
+      if (c.id != NONE && (c.key < best || (c.key == best && c.id < bid))) {
+        best = c.key;
+        bid = c.id;
+      }
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+      const float b2 = __shfl_xor(best, o, WAVE);
+      const uint32_t i2 = __shfl_xor(bid, o, WAVE);
+      if (i2 != NONE && (b2 < best || (b2 == best && i2 < bid))) {
+        best = b2;
+        bid = i2;
+      }
+    }
+    if (lane == r) {
+      mybest = best;
+      mybid = bid;
+      myp = p;
+    }
+  }
+  float xn = 0.f;
+  if (!ip) {
+    for (int t0 = 0; t0 < d; t0 += SEG) {
+      const int tl = min(SEG, d - t0);
+#pragma unroll
+      for (int r = 0; r < RG; r++) {
+        if (!ok[r]) continue;  // uniform
+        for (int i0 = 0; i0 < tl; i0 += WAVE * 8) {
+          float v[8];
+#pragma unroll
+          for (int u = 0; u < 8; u++) {
+            const int i = i0 + lane + WAVE * u;
+            v[u] = i < tl ? xr[r][t0 + i] : 0.f;
+          }
+#pragma unroll
+          for (int u = 0; u < 8; u++) {
+            const int i = i0 + lane + WAVE * u;
+            if (i < tl) sq[r * SEG + i] = v[u] * v[u];
+          }
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      if (lane < RG && ok[lane]) {  // in order, 16 LDS reads in flight
+        const float* row = sq + lane * SEG;
+        int i = 0;
+        for (; i + 16 <= tl; i += 16) {
+          float v[16];
+#pragma unroll
+          for (int u = 0; u < 16; u++) v[u] = row[i + u];
+#pragma unroll
+          for (int u = 0; u < 16; u++) xn = xn + v[u];
+        }
+        for (; i < tl; i++) xn = xn + row[i];
+      }
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+  if (lane < RG && ok[lane]) {
+    if (mybid == NONE) {
+      mybid = 0;
+      mybest = INFINITY;
+    }
+    labels[myp] = mybid;
+    scores[myp] = ip ? -mybest : fmaxf(xn + mybest, 0.0f);
+  }
+}
+
 template <bool VEC4>
-__global__ __launch_bounds__(64) void k_exact_part(
+__global__ __launch_bounds__(64) void k_exact1(
     const float* __restrict__ x, size_t nx, int d, const uint32_t* __restrict__ ids, size_t lo,
-    int n_direct, const uint32_t* __restrict__ list, const uint32_t* __restrict__ small,
+    int n_direct, const uint32_t* __restrict__ list, uint32_t* __restrict__ small,
     const float* __restrict__ cents, const float* __restrict__ cnorm, int k, int ip,
-    Cand* __restrict__ partial) {
+    Cand* __restrict__ partial, uint32_t* __restrict__ tickets, uint32_t* __restrict__ labels,
+    float* __restrict__ scores) {
   __shared__ __attribute__((aligned(16))) float ct[CJ * TDP];
   __shared__ __attribute__((aligned(16))) float xt[RG * TD];
   __shared__ uint32_t xid_s[RG];
+  __shared__ int last_s;
   const int nrows = list ? (int)small[SW_FALLBACK_COUNT] : n_direct;
+  if (list && blockIdx.x == 0 && threadIdx.x == 0) small[SW_FALLBACK_TOTAL] += (uint32_t)nrows;
   const int nch = (k + CJ - 1) / CJ;
   const int ngr = (nrows + RG - 1) / RG;
   const int ntd = (d + TD - 1) / TD;
@@ -147,89 +255,18 @@ __global__ __launch_bounds__(64) void k_exact_part(
       const int f = g * RG + r;
       if (lane == 0 && f < nrows) partial[(size_t)f * nch + q] = Cand{kx, id};
     }
-    __syncthreads();
-  }
-}
-
-// One wave per row: the smallest of the row's chunk minima (lower id on ties),
-// and for L2 the row's |x|^2 as a sequential sum of rounded squares: the wave
-// loads 1024 dimensions at a time into LDS and lane 0 adds them in order.
-constexpr int FW = 4;      // rows (waves) per block
-constexpr int FSEG = 1024;  // dimensions staged per pass
-__global__ __launch_bounds__(64 * FW) void k_exact_final(
-    const float* __restrict__ x, size_t nx, int d, const uint32_t* __restrict__ ids, size_t lo,
-    int n_direct, const uint32_t* __restrict__ list, uint32_t* __restrict__ small, int k, int ip,
-    const Cand* __restrict__ partial, uint32_t* __restrict__ labels, float* __restrict__ scores) {
-  __shared__ float sq[FW][FSEG];
-  const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-  const int nrows = list ? (int)small[SW_FALLBACK_COUNT] : n_direct;
-  const int nch = (k + CJ - 1) / CJ;
-  if (list && blockIdx.x == 0 && threadIdx.x == 0) small[SW_FALLBACK_TOTAL] += (uint32_t)nrows;
-  for (int f = blockIdx.x * FW + w; f < nrows; f += gridDim.x * FW) {  // uniform per wave
-    const size_t p = list ? (size_t)list[f] : lo + (size_t)f;
-    const size_t xid = ids ? (size_t)ids[p] : p;
-    if (xid >= nx) {
-      if (lane == 0) small[SW_BAD_ID] = 1;
-      continue;
-    }
-    float best = INFINITY;
-    uint32_t bid = NONE;
-    for (int q = lane; q < nch; q += WAVE) {
-      const Cand c = partial[(size_t)f * nch + q];
-      if (c.id != NONE && (c.key < best || (c.key == best && c.id < bid))) {
-        best = c.key;
-        bid = c.id;
-      }
-    }
-    for (int o = 32; o > 0; o >>= 1) {
-      float b2 = __shfl_xor(best, o, WAVE);
-      uint32_t i2 = __shfl_xor(bid, o, WAVE);
-      if (i2 != NONE && (b2 < best || (b2 == best && i2 < bid))) {
-        best = b2;
-        bid = i2;
-      }
-    }
-    if (bid == NONE) {
-      bid = 0;
-      best = INFINITY;
-    }
-    float xn = 0.f;
-    if (!ip) {
-      const float* xr = x + xid * (size_t)d;
-      for (int t0 = 0; t0 < d; t0 += FSEG) {
-        const int tl = min(FSEG, d - t0);
-        float v[FSEG / WAVE];
-#pragma unroll
-        for (int u = 0; u < FSEG / WAVE; u++) {
-          const int i = lane + WAVE * u;
-          v[u] = i < tl ? xr[t0 + i] : 0.f;
-        }
-#pragma unroll
-        for (int u = 0; u < FSEG / WAVE; u++) {
-          const int i = lane + WAVE * u;
-          if (i < tl) sq[w][i] = v[u] * v[u];
-        }
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        if (lane == 0) {  // in order, 16 LDS reads in flight
-          int i = 0;
-          for (; i + 16 <= tl; i += 16) {
-            float v[16];
-#pragma unroll
-            for (int u = 0; u < 16; u++) v[u] = sq[w][i + u];
-#pragma unroll
-            for (int u = 0; u < 16; u++) xn = xn + v[u];
-          }
-          for (; i < tl; i++) xn = xn + sq[w][i];
-        }
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-      }
-    }
+    // The group's ticket: the block that completes its last chunk finishes it.
     if (lane == 0) {
-      labels[p] = bid;
-      scores[p] = ip ? -best : fmaxf(xn + best, 0.0f);
+      __threadfence();
+      last_s = atomicAdd(&tickets[g], 1u) == (uint32_t)(nch - 1);
     }
+    __syncthreads();
+    if (last_s) {
+      __threadfence();
+      finish_group(x, nx, d, ids, lo, list, small, nch, ip, partial, g, nrows, ct, labels, scores);
+      if (lane == 0) tickets[g] = 0;
+    }
+    __syncthreads();
   }
 }
 
@@ -362,22 +399,22 @@ void launch_exact1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32
                    const float* cnorm, size_t k, bool ip, uint32_t* labels, float* scores) {
   if (n == 0) return;
   const size_t nch = (k + CJ - 1) / CJ;
+  const size_t ngr = (n + RG - 1) / RG;
   Cand* partial = (Cand*)c->knn_tmp.get(n * nch * sizeof(Cand));
-  // Queued rows: the count lives on the device, so the grid covers the worst case.
-  const size_t items = ((n + RG - 1) / RG) * nch;
-  // Queued rows are few: a grid of 2 blocks per CU covers them, and blocks
-  // past the device-side count exit at once.
+  uint32_t* tickets = (uint32_t*)c->tickets.get_zeroed(ngr * 4, c->stream);
+  // Queued rows: the count lives on the device, so the grid covers the worst
+  // case. Queued rows are few: a grid of 2 blocks per CU covers them, and
+  // blocks past the device-side count exit at once.
+  const size_t items = ngr * nch;
   const unsigned g = (unsigned)std::min<size_t>(items, (size_t)(list ? 2 : 8) * c->cus);
   if (d % 4 == 0)
-    hipLaunchKernelGGL(k_exact_part<true>, dim3(g), dim3(64), 0, c->stream, x, nx, (int)d, ids,
-                       lo, (int)n, list, c->small, cents, cnorm, (int)k, ip ? 1 : 0, partial);
+    hipLaunchKernelGGL(k_exact1<true>, dim3(g), dim3(64), 0, c->stream, x, nx, (int)d, ids, lo,
+                       (int)n, list, c->small, cents, cnorm, (int)k, ip ? 1 : 0, partial, tickets,
+                       labels, scores);
   else
-    hipLaunchKernelGGL(k_exact_part<false>, dim3(g), dim3(64), 0, c->stream, x, nx, (int)d, ids,
-                       lo, (int)n, list, c->small, cents, cnorm, (int)k, ip ? 1 : 0, partial);
-  EMH_HIP(hipGetLastError());
-  const unsigned g2 = (unsigned)std::min<size_t>((n + FW - 1) / FW, (size_t)4 * c->cus);
-  hipLaunchKernelGGL(k_exact_final, dim3(g2), dim3(64 * FW), 0, c->stream, x, nx, (int)d, ids, lo,
-                     (int)n, list, c->small, (int)k, ip ? 1 : 0, partial, labels, scores);
+    hipLaunchKernelGGL(k_exact1<false>, dim3(g), dim3(64), 0, c->stream, x, nx, (int)d, ids, lo,
+                       (int)n, list, c->small, cents, cnorm, (int)k, ip ? 1 : 0, partial, tickets,
+                       labels, scores);
   EMH_HIP(hipGetLastError());
 }
 
