@@ -143,10 +143,12 @@ __device__ __forceinline__ float ema_mass(float u, uint32_t cnt, float alpha, fl
 // batch's L2 readout, assign.rs:150-155); rows without members keep theirs.
 // Workgroup = EC clusters: the 256 threads update the clusters' positions
 // element by element, then lane c of the first wave adds cluster c's rounded
-// squares in order from LDS (rows padded by one float so the EC lanes read
-// different banks); the chains of EC clusters run side by side.
-constexpr int EC = 16;
-constexpr int ECH = 512;  // dimensions per LDS pass
+// squares in order from LDS (rows padded by four floats so the EC lanes read
+// different banks with aligned 16-byte reads); the chains of EC clusters run
+// side by side.
+constexpr int EC = 4;
+constexpr int TPC = 256 / EC;  // threads per cluster in the update
+constexpr int ECH = 1024;  // dimensions per LDS pass
 constexpr int EU = 16;    // elements per thread whose loads are in flight together
 __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __restrict__ usage,
                                              const float* __restrict__ sums,
@@ -155,7 +157,8 @@ __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __r
                                              float* __restrict__ norms,
                                              uint32_t* __restrict__ clear3,
                                              uint32_t* __restrict__ tally) {
-  extern __shared__ float sq[];  // EC rows of min(d, ECH) + 1 floats (norms only)
+  // EC rows of min(d, ECH) + 4 floats (norms only)
+  extern __shared__ __attribute__((aligned(16))) float sq[];
   __shared__ float wgt[EC], cntf[EC];
   const int tid = threadIdx.x;
   const size_t j0 = (size_t)blockIdx.x * EC;
@@ -170,10 +173,10 @@ __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __r
     cntf[tid] = (float)cnt;
   }
   __syncthreads();
-  const int seg = (int)min(d, (size_t)ECH), row = seg + 1;
-  // Thread layout of the update: 16 threads per cluster, thread q of cluster
-  // c takes dimensions q, q + 16, ...
-  const int c = tid / (256 / EC), q = tid % (256 / EC);
+  const int seg = (int)min(d, (size_t)ECH), row = seg + 4;  // rows stay 16-byte aligned
+  // Thread layout of the update: TPC threads per cluster, thread q of cluster
+  // c takes dimensions q, q + TPC, ...
+  const int c = tid / TPC, q = tid % TPC;
   const float weight = c < nc ? wgt[c] : -1.0f;
   const float count = c < nc ? cntf[c] : 1.0f;
   float nrm = 0.0f;  // lane c < nc of wave 0: cluster c's chain
@@ -182,17 +185,17 @@ __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __r
     if (weight >= 0.0f) {
       float* p = pos + (j0 + c) * d + c0;
       const float* s = sums + (j0 + c) * d + c0;
-      for (int t0 = q; t0 < len; t0 += 16 * EU) {
+      for (int t0 = q; t0 < len; t0 += TPC * EU) {
         float sv[EU], pv[EU];
 #pragma unroll
         for (int u = 0; u < EU; u++) {
-          const int t = t0 + 16 * u;
+          const int t = t0 + TPC * u;
           sv[u] = t < len ? s[t] : 0.0f;
           pv[u] = t < len ? p[t] : 0.0f;
         }
 #pragma unroll
         for (int u = 0; u < EU; u++) {
-          const int t = t0 + 16 * u;
+          const int t = t0 + TPC * u;
           if (t >= len) continue;
           const float mean = sv[u] / count;
           float v;
@@ -211,14 +214,29 @@ __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __r
     if (!norms) continue;
     __syncthreads();
     if (tid < nc && wgt[tid] >= 0.0f) {
+      // Adds in order; the next 16 squares' LDS reads are in flight while the
+      // current 16 are added.
       const float* r = sq + tid * row;
+      const int len16 = len & ~15;
       int t = 0;
-      for (; t + 16 <= len; t += 16) {  // 16 LDS reads in flight, adds in order
-        float v[16];
+      if (len16 > 0) {
+        float4 cur[4], nxt[4];
 #pragma unroll
-        for (int u = 0; u < 16; u++) v[u] = r[t + u];
+        for (int u = 0; u < 4; u++) cur[u] = *reinterpret_cast<const float4*>(r + 4 * u);
+        for (; t < len16; t += 16) {
+          const int tn = min(t + 16, len16 - 16);  // the last step reloads its own group
 #pragma unroll
-        for (int u = 0; u < 16; u++) nrm = nrm + v[u];
+          for (int u = 0; u < 4; u++) nxt[u] = *reinterpret_cast<const float4*>(r + tn + 4 * u);
+#pragma unroll
+          for (int u = 0; u < 4; u++) {
+            nrm = nrm + cur[u].x;
+            nrm = nrm + cur[u].y;
+            nrm = nrm + cur[u].z;
+            nrm = nrm + cur[u].w;
+          }
+#pragma unroll
+          for (int u = 0; u < 4; u++) cur[u] = nxt[u];
+        }
       }
       for (; t < len; t++) nrm = nrm + r[t];
     }
@@ -387,7 +405,7 @@ void launch_ema(emh_ctx* c, float* pos, float* usage, const float* sums, const u
                 size_t k, size_t d, float alpha, float decay, int replace, float* norms,
                 bool clear_screen_words, uint32_t* tally) {
   if (k == 0) return;
-  const size_t lds = norms ? (size_t)EC * (std::min(d, (size_t)ECH) + 1) * sizeof(float) : 0;
+  const size_t lds = norms ? (size_t)EC * (std::min(d, (size_t)ECH) + 4) * sizeof(float) : 0;
   hipLaunchKernelGGL(k_ema, grid1(k, EC), dim3(256), lds, c->stream, pos, usage, sums, counts, k,
                      d, alpha, decay, replace, norms, clear_screen_words ? c->small : nullptr,
                      tally);

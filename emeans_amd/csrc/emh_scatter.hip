@@ -313,7 +313,9 @@ __global__ __launch_bounds__(256) void k_sum(const float* __restrict__ x, size_t
 
 // Clusters with more than SMALL rows (listed by k_count): workgroup =
 // (listed cluster, strip of BC columns). Chunks of BR rows are double-buffered
-// in LDS; thread t loads column t % BC of rows t / BC + (BT / BC) u.
+// in LDS, column-major (stride BRP) so that a column's lane reads four rows per
+// LDS load; thread t loads column t % BC of rows t / BC + (BT / BC) u.
+constexpr int BRP = BR + 4;  // column stride in LDS: 4-row reads stay aligned, stores 2-way
 __global__ __launch_bounds__(BT) void k_sum_big(const float* __restrict__ x, size_t nx, size_t d,
                                                 const uint32_t* __restrict__ ids,
                                                 const uint32_t* __restrict__ rid,
@@ -323,7 +325,7 @@ __global__ __launch_bounds__(BT) void k_sum_big(const float* __restrict__ x, siz
                                                 uint32_t* __restrict__ small) {
   constexpr int RPT = BR * BC / BT;  // rows loaded per thread per chunk
   constexpr int RS = BT / BC;        // row stride between a thread's loads
-  __shared__ float vals[2][BR * BC];
+  __shared__ __attribute__((aligned(16))) float vals[2][BC * BRP];
   __shared__ uint32_t rows[2][BR];
   const int bi = blockIdx.x / strips, strip = blockIdx.x % strips;
   if (bi >= (int)small[SW_NBIG]) return;
@@ -347,7 +349,7 @@ __global__ __launch_bounds__(BT) void k_sum_big(const float* __restrict__ x, siz
   };
   auto lstore = [&](int buf) {
 #pragma unroll
-    for (int u = 0; u < RPT; u++) vals[buf][(r0 + RS * u) * BC + c] = v[u];
+    for (int u = 0; u < RPT; u++) vals[buf][c * BRP + r0 + RS * u] = v[u];
   };
   stage(0, 0);
   __syncthreads();
@@ -359,10 +361,23 @@ __global__ __launch_bounds__(BT) void k_sum_big(const float* __restrict__ x, siz
   for (uint32_t ch = 0; ch < nchunks; ch++) {
     const int cur = ch & 1, nxt = cur ^ 1;
     if (ch + 1 < nchunks) gload(nxt);  // in flight while the current chunk is added
-    if (tid < BC) {
+    if (tid < BC) {  // rows in order; 32 rows of LDS reads in flight
       const uint32_t len = min((uint32_t)BR, cnt - ch * BR);
-      const float* vc = vals[cur];
-      for (uint32_t i = 0; i < len; i++) s = s + vc[i * BC + tid];
+      const float* vc = vals[cur] + tid * BRP;
+      uint32_t i = 0;
+      for (; i + 32 <= len; i += 32) {
+        float4 q[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) q[u] = *reinterpret_cast<const float4*>(vc + i + 4 * u);
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+          s = s + q[u].x;
+          s = s + q[u].y;
+          s = s + q[u].z;
+          s = s + q[u].w;
+        }
+      }
+      for (; i < len; i++) s = s + vc[i];
     }
     __syncthreads();  // the current chunk's values and row ids are consumed
     if (ch + 1 < nchunks) lstore(nxt);
