@@ -13,8 +13,9 @@
 //              chunk in LDS; else one wave per cluster walking the labels with
 //              ballots), so each cluster's positions land in order at its
 //              start offset;
-//   3. sum:    clusters of up to SMALL rows: a thread per (cluster, column)
-//              adds the rows in order with SU row loads in flight;
+//   3. sum:    clusters of up to SMALL rows: a workgroup per cluster, a
+//              thread per four columns (d % 4 == 0; else per column) adds the
+//              rows in order with SU4 (SU) row loads in flight;
 //   4. sum_big larger clusters: a workgroup per (cluster, 32-column strip);
 //              eight threads per column load the next 256 rows into LDS while
 //              one lane per column adds the current 256 in order, so a long
@@ -280,7 +281,11 @@ __device__ __forceinline__ uint32_t row_of(const uint32_t* __restrict__ ids, siz
   return (uint32_t)r;
 }
 
-// Clusters of up to SMALL rows: thread = column of cluster j; rows in order.
+// Clusters of up to SMALL rows: workgroup = cluster j; rows in order. With
+// VEC4 a thread adds four columns (16-byte loads, SU4 rows in flight), else
+// one column (SU rows in flight).
+constexpr int SU4 = 32;
+template <bool VEC4>
 __global__ __launch_bounds__(256) void k_sum(const float* __restrict__ x, size_t nx, size_t d,
                                              const uint32_t* __restrict__ ids,
                                              const uint32_t* __restrict__ rid,
@@ -293,22 +298,53 @@ __global__ __launch_bounds__(256) void k_sum(const float* __restrict__ x, size_t
   if (cnt > (uint32_t)SMALL) return;  // k_sum_big
   if (threadIdx.x < cnt) rows[threadIdx.x] = row_of(ids, nx, rid[b + threadIdx.x], small);
   __syncthreads();
-  const size_t col = (size_t)blockIdx.y * blockDim.x + threadIdx.x;
-  if (col >= d) return;
-  float s = 0.0f;
-  for (uint32_t q = 0; q < cnt; q += SU) {
-    float v[SU];
+  if (VEC4) {
+    const size_t d4 = d / 4;
+    for (size_t c4 = threadIdx.x; c4 < d4; c4 += blockDim.x) {
+      float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (uint32_t q = 0; q < cnt; q += SU4) {
+        float4 v[SU4];
 #pragma unroll
-    for (int u = 0; u < SU; u++) {
-      const uint32_t r = q + u < cnt ? rows[q + u] : NOROW;
-      v[u] = r != NOROW ? x[(size_t)r * d + col] : 0.0f;
+        for (int u = 0; u < SU4; u++) {
+          const uint32_t r = q + u < cnt ? rows[q + u] : NOROW;
+          v[u] = r != NOROW ? *reinterpret_cast<const float4*>(x + (size_t)r * d + 4 * c4)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < SU4; u++)
+          if (q + u < cnt) {  // +0 for a bad row: s is never -0, so this adds nothing
+            s.x = s.x + v[u].x;
+            s.y = s.y + v[u].y;
+            s.z = s.z + v[u].z;
+            s.w = s.w + v[u].w;
+          }
+      }
+      float4* so = reinterpret_cast<float4*>(sums + j * d) + c4;
+      *so = s;
+      if (acc) {
+        float4* ao = reinterpret_cast<float4*>(acc + j * d) + c4;
+        const float4 a0 = *ao;
+        *ao = make_float4(a0.x + s.x, a0.y + s.y, a0.z + s.z, a0.w + s.w);
+      }
     }
-#pragma unroll
-    for (int u = 0; u < SU; u++)
-      if (q + u < cnt) s = s + v[u];  // +0 for a bad row: s is never -0, so this adds nothing
+    return;
   }
-  sums[j * d + col] = s;
-  if (acc) acc[j * d + col] = acc[j * d + col] + s;
+  for (size_t col = threadIdx.x; col < d; col += blockDim.x) {
+    float s = 0.0f;
+    for (uint32_t q = 0; q < cnt; q += SU) {
+      float v[SU];
+#pragma unroll
+      for (int u = 0; u < SU; u++) {
+        const uint32_t r = q + u < cnt ? rows[q + u] : NOROW;
+        v[u] = r != NOROW ? x[(size_t)r * d + col] : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < SU; u++)
+        if (q + u < cnt) s = s + v[u];  // +0 for a bad row: s is never -0, so this adds nothing
+    }
+    sums[j * d + col] = s;
+    if (acc) acc[j * d + col] = acc[j * d + col] + s;
+  }
 }
 
 // Clusters with more than SMALL rows (listed by k_count): workgroup =
@@ -447,9 +483,12 @@ void launch_scatter_sums(emh_ctx* c, const float* x, size_t nx, size_t d, const 
                        start, rid);
     EMH_HIP(hipGetLastError());
   }
-  dim3 g((unsigned)k, (unsigned)((d + 255) / 256));
-  hipLaunchKernelGGL(k_sum, g, dim3(256), 0, c->stream, x, nx, d, ids, rid, start, k, sums, acc,
-                     c->small);
+  if (d % 4 == 0)
+    hipLaunchKernelGGL(k_sum<true>, dim3((unsigned)k), dim3(256), 0, c->stream, x, nx, d, ids, rid,
+                       start, k, sums, acc, c->small);
+  else
+    hipLaunchKernelGGL(k_sum<false>, dim3((unsigned)k), dim3(256), 0, c->stream, x, nx, d, ids,
+                       rid, start, k, sums, acc, c->small);
   EMH_HIP(hipGetLastError());
   if (n > (size_t)SMALL) {
     const int strips = (int)((d + BC - 1) / BC);
