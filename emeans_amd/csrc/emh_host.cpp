@@ -463,7 +463,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   float* h_out = (float*)c->pin_out.get((2 * k * d + k) * 4);
   // ev_order[b]: epoch order b is on the device and h_order[b] free again (copy
   // stream); ev_done[b]: the epoch that used order/labels/scores b has run
-  // (main stream); ev_epoch[b]: its labels and scores are on the host.
+  // (main stream); ev_epoch[b]: its scores and label counts are on the host.
   Event ev_init, ev_check, ev_order[2], ev_done[2], ev_epoch[2], ev_last, ev_posout;
 
   // Epochs alternate between two sets of order/labels/scores buffers, so the
@@ -471,9 +471,12 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   Buf order0(c, n * 4), order1(c, n * 4), lab0(c, n * 4), lab1(c, n * 4), sco0(c, n * 4),
       sco1(c, n * 4), pos(c, k * d * 4), mass(c, k * 4),
       readout(c, (sph ? k * d : k) * 4), sums(c, k * d * 4), counts(c, k * 4),
-      pass(c, k * d * 4), passc(c, k * 4), init_ids(c, k * 4);
+      pass(c, k * d * 4), tally0(c, k * 4), tally1(c, k * 4), init_ids(c, k * 4);
   uint32_t* d_order[2] = {order0.u(), order1.u()};
   uint32_t* d_lab[2] = {lab0.u(), lab1.u()};
+  // The epoch's label counts, tallied batch by batch by the EMA launches: the
+  // statistics' histogram, and for the last pass the closing means' counts.
+  uint32_t* d_tally[2] = {tally0.u(), tally1.u()};
   float* d_sco[2] = {sco0.f(), sco1.f()};
   struct Drain {  // nothing queued may outlive the buffers, also on an error
     emh_ctx* c;
@@ -517,7 +520,6 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   std::memcpy(&init_bits, &init_usage, 4);
   launch_fill_u32(c, mass.u(), k, init_bits);
   launch_fill_u32(c, pass.u(), k * d, 0);
-  launch_fill_u32(c, passc.u(), k, 0);
   copy_async(c, h_small0, c->small, SW_WORDS * 4, hipMemcpyDeviceToHost);
   ev_order[1].record(c->stream);  // the initial ids are out of h_order[1]
   ev_init.record(c->stream);
@@ -546,6 +548,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
     EMH_HIP(hipStreamWaitEvent(c->stream, ev_order[buf].e, 0));  // this epoch's order is in
     EMH_HIP(hipStreamWaitEvent(c->stream, ev_epoch[buf].e, 0));  // labels of epoch - 2 are out
     if (!last) next = beside([&, e1 = epoch + 1] { fill_order(e1); });
+    launch_fill_u32(c, d_tally[buf], k, 0);
     uint32_t* order = d_order[buf];
     uint32_t* lab = d_lab[buf];
     float* sco = d_sco[buf];
@@ -577,7 +580,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
       }
       launch_scatter_sums(c, x, n, d, order, b, e, lab, k, sums.f(), last ? pass.f() : nullptr);
       launch_ema(c, pos.f(), mass.f(), sums.f(), counts.u(), k, d, af, df, replace,
-                 sph ? nullptr : readout.f(), true, last ? passc.u() : nullptr);
+                 sph ? nullptr : readout.f(), true, d_tally[buf]);
       if (check) {
         ev_check.wait();
         raise_flags(c, h_small);
@@ -599,7 +602,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
     // wait for them on a helper thread.
     ev_done[buf].record(c->stream);
     EMH_HIP(hipStreamWaitEvent(c->copy_stream, ev_done[buf].e, 0));
-    EMH_HIP(hipMemcpyAsync(h_lab[buf], lab, rows * 4, hipMemcpyDeviceToHost, c->copy_stream));
+    EMH_HIP(hipMemcpyAsync(h_lab[buf], d_tally[buf], k * 4, hipMemcpyDeviceToHost, c->copy_stream));
     EMH_HIP(hipMemcpyAsync(h_sco[buf], sco, rows * 4, hipMemcpyDeviceToHost, c->copy_stream));
     ev_epoch[buf].record(c->copy_stream);
     if (pending.valid()) stats.push_back(pending.get());  // frees the other buffer pair
@@ -609,26 +612,51 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
       const double t =
           std::chrono::duration<double>(std::chrono::steady_clock::now() - t_start).count();
       const float* sc = h_sco[buf];
-      double obj_epoch = 0.0;
+      // The objective: one in-order f64 chain per (batch, chunk), as
+      // train.rs adds them; eight chains run interleaved (each with the same
+      // adds in the same order), then the batches' sums are added in order.
+      struct Chain {
+        size_t c0, c1;
+        double s;
+      };
+      std::vector<Chain> ch;
+      std::vector<size_t> nper;  // chunks per batch
       for (size_t b = 0; b < rows; b += bsz) {
         const size_t e = std::min(b + bsz, rows);
-        double obj_batch = 0.0;
-        for (size_t c0 = b; c0 < e; c0 += chunk) {
+        size_t m = 0;
+        for (size_t c0 = b; c0 < e; c0 += chunk, m++) {
           const size_t c1 = std::min(c0 + chunk, e);
-          double obj = 0.0;
-          if (sph) {
-            obj += 2.0 * (double)(c1 - c0);
-            for (size_t p = c0; p < c1; p++) obj += (double)(-2.0f * sc[p]);
-          } else {
-            for (size_t p = c0; p < c1; p++) obj += (double)sc[p];
-          }
-          obj_batch += obj;
+          ch.push_back({c0, c1, sph ? 2.0 * (double)(c1 - c0) : 0.0});
         }
+        nper.push_back(m);
+      }
+      auto term = [&](float v) { return sph ? (double)(-2.0f * v) : (double)v; };
+      for (size_t g0 = 0; g0 < ch.size(); g0 += 8) {
+        const size_t ng = std::min<size_t>(8, ch.size() - g0);
+        size_t len = ch[g0].c1 - ch[g0].c0;
+        for (size_t g = 1; g < ng; g++) len = std::min(len, ch[g0 + g].c1 - ch[g0 + g].c0);
+        double acc[8];
+        const float* ptr[8];
+        for (size_t g = 0; g < 8; g++) {  // lanes past ng repeat chain g0 and are discarded
+          const Chain& q = ch[g0 + (g < ng ? g : 0)];
+          acc[g] = q.s;
+          ptr[g] = sc + q.c0;
+        }
+        for (size_t i = 0; i < len; i++)
+          for (int g = 0; g < 8; g++) acc[g] += term(ptr[g][i]);
+        for (size_t g = 0; g < ng; g++) {
+          Chain& q = ch[g0 + g];
+          for (size_t i = len; i < q.c1 - q.c0; i++) acc[g] += term(ptr[g][i]);
+          q.s = acc[g];
+        }
+      }
+      double obj_epoch = 0.0;
+      for (size_t b = 0, i = 0; b < nper.size(); b++) {
+        double obj_batch = 0.0;
+        for (size_t m = 0; m < nper[b]; m++, i++) obj_batch += ch[i].s;
         obj_epoch += obj_batch;
       }
-      std::vector<uint64_t> hist(k, 0);
-      for (size_t p = 0; p < rows; p++)
-        if (h_lab[buf][p] < k) hist[h_lab[buf][p]]++;
+      const uint32_t* hist = h_lab[buf];  // the epoch's tallied counts
       double sq = 0.0;
       for (size_t j = 0; j < k; j++) sq += (double)hist[j] * (double)hist[j];
       emh_epoch_stats es;
@@ -654,7 +682,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   EMH_HIP(hipMemcpyAsync(h_out + k * d, pos.p, k * d * 4, hipMemcpyDeviceToHost, c->copy_stream));
   EMH_HIP(hipMemcpyAsync(h_out + 2 * k * d, mass.p, k * 4, hipMemcpyDeviceToHost, c->copy_stream));
   ev_posout.record(c->copy_stream);
-  launch_closing(c, pos.f(), pass.f(), passc.u(), k, d, sums.f());
+  launch_closing(c, pos.f(), pass.f(), d_tally[lb], k, d, sums.f());
   const float* C = sums.f();
   if (sph) {
     launch_normalize_rows(c, sums.f(), k, d, pass.f());

@@ -19,9 +19,13 @@
 
 #include <immintrin.h>
 
+#include <atomic>
 #include <cstddef>
 #include <cstdint>
+#include <cstring>
+#include <thread>
 #include <utility>
+#include <vector>
 
 namespace emh {
 namespace host {
@@ -124,16 +128,13 @@ struct Words {
   }
 };
 
-}  // namespace
-
-void mt_permutation(uint32_t seed, size_t n, uint32_t* p) {
-  Words w(seed);
-  for (size_t i = 0; i < n; i++) p[i] = (uint32_t)i;
-  size_t i = n;
-  for (; i > 1 && i - 1 > 0xffffffffull; i--) std::swap(p[i - 1], p[w.interval64(i - 1)]);
-  if (i <= 1) return;
-  // Draws with max < 2^32: the running max mx, its mask m, and lo = m >> 1,
-  // the max at which the mask halves.
+// The draws for i = n - 1 .. 1 below 2^32 (max = i - 1 for draw i, from i = n
+// down), a block of words at a time: sink(i0, jb, nj) gets the block's nj
+// taken values in draw order, the first for i = i0.
+template <class Sink>
+void draws(Words& w, size_t i, Sink&& sink) {
+  // The running max mx, its mask m, and lo = m >> 1, the max at which the
+  // mask halves.
   uint32_t m = 0xffffffffu >> __builtin_clz((uint32_t)(i - 1));
   uint32_t lo = m >> 1;
   uint32_t jb[N + 8];    // a block's draws (slack for 8-wide stores)
@@ -192,8 +193,48 @@ void mt_permutation(uint32_t seed, size_t n, uint32_t* p) {
     }
     w.pos = k;
     i = (size_t)mx + 1;
-    for (int t = 0; t < nj; t++) std::swap(p[i0 - 1 - t], p[jb[t]]);
+    sink(i0, jb, nj);
   }
 }
+
+}  // namespace
+
+void mt_permutation(uint32_t seed, size_t n, uint32_t* p) {
+  Words w(seed);
+  if (n - 1 > 0xffffffffull || n < (size_t)(1u << 15)) {
+    for (size_t i = 0; i < n; i++) p[i] = (uint32_t)i;
+    size_t i = n;
+    for (; i > 1 && i - 1 > 0xffffffffull; i--) std::swap(p[i - 1], p[w.interval64(i - 1)]);
+    if (i <= 1) return;
+    draws(w, i, [&](size_t i0, const uint32_t* jb, int nj) {
+      for (int t = 0; t < nj; t++) std::swap(p[i0 - 1 - t], p[jb[t]]);
+    });
+    return;
+  }
+  // Larger n: the swaps depend only on the draws, so a second thread makes
+  // them in draw order, following the drawing thread through `avail`.
+  static thread_local std::vector<uint32_t> buf;  // this (drawing) thread's
+  if (buf.size() < n) buf.resize(n);
+  uint32_t* const js = buf.data();
+  std::atomic<size_t> avail{0};
+  const size_t total = n - 1;  // draws for i = n .. 2
+  std::thread swapper([&] {
+    for (size_t i = 0; i < n; i++) p[i] = (uint32_t)i;
+    size_t t = 0;
+    while (t < total) {
+      size_t lim;
+      while ((lim = avail.load(std::memory_order_acquire)) == t) _mm_pause();
+      for (; t < lim; t++) std::swap(p[n - 1 - t], p[js[t]]);
+    }
+  });
+  size_t made = 0;
+  draws(w, n, [&](size_t, const uint32_t* jb, int nj) {
+    std::memcpy(js + made, jb, (size_t)nj * 4);
+    made += (size_t)nj;
+    avail.store(made, std::memory_order_release);
+  });
+  swapper.join();
+}
+
 }  // namespace host
 }  // namespace emh
