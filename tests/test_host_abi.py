@@ -81,6 +81,17 @@ def test_host_permutation_and_samples_match_the_fixture(lib, ref):
         assert int(np.dot(np.arange(m, dtype=np.int64), p[:m].astype(np.int64))) == c["sum"]
 
 
+def test_host_permutation_equals_numpy_across_sizes(lib):
+    """Whole permutations against numpy's legacy RandomState, on both sides of
+    the size where the swaps move to a second thread (2^15) and of the masks'
+    power-of-two boundaries."""
+    for seed, n in [(0, 1), (1, 2), (2, 3), (3, 624), (4, 625), (5, 32767), (6, 32768),
+                    (7, 65536), (8, 65537), (9, 200000), (10, 262145)]:
+        p = np.empty(n, np.uint32)
+        lib.emh_host_permutation(seed, n, p.ctypes.data)
+        assert np.array_equal(p, np.random.RandomState(seed).permutation(n)), (seed, n)
+
+
 def _cfg(c):
     cfg = _lib.Config()
     cfg.k, cfg.d, cfg.nepochs, cfg.seed = c["k"], c["d"], float(c["nepochs"]), 1234
