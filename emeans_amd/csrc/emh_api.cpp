@@ -119,6 +119,7 @@ int emh_create(int device, emh_ctx** out) {
     try {
       EMH_HIP(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
       EMH_HIP(hipStreamCreateWithFlags(&c->copy_stream, hipStreamNonBlocking));
+      for (hipEvent_t& e : c->ev_stage) EMH_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
       EMH_HIP(hipMalloc(&c->small, emh::SW_WORDS * 4));
       EMH_HIP(hipMemsetAsync(c->small, 0, emh::SW_WORDS * 4, c->stream));
       EMH_HIP(hipStreamSynchronize(c->stream));
@@ -126,6 +127,8 @@ int emh_create(int device, emh_ctx** out) {
       if (c->small) (void)hipFree(c->small);
       if (c->stream) (void)hipStreamDestroy(c->stream);
       if (c->copy_stream) (void)hipStreamDestroy(c->copy_stream);
+      for (hipEvent_t e : c->ev_stage)
+        if (e) (void)hipEventDestroy(e);
       delete c;
       throw;
     }
@@ -138,16 +141,17 @@ int emh_destroy(emh_ctx* c) {
     if (!c) return;
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
+    (void)hipStreamSynchronize(c->copy_stream);  // copies may still read pinned staging
     for (emh::Scratch* s : {&c->cand, &c->fblist, &c->order, &c->start, &c->misc, &c->knn_tmp,
                             &c->xnorm, &c->bigj, &c->chunkcnt, &c->tickets})
       s->release();
     for (emh::Pinned* s : {&c->pin_usage, &c->pin_plan, &c->pin_small, &c->pin_order[0],
                            &c->pin_order[1], &c->pin_lab[0], &c->pin_lab[1], &c->pin_sco[0],
-                           &c->pin_sco[1], &c->pin_out})
+                           &c->pin_sco[1], &c->pin_out, &c->pin_stage[0], &c->pin_stage[1]})
       s->release();
     if (c->small) (void)hipFree(c->small);
-    (void)hipStreamSynchronize(c->copy_stream);
     for (hipEvent_t e : c->ev_pool) (void)hipEventDestroy(e);
+    for (hipEvent_t e : c->ev_stage) (void)hipEventDestroy(e);
     (void)hipStreamDestroy(c->stream);
     (void)hipStreamDestroy(c->copy_stream);
     delete c;

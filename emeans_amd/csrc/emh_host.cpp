@@ -395,6 +395,39 @@ auto beside(F&& f) {
   return Helpers::get().run(std::forward<F>(f));
 }
 
+// Pageable host memory to the device at DMA speed: pieces of STAGE bytes go
+// through the context's two pinned staging halves, copied in by this thread
+// and three helpers while the copy stream moves the other half to the device.
+// The copy stream first waits for `after` (when given); work queued on the
+// context stream after the call sees the data. Returns once every piece is in
+// staging; the last DMAs may still run.
+constexpr size_t STAGE = size_t(32) << 20;
+void upload(emh_ctx* c, void* dst, const void* src, size_t bytes, hipEvent_t after = nullptr) {
+  if (!bytes) return;
+  if (after) EMH_HIP(hipStreamWaitEvent(c->copy_stream, after, 0));
+  char* half[2] = {(char*)c->pin_stage[0].get(STAGE), (char*)c->pin_stage[1].get(STAGE)};
+  const char* s = (const char*)src;
+  for (size_t off = 0, pc = 0; off < bytes; off += STAGE, pc++) {
+    const int h = (int)(pc & 1);
+    const size_t len = std::min(STAGE, bytes - off);
+    EMH_HIP(hipEventSynchronize(c->ev_stage[h]));  // the last copy out of this half is done
+    constexpr int T = 4;
+    const size_t part = (len / T + 63) & ~size_t(63);
+    std::future<void> f[T - 1];
+    for (int t = 1; t < T; t++) {
+      const size_t a = std::min(len, t * part), b = std::min(len, a + part);
+      f[t - 1] = beside([=] { std::memcpy(half[h] + a, s + off + a, b - a); });
+    }
+    std::memcpy(half[h], s + off, std::min(len, part));
+    for (auto& x : f) x.get();
+    EMH_HIP(hipMemcpyAsync((char*)dst + off, half[h], len, hipMemcpyHostToDevice,
+                           c->copy_stream));
+    EMH_HIP(hipEventRecord(c->ev_stage[h], c->copy_stream));
+  }
+  EMH_HIP(hipEventRecord(c->ev_stage[2], c->copy_stream));
+  EMH_HIP(hipStreamWaitEvent(c->stream, c->ev_stage[2], 0));
+}
+
 void copy_async(emh_ctx* c, void* dst, const void* src, size_t bytes, hipMemcpyKind kind) {
   if (bytes) EMH_HIP(hipMemcpyAsync(dst, src, bytes, kind, c->stream));
 }
@@ -868,7 +901,7 @@ int emh_train(emh_ctx* c, const float* x, size_t n, const emh_config* cfg, emh_t
     check_cfg(n, cfg, out);
     EMH_HIP(hipSetDevice(c->device));
     Buf xd(c, n * cfg->d * 4);  // Device::bind: the data set goes to the device once
-    h2d(c, xd.p, x, n * cfg->d * 4);
+    upload(c, xd.p, x, n * cfg->d * 4);
     train_dev(c, xd.f(), n, *cfg, out);
   });
 }
@@ -884,19 +917,44 @@ int emh_assign(emh_ctx* c, const float* x, size_t n, size_t d, const float* cent
     chunk = chunk ? chunk : 65536;
     // Centroids and their norms go up once for all chunks.
     Buf cb(c, k * d * 4), cn(c, k * 4);
-    h2d(c, cb.p, cents, k * d * 4);
+    upload(c, cb.p, cents, k * d * 4);
     if (metric == EMH_L2) emh::launch_row_norms(c, cb.f(), k, d, cn.f());
+    // A pipeline over the chunks: chunk i + 1 is staged in and copied to the
+    // device while chunk i's kernels run; the device row buffers, labels and
+    // scores alternate, and chunk i's results reach the caller's arrays (from
+    // pinned memory) while chunk i + 1 runs.
     const size_t m = std::min(chunk, n);
-    Buf xb(c, m * d * 4), lb(c, m * 4), sb(c, m * 4);
-    for (size_t b = 0; b < n; b += chunk) {
+    Buf xb0(c, m * d * 4), xb1(c, m * d * 4), lb0(c, m * 4), lb1(c, m * 4), sb0(c, m * 4),
+        sb1(c, m * 4);
+    float* xb[2] = {xb0.f(), xb1.f()};
+    uint32_t* lb[2] = {lb0.u(), lb1.u()};
+    float* sb[2] = {sb0.f(), sb1.f()};
+    uint32_t* hl[2] = {(uint32_t*)c->pin_lab[0].get(m * 4), (uint32_t*)c->pin_lab[1].get(m * 4)};
+    float* hs[2] = {(float*)c->pin_sco[0].get(m * 4), (float*)c->pin_sco[1].get(m * 4)};
+    Event used[2], out[2];  // chunk's kernels done with its rows; its results in pinned memory
+    size_t pend = SIZE_MAX;  // the chunk whose results wait for the caller's arrays
+    auto deliver = [&](size_t i) {
+      const size_t b = i * chunk, e = std::min(b + chunk, n);
+      out[i & 1].wait();
+      std::memcpy(labels + b, hl[i & 1], (e - b) * 4);
+      std::memcpy(scores + b, hs[i & 1], (e - b) * 4);
+    };
+    for (size_t i = 0, b = 0; b < n; i++, b += chunk) {
       const size_t e = std::min(b + chunk, n);
-      h2d(c, xb.p, x + b * d, (e - b) * d * 4);
-      emh::launch_top1(c, xb.f(), e - b, d, nullptr, 0, e - b, cb.f(),
-                       metric == EMH_L2 ? cn.f() : nullptr, k, metric == EMH_IP, lb.u(), sb.f());
-      d2h(c, labels + b, lb.p, (e - b) * 4);
-      d2h(c, scores + b, sb.p, (e - b) * 4);
+      const int h = (int)(i & 1);
+      upload(c, xb[h], x + b * d, (e - b) * d * 4, i >= 2 ? used[h].e : nullptr);
+      emh::launch_top1(c, xb[h], e - b, d, nullptr, 0, e - b, cb.f(),
+                       metric == EMH_L2 ? cn.f() : nullptr, k, metric == EMH_IP, lb[h], sb[h]);
+      used[h].record(c->stream);
+      if (pend != SIZE_MAX) deliver(pend);  // before reusing its pinned halves
+      copy_async(c, hl[h], lb[h], (e - b) * 4, hipMemcpyDeviceToHost);
+      copy_async(c, hs[h], sb[h], (e - b) * 4, hipMemcpyDeviceToHost);
+      out[h].record(c->stream);
+      pend = i;
     }
+    deliver(pend);
     check_flags(c);
+    EMH_HIP(hipStreamSynchronize(c->copy_stream));  // staging is free again
   });
 }
 

@@ -137,6 +137,11 @@ struct emh_ctx {
   // Host staging of the device loop: masses, plan, flags, epoch orders and
   // epoch labels/scores (double-buffered), results.
   emh::Pinned pin_usage, pin_plan, pin_small, pin_order[2], pin_lab[2], pin_sco[2], pin_out;
+  // Staged uploads from pageable host memory (emh_host.cpp, upload): two
+  // pinned halves, each with the event of the last copy that read it, and the
+  // event the context stream waits on for the whole upload.
+  emh::Pinned pin_stage[2];
+  hipEvent_t ev_stage[3] = {nullptr, nullptr, nullptr};
   std::string name = "hip-gfx950";
   // Screen-kernel timing (emh_profile): event pairs and the FLOP each covers.
   bool prof = false;

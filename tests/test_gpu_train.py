@@ -138,3 +138,18 @@ def test_assign_at_scale_sample(dev):
     sub = slice(0, 4000)  # the oracle on a tenth of the queries
     ol, osc = O.assign(q[sub], 1024, c, "ip")
     assert np.array_equal(gl[sub], ol) and gs[sub].tobytes() == osc.tobytes()
+
+
+@pytest.mark.parametrize("metric", ["l2", "ip"])
+def test_assign_host_buffers_in_chunks(dev, metric):
+    """The host-buffer assignment pipelines its chunks (the next chunk's rows are
+    staged and copied in while the current chunk's kernels run, results go out
+    through alternating pinned buffers): six chunks of 1,000 rows, the last one
+    partial, bit-equal to the oracle."""
+    n, d, k = 5_500, 96, 300
+    x = O.contract_mixture(n, d, 40, 0.3, metric == "ip", 17).reshape(n, d)
+    c = x[(np.arange(k) * 11) % n] * np.float32(0.97)
+    gl, gs = dev.assign(x, d, c, metric, chunk=1000)
+    ol, osc = O.assign(x, d, c, metric)
+    assert np.array_equal(gl, ol)
+    assert gs.tobytes() == osc.tobytes()
