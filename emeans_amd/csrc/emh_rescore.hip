@@ -1,7 +1,7 @@
-// The check behind the MFMA screen (emh_screen.hip): per row, merge the
-// centroid parts' candidate lists, bound the screen's error, and either queue
-// the row for the exact scan (emh_verify.hip) or re-score its candidates with
-// the reference's float order:
+// The check behind the MFMA screen (emh_screen.hip): per row, bound the
+// screen's error, decide from the centroid parts' candidate lists whether the
+// candidates are complete, and either queue the row for the exact scan
+// (emh_verify.hip) or re-score its candidates with the reference's float order:
 //   dot = one fma chain over t = 0..d-1 from +0 (assign/fused.rs:241-260);
 //   L2 key = cnorm[j] - 2 dot (two roundings, assign.rs:461);
 //   |x|^2 = sequential sum of rounded squares (assign.rs:150-155);
@@ -107,7 +107,7 @@ __global__ __launch_bounds__(256) void k_verify(
     int kk, const Cand* __restrict__ cand, int parts, const float* __restrict__ xnorm,
     uint32_t* __restrict__ labels, float* __restrict__ scores, uint32_t* __restrict__ fb,
     uint32_t* __restrict__ small) {
-  constexpr int PMAX = R * L;
+  constexpr int PMAX = R * (KNN ? L : C1 + 1);  // pairs (+ the |x|^2 chain per top-1 row)
   __shared__ Cand cst[R * MAX_PARTS * L];
   __shared__ uint32_t prow[PMAX], pcid[PMAX];
   __shared__ float pres[PMAX];
@@ -141,37 +141,65 @@ __global__ __launch_bounds__(256) void k_verify(
     }
   }
   __syncthreads();
-  // One thread per row: merge (each part's list is ascending, so a part is
-  // done at its first entry not below the current L-th key), bound, decide.
+  // One thread per row. kNN: merge (each part's list is ascending, so a part
+  // is done at its first entry not below the current L-th key), bound, decide.
+  // Top-1: per part, as k_check1 decides (a part's list holds all of its
+  // centroids within thr when not full or when its last key is above thr).
   float key[L];
   uint32_t id[L];
   float thr = 0.f;
   if (tid < rows) {
-#pragma unroll
-    for (int e = 0; e < L; e++) {
-      key[e] = INFINITY;
-      id[e] = NONE;
-    }
     const Cand* c = cst + tid * parts * L;
-    for (int q = 0; q < parts; q++)
+    if (KNN) {
+#pragma unroll
       for (int e = 0; e < L; e++) {
-        const Cand v = c[q * L + e];
-        if (v.id == NONE || !(v.key < key[L - 1])) break;
-        insert<L>(key, id, v.key, v.id);
+        key[e] = INFINITY;
+        id[e] = NONE;
       }
+      for (int q = 0; q < parts; q++)
+        for (int e = 0; e < L; e++) {
+          const Cand v = c[q * L + e];
+          if (v.id == NONE || !(v.key < key[L - 1])) break;
+          insert<L>(key, id, v.key, v.id);
+        }
+    }
     int state = 0, nc = 0;
     if (rowid[tid] != NONE) {
       const float E = screen_bound(xnorm[r0 + tid], __uint_as_float(small[SW_CMAX2]),
                                    __uint_as_float(small[SW_CNMAX]), d, l2);
-      thr = (KNN ? key[kk - 1] : key[0]) + 2.0f * E;
-      const bool complete = KNN ? (id[L - 1] == NONE || key[L - 1] > thr)
-                                : (id[0] != NONE && (id[L - 1] == NONE || key[L - 1] > thr));
+      bool complete;
+      if (KNN) {
+        thr = key[kk - 1] + 2.0f * E;
+        complete = id[L - 1] == NONE || key[L - 1] > thr;
+        if (complete)
+#pragma unroll
+          for (int e = 0; e < L - 1; e++) nc += id[e] != NONE && (key[e] <= thr || thr != thr);
+      } else {
+        float best = INFINITY;
+        bool anyv = false;
+        for (int q = 0; q < parts; q++)
+          if (c[q * L].id != NONE) {
+            anyv = true;
+            best = fminf(best, c[q * L].key);
+          }
+        thr = best + 2.0f * E;
+        bool cert = true;
+        int tot = 0;
+        for (int q = 0; q < parts; q++) {
+          const Cand last = c[q * L + L - 1];
+          if (last.id != NONE && !(last.key > thr)) cert = false;
+          for (int e = 0; e < L; e++) {
+            const Cand v = c[q * L + e];
+            tot += v.id != NONE && (v.key <= thr || thr != thr);
+          }
+        }
+        complete = anyv && cert && tot <= C1;
+        if (complete) nc = tot + (l2 ? 1 : 0);
+      }
       if (complete) {
         state = 1;
-#pragma unroll
-        for (int e = 0; e < L - 1; e++) nc += id[e] != NONE && (key[e] <= thr || thr != thr);
-        nc += l2;
       } else {
+        nc = 0;
         const uint32_t f = atomicAdd(&small[SW_FALLBACK_COUNT], 1u);
         fb[f] = KNN ? (uint32_t)(r0 + tid) : (uint32_t)(lo + r0 + tid);
       }
@@ -191,13 +219,25 @@ __global__ __launch_bounds__(256) void k_verify(
   __syncthreads();
   if (tid < rows && rstate[tid]) {
     int o = off[tid];
+    if (KNN) {
 #pragma unroll
-    for (int e = 0; e < L - 1; e++)
-      if (id[e] != NONE && (key[e] <= thr || thr != thr)) {
-        prow[o] = tid;
-        pcid[o] = id[e];
-        o++;
+      for (int e = 0; e < L - 1; e++)
+        if (id[e] != NONE && (key[e] <= thr || thr != thr)) {
+          prow[o] = tid;
+          pcid[o] = id[e];
+          o++;
+        }
+    } else {
+      const Cand* c = cst + tid * parts * L;
+      for (int i = 0; i < parts * L; i++) {
+        const Cand v = c[i];
+        if (v.id != NONE && (v.key <= thr || thr != thr)) {
+          prow[o] = tid;
+          pcid[o] = v.id;
+          o++;
+        }
       }
+    }
     if (l2) {
       prow[o] = tid;
       pcid[o] = NONE;
@@ -287,14 +327,14 @@ constexpr int RK = 16;  // rows per block, top-k
 
 // ---- Top-1 check with the rows staged through LDS (d % 4 == 0).
 //
-// Decision without a merge. The merged list is the L1 smallest keys of the
-// parts' lists, so with thr = best + 2E and le(key) = key <= thr || thr is NaN,
-// and lists holding only finite keys (the screen never keeps +inf or NaN):
-//   the row is settled  <=>  some entry is valid and at most L1 - 1 valid
-//                            entries satisfy le,
-// and then its candidates are exactly the valid entries satisfying le (all of
-// them are among the merged list's first L1 - 1). Eight threads per row scan
-// one part's list each and combine with lane shuffles.
+// Decision per part, without a merge. With thr = best + 2E, le(key) = key <=
+// thr || thr is NaN, and lists holding only finite keys (the screen never
+// keeps +inf or NaN), a part's list holds every centroid of the part whose
+// screen key satisfies le when the list is not full or its last key is above
+// thr. The row is settled when some entry is valid, every part is so, and at
+// most C1 entries satisfy le; its candidates are then exactly those entries.
+// Eight threads per row scan one part's list each and combine with lane
+// shuffles.
 //
 // Chains. The block's settled rows (x) and their candidates (centroid rows)
 // are staged in CDC-float chunks into a double-buffered LDS tile by waves 2-3,
@@ -324,8 +364,8 @@ __global__ __launch_bounds__(256) void k_check1(
   __shared__ v4f stage[2][CSLOT * CDP4];
   __shared__ uint32_t xrow[CR];  // x row of each settled row, NONE otherwise
   __shared__ int rcnt[CR], roff[CR + 1], rset[CR];
-  __shared__ uint32_t prow[CR * (L1 - 1)], pcid[CR * (L1 - 1)];
-  __shared__ float pdot[CR * (L1 - 1)], pcn[CR * (L1 - 1)], rnorm[CR];
+  __shared__ uint32_t prow[CR * C1], pcid[CR * C1];
+  __shared__ float pdot[CR * C1], pcn[CR * C1], rnorm[CR];
   const int tid = threadIdx.x;
   const int r0 = blockIdx.x * CR;
   const int rows = min(CR, nrows - r0);
@@ -370,7 +410,7 @@ __global__ __launch_bounds__(256) void k_check1(
     }
     const bool vrow = live && !badid;
     uint32_t inc = 0;
-    int cj = 0;
+    int cj = 0, cert = 1;
     if (vrow) {
       const float E = screen_bound(xn, __uint_as_float(small[SW_CMAX2]),
                                    __uint_as_float(small[SW_CNMAX]), d, l2);
@@ -381,15 +421,19 @@ __global__ __launch_bounds__(256) void k_check1(
           inc |= 1u << e;
           cj++;
         }
+      // This part's list holds all of its centroids within thr: not full, or
+      // its last key above thr (never with a NaN thr).
+      cert = idv[L1 - 1] == NONE || key[L1 - 1] > thr;
     }
     int tot = cj, incl = cj;
 #pragma unroll
     for (int m = 1; m < 8; m <<= 1) {
       tot += __shfl_xor(tot, m);
+      cert &= __shfl_xor(cert, m);
       const int v = __shfl_up(incl, m, 8);
       if (j >= m) incl += v;
     }
-    const bool settled = vrow && anyv && tot <= L1 - 1;
+    const bool settled = vrow && anyv && cert && tot <= C1;
     if (j == 0) {
       xrow[r] = settled ? xid : NONE;
       rcnt[r] = settled ? tot : 0;

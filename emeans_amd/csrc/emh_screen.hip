@@ -7,24 +7,28 @@
 // dimensions. FP32 MFMA accumulates in its own order, so its scores can differ
 // from the chain's by a few ulps times d. The path therefore has three stages:
 //
-//  1. screen (MFMA, the dense x . C^T contraction): each row keeps the L
-//     smallest screen keys (key = -dot for IP, |c|^2 - 2 dot for L2) with
-//     their ids, in registers; the n x k score matrix never leaves the CU.
-//  2. verify: merge the partial lists; bound the screen error E rigorously
-//     from |x| and max|c|; if the L-th smallest key is above best + 2E, every
-//     centroid that can win is among the first L-1, so re-score exactly those
-//     within best + 2E with the fma chain and take the smallest exact key,
-//     lower id on ties. Otherwise queue the row.
+//  1. screen (MFMA, the dense x . C^T contraction): per part (a range of
+//     centroid tiles) each row keeps the L smallest screen keys (key = -dot
+//     for IP, |c|^2 - 2 dot for L2) with their ids, in registers; the n x k
+//     score matrix never leaves the CU.
+//  2. check: bound the screen error E rigorously from |x| and max|c|. A
+//     part's list holds every centroid of the part whose screen key is at
+//     most best + 2E when the list is not full or its L-th key is above
+//     best + 2E; with every part so, the centroids that can win are among
+//     the lists' entries within best + 2E: re-score exactly those (at most
+//     C1) with the fma chain and take the smallest exact key, lower id on
+//     ties. Otherwise queue the row.
 //  3. exact: the full fma-chain scan of the queued rows over all k centroids.
 //
-// The same stages with a longer list give the exact top-k of kNN.
+// The same stages with a longer list, merged over the parts, give the exact
+// top-k of kNN.
 //
 // Bound: for any summation order of d products, |computed - exact dot| <=
 // gamma_d * sum|x_t c_t| (gamma_d = d u / (1 - d u), u = 2^-24), and
 // sum|x_t c_t| <= |x| |c|. The chain and the MFMA (taken at 2 gamma_d, plus a
 // denormal-flush floor of d 2^-124) give |dot' - dot| <= 3 gamma_d |x| cmax;
-// L2 keys add the rounding of |c|^2 - 2 dot on both sides. E carries a 12.5%
-// margin for its own rounding.
+// L2 keys add the rounding of |c|^2 - 2 dot on both sides (one rounding in the
+// screen's fma, two in the check's). E carries a 12.5% margin for its own rounding.
 
 #include "emh_select.h"
 
@@ -308,7 +312,7 @@ __global__ __launch_bounds__(256, 2) void k_screen(
 #pragma unroll
           for (int y = 0; y < WN; y++) {
             float v = acc[a][y][r];
-            float key = L2 ? nn - 2.0f * v : nn - v;
+            float key = L2 ? fmaf(-2.0f, v, nn) : nn - v;  // one rounding: within E
             if (KNN && gj == qrow[y]) key = INFINITY;
             // Skipped by the whole wave when no lane's key beats its list's
             // last entry (the common case once the lists have filled).

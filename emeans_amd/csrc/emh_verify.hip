@@ -2,9 +2,12 @@
 // (emh_rescore.hip), for the rows the check could not settle:
 //
 //  k_exact1    top-1: the rows' scan over all centroids, split into
-//              (4 rows x 64 centroids) items so that a handful of rows still
-//              spreads over the whole chip; the block that completes a row
-//              group's last item reduces the group's rows (one launch);
+//              (4 rows x 64 centroids) items; the block that completes a row
+//              group's last item reduces the group's rows (one launch). For
+//              a selection without the screen, and queued rows when d % 4 != 0;
+//  k_queued1   top-1 for the rows the check queues (d % 4 == 0): short
+//              (4 rows x 16 centroids) items, one burst of DMA copies and one
+//              chain per lane each, the winners folded by 64-bit atomics;
 //  k_exactk    top-k: one block per queued query over all data rows.
 //
 // Float order (the reference CPU backend, assign/fused.rs + assign.rs):
@@ -25,15 +28,27 @@ constexpr int WAVE = 64;
 // RG chains per lane. The dimensions go in tiles of TD: a tile of the chunk's
 // centroids and the group's rows is loaded into registers (every load of the
 // tile in flight at once) while the previous tile is consumed from LDS.
-constexpr int CJ = 64, RG = 4, TD = 128, TDP = TD + 4;
+constexpr int CJ = 64, RG = 4, TD = 64, TDP = TD + 4;
 constexpr int CL4 = CJ * TD / 4 / WAVE;  // float4 loads per lane per tile (centroids)
 constexpr int XL4 = RG * TD / 4 / WAVE;  // float4 loads per lane per tile (rows)
 
+// Columns col..col+3 of a row, zero past d. Branch-free: every load is issued
+// (at a clamped column) and the zeros are selected afterwards, so a tile's
+// loads stay in flight together instead of each waiting on a branch.
 template <bool VEC4>
-__device__ __forceinline__ float4 load_tile4(const float* row, int col, int d) {
-  if (VEC4 && col + 4 <= d) return *reinterpret_cast<const float4*>(row + col);
-  return make_float4(col < d ? row[col] : 0.f, col + 1 < d ? row[col + 1] : 0.f,
-                     col + 2 < d ? row[col + 2] : 0.f, col + 3 < d ? row[col + 3] : 0.f);
+__device__ __forceinline__ float4 load_tile4(const float* row, int col, int d, bool valid = true) {
+  if (VEC4) {  // d % 4 == 0: col < d implies col + 4 <= d
+    const float4 v = *reinterpret_cast<const float4*>(row + min(col, d - 4));
+    const bool in = valid && col < d;
+    return make_float4(in ? v.x : 0.f, in ? v.y : 0.f, in ? v.z : 0.f, in ? v.w : 0.f);
+  }
+  float e[4];
+#pragma unroll
+  for (int u = 0; u < 4; u++) {
+    const float v = row[min(col + u, d - 1)];
+    e[u] = valid && col + u < d ? v : 0.f;
+  }
+  return make_float4(e[0], e[1], e[2], e[3]);
 }
 
 // The end of row group g (rows g*RG ...): each row's smallest chunk minimum
@@ -188,7 +203,7 @@ __global__ __launch_bounds__(64) void k_exact1(
         cr[u] = load_tile4<VEC4>(cents + (size_t)min(q * CJ + r0 + RSTEP * u, k - 1) * d, col, d);
 #pragma unroll
       for (int u = 0; u < XL4; u++)
-        xr[u] = xv[u] ? load_tile4<VEC4>(xp[u], col, d) : make_float4(0.f, 0.f, 0.f, 0.f);
+        xr[u] = load_tile4<VEC4>(xp[u], col, d, xv[u]);  // xp[u] is row 0 when invalid
     };
     float acc[RG];
 #pragma unroll
@@ -264,6 +279,173 @@ __global__ __launch_bounds__(64) void k_exact1(
     if (last_s) {
       __threadfence();
       finish_group(x, nx, d, ids, lo, list, small, nch, ip, partial, g, nrows, ct, labels, scores);
+      if (lane == 0) tickets[g] = 0;
+    }
+    __syncthreads();
+  }
+}
+
+// ------------------------------------------------- exact top-1, queued rows
+// The check queues few rows (often one to eight per batch), so this scan is
+// built for latency: many short items, each a single wave that copies its
+// data to LDS in one burst and then runs one fma chain per lane.
+//
+// Item = (group of QR rows, chunk of QJ centroids), plus one norm item per
+// group for L2. Lane (j = lane / QR, r = lane % QR) runs row r's chain against
+// centroid j of the chunk. The dimensions go in phases of up to QPH: the
+// phase's slice of the chunk's centroids and of the group's rows is copied to
+// LDS by the DMA path (global_load_lds, 16 bytes per lane, all instructions in
+// flight together), then the chains read it. LDS slots (16 bytes, 4 dims):
+// centroids at u * QJ + j, rows at u * QR + r for dims 4u..4u+3 of the phase,
+// so a read touches consecutive slots (no bank conflicts) and lanes sharing a
+// centroid or a row read it by broadcast.
+//
+// Each item folds its chunk's winners into one 64-bit word per row with an
+// atomic max of the complement of (ordered key << 32 | id << 1 | sign of a
+// zero key): the smallest key wins, then the lower id (keys -0 and +0 are
+// equal, as in the reference's comparison; the sign bit restores the winner's
+// own zero), so the reduction is exact and independent of the item order. The
+// item that takes a group's last ticket writes the group's labels and scores
+// and leaves the words and the ticket at zero for the next launch.
+constexpr int QR = 4, QJ = 16, QPH = 768;
+constexpr int QU = QPH / 4;  // 4-dim slots per phase
+
+__device__ __forceinline__ uint64_t pack_best(float key, uint32_t id) {
+  uint32_t b = __float_as_uint(key), z = 0;
+  if (key == 0.0f) {  // -0 and +0 compare equal: one code, the sign kept apart
+    z = b >> 31;
+    b = 0u;
+  }
+  const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ~(((uint64_t)o << 32) | ((uint64_t)id << 1) | z);
+}
+
+__device__ __forceinline__ bool unpack_best(uint64_t w, float& key, uint32_t& id) {
+  if (w == 0) return false;
+  const uint64_t v = ~w;
+  const uint32_t o = (uint32_t)(v >> 32);
+  uint32_t b = (o & 0x80000000u) ? (o & 0x7fffffffu) : ~o;
+  if (b == 0u && (v & 1u)) b = 0x80000000u;
+  key = __uint_as_float(b);
+  id = (uint32_t)((v >> 1) & 0x7fffffffu);
+  return true;
+}
+
+__global__ __launch_bounds__(64) void k_queued1(
+    const float* __restrict__ x, size_t nx, int d, const uint32_t* __restrict__ ids,
+    const uint32_t* __restrict__ list, uint32_t* __restrict__ small,
+    const float* __restrict__ cents, const float* __restrict__ cnorm, int k, int ip,
+    unsigned long long* __restrict__ best, uint32_t* __restrict__ tickets,
+    float* __restrict__ xnq, uint32_t* __restrict__ labels, float* __restrict__ scores) {
+  typedef float v4f __attribute__((ext_vector_type(4)));
+  __shared__ v4f cs[QU * QJ];
+  __shared__ v4f xs[QU * QR];
+  __shared__ uint32_t xid_s[QR];
+  const int nrows = (int)small[SW_FALLBACK_COUNT];
+  if (blockIdx.x == 0 && threadIdx.x == 0) small[SW_FALLBACK_TOTAL] += (uint32_t)nrows;
+  const int nch = (k + QJ - 1) / QJ;
+  const int per = nch + (ip ? 0 : 1);  // items per group (the last one: |x|^2)
+  const int ngr = (nrows + QR - 1) / QR;
+  const int lane = threadIdx.x;
+  const int j = lane / QR, r = lane % QR;
+  for (int item = blockIdx.x; item < ngr * per; item += gridDim.x) {
+    const int g = item / per, q = item - g * per;
+    const bool norm = q == nch;
+    if (lane < QR) {
+      const int f = g * QR + lane;
+      uint32_t xid = NONE;
+      if (f < nrows) {
+        const size_t id = ids ? (size_t)ids[list[f]] : (size_t)list[f];
+        if (id < nx)
+          xid = (uint32_t)id;
+        else
+          small[SW_BAD_ID] = 1;
+      }
+      xid_s[lane] = xid;
+    }
+    __syncthreads();
+    // This lane's DMA sources: rows (slot l of each row instruction covers
+    // dims 4 * (16 i + l / QR) of row l % QR) and centroids (dims
+    // 4 * (4 i + l / QJ) of centroid l % QJ).
+    const uint32_t xr = xid_s[lane % QR];
+    const float* xrow = x + (size_t)(xr == NONE ? 0u : xr) * d;
+    const float* crow = cents + (size_t)min(q * QJ + lane % QJ, k - 1) * d;
+    float acc = 0.f;
+    for (int t0 = 0; t0 < d; t0 += QPH) {
+      const int nu = min(QU, (d - t0) / 4);  // d % 4 == 0
+      for (int i = 0; i < (nu + 15) / 16; i++) {
+        const int col = min(t0 + 4 * (16 * i + lane / QR), d - 4);
+        __builtin_amdgcn_global_load_lds(xrow + col, &xs[i * 64], 16, 0, 0);
+      }
+      if (!norm)
+        for (int i = 0; i < (nu + 3) / 4; i++) {
+          const int col = min(t0 + 4 * (4 * i + lane / QJ), d - 4);
+          __builtin_amdgcn_global_load_lds(crow + col, &cs[i * 64], 16, 0, 0);
+        }
+      __syncthreads();  // waits for the copies
+      if (norm) {  // |x|^2 of row r: sequential sum of rounded squares
+#pragma unroll 8
+        for (int u = 0; u < nu; u++) {
+          const v4f v = xs[u * QR + r];
+          acc = acc + v.x * v.x;
+          acc = acc + v.y * v.y;
+          acc = acc + v.z * v.z;
+          acc = acc + v.w * v.w;
+        }
+      } else {
+#pragma unroll 8
+        for (int u = 0; u < nu; u++) {
+          const v4f cv = cs[u * QJ + j];
+          const v4f v = xs[u * QR + r];
+          acc = fmaf(v.x, cv.x, acc);
+          acc = fmaf(v.y, cv.y, acc);
+          acc = fmaf(v.z, cv.z, acc);
+          acc = fmaf(v.w, cv.w, acc);
+        }
+      }
+      __syncthreads();  // the next phase's copies overwrite these slots
+    }
+    const int f = g * QR + r;
+    const bool valid = f < nrows && xid_s[r] != NONE;
+    if (norm) {
+      if (j == 0 && valid) xnq[f] = acc;
+    } else {
+      const int cj = q * QJ + j;
+      float kx = INFINITY;
+      uint32_t id = NONE;
+      if (valid && cj < k) {
+        kx = ip ? -acc : cnorm[cj] - 2.0f * acc;
+        id = (uint32_t)cj;
+        if (!(kx < INFINITY)) id = NONE;  // NaN or +inf never wins
+      }
+      uint64_t w = id == NONE ? 0ull : pack_best(kx, id);
+#pragma unroll
+      for (int o = QR; o < WAVE; o <<= 1) {  // across the centroids of row r
+        const uint64_t w2 = __shfl_xor(w, o, WAVE);
+        w = w2 > w ? w2 : w;
+      }
+      if (j == 0 && w != 0) atomicMax(&best[f], (unsigned long long)w);
+    }
+    // The group's ticket: the item that completes it writes the rows.
+    __shared__ int last_s;
+    if (lane == 0) {
+      __threadfence();
+      last_s = atomicAdd(&tickets[g], 1u) == (uint32_t)(per - 1);
+    }
+    __syncthreads();
+    if (last_s) {
+      __threadfence();
+      if (lane < QR && f < nrows) {
+        const unsigned long long w = atomicExch(&best[f], 0ull);
+        if (xid_s[r] != NONE) {
+          float bk = INFINITY;
+          uint32_t bid = 0;  // nothing wins: label 0 and the initial score
+          unpack_best(w, bk, bid);
+          const size_t p = list[f];
+          labels[p] = bid;
+          scores[p] = ip ? -bk : fmaxf(xnq[f] + bk, 0.0f);
+        }
+      }
       if (lane == 0) tickets[g] = 0;
     }
     __syncthreads();
@@ -398,6 +580,21 @@ void launch_exact1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32
                    size_t lo, size_t n, const uint32_t* list, const float* cents,
                    const float* cnorm, size_t k, bool ip, uint32_t* labels, float* scores) {
   if (n == 0) return;
+  // Both kernels read row 0 in place of a row whose id is out of range.
+  EMH_ENSURE(nx > 0, "top1: a selection of %zu rows over no data rows", n);
+  if (list && d % 4 == 0) {  // queued rows, few: the latency-bound scan
+    const size_t ngr = (n + QR - 1) / QR;
+    const size_t per = (k + QJ - 1) / QJ + (ip ? 0 : 1);
+    // Self-cleaning: the best words, then the tickets, all left at zero.
+    char* z = (char*)c->tickets.get_zeroed(n * 8 + ngr * 4, c->stream);
+    float* xnq = (float*)c->knn_tmp.get(n * 4);
+    const unsigned g = (unsigned)std::min<size_t>(ngr * per, (size_t)2 * c->cus);
+    hipLaunchKernelGGL(k_queued1, dim3(g), dim3(64), 0, c->stream, x, nx, (int)d, ids, list,
+                       c->small, cents, cnorm, (int)k, ip ? 1 : 0, (unsigned long long*)z,
+                       (uint32_t*)(z + n * 8), xnq, labels, scores);
+    EMH_HIP(hipGetLastError());
+    return;
+  }
   const size_t nch = (k + CJ - 1) / CJ;
   const size_t ngr = (n + RG - 1) / RG;
   Cand* partial = (Cand*)c->knn_tmp.get(n * nch * sizeof(Cand));

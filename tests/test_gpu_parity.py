@@ -140,18 +140,24 @@ def test_screen_bit_equal_on_near_ties(dev, n, d, k, metric):
     assert outs[0][1].tobytes() == osc.tobytes()
 
 
+@pytest.mark.parametrize("layout", ["spread", "together"])
 @pytest.mark.parametrize("metric", ["ip", "l2"])
-def test_check_several_candidates_per_row(dev, metric):
+def test_check_several_candidates_per_row(dev, metric, layout):
     """Centroids in groups of six within a relative 1e-7 of each other, rows near
-    the groups: every row keeps six candidates inside the screen bound, so each
-    32-row block of the check holds 192 (row, candidate) pairs and takes several
-    passes over its staged chunks. Labels and scores bit-equal to the oracle,
-    and to the exact kernel."""
+    the groups: every row keeps six candidates inside the screen bound.
+    spread: a group's members sit 32 ids apart, so no centroid part (128 ids)
+    holds more of them than its list keeps; each 32-row block of the check then
+    holds 192 (row, candidate) pairs and takes several passes over its staged
+    chunks, and the check settles the rows. together: a group's members are
+    consecutive, one part holds all six, its list overflows and the rows go to
+    the exact scan. Labels and scores bit-equal to the oracle, and to the exact
+    kernel, either way."""
     n, d, k, g = 2048, 256, 192, 6
     groups = k // g
     bases = _mix(groups, d, groups, 0.0, True, 7)
     t = np.arange(d)
-    c = np.stack([(bases[j // g].astype(np.float64) * (1.0 + 1e-7 * _noise(j * d + t)))
+    group_of = (np.arange(k) % groups) if layout == "spread" else (np.arange(k) // g)
+    c = np.stack([(bases[group_of[j]].astype(np.float64) * (1.0 + 1e-7 * _noise(j * d + t)))
                   .astype(np.float32) for j in range(k)])
     x = _mix(n, d, groups, 0.05, True, 7)
     perm = ((np.arange(n, dtype=np.uint64) * 7919 + 3) % n).astype(np.uint32)
@@ -161,7 +167,10 @@ def test_check_several_candidates_per_row(dev, metric):
     ol, osc = O.top1(x, d, c, metric, ids=perm)
     assert np.array_equal(gl, ol)
     assert gs.tobytes() == osc.tobytes()
-    assert rescanned < n // 10, rescanned  # the check settled them, not the exact scan
+    if layout == "spread":
+        assert rescanned < n // 10, rescanned  # the check settled them, not the exact scan
+    else:
+        assert rescanned > n // 2, rescanned  # a full list that cannot certify its part
     dev.set_screen(False)
     el, es = _gpu_top1(dev, x, c, metric, ids=perm)
     dev.set_screen(True)
