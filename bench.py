@@ -11,10 +11,16 @@ assignment of all 200,000 rows, with the data resident in HBM.
 value = top-1 rows processed per second over the whole step (5 training passes
 plus the final assignment: 1.2 M rows per step), in Mrows/s. The line also
 reports train seconds, assignment Mrows/s, the MFMA screen kernel's roofline
-(algorithmic 2 rows k d FLOP per launch over its HIP-event-timed duration, vs
-the 157.3 TFLOP/s dense FP32 MFMA peak), and the CPU baseline: the oracle's C++
-restatement of the reference CPU backend (cpu-fused float order) running the
-same training and assignment on this host, with a bit-exact parity check.
+and the CPU baseline. The screen (the dense x.C^T contraction ahead of the
+exact f32 check) runs on the bf16 MFMA in three passes (x.c ~ xh.ch + xh.cl +
+xl.ch); its roofline is the bf16 MFMA work it issues (3 x 2 rows k d FLOP per
+launch over its HIP-event-timed duration) against the 2.5 PFLOP/s dense bf16
+peak, with the f32-equivalent rate (2 rows k d FLOP per launch) against the
+157.3 TFLOP/s dense f32 MFMA peak beside it. `f32_screen` repeats the step
+with the screen on v_mfma_f32_32x32x2_f32 (same bits, checked). The CPU
+baseline is the oracle's C++ restatement of the reference CPU backend
+(cpu-fused float order) running the same training and assignment on this
+host, with a bit-exact parity check.
 """
 
 import argparse
@@ -29,6 +35,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 FP32_MFMA_PEAK = 157.3  # TFLOP/s, MI355X dense
+BF16_MFMA_PEAK = 2500.0  # TFLOP/s, MI355X dense
 HBM_PEAK = 8000.0       # GB/s
 METRIC = "train s & assign Mrows/s at 200k×768 k=1024 FP32; % of FP32 MFMA peak"
 # HBM bytes per k_screen launch over this workload's launch mix (calibrated
@@ -40,6 +47,19 @@ SCREEN_TRAFFIC_BYTES = 190.0e6
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def screen_roofline(ms, launches, flop, kernel, traffic=None):
+    """The bf16 screen's roofline: the MFMA work it issues (three bf16 products
+    per multiply-add of the algorithmic 2 rows k d FLOP) over its HIP-event
+    time, against the dense bf16 peak; the f32-equivalent rate beside it."""
+    alg = flop / (ms * 1e-3) / 1e12 if ms > 0 else 0.0
+    return {"bound": "mfma", "kernel": kernel, "achieved": 3.0 * alg, "peak": BF16_MFMA_PEAK,
+            "unit": "TFLOP/s", "frac": 3.0 * alg / BF16_MFMA_PEAK, "traffic": traffic,
+            "launches": launches, "avg_launch_ms": ms / max(launches, 1),
+            "flop_per_launch": 3.0 * flop / max(launches, 1),
+            "fp32_equivalent": {"achieved": alg, "peak": FP32_MFMA_PEAK, "frac": alg / FP32_MFMA_PEAK,
+                                "flop_per_launch": flop / max(launches, 1)}}
 
 
 def headline(args):
@@ -65,28 +85,39 @@ def headline(args):
         t2 = time.perf_counter()
         return t1 - t0, t2 - t1, cent, info
 
-    for i in range(args.warmup):
-        tr, asg, _, info = step()
-        log(f"warmup {i}: train {tr * 1e3:.1f} ms, assign {asg * 1e3:.1f} ms, "
-            f"fallback rows {info['fallback_rows']}")
-    dev.sync()
-    dev.profile(True)
-    trains, assigns = [], []
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        tr, asg, cent, info = step()
-        trains.append(tr)
-        assigns.append(asg)
-    dev.sync()
-    t1 = time.perf_counter()
-    dev.profile(False)
-    ms, launches, flop = dev.profile_read()
-    step_s = (t1 - t0) / args.steps
+    def timed(mode, steps, warmup):
+        """Warmup, then `steps` timed steps with the screen in `mode`
+        (1: bf16 three-pass, 2: f32), the screen's launches profiled."""
+        dev.set_screen(mode)
+        for i in range(warmup):
+            tr, asg, _, info = step()
+            log(f"warmup {i} (screen {mode}): train {tr * 1e3:.1f} ms, assign {asg * 1e3:.1f} ms, "
+                f"fallback rows {info['fallback_rows']}")
+        dev.sync()
+        dev.profile(True)
+        trains, assigns = [], []
+        t0 = time.perf_counter()
+        for i in range(steps):
+            tr, asg, cent, info = step()
+            trains.append(tr)
+            assigns.append(asg)
+        dev.sync()
+        t1 = time.perf_counter()
+        dev.profile(False)
+        ms, launches, flop = dev.profile_read()
+        r = {"step_s": (t1 - t0) / steps, "train_s": float(np.median(trains)),
+             "assign_s": float(np.median(assigns)), "ms": ms, "launches": launches, "flop": flop,
+             "cent": cent, "info": info, "labels": dev.read_u32(labels),
+             "scores": dev.read_f32(scores)}
+        dev.set_screen(1)
+        return r
+
+    main = timed(1, args.steps, args.warmup)
+    step_s, info, cent = main["step_s"], main["info"], main["cent"]
+    ms, launches, flop = main["ms"], main["launches"], main["flop"]
     epochs = len(info["stats"])
     rows_per_step = epochs * n + n
-    gpu_labels = dev.read_u32(labels)
-    gpu_scores = dev.read_f32(scores)
-    achieved = flop / (ms * 1e-3) / 1e12 if ms > 0 else 0.0
+    gpu_labels, gpu_scores = main["labels"], main["scores"]
     out = {
         "metric": METRIC,
         "value": rows_per_step / step_s / 1e6,
@@ -103,24 +134,30 @@ def headline(args):
         "config": {"workload": "train+assign 200000x768 k=1024 L2, GMM 1024 comps Zipf(1.1), seed 0",
                    "n": n, "d": d, "k": k, "epochs": epochs,
                    "batch": info["batch_size"], "steps_per_run": info["total_steps"]},
-        "train_s": float(np.median(trains)),
-        "assign_s": float(np.median(assigns)),
-        "assign_mrows_s": n / float(np.median(assigns)) / 1e6,
-        "train_mrows_s": epochs * n / float(np.median(trains)) / 1e6,
+        "train_s": main["train_s"],
+        "assign_s": main["assign_s"],
+        "assign_mrows_s": n / main["assign_s"] / 1e6,
+        "train_mrows_s": epochs * n / main["train_s"] / 1e6,
         "fallback_rows_per_run": info["fallback_rows"],
-        "roofline": {
-            "bound": "mfma",
-            "kernel": "k_screen (FP32 MFMA x.C^T + per-row 9-entry candidate list)",
-            "achieved": achieved,
-            "peak": FP32_MFMA_PEAK,
-            "unit": "TFLOP/s",
-            "frac": achieved / FP32_MFMA_PEAK,
-            "traffic": SCREEN_TRAFFIC_BYTES,
-            "launches": launches,
-            "avg_launch_ms": ms / max(launches, 1),
-            "flop_per_launch": flop / max(launches, 1),
-        },
+        "roofline": screen_roofline(
+            ms, launches, flop,
+            "k_screen (bf16 MFMA, three passes xh.ch + xh.cl + xl.ch, f32 accumulation, "
+            "+ per-row 5-entry candidate lists per centroid part)", SCREEN_TRAFFIC_BYTES),
     }
+    if not args.no_f32:
+        f = timed(2, max(2, args.steps // 2), 1)
+        fa = f["flop"] / (f["ms"] * 1e-3) / 1e12 if f["ms"] > 0 else 0.0
+        out["f32_screen"] = {
+            "value": rows_per_step / f["step_s"] / 1e6, "train_s": f["train_s"],
+            "assign_s": f["assign_s"],
+            "roofline": {"bound": "mfma", "kernel": "k_screen (f32 MFMA, v_mfma_f32_32x32x2_f32)",
+                         "achieved": fa, "peak": FP32_MFMA_PEAK, "unit": "TFLOP/s",
+                         "frac": fa / FP32_MFMA_PEAK, "launches": f["launches"],
+                         "avg_launch_ms": f["ms"] / max(f["launches"], 1)},
+            "equal_to_bf16_screen": bool(np.array_equal(f["labels"], gpu_labels)
+                                         and f["scores"].tobytes() == gpu_scores.tobytes()
+                                         and f["cent"].tobytes() == cent.tobytes()),
+        }
     if not args.no_host:
         out["from_host"] = from_host(dev, x, cfg, gpu_labels, gpu_scores)
     if not args.no_cpu:
@@ -213,17 +250,12 @@ def knn_workload(args):
     dev.profile(False)
     ms, launches, flop = dev.profile_read()
     gi, gs = dev.read_u32(ids).reshape(n, kk), dev.read_f32(sims).reshape(n, kk)
-    achieved = flop / (ms * 1e-3) / 1e12 if ms > 0 else 0.0
     out = {"metric": "knn_self top-10 TFLOP/s at 500k x 384 FP32", "value": 2.0 * n * n * d / step_s / 1e12,
            "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "ms_per_step": step_s * 1e3, "higher_is_better": True, "scaling": "weak",
            "vs_baseline": None, "dtype": "f32", "data": "synthetic",
            "config": {"workload": f"knn_self k=10 {n}x{d} unit rows, 5% near-duplicates, seed 2"},
-           "roofline": {"bound": "mfma", "kernel": "k_screen (kNN, 24-entry lists)",
-                        "achieved": achieved, "peak": FP32_MFMA_PEAK, "unit": "TFLOP/s",
-                        "frac": achieved / FP32_MFMA_PEAK, "traffic": None, "launches": launches,
-                        "avg_launch_ms": ms / max(launches, 1),
-                        "flop_per_launch": flop / max(launches, 1)}}
+           "roofline": screen_roofline(ms, launches, flop, "k_screen (kNN, bf16 three-pass MFMA, 24-entry lists)")}
     if not args.no_cpu:
         from oracle import oracle as O
         g = np.random.default_rng(0)
@@ -268,18 +300,13 @@ def assign_workload(args):
     step_s = (time.perf_counter() - t0) / args.steps
     dev.profile(False)
     ms, launches, flop = dev.profile_read()
-    achieved = flop / (ms * 1e-3) / 1e12 if ms > 0 else 0.0
     out = {"metric": "assign Mrows/s at 2M x 1024 vs k=16384 IP FP32", "value": n / step_s / 1e6,
            "unit": "Mrows/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "ms_per_step": step_s * 1e3, "higher_is_better": True, "scaling": "weak",
            "vs_baseline": None, "dtype": "f32", "data": "synthetic",
            "config": {"workload": f"assign {n}x{d} vs {k} centroids, IP, unit rows, seed 1"},
            "tflops": 2.0 * n * k * d / step_s / 1e12,
-           "roofline": {"bound": "mfma", "kernel": "k_screen (FP32 MFMA x.C^T + per-row 9-entry candidate list)",
-                        "achieved": achieved, "peak": FP32_MFMA_PEAK, "unit": "TFLOP/s",
-                        "frac": achieved / FP32_MFMA_PEAK, "traffic": None, "launches": launches,
-                        "avg_launch_ms": ms / max(launches, 1),
-                        "flop_per_launch": flop / max(launches, 1)}}
+           "roofline": screen_roofline(ms, launches, flop, "k_screen (bf16 three-pass MFMA x.C^T + per-row 5-entry candidate lists)")}
     if not args.no_host:
         # The same assignment from host arrays (8.2 GB of queries staged in
         # while earlier chunks run): the PCIe-inclusive rate, not the value.
@@ -327,6 +354,8 @@ def main():
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and parity")
+    ap.add_argument("--no-f32", action="store_true",
+                    help="skip the headline's comparison run with the f32 MFMA screen")
     ap.add_argument("--no-host", action="store_true",
                     help="skip the runs from host arrays (PCIe-inclusive times)")
     ap.add_argument("--cpu-threads", type=int, default=0)

@@ -273,8 +273,11 @@ class HipDevice:
     def fallback_rows(self) -> int:
         return lib().emh_fallback_rows(self._ctx)
 
-    def set_screen(self, on: bool):
-        check(lib().emh_set_screen(self._ctx, int(on)))
+    def set_screen(self, mode):
+        """Top-1 / top-k path: 1 or True = bf16 three-pass MFMA screen + exact
+        check (default), 2 = f32 MFMA screen + exact check, 0 or False = the
+        exact kernels alone. Every mode gives the same bits."""
+        check(lib().emh_set_screen(self._ctx, int(mode)))
 
 
 def make_assigner(backend: str = BACKEND_NAME, device: int = 0) -> HipDevice:

@@ -115,7 +115,10 @@ int emh_create(int device, emh_ctx** out) {
     auto* c = new emh_ctx;
     c->device = device;
     c->cus = p.multiProcessorCount;
-    if (const char* s = getenv("EMEANS_HIP_SCREEN")) c->screen = atoi(s) != 0;
+    if (const char* s = getenv("EMEANS_HIP_SCREEN")) {
+      const int m = atoi(s);
+      c->screen = m == emh::SCREEN_F32 ? emh::SCREEN_F32 : m ? emh::SCREEN_BF3 : emh::SCREEN_OFF;
+    }
     try {
       EMH_HIP(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
       EMH_HIP(hipStreamCreateWithFlags(&c->copy_stream, hipStreamNonBlocking));
@@ -475,7 +478,8 @@ uint64_t emh_fallback_rows(emh_ctx* c) {
 int emh_set_screen(emh_ctx* c, int on) {
   return guard([&] {
     EMH_ENSURE(c, "null context");
-    c->screen = on != 0;
+    EMH_ENSURE(on >= 0 && on <= 2, "screen mode %d: 0 (off), 1 (bf16) or 2 (f32)", on);
+    c->screen = on;
   });
 }
 

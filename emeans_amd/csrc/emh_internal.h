@@ -102,6 +102,10 @@ struct Pinned {
   }
 };
 
+// Top-1 / top-k path (emh_set_screen): the exact kernels alone, or the MFMA
+// screen in bf16 three-pass or f32 arithmetic ahead of the exact check.
+enum ScreenMode : int { SCREEN_OFF = 0, SCREEN_BF3 = 1, SCREEN_F32 = 2 };
+
 // Words of the context's small device block.
 enum SmallWord : int {
   SW_FALLBACK_COUNT = 0,  // rows appended to the exact kernel's list by the current call
@@ -130,7 +134,7 @@ struct emh_ctx {
   hipStream_t stream = nullptr;
   hipStream_t copy_stream = nullptr;  // host<->device staging that overlaps the kernels
   int cus = 256;
-  int screen = 1;
+  int screen = emh::SCREEN_BF3;
   uint32_t* small = nullptr;  // SW_WORDS u32 on the device
   uint64_t fallback_total = 0;
   emh::Scratch cand, fblist, order, start, misc, knn_tmp, xnorm, bigj, chunkcnt, tickets;

@@ -106,7 +106,7 @@ __global__ __launch_bounds__(256) void k_verify(
     int nrows, const float* __restrict__ cents, const float* __restrict__ cnorm, int k, int ip,
     int kk, const Cand* __restrict__ cand, int parts, const float* __restrict__ xnorm,
     uint32_t* __restrict__ labels, float* __restrict__ scores, uint32_t* __restrict__ fb,
-    uint32_t* __restrict__ small) {
+    uint32_t* __restrict__ small, int bf3) {
   constexpr int PMAX = R * (KNN ? L : C1 + 1);  // pairs (+ the |x|^2 chain per top-1 row)
   __shared__ Cand cst[R * MAX_PARTS * L];
   __shared__ uint32_t prow[PMAX], pcid[PMAX];
@@ -166,7 +166,7 @@ __global__ __launch_bounds__(256) void k_verify(
     int state = 0, nc = 0;
     if (rowid[tid] != NONE) {
       const float E = screen_bound(xnorm[r0 + tid], __uint_as_float(small[SW_CMAX2]),
-                                   __uint_as_float(small[SW_CNMAX]), d, l2);
+                                   __uint_as_float(small[SW_CNMAX]), d, l2, bf3 != 0);
       bool complete;
       if (KNN) {
         thr = key[kk - 1] + 2.0f * E;
@@ -360,7 +360,7 @@ __global__ __launch_bounds__(256) void k_check1(
     int nrows, const float* __restrict__ cents, const float* __restrict__ cnorm, int ip,
     const Cand* __restrict__ cand, int parts, const float* __restrict__ xnorm,
     uint32_t* __restrict__ labels, float* __restrict__ scores, uint32_t* __restrict__ fb,
-    uint32_t* __restrict__ small) {
+    uint32_t* __restrict__ small, int bf3) {
   __shared__ v4f stage[2][CSLOT * CDP4];
   __shared__ uint32_t xrow[CR];  // x row of each settled row, NONE otherwise
   __shared__ int rcnt[CR], roff[CR + 1], rset[CR];
@@ -413,7 +413,7 @@ __global__ __launch_bounds__(256) void k_check1(
     int cj = 0, cert = 1;
     if (vrow) {
       const float E = screen_bound(xn, __uint_as_float(small[SW_CMAX2]),
-                                   __uint_as_float(small[SW_CNMAX]), d, l2);
+                                   __uint_as_float(small[SW_CNMAX]), d, l2, bf3 != 0);
       const float thr = best + 2.0f * E;
 #pragma unroll
       for (int e = 0; e < L1; e++)
@@ -627,14 +627,15 @@ void launch_verify1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint3
                     const Cand* cand, int parts, const float* xnorm, uint32_t* labels,
                     float* scores, uint32_t* fb) {
   const dim3 g((unsigned)((n + R1 - 1) / R1));
+  const int bf3 = c->screen != SCREEN_F32;  // the bound follows the screen's arithmetic
   if (d % 4 == 0)
     hipLaunchKernelGGL(k_check1, dim3((unsigned)((n + CR - 1) / CR)), dim3(256), 0, c->stream, x,
                        nx, (int)d, ids, lo, (int)n, cents, cnorm, ip ? 1 : 0, cand, parts, xnorm,
-                       labels, scores, fb, c->small);
+                       labels, scores, fb, c->small, bf3);
   else
     hipLaunchKernelGGL((k_verify<L1, R1, false, false>), g, dim3(256), 0, c->stream, x, nx,
                        (int)d, ids, lo, (int)n, cents, cnorm, (int)k, ip ? 1 : 0, 1, cand, parts,
-                       xnorm, labels, scores, fb, c->small);
+                       xnorm, labels, scores, fb, c->small, bf3);
   EMH_HIP(hipGetLastError());
 }
 
@@ -642,14 +643,15 @@ void launch_verifyk(emh_ctx* c, const float* q, size_t m, const float* data, siz
                     size_t kk, const Cand* cand, int parts, const float* xnorm, uint32_t* ids,
                     float* sims, uint32_t* fb) {
   const dim3 g((unsigned)((m + RK - 1) / RK));
+  const int bf3 = c->screen != SCREEN_F32;
   if (d % 4 == 0)
     hipLaunchKernelGGL((k_verify<LK, RK, true, true>), g, dim3(256), 0, c->stream, q, m, (int)d,
                        nullptr, (size_t)0, (int)m, data, nullptr, (int)n, 1, (int)kk, cand, parts,
-                       xnorm, ids, sims, fb, c->small);
+                       xnorm, ids, sims, fb, c->small, bf3);
   else
     hipLaunchKernelGGL((k_verify<LK, RK, true, false>), g, dim3(256), 0, c->stream, q, m,
                        (int)d, nullptr, (size_t)0, (int)m, data, nullptr, (int)n, 1, (int)kk,
-                       cand, parts, xnorm, ids, sims, fb, c->small);
+                       cand, parts, xnorm, ids, sims, fb, c->small, bf3);
   EMH_HIP(hipGetLastError());
 }
 

@@ -4,8 +4,11 @@
 //
 // Exactness: the reference CPU backend (cpu-fused, assign/fused.rs) scores
 // every (row, centroid) pair with one sequential f32 fma chain over the d
-// dimensions. FP32 MFMA accumulates in its own order, so its scores can differ
-// from the chain's by a few ulps times d. The path therefore has three stages:
+// dimensions. The screen computes the same dot products on the bf16 MFMA in
+// three passes (x.c ~ xh.ch + xh.cl + xl.ch, the halves rounded to nearest
+// even, f32 accumulation), so its scores differ from the chain's by about
+// 2^-16 |x| |c| plus the accumulation's rounding. The path therefore has three
+// stages:
 //
 //  1. screen (MFMA, the dense x . C^T contraction): per part (a range of
 //     centroid tiles) each row keeps the L smallest screen keys (key = -dot
@@ -23,12 +26,13 @@
 // The same stages with a longer list, merged over the parts, give the exact
 // top-k of kNN.
 //
-// Bound: for any summation order of d products, |computed - exact dot| <=
-// gamma_d * sum|x_t c_t| (gamma_d = d u / (1 - d u), u = 2^-24), and
-// sum|x_t c_t| <= |x| |c|. The chain and the MFMA (taken at 2 gamma_d, plus a
-// denormal-flush floor of d 2^-124) give |dot' - dot| <= 3 gamma_d |x| cmax;
-// L2 keys add the rounding of |c|^2 - 2 dot on both sides (one rounding in the
-// screen's fma, two in the check's). E carries a 12.5% margin for its own rounding.
+// Bound (screen_bound, emh_select.h): the chain is within gamma_d sum|x_t c_t|
+// of the exact dot (gamma_d = d u / (1 - d u), u = 2^-24) and sum|x_t c_t| <=
+// |x| |c|; the screen adds the split's dropped and rounded parts
+// (<= 3.05 * 2^-16 |x| |c|) and the MFMA chain's rounding (each MFMA within
+// 16 u of its terms' magnitudes); L2 keys add the rounding of |c|^2 - 2 dot
+// on both sides (one rounding in the screen's fma, two in the check's). E
+// carries a 12.5% margin for its own rounding.
 
 #include "emh_select.h"
 
@@ -36,10 +40,12 @@ namespace emh {
 namespace {
 
 constexpr int BK = 32;       // dimensions per LDS slab
-constexpr int LDK = BK + 4;  // padded LDS row (floats): 144 B, conflict-free b128 reads
 constexpr int TC = 128;      // centroids per tile (two 32-blocks per wave, two waves)
+constexpr int RB = BK * 2;   // bf16 screen: bytes per LDS row of one half, four 16-byte chunks
+constexpr int LDK = BK + 4;  // f32 screen: padded LDS row (floats), conflict-free b128 reads
 
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
 // Work item of block `bid` of `nb`: blocks are dealt round-robin to the 8 XCDs
 // (consecutive ids land on different XCDs), so number each XCD's blocks
@@ -67,31 +73,61 @@ __device__ __forceinline__ float4 mask4(float4 v, int col, int d) {
                      col + 3 < d ? v.w : 0.f);
 }
 
+// Byte offset of 16-byte chunk q (dimensions 8q..8q+7 of the slab) of LDS row r:
+// rows of RB bytes, chunks XOR-swizzled by row so that the eight lanes of a
+// b128 access (eight consecutive rows, one chunk) hit eight different bank
+// groups, and a thread's four-row store quad too.
+__device__ __forceinline__ int chunk_at(int r, int q) { return r * RB + ((q ^ ((r >> 1) & 3)) << 4); }
+
+// x ~ hi + lo with hi = bf16(x) and lo = bf16(x - hi), both rounded to nearest
+// even (x - hi is exact in f32): |x - hi - lo| <= 2^-16 |x| for normal values,
+// <= 2^-134 in the bf16 subnormal range.
+__device__ __forceinline__ void split8(float4 a, float4 b, v8bf& hi, v8bf& lo) {
+  const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const __bf16 h = (__bf16)v[e];
+    hi[e] = h;
+    lo[e] = (__bf16)(v[e] - (float)h);
+  }
+}
+
 // ---------------------------------------------------------------- screen
 // Block: 256 threads = 4 waves; wave w: wr = w & 1 (row half), wc = w >> 1
 // (centroid half). Block tile: TR = 64*WN rows x TC centroids per tile;
-// each wave owns 32*WN rows x 64 centroids = (2 x WN) 32x32 MFMA blocks.
-// MFMA v_mfma_f32_32x32x2_f32: A = centroids (M), B = rows (N); lane l holds
-// row n = l % 32 of each block, so a row's keys stay in two lanes of a wave.
-// The screen sums the K dimension in any order: lane half h = l / 32 takes
-// dimensions [h*16, h*16 + 16) of each slab, four per b128 LDS read. Slabs
-// are double-buffered in LDS; the global loads of the next slab are issued
-// before the MFMAs of the current one and stored to the other buffer after
-// them.
-template <int WN, int L, bool L2, bool KNN, bool VEC4>
+// each wave owns 32*WN rows x 64 centroids = (2 x WN) 32x32 MFMA blocks,
+// A = centroids (M), B = rows (N); lane l holds row n = l % 32 of each block,
+// so a row's keys stay in two lanes of a wave. The screen sums the K
+// dimension in any order. Two arithmetics:
+//  BF3 (default): the bf16 MFMA (v_mfma_f32_32x32x16_bf16, f32 accumulation)
+//    in three passes, x.c ~ xh.ch + xh.cl + xl.ch, each slab's rows and
+//    centroids split into bf16 halves when staged in LDS; lane half h takes
+//    chunk 2s + h (8 dimensions) of k-step s of each slab;
+//  f32: v_mfma_f32_32x32x2_f32, lane half h takes dimensions
+//    [16h, 16h + 16) of each slab, four per b128 LDS read.
+// Slabs are double-buffered in LDS; the global loads of the next slab are
+// issued before the MFMAs of the current one and stored to the other buffer
+// after them.
+template <int WN, int L, bool L2, bool KNN, bool VEC4, bool BF3>
 __global__ __launch_bounds__(256, 2) void k_screen(
     const float* __restrict__ x, size_t nx, int d, const uint32_t* __restrict__ ids, size_t lo,
     int nrows, const float* __restrict__ cents, const float* __restrict__ cnorm, int k,
     int tiles_per_part, int parts, int ntiles, Cand* __restrict__ cand,
     uint32_t* __restrict__ small, float* __restrict__ xnorm) {
   constexpr int TR = 64 * WN;
-  constexpr int XL = TR * BK / 4 / 256;  // float4 loads per thread per slab (rows)
-  constexpr int CL = TC * BK / 4 / 256;  // float4 loads per thread per slab (centroids)
-  // One LDS block: the X and C slabs (double-buffered), reused for the final merge.
-  __shared__ __attribute__((aligned(16))) float smem[2 * (TR + TC) * LDK];
+  constexpr int XI = TR / 64;  // 8-dimension chunks per thread per slab (rows)
+  constexpr int CI = TC / 64;  // 8-dimension chunks per thread per slab (centroids)
+  // Bytes of one slab buffer: bf16 xh, xl, ch, cl, or f32 x, c.
+  constexpr int BUF = BF3 ? 2 * (TR + TC) * RB : (TR + TC) * LDK * 4;
+  // One LDS block: the slabs (double-buffered), reused for the final merge.
+  __shared__ __attribute__((aligned(16))) char smem[2 * BUF];
   __shared__ float Ns[2][TC];
-  float (*Xs)[TR * LDK] = reinterpret_cast<float (*)[TR * LDK]>(smem);
-  float (*Cs)[TC * LDK] = reinterpret_cast<float (*)[TC * LDK]>(smem + 2 * TR * LDK);
+  auto xh_at = [&](int buf) { return smem + buf * BUF; };
+  auto xl_at = [&](int buf) { return smem + buf * BUF + TR * RB; };
+  auto ch_at = [&](int buf) { return smem + buf * BUF + 2 * TR * RB; };
+  auto cl_at = [&](int buf) { return smem + buf * BUF + 2 * TR * RB + TC * RB; };
+  auto xf_at = [&](int buf) { return reinterpret_cast<float*>(smem + buf * BUF); };
+  auto cf_at = [&](int buf) { return reinterpret_cast<float*>(smem + buf * BUF + TR * LDK * 4); };
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int wr = w & 1, wc = w >> 1;
@@ -103,13 +139,14 @@ __global__ __launch_bounds__(256, 2) void k_screen(
   if (t0 >= t1) return;
   const int row0 = rt * TR;
 
-  // Rows this thread loads: (tid >> 3) + 32u, float4 column (tid & 7). Rows
-  // past the selection (or with a bad id) read data row 0; their lists are
-  // never written.
-  const float* xp[XL];
+  // Loads: thread tid stages chunk q = tid & 3 (8 dimensions) of rows
+  // (tid >> 2) + 64u of the slab. Rows past the selection (or with a bad id)
+  // read data row 0; their lists are never written.
+  const int q8 = tid & 3, r4 = tid >> 2;
+  const float* xp[XI];
 #pragma unroll
-  for (int u = 0; u < XL; u++) {
-    int r = row0 + (tid >> 3) + 32 * u;
+  for (int u = 0; u < XI; u++) {
+    int r = row0 + r4 + 64 * u;
     size_t xid = 0;
     if (r < nrows) {
       size_t p = lo + (size_t)r;
@@ -118,7 +155,6 @@ __global__ __launch_bounds__(256, 2) void k_screen(
     }
     xp[u] = x + xid * (size_t)d;
   }
-  const int c4 = (tid & 7) * 4;
 
   // Global query index of each row this lane scores (kNN exclude_self).
   uint32_t qrow[WN];
@@ -145,17 +181,17 @@ __global__ __launch_bounds__(256, 2) void k_screen(
 
   const int nslabs = (d + BK - 1) / BK;
   const int nsteps = (t1 - t0) * nslabs;
-  float4 xr[XL], cr[CL];
+  float4 xr[XI][2], cr[CI][2];
   float nreg = 0.f;
   bool nvalid = false;
 
   // Load cursor (tile lt, slab ls) runs one step ahead of the compute cursor.
   int lt = t0, ls = 0;
-  const float* cp[CL];  // centroid rows of tile lt (ids past k read centroid k-1)
+  const float* cp[CI];  // centroid rows of tile lt (ids past k read centroid k-1)
   auto set_tile = [&](int tile) {
 #pragma unroll
-    for (int u = 0; u < CL; u++) {
-      int j = min(tile * TC + (tid >> 3) + 32 * u, k - 1);
+    for (int u = 0; u < CI; u++) {
+      int j = min(tile * TC + r4 + 64 * u, k - 1);
       cp[u] = cents + (size_t)j * d;
     }
   };
@@ -163,60 +199,95 @@ __global__ __launch_bounds__(256, 2) void k_screen(
   // centroids (each row's squares summed in any order; by the blocks of row
   // tile 0), and max cnorm[j]. Compared as f32 bit patterns: a NaN or negative
   // value wins and sends every row of the call to the exact scan.
-  float csq[CL];
+  float csq[CI];
 #pragma unroll
-  for (int u = 0; u < CL; u++) csq[u] = 0.f;
+  for (int u = 0; u < CI; u++) csq[u] = 0.f;
   uint32_t cmax_bits = 0, cnmax_bits = 0;
   // Each row's |x|^2 in any order (for the verify's bound), summed while the
   // first tile streams the rows through; written by the blocks of part 0.
-  float xsq[XL];
+  float xsq[XI];
 #pragma unroll
-  for (int u = 0; u < XL; u++) xsq[u] = 0.f;
+  for (int u = 0; u < XI; u++) xsq[u] = 0.f;
   auto gload = [&]() {
-    const int col = ls * BK + c4;
+    const int col = ls * BK + 8 * q8;
 #pragma unroll
-    for (int u = 0; u < XL; u++) xr[u] = load4<VEC4>(xp[u], col, d);
+    for (int u = 0; u < XI; u++) {
+      xr[u][0] = load4<VEC4>(xp[u], col, d);
+      xr[u][1] = load4<VEC4>(xp[u], col + 4, d);
+    }
 #pragma unroll
-    for (int u = 0; u < CL; u++) cr[u] = load4<VEC4>(cp[u], col, d);
+    for (int u = 0; u < CI; u++) {
+      cr[u][0] = load4<VEC4>(cp[u], col, d);
+      cr[u][1] = load4<VEC4>(cp[u], col + 4, d);
+    }
     if (ls == 0 && tid < TC) {
       int j = lt * TC + tid;
       nvalid = j < k;
       nreg = L2 ? cnorm[min(j, k - 1)] : 0.f;
     }
   };
-  // Stores the slab loaded by gload (masked past d); the first use of the
-  // loaded registers, so the loads overlap the MFMAs issued in between. The
-  // mask and the norm sums are block-uniform branches: only a final partial
-  // slab is masked; only part 0 sums its rows' squares (during its first
-  // tile), and only row tile 0 the centroids' (its parts together cover every
-  // centroid tile).
+  auto sq8 = [](const float4 (&v)[2]) {
+    return v[0].x * v[0].x + v[0].y * v[0].y + v[0].z * v[0].z + v[0].w * v[0].w +
+           v[1].x * v[1].x + v[1].y * v[1].y + v[1].z * v[1].z + v[1].w * v[1].w;
+  };
+  // Stores the slab loaded by gload (masked past d), split into bf16 halves;
+  // the first use of the loaded registers, so the loads overlap the MFMAs
+  // issued in between. The mask and the norm sums are block-uniform branches:
+  // only a final partial slab is masked; only part 0 sums its rows' squares
+  // (during its first tile), and only row tile 0 the centroids' (its parts
+  // together cover every centroid tile).
   auto lstore = [&](int buf) {
-    const int col = ls * BK + c4;
+    const int col = ls * BK + 8 * q8;
     if (ls == nslabs - 1 && d % BK != 0) {
 #pragma unroll
-      for (int u = 0; u < XL; u++) xr[u] = mask4(xr[u], col, d);
+      for (int u = 0; u < XI; u++) {
+        xr[u][0] = mask4(xr[u][0], col, d);
+        xr[u][1] = mask4(xr[u][1], col + 4, d);
+      }
 #pragma unroll
-      for (int u = 0; u < CL; u++) cr[u] = mask4(cr[u], col, d);
+      for (int u = 0; u < CI; u++) {
+        cr[u][0] = mask4(cr[u][0], col, d);
+        cr[u][1] = mask4(cr[u][1], col + 4, d);
+      }
     }
+    if constexpr (BF3) {
 #pragma unroll
-    for (int u = 0; u < XL; u++)
-      *reinterpret_cast<float4*>(&Xs[buf][((tid >> 3) + 32 * u) * LDK + c4]) = xr[u];
+      for (int u = 0; u < XI; u++) {
+        v8bf hi, lo8;
+        split8(xr[u][0], xr[u][1], hi, lo8);
+        const int at = chunk_at(r4 + 64 * u, q8);
+        *reinterpret_cast<v8bf*>(xh_at(buf) + at) = hi;
+        *reinterpret_cast<v8bf*>(xl_at(buf) + at) = lo8;
+      }
 #pragma unroll
-    for (int u = 0; u < CL; u++)
-      *reinterpret_cast<float4*>(&Cs[buf][((tid >> 3) + 32 * u) * LDK + c4]) = cr[u];
+      for (int u = 0; u < CI; u++) {
+        v8bf hi, lo8;
+        split8(cr[u][0], cr[u][1], hi, lo8);
+        const int at = chunk_at(r4 + 64 * u, q8);
+        *reinterpret_cast<v8bf*>(ch_at(buf) + at) = hi;
+        *reinterpret_cast<v8bf*>(cl_at(buf) + at) = lo8;
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < XI; u++) {
+        float* dst = xf_at(buf) + (r4 + 64 * u) * LDK + 8 * q8;
+        *reinterpret_cast<float4*>(dst) = xr[u][0];
+        *reinterpret_cast<float4*>(dst + 4) = xr[u][1];
+      }
+#pragma unroll
+      for (int u = 0; u < CI; u++) {
+        float* dst = cf_at(buf) + (r4 + 64 * u) * LDK + 8 * q8;
+        *reinterpret_cast<float4*>(dst) = cr[u][0];
+        *reinterpret_cast<float4*>(dst + 4) = cr[u][1];
+      }
+    }
     if (part == 0 && lt == t0) {
 #pragma unroll
-      for (int u = 0; u < XL; u++) {
-        const float4 v = xr[u];
-        xsq[u] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-      }
+      for (int u = 0; u < XI; u++) xsq[u] += sq8(xr[u]);
     }
     if (rt == 0) {
 #pragma unroll
-      for (int u = 0; u < CL; u++) {
-        const float4 v = cr[u];
-        csq[u] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-      }
+      for (int u = 0; u < CI; u++) csq[u] += sq8(cr[u]);
     }
     if (ls == 0 && tid < TC) {
       Ns[lt & 1][tid] = nvalid ? nreg : INFINITY;
@@ -225,27 +296,25 @@ __global__ __launch_bounds__(256, 2) void k_screen(
   };
   auto advance = [&]() {
     if (++ls == nslabs) {
-      // Tile lt fully loaded: its rows' squared norms (8 lanes per row).
+      // Tile lt fully loaded: its rows' squared norms (4 lanes per row).
       if (rt == 0) {
 #pragma unroll
-        for (int u = 0; u < CL; u++) {
+        for (int u = 0; u < CI; u++) {
           float s = csq[u];
           s += __shfl_xor(s, 1, 64);
           s += __shfl_xor(s, 2, 64);
-          s += __shfl_xor(s, 4, 64);
           cmax_bits = max(cmax_bits, __float_as_uint(s));
           csq[u] = 0.f;
         }
       }
       if (part == 0 && lt == t0) {
 #pragma unroll
-        for (int u = 0; u < XL; u++) {
+        for (int u = 0; u < XI; u++) {
           float s = xsq[u];
           s += __shfl_xor(s, 1, 64);
           s += __shfl_xor(s, 2, 64);
-          s += __shfl_xor(s, 4, 64);
-          const int r = row0 + (tid >> 3) + 32 * u;
-          if ((tid & 7) == 0 && r < nrows) xnorm[r] = s;
+          const int r = row0 + r4 + 64 * u;
+          if (q8 == 0 && r < nrows) xnorm[r] = s;
         }
       }
       ls = 0;
@@ -264,36 +333,75 @@ __global__ __launch_bounds__(256, 2) void k_screen(
     const int buf = st & 1;
     const bool more = st + 1 < nsteps;
     if (more) gload();
-    const float* cs = Cs[buf];
-    const float* xs = Xs[buf];
+    if constexpr (BF3) {
+      const char* chs = ch_at(buf);
+      const char* cls = cl_at(buf);
+      const char* xhs = xh_at(buf);
+      const char* xls = xl_at(buf);
 #pragma unroll
-    for (int s4 = 0; s4 < 4; s4++) {
-      const int kk = h * 16 + s4 * 4;
-      float4 a0 = *reinterpret_cast<const float4*>(&cs[(wc * 64 + li) * LDK + kk]);
-      float4 a1 = *reinterpret_cast<const float4*>(&cs[(wc * 64 + 32 + li) * LDK + kk]);
-      float4 b[WN];
+      for (int s2 = 0; s2 < BK / 16; s2++) {
+        const int q = 2 * s2 + h;
+        v8bf ah[2], al[2], bh[WN], bl[WN];
 #pragma unroll
-      for (int y = 0; y < WN; y++)
-        b[y] = *reinterpret_cast<const float4*>(&xs[(wr * 32 * WN + y * 32 + li) * LDK + kk]);
+        for (int a = 0; a < 2; a++) {
+          const int at = chunk_at(wc * 64 + a * 32 + li, q);
+          ah[a] = *reinterpret_cast<const v8bf*>(chs + at);
+          al[a] = *reinterpret_cast<const v8bf*>(cls + at);
+        }
 #pragma unroll
-      for (int y = 0; y < WN; y++) {
-        acc[0][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.x, b[y].x, acc[0][y], 0, 0, 0);
-        acc[1][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.x, b[y].x, acc[1][y], 0, 0, 0);
+        for (int y = 0; y < WN; y++) {
+          const int at = chunk_at(wr * 32 * WN + y * 32 + li, q);
+          bh[y] = *reinterpret_cast<const v8bf*>(xhs + at);
+          bl[y] = *reinterpret_cast<const v8bf*>(xls + at);
+        }
+#pragma unroll
+        for (int y = 0; y < WN; y++)
+#pragma unroll
+          for (int a = 0; a < 2; a++)
+            acc[a][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[a], bh[y], acc[a][y], 0, 0, 0);
+#pragma unroll
+        for (int y = 0; y < WN; y++)
+#pragma unroll
+          for (int a = 0; a < 2; a++)
+            acc[a][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[a], bl[y], acc[a][y], 0, 0, 0);
+#pragma unroll
+        for (int y = 0; y < WN; y++)
+#pragma unroll
+          for (int a = 0; a < 2; a++)
+            acc[a][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[a], bh[y], acc[a][y], 0, 0, 0);
       }
+    } else {
+      const float* cs = cf_at(buf);
+      const float* xs = xf_at(buf);
 #pragma unroll
-      for (int y = 0; y < WN; y++) {
-        acc[0][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.y, b[y].y, acc[0][y], 0, 0, 0);
-        acc[1][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.y, b[y].y, acc[1][y], 0, 0, 0);
-      }
+      for (int s4 = 0; s4 < 4; s4++) {
+        const int kk = h * 16 + s4 * 4;
+        float4 a0 = *reinterpret_cast<const float4*>(&cs[(wc * 64 + li) * LDK + kk]);
+        float4 a1 = *reinterpret_cast<const float4*>(&cs[(wc * 64 + 32 + li) * LDK + kk]);
+        float4 b[WN];
 #pragma unroll
-      for (int y = 0; y < WN; y++) {
-        acc[0][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.z, b[y].z, acc[0][y], 0, 0, 0);
-        acc[1][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.z, b[y].z, acc[1][y], 0, 0, 0);
-      }
+        for (int y = 0; y < WN; y++)
+          b[y] = *reinterpret_cast<const float4*>(&xs[(wr * 32 * WN + y * 32 + li) * LDK + kk]);
 #pragma unroll
-      for (int y = 0; y < WN; y++) {
-        acc[0][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.w, b[y].w, acc[0][y], 0, 0, 0);
-        acc[1][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.w, b[y].w, acc[1][y], 0, 0, 0);
+        for (int y = 0; y < WN; y++) {
+          acc[0][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.x, b[y].x, acc[0][y], 0, 0, 0);
+          acc[1][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.x, b[y].x, acc[1][y], 0, 0, 0);
+        }
+#pragma unroll
+        for (int y = 0; y < WN; y++) {
+          acc[0][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.y, b[y].y, acc[0][y], 0, 0, 0);
+          acc[1][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.y, b[y].y, acc[1][y], 0, 0, 0);
+        }
+#pragma unroll
+        for (int y = 0; y < WN; y++) {
+          acc[0][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.z, b[y].z, acc[0][y], 0, 0, 0);
+          acc[1][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.z, b[y].z, acc[1][y], 0, 0, 0);
+        }
+#pragma unroll
+        for (int y = 0; y < WN; y++) {
+          acc[0][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.w, b[y].w, acc[0][y], 0, 0, 0);
+          acc[1][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.w, b[y].w, acc[1][y], 0, 0, 0);
+        }
       }
     }
     if (cs_ == nslabs - 1) {
@@ -348,7 +456,7 @@ __global__ __launch_bounds__(256, 2) void k_screen(
   }
   // Merge the four partial lists of each row (two lane halves x two waves).
   Cand* M = reinterpret_cast<Cand*>(smem);  // [TR][4][L]
-  static_assert(TR * 4 * L * 8 <= (int)(sizeof(float) * 2 * (TR + TC) * LDK), "merge space");
+  static_assert(TR * 4 * L * 8 <= 2 * BUF, "merge space");
   __syncthreads();
   if (tid == 0) {
     atomicMax(&small[SW_CMAX2], max(max(red[0], red[1]), max(red[2], red[3])));
@@ -388,20 +496,34 @@ int choose_parts(int row_tiles, int ntiles, int cus) {
   return std::max(1, std::min(std::min(want, ntiles), MAX_PARTS));
 }
 
+template <int WN, int L, bool L2, bool KNN, bool BF3>
+void launch_screen_as(emh_ctx* c, unsigned blocks, const float* x, size_t nx, size_t d,
+                      const uint32_t* ids, size_t lo, size_t n, const float* cents,
+                      const float* cnorm, size_t k, int tpp, int parts, int ntiles, Cand* cand,
+                      float* xnorm) {
+  if (d % 4 == 0)
+    hipLaunchKernelGGL((k_screen<WN, L, L2, KNN, true, BF3>), dim3(blocks), dim3(256), 0,
+                       c->stream, x, nx, (int)d, ids, lo, (int)n, cents, cnorm, (int)k, tpp, parts,
+                       ntiles, cand, c->small, xnorm);
+  else
+    hipLaunchKernelGGL((k_screen<WN, L, L2, KNN, false, BF3>), dim3(blocks), dim3(256), 0,
+                       c->stream, x, nx, (int)d, ids, lo, (int)n, cents, cnorm, (int)k, tpp, parts,
+                       ntiles, cand, c->small, xnorm);
+  EMH_HIP(hipGetLastError());
+}
+
+// The screen's arithmetic follows the context's mode (SCREEN_BF3 or SCREEN_F32).
 template <int WN, int L, bool L2, bool KNN>
 void launch_screen(emh_ctx* c, unsigned blocks, const float* x, size_t nx, size_t d,
                    const uint32_t* ids, size_t lo, size_t n, const float* cents,
                    const float* cnorm, size_t k, int tpp, int parts, int ntiles, Cand* cand,
                    float* xnorm) {
-  if (d % 4 == 0)
-    hipLaunchKernelGGL((k_screen<WN, L, L2, KNN, true>), dim3(blocks), dim3(256), 0, c->stream,
-                       x, nx, (int)d, ids, lo, (int)n, cents, cnorm, (int)k, tpp, parts, ntiles,
-                       cand, c->small, xnorm);
+  if (c->screen == SCREEN_F32)
+    launch_screen_as<WN, L, L2, KNN, false>(c, blocks, x, nx, d, ids, lo, n, cents, cnorm, k, tpp,
+                                            parts, ntiles, cand, xnorm);
   else
-    hipLaunchKernelGGL((k_screen<WN, L, L2, KNN, false>), dim3(blocks), dim3(256), 0, c->stream,
-                       x, nx, (int)d, ids, lo, (int)n, cents, cnorm, (int)k, tpp, parts, ntiles,
-                       cand, c->small, xnorm);
-  EMH_HIP(hipGetLastError());
+    launch_screen_as<WN, L, L2, KNN, true>(c, blocks, x, nx, d, ids, lo, n, cents, cnorm, k, tpp,
+                                           parts, ntiles, cand, xnorm);
 }
 
 }  // namespace

@@ -241,8 +241,10 @@ float emh_host_numpy_sum_f32(const float* a, uint64_t n);
 /* Rows the exact top-1 / top-k kernels rescanned since the context was made
  * (the screen's misses; EMEANS_CUDA_SCREEN_STATS analogue, emeans-cuda lib.rs:278-287). */
 uint64_t emh_fallback_rows(emh_ctx* ctx);
-/* Select the top-1 path: 1 = MFMA screen + exact check (default), 0 = exact
- * kernel only (the reference "FP32 kernel alone", emeans-cuda tests/contract.rs:27-37). */
+/* Select the top-1 / top-k path: 1 = MFMA screen in bf16 three-pass arithmetic
+ * + exact check (default), 2 = MFMA screen in f32 arithmetic + exact check,
+ * 0 = exact kernels only (the reference "FP32 kernel alone", emeans-cuda
+ * tests/contract.rs:27-37). Results are the same bits in every mode. */
 int emh_set_screen(emh_ctx* ctx, int on);
 /* Time every launch of the MFMA screen kernel (top-1 and top-k) with HIP events
  * on the context's stream while on; emh_profile_read waits, sums and resets:

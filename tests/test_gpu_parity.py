@@ -23,6 +23,14 @@ def dev():
     d.close()
 
 
+@pytest.fixture(params=[1, 2], ids=["bf16x3", "f32"])
+def screen(request, dev):
+    """The MFMA screen's arithmetic: bf16 three-pass (default) or f32."""
+    dev.set_screen(request.param)
+    yield request.param
+    dev.set_screen(1)
+
+
 def _mix(n, d, centers, sigma, unit, seed):
     return O.contract_mixture(n, d, centers, sigma, unit, seed).reshape(n, d)
 
@@ -69,7 +77,7 @@ CONTRACT_SHAPES = [(1000, 768, 64), (777, 768, 100), (513, 13, 70), (2000, 20, 3
 
 @pytest.mark.parametrize("n,d,k", CONTRACT_SHAPES)
 @pytest.mark.parametrize("metric", ["ip", "l2"])
-def test_top1_contract_shapes(dev, n, d, k, metric):
+def test_top1_contract_shapes(dev, screen, n, d, k, metric):
     x = _mix(n, d, 11, 0.6, metric == "ip", 3 * n + k)
     c = (np.resize(x[: min(k, n)].reshape(-1), k * d) * np.float32(0.95)).reshape(k, d)
     _check_top1(dev, x, c, metric, f"n={n} d={d} k={k} {metric}")
@@ -77,7 +85,7 @@ def test_top1_contract_shapes(dev, n, d, k, metric):
 
 @pytest.mark.parametrize("k", [1024, 1000])
 @pytest.mark.parametrize("metric", ["ip", "l2"])
-def test_top1_production_shape_with_duplicates(dev, k, metric):
+def test_top1_production_shape_with_duplicates(dev, screen, k, metric):
     """contract.rs:120-146: 16,384 x 768; the last 256 centroids copy earlier ones."""
     n, d = 16384, 768
     x = _mix(n, d, 64, 0.6, metric == "ip", 5 * n + k)
@@ -129,15 +137,14 @@ def test_screen_bit_equal_on_near_ties(dev, n, d, k, metric):
     x = (rows * scale[:, None]).astype(np.float32)
     perm = ((np.arange(n, dtype=np.uint64) * 7919 + 5) % n).astype(np.uint32)
     outs = []
-    for screen in (True, False):
-        dev.set_screen(screen)
+    for mode in (1, 2, 0):  # bf16 screen, f32 screen, exact kernel alone
+        dev.set_screen(mode)
         outs.append(_gpu_top1(dev, x, c, metric, ids=perm))
-    dev.set_screen(True)
-    assert np.array_equal(outs[0][0], outs[1][0]), "screen vs exact kernel labels"
-    assert outs[0][1].tobytes() == outs[1][1].tobytes(), "screen vs exact kernel scores"
+    dev.set_screen(1)
     ol, osc = O.top1(x, d, c, metric, ids=perm)
-    assert np.array_equal(outs[0][0], ol)
-    assert outs[0][1].tobytes() == osc.tobytes()
+    for mode, (gl, gs) in zip((1, 2, 0), outs):
+        assert np.array_equal(gl, ol), f"mode {mode} labels"
+        assert gs.tobytes() == osc.tobytes(), f"mode {mode} scores"
 
 
 @pytest.mark.parametrize("layout", ["spread", "together"])
@@ -177,7 +184,7 @@ def test_check_several_candidates_per_row(dev, metric, layout):
     assert np.array_equal(gl, el) and gs.tobytes() == es.tobytes()
 
 
-def test_screen_fallback_is_rare_on_separated_data(dev):
+def test_screen_fallback_is_rare_on_separated_data(dev, screen):
     """On data without near-ties the exact kernel rescans few rows."""
     n, d, k = 16384, 768, 1024
     x = _mix(n, d, 64, 0.6, False, 99)
@@ -188,6 +195,31 @@ def test_screen_fallback_is_rare_on_separated_data(dev):
     ol, osc = O.top1(x, d, c, "l2")
     assert np.array_equal(gl, ol) and gs.tobytes() == osc.tobytes()
     assert rescanned <= n // 20, rescanned
+
+
+@pytest.mark.parametrize("metric", ["ip", "l2"])
+def test_screen_extreme_scales(dev, screen, metric):
+    """Rows and centroids far from unit scale: rows whose bf16 halves fall in
+    the subnormal range (1e-40 .. 1e-36) against centroids up to 1e34 (IP), a
+    row near FLT_MAX whose bf16 half rounds to infinity, and, for L2, scales
+    whose squared norms stay finite. Every row bit-equal to the oracle."""
+    n, d, k = 1024, 768, 256
+    base = _mix(n, d, 16, 0.2, True, 31)
+    cb = _mix(k, d, 16, 0.2, True, 32)
+    if metric == "ip":
+        xs = np.array([1e-40, 1e-38, 1e-36, 1e-20, 1.0, 1e30], np.float64)
+        cs = np.array([1e30, 1e34, 1e-38, 1.0], np.float64)
+    else:
+        xs = np.array([1e-30, 1e-18, 1.0, 1e15], np.float64)
+        cs = np.array([1e-18, 1.0, 1e15], np.float64)
+    x = (base * xs[np.arange(n) % len(xs)][:, None]).astype(np.float32)
+    c = (cb * cs[np.arange(k) % len(cs)][:, None]).astype(np.float32)
+    if metric == "ip":
+        x[5, 0] = np.float32(3.4e38)  # bf16(3.4e38) = inf
+    gl, gs = _gpu_top1(dev, x, c, metric)
+    ol, osc = O.top1(x, d, c, metric)
+    assert np.array_equal(gl, ol)
+    assert gs.tobytes() == osc.tobytes()
 
 
 @pytest.mark.parametrize("n,d,k", CONTRACT_SHAPES)
@@ -303,7 +335,7 @@ def test_split_zero_row_nudge_and_sequential_plan(dev):
 
 
 @pytest.mark.parametrize("m,n,d,kk", [(300, 300, 768, 16), (200, 900, 20, 5), (130, 7, 33, 10)])
-def test_topk_contract_shapes(dev, m, n, d, kk):
+def test_topk_contract_shapes(dev, screen, m, n, d, kk):
     """contract.rs:103-110 shapes: ids and sims bit-equal to the oracle (fma-chain dots)."""
     data = _mix(n, d, 9, 0.3, True, m + n)
     q = _mix(m, d, 9, 0.3, True, m * 7 + n)
@@ -316,7 +348,7 @@ def test_topk_contract_shapes(dev, m, n, d, kk):
         assert np.array_equal(gi, oi) and gs.tobytes() == osims.tobytes()
 
 
-def test_topk_production_duplicates(dev):
+def test_topk_production_duplicates(dev, screen):
     """contract.rs:147-159: 64 queries vs 16,384 rows with 512 duplicated rows, k = 16."""
     n, d = 16384, 768
     data = _mix(n, d, 9, 0.3, True, 77)
