@@ -74,10 +74,13 @@ __device__ __forceinline__ float4 mask4(float4 v, int col, int d) {
 }
 
 // Byte offset of 16-byte chunk q (dimensions 8q..8q+7 of the slab) of LDS row r:
-// rows of RB bytes, chunks XOR-swizzled by row so that the eight lanes of a
-// b128 access (eight consecutive rows, one chunk) hit eight different bank
-// groups, and a thread's four-row store quad too.
-__device__ __forceinline__ int chunk_at(int r, int q) { return r * RB + ((q ^ ((r >> 1) & 3)) << 4); }
+// rows of RB bytes, chunks XOR-swizzled by row so that the sixteen lanes of a
+// b128 access served together (sixteen consecutive rows, one chunk) hit
+// sixteen different 16-byte bank groups of the 64-bank LDS, and eight too
+// for eight lanes; a thread quad's store (one row, four chunks) likewise.
+__device__ __forceinline__ int chunk_at(int r, int q) {
+  return r * RB + ((q ^ ((r >> 1) & 3) ^ ((r >> 3) & 1)) << 4);
+}
 
 // x ~ hi + lo with hi = bf16(x) and lo = bf16(x - hi), both rounded to nearest
 // even (x - hi is exact in f32): |x - hi - lo| <= 2^-16 |x| for normal values,
