@@ -492,10 +492,306 @@ __global__ __launch_bounds__(256, 2) void k_screen(
   }
 }
 
-int choose_parts(int row_tiles, int ntiles, int cus) {
-  // Enough blocks for two per CU (both resident at once), never more parts
+// ------------------------------------------------- screen, large tiles
+// The bf16 three-pass screen for top-1 when d % 4 == 0, on bigger tiles: with
+// 64 x 64 per wave the slab stores and operand reads need ~0.9 KB of LDS
+// traffic per MFMA, about what the LDS can serve while the MFMA pipe runs, so
+// the pipe idled. Here a block is 8 waves (512 threads, one block per CU, two
+// waves per SIMD) over TR3 = 256 rows x TC3 = 256 centroids per tile; wave w
+// owns rows 64 (w & 3) .. + 64 (two 32-row B blocks) and centroids
+// 128 (w >> 2) .. + 128 (four 32-centroid A blocks): 24 MFMAs per 12 b128
+// operand reads per k-step, a third fewer LDS bytes per MFMA. The 128
+// accumulator registers per lane sit in AGPRs. Staging, split, bound inputs,
+// epilogue and merge are those of k_screen (one chunk quad per row per slab,
+// 4 threads per row, two rows per thread for each operand).
+constexpr int TR3 = 256, TC3 = 256;
+
+template <int L, bool L2>
+__global__ __launch_bounds__(512, 1) void k_screen3(
+    const float* __restrict__ x, size_t nx, int d, const uint32_t* __restrict__ ids, size_t lo,
+    int nrows, const float* __restrict__ cents, const float* __restrict__ cnorm, int k,
+    int tiles_per_part, int parts, int ntiles, Cand* __restrict__ cand,
+    uint32_t* __restrict__ small, float* __restrict__ xnorm) {
+  constexpr int WA = 4, WN = 2;       // A (centroid) and B (row) 32-blocks per wave
+  constexpr int BUF = 2 * (TR3 + TC3) * RB;  // xh, xl, ch, cl of one slab: 64 KB
+  __shared__ __attribute__((aligned(16))) char smem[2 * BUF];
+  __shared__ float Ns[2][TC3];
+  auto xh_at = [&](int buf) { return smem + buf * BUF; };
+  auto xl_at = [&](int buf) { return smem + buf * BUF + TR3 * RB; };
+  auto ch_at = [&](int buf) { return smem + buf * BUF + 2 * TR3 * RB; };
+  auto cl_at = [&](int buf) { return smem + buf * BUF + 2 * TR3 * RB + TC3 * RB; };
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int wr = w & 3, wc = w >> 2;
+  const int li = lane & 31, h = lane >> 5;
+  const uint32_t wi = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int rt = (int)(wi / (uint32_t)parts), part = (int)(wi % (uint32_t)parts);
+  const int t0 = part * tiles_per_part;
+  const int t1 = min(ntiles, t0 + tiles_per_part);
+  if (t0 >= t1) return;
+  const int row0 = rt * TR3;
+
+  // Staging: thread tid takes chunk q8 = tid & 3 of rows r4 + 128u (u < 2) of
+  // both operands. Rows past the selection (or with a bad id) read data row 0;
+  // their lists are never written.
+  const int q8 = tid & 3, r4 = tid >> 2;
+  const float* xp[2];
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    int r = row0 + r4 + 128 * u;
+    size_t xid = 0;
+    if (r < nrows) {
+      size_t p = lo + (size_t)r;
+      xid = ids ? (size_t)ids[p] : p;
+      if (xid >= nx) xid = 0;
+    }
+    xp[u] = x + xid * (size_t)d;
+  }
+
+  float lkey[WN][L];
+  uint32_t lid[WN][L];
+#pragma unroll
+  for (int y = 0; y < WN; y++)
+#pragma unroll
+    for (int e = 0; e < L; e++) {
+      lkey[y][e] = INFINITY;
+      lid[y][e] = NONE;
+    }
+
+  v16f acc[WA][WN];
+#pragma unroll
+  for (int a = 0; a < WA; a++)
+#pragma unroll
+    for (int y = 0; y < WN; y++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[a][y][r] = 0.f;
+
+  const int nslabs = (d + BK - 1) / BK;
+  const int nsteps = (t1 - t0) * nslabs;
+  float4 xr[2][2], cr[2][2];
+  float nreg = 0.f;
+  bool nvalid = false;
+  int lt = t0, ls = 0;  // load cursor, one step ahead of the compute cursor
+  const float* cp[2];
+  auto set_tile = [&](int tile) {
+#pragma unroll
+    for (int u = 0; u < 2; u++) cp[u] = cents + (size_t)min(tile * TC3 + r4 + 128 * u, k - 1) * d;
+  };
+  float csq[2] = {0.f, 0.f}, xsq[2] = {0.f, 0.f};
+  uint32_t cmax_bits = 0, cnmax_bits = 0;
+  auto gload = [&]() {
+    const int col = ls * BK + 8 * q8;
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      xr[u][0] = load4<true>(xp[u], col, d);
+      xr[u][1] = load4<true>(xp[u], col + 4, d);
+      cr[u][0] = load4<true>(cp[u], col, d);
+      cr[u][1] = load4<true>(cp[u], col + 4, d);
+    }
+    if (ls == 0 && tid < TC3) {
+      int j = lt * TC3 + tid;
+      nvalid = j < k;
+      nreg = L2 ? cnorm[min(j, k - 1)] : 0.f;
+    }
+  };
+  auto sq8 = [](const float4 (&v)[2]) {
+    return v[0].x * v[0].x + v[0].y * v[0].y + v[0].z * v[0].z + v[0].w * v[0].w +
+           v[1].x * v[1].x + v[1].y * v[1].y + v[1].z * v[1].z + v[1].w * v[1].w;
+  };
+  auto lstore = [&](int buf) {
+    const int col = ls * BK + 8 * q8;
+    if (ls == nslabs - 1 && d % BK != 0) {
+#pragma unroll
+      for (int u = 0; u < 2; u++) {
+        xr[u][0] = mask4(xr[u][0], col, d);
+        xr[u][1] = mask4(xr[u][1], col + 4, d);
+        cr[u][0] = mask4(cr[u][0], col, d);
+        cr[u][1] = mask4(cr[u][1], col + 4, d);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      const int at = chunk_at(r4 + 128 * u, q8);
+      v8bf hi, lo8;
+      split8(xr[u][0], xr[u][1], hi, lo8);
+      *reinterpret_cast<v8bf*>(xh_at(buf) + at) = hi;
+      *reinterpret_cast<v8bf*>(xl_at(buf) + at) = lo8;
+      split8(cr[u][0], cr[u][1], hi, lo8);
+      *reinterpret_cast<v8bf*>(ch_at(buf) + at) = hi;
+      *reinterpret_cast<v8bf*>(cl_at(buf) + at) = lo8;
+    }
+    if (part == 0 && lt == t0) {
+#pragma unroll
+      for (int u = 0; u < 2; u++) xsq[u] += sq8(xr[u]);
+    }
+    if (rt == 0) {
+#pragma unroll
+      for (int u = 0; u < 2; u++) csq[u] += sq8(cr[u]);
+    }
+    if (ls == 0 && tid < TC3) {
+      Ns[lt & 1][tid] = nvalid ? nreg : INFINITY;
+      if (L2 && nvalid) cnmax_bits = max(cnmax_bits, __float_as_uint(nreg));
+    }
+  };
+  auto advance = [&]() {
+    if (++ls == nslabs) {
+      if (rt == 0) {
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+          float s = csq[u];
+          s += __shfl_xor(s, 1, 64);
+          s += __shfl_xor(s, 2, 64);
+          cmax_bits = max(cmax_bits, __float_as_uint(s));
+          csq[u] = 0.f;
+        }
+      }
+      if (part == 0 && lt == t0) {
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+          float s = xsq[u];
+          s += __shfl_xor(s, 1, 64);
+          s += __shfl_xor(s, 2, 64);
+          const int r = row0 + r4 + 128 * u;
+          if (q8 == 0 && r < nrows) xnorm[r] = s;
+        }
+      }
+      ls = 0;
+      ++lt;
+      if (lt < t1) set_tile(lt);
+    }
+  };
+
+  set_tile(lt);
+  gload();
+  lstore(0);
+  advance();
+  __syncthreads();
+  int ct = t0, cs_ = 0;
+  for (int st = 0; st < nsteps; st++) {
+    const int buf = st & 1;
+    const bool more = st + 1 < nsteps;
+    if (more) gload();
+    const char* chs = ch_at(buf);
+    const char* cls = cl_at(buf);
+    const char* xhs = xh_at(buf);
+    const char* xls = xl_at(buf);
+#pragma unroll
+    for (int s2 = 0; s2 < BK / 16; s2++) {
+      const int q = 2 * s2 + h;
+      v8bf bh[WN], bl[WN];
+#pragma unroll
+      for (int y = 0; y < WN; y++) {
+        const int at = chunk_at(wr * 64 + y * 32 + li, q);
+        bh[y] = *reinterpret_cast<const v8bf*>(xhs + at);
+        bl[y] = *reinterpret_cast<const v8bf*>(xls + at);
+      }
+#pragma unroll
+      for (int a = 0; a < WA; a++) {
+        const int at = chunk_at(wc * 128 + a * 32 + li, q);
+        const v8bf ah = *reinterpret_cast<const v8bf*>(chs + at);
+        const v8bf al = *reinterpret_cast<const v8bf*>(cls + at);
+#pragma unroll
+        for (int y = 0; y < WN; y++)
+          acc[a][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh[y], acc[a][y], 0, 0, 0);
+#pragma unroll
+        for (int y = 0; y < WN; y++)
+          acc[a][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl[y], acc[a][y], 0, 0, 0);
+#pragma unroll
+        for (int y = 0; y < WN; y++)
+          acc[a][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh[y], acc[a][y], 0, 0, 0);
+      }
+    }
+    if (cs_ == nslabs - 1) {
+      // Tile done: fold its keys into the per-row lists.
+      const int tile = ct;
+      const float* ns = Ns[tile & 1];
+#pragma unroll
+      for (int a = 0; a < WA; a++) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          // 32x32 accumulator layout: element (m, n) with n = lane % 32,
+          // m = 8 (r / 4) + 4 (lane / 32) + r % 4.
+          const int ci = wc * 128 + a * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          const uint32_t gj = (uint32_t)(tile * TC3 + ci);
+          const float nn = ns[ci];
+#pragma unroll
+          for (int y = 0; y < WN; y++) {
+            float v = acc[a][y][r];
+            float key = L2 ? fmaf(-2.0f, v, nn) : nn - v;  // one rounding: within E
+            if (__ballot(key < lkey[y][L - 1]) != 0ull) insert_nb<L>(lkey[y], lid[y], key, gj);
+            acc[a][y][r] = 0.f;
+          }
+        }
+      }
+    }
+    if (++cs_ == nslabs) {
+      cs_ = 0;
+      ++ct;
+    }
+    if (more) {
+      lstore(buf ^ 1);
+      advance();
+    }
+    __syncthreads();
+  }
+
+  // Bound inputs: one atomic per block.
+  __shared__ uint32_t red[16];
+  {
+    uint32_t a = cmax_bits, b = cnmax_bits;
+    for (int o = 32; o > 0; o >>= 1) {
+      a = max(a, (uint32_t)__shfl_xor((int)a, o, 64));
+      b = max(b, (uint32_t)__shfl_xor((int)b, o, 64));
+    }
+    if (lane == 0) {
+      red[w] = a;
+      red[8 + w] = b;
+    }
+  }
+  // Merge the four partial lists of each row (two lane halves x two centroid waves).
+  Cand* M = reinterpret_cast<Cand*>(smem);  // [TR3][4][L]
+  static_assert(TR3 * 4 * L * 8 <= 2 * BUF, "merge space");
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t a = 0, b = 0;
+    for (int i = 0; i < 8; i++) {
+      a = max(a, red[i]);
+      b = max(b, red[8 + i]);
+    }
+    atomicMax(&small[SW_CMAX2], a);
+    if (L2) atomicMax(&small[SW_CNMAX], b);
+  }
+#pragma unroll
+  for (int y = 0; y < WN; y++) {
+    const int row = wr * 64 + y * 32 + li;
+    const int contrib = wc * 2 + h;
+#pragma unroll
+    for (int e = 0; e < L; e++) M[(row * 4 + contrib) * L + e] = Cand{lkey[y][e], lid[y][e]};
+  }
+  __syncthreads();
+  for (int row = tid; row < TR3; row += 512) {
+    if (row0 + row >= nrows) continue;
+    float mk[L];
+    uint32_t mi[L];
+#pragma unroll
+    for (int e = 0; e < L; e++) {
+      mk[e] = INFINITY;
+      mi[e] = NONE;
+    }
+    for (int q = 0; q < 4 * L; q++) {
+      Cand cq = M[row * 4 * L + q];
+      if (cq.id != NONE) insert<L>(mk, mi, cq.key, cq.id);
+    }
+    Cand* out = cand + ((size_t)(row0 + row) * parts + part) * L;  // [row][part][L]
+#pragma unroll
+    for (int e = 0; e < L; e++) out[e] = Cand{mk[e], mi[e]};
+  }
+}
+
+int choose_parts(int row_tiles, int ntiles, int cus, int per_cu = 2) {
+  // Enough blocks for per_cu per CU (all resident at once), never more parts
   // than tiles, and at most MAX_PARTS lists per row for the verify to merge.
-  int want = (2 * cus + row_tiles - 1) / row_tiles;
+  int want = (per_cu * cus + row_tiles - 1) / row_tiles;
   return std::max(1, std::min(std::min(want, ntiles), MAX_PARTS));
 }
 
@@ -543,10 +839,12 @@ void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t
     launch_exact1(c, x, nx, d, ids, lo, n, nullptr, cents, cnorm, k, ip, labels, scores);
     return;
   }
-  const int TR = 128;
+  // The large-tile bf16 screen (one 512-thread block per CU) when d % 4 == 0.
+  const bool big = c->screen != SCREEN_F32 && d % 4 == 0;
+  const int TR = big ? TR3 : 128;
   const int row_tiles = (int)((n + TR - 1) / TR);
-  const int ntiles = (int)((k + TC - 1) / TC);
-  int parts = choose_parts(row_tiles, ntiles, c->cus);
+  const int ntiles = (int)((k + (big ? TC3 : TC) - 1) / (big ? TC3 : TC));
+  int parts = choose_parts(row_tiles, ntiles, c->cus, big ? 1 : 2);
   const int tpp = (ntiles + parts - 1) / parts;
   parts = (ntiles + tpp - 1) / tpp;
   Cand* cand = (Cand*)c->cand.get((size_t)parts * n * L1 * sizeof(Cand));
@@ -557,12 +855,21 @@ void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t
   const unsigned blocks = (unsigned)(row_tiles * parts);
   {
     ProfScope prof(c, 2.0 * (double)n * (double)k * (double)d);
-    if (ip)
+    if (big && ip)
+      hipLaunchKernelGGL((k_screen3<L1, false>), dim3(blocks), dim3(512), 0, c->stream, x, nx,
+                         (int)d, ids, lo, (int)n, cents, cnorm, (int)k, tpp, parts, ntiles, cand,
+                         c->small, xnorm);
+    else if (big)
+      hipLaunchKernelGGL((k_screen3<L1, true>), dim3(blocks), dim3(512), 0, c->stream, x, nx,
+                         (int)d, ids, lo, (int)n, cents, cnorm, (int)k, tpp, parts, ntiles, cand,
+                         c->small, xnorm);
+    else if (ip)
       launch_screen<2, L1, false, false>(c, blocks, x, nx, d, ids, lo, n, cents, cnorm, k, tpp,
                                          parts, ntiles, cand, xnorm);
     else
       launch_screen<2, L1, true, false>(c, blocks, x, nx, d, ids, lo, n, cents, cnorm, k, tpp,
                                         parts, ntiles, cand, xnorm);
+    if (big) EMH_HIP(hipGetLastError());
   }
   launch_verify1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, cand, parts, xnorm, labels, scores,
                  fb);

@@ -149,17 +149,17 @@ def test_screen_bit_equal_on_near_ties(dev, n, d, k, metric):
 
 @pytest.mark.parametrize("layout", ["spread", "together"])
 @pytest.mark.parametrize("metric", ["ip", "l2"])
-def test_check_several_candidates_per_row(dev, metric, layout):
-    """Centroids in groups of six within a relative 1e-7 of each other, rows near
-    the groups: every row keeps six candidates inside the screen bound.
-    spread: a group's members sit 32 ids apart, so no centroid part (128 ids)
-    holds more of them than its list keeps; each 32-row block of the check then
-    holds 192 (row, candidate) pairs and takes several passes over its staged
-    chunks, and the check settles the rows. together: a group's members are
-    consecutive, one part holds all six, its list overflows and the rows go to
-    the exact scan. Labels and scores bit-equal to the oracle, and to the exact
+def test_check_several_candidates_per_row(dev, screen, metric, layout):
+    """Centroids in groups within a relative 1e-7 of each other, rows near the
+    groups: every row keeps all of its group's members inside the screen bound.
+    spread: groups of four, fewer than a part's list keeps, so each 32-row block
+    of the check holds 128 (row, candidate) pairs and takes several passes over
+    its staged chunks, and the check settles the rows. together: groups of six
+    consecutive ids in one part, whose list overflows, so the rows go to the
+    exact scan. Labels and scores bit-equal to the oracle, and to the exact
     kernel, either way."""
-    n, d, k, g = 2048, 256, 192, 6
+    n, d, k = 2048, 256, 192
+    g = 4 if layout == "spread" else 6
     groups = k // g
     bases = _mix(groups, d, groups, 0.0, True, 7)
     t = np.arange(d)
@@ -178,9 +178,9 @@ def test_check_several_candidates_per_row(dev, metric, layout):
         assert rescanned < n // 10, rescanned  # the check settled them, not the exact scan
     else:
         assert rescanned > n // 2, rescanned  # a full list that cannot certify its part
-    dev.set_screen(False)
+    dev.set_screen(0)
     el, es = _gpu_top1(dev, x, c, metric, ids=perm)
-    dev.set_screen(True)
+    dev.set_screen(screen)
     assert np.array_equal(gl, el) and gs.tobytes() == es.tobytes()
 
 
