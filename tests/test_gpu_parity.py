@@ -184,6 +184,29 @@ def test_check_several_candidates_per_row(dev, screen, metric, layout):
     assert np.array_equal(gl, el) and gs.tobytes() == es.tobytes()
 
 
+@pytest.mark.parametrize("d", [1000, 100])
+@pytest.mark.parametrize("metric", ["ip", "l2"])
+def test_queued_rows_across_phases(dev, metric, d):
+    """Groups of six near-identical consecutive centroids overflow their part's
+    list, so every row is queued for the exact scan: d = 1000 takes the scan's
+    copies in two phases (768 + 232 dimensions), d = 100 in one partial phase,
+    and k = 200 leaves the last 16-centroid item part-empty. Bit-equal to the
+    oracle."""
+    n, k, g = 700, 200, 6
+    groups = (k + g - 1) // g
+    bases = _mix(groups, d, groups, 0.0, True, 17)
+    t = np.arange(d)
+    c = np.stack([(bases[j // g].astype(np.float64) * (1.0 + 1e-7 * _noise(j * d + t)))
+                  .astype(np.float32) for j in range(k)])
+    x = _mix(n, d, groups, 0.05, True, 17)
+    before = dev.fallback_rows()
+    gl, gs = _gpu_top1(dev, x, c, metric)
+    assert dev.fallback_rows() - before > n // 2
+    ol, osc = O.top1(x, d, c, metric)
+    assert np.array_equal(gl, ol)
+    assert gs.tobytes() == osc.tobytes()
+
+
 def test_screen_fallback_is_rare_on_separated_data(dev, screen):
     """On data without near-ties the exact kernel rescans few rows."""
     n, d, k = 16384, 768, 1024
