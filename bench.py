@@ -42,7 +42,7 @@ METRIC = "train s & assign Mrows/s at 200k×768 k=1024 FP32; % of FP32 MFMA peak
 # FETCH_SIZE + WRITE_SIZE from two rocprofv3 --pmc passes of this script, with
 # a plain copy kernel of known size as the scale;
 # profiles/k_screen_train_assign_200kx768_k1024_hbm_traffic.md).
-SCREEN_TRAFFIC_BYTES = 187.4e6
+SCREEN_TRAFFIC_BYTES = 108.4e6
 
 
 def log(*a):
