@@ -14,8 +14,8 @@ reports train seconds, assignment Mrows/s, the MFMA screen kernel's roofline
 and the CPU baseline. The screen (the dense x.C^T contraction ahead of the
 exact f32 check) runs on the bf16 MFMA in three passes (x.c ~ xh.ch + xh.cl +
 xl.ch); its roofline is the bf16 MFMA work it issues (3 x 2 rows k d FLOP per
-launch over its HIP-event-timed duration) against the 2.5 PFLOP/s dense bf16
-peak, with the f32-equivalent rate (2 rows k d FLOP per launch) against the
+launch over the HIP-event-timed duration of every 8th launch in the timed
+steps) against the 2.5 PFLOP/s dense bf16 peak, with the f32-equivalent rate (2 rows k d FLOP per launch) against the
 157.3 TFLOP/s dense f32 MFMA peak beside it. `f32_screen` repeats the step
 with the screen on v_mfma_f32_32x32x2_f32 (same bits, checked). The CPU
 baseline is the oracle's C++ restatement of the reference CPU backend
@@ -43,6 +43,10 @@ METRIC = "train s & assign Mrows/s at 200k×768 k=1024 FP32; % of FP32 MFMA peak
 # a plain copy kernel of known size as the scale;
 # profiles/k_screen_train_assign_200kx768_k1024_hbm_traffic.md).
 SCREEN_TRAFFIC_BYTES = 108.4e6
+# The screen's roofline times every PROFILE_EVERY-th launch of the timed steps
+# with HIP events (an event pair between two kernels costs the stream a few
+# microseconds; on every launch that was ~5 % of the headline step).
+PROFILE_EVERY = 8
 
 
 def log(*a):
@@ -94,7 +98,7 @@ def headline(args):
             log(f"warmup {i} (screen {mode}): train {tr * 1e3:.1f} ms, assign {asg * 1e3:.1f} ms, "
                 f"fallback rows {info['fallback_rows']}")
         dev.sync()
-        dev.profile(True)
+        dev.profile(PROFILE_EVERY)
         trains, assigns = [], []
         t0 = time.perf_counter()
         for i in range(steps):

@@ -260,9 +260,10 @@ class HipDevice:
                 "labels": labels}
         return cent, info
 
-    def profile(self, on: bool):
-        """Time each MFMA screen launch with HIP events on the context's stream."""
-        check(lib().emh_profile(self._ctx, int(on)))
+    def profile(self, every):
+        """Time every `every`-th MFMA screen launch with HIP events on the
+        context's stream (0 or False: off; 1 or True: every launch)."""
+        check(lib().emh_profile(self._ctx, int(every)))
 
     def profile_read(self):
         """(total ms, launches, algorithmic FLOP) of the timed screen launches; resets."""

@@ -486,7 +486,9 @@ int emh_set_screen(emh_ctx* c, int on) {
 int emh_profile(emh_ctx* c, int on) {
   return guard([&] {
     EMH_ENSURE(c, "null context");
-    c->prof = on != 0;
+    EMH_ENSURE(on >= 0, "profile period %d must be >= 0", on);
+    c->prof = on;
+    c->prof_count = 0;
   });
 }
 

@@ -148,7 +148,8 @@ struct emh_ctx {
   hipEvent_t ev_stage[3] = {nullptr, nullptr, nullptr};
   std::string name = "hip-gfx950";
   // Screen-kernel timing (emh_profile): event pairs and the FLOP each covers.
-  bool prof = false;
+  int prof = 0;             // time every prof-th screen launch (0: off)
+  uint64_t prof_count = 0;  // screen launches since profiling was switched on
   struct Timed {
     hipEvent_t a, b;
     double flop;
@@ -176,7 +177,7 @@ struct ProfScope {
   hipEvent_t a = nullptr, b = nullptr;
   double flop;
   ProfScope(emh_ctx* ctx, double f) : c(ctx), flop(f) {
-    if (!c->prof) return;
+    if (!c->prof || c->prof_count++ % (uint64_t)c->prof != 0) return;
     a = c->pool_event();
     b = c->pool_event();
     EMH_HIP(hipEventRecord(a, c->stream));

@@ -355,6 +355,15 @@ static_assert(CSLOT * CDC4 % 128 == 0, "chunk split");
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
+// f(integral_constant<0>) ... f(integral_constant<N - 1>), in order.
+template <int N, typename F>
+__device__ __forceinline__ void unroll_steps(F&& f) {
+  if constexpr (N > 0) {
+    unroll_steps<N - 1>(f);
+    f(std::integral_constant<int, N - 1>{});
+  }
+}
+
 __global__ __launch_bounds__(256) void k_check1(
     const float* __restrict__ x, size_t nx, int d, const uint32_t* __restrict__ ids, size_t lo,
     int nrows, const float* __restrict__ cents, const float* __restrict__ cnorm, int ip,
@@ -523,10 +532,8 @@ __global__ __launch_bounds__(256) void k_check1(
         for (int q = 0; q < CNQ; q++) rb[s][q] = src[q][min(cn2 * CDC4 + col[q], d4 - 1)];
         __syncthreads();
       };
-      for (int c0 = 0; c0 < nch; c0 += CNR) {
-        step(std::integral_constant<int, 0>{}, c0);
-        step(std::integral_constant<int, 1>{}, c0);
-      }
+      for (int c0 = 0; c0 < nch; c0 += CNR)
+        unroll_steps<CNR>([&](auto U) __attribute__((always_inline)) { step(U, c0); });
     } else {
       const int xs = dl ? (int)prow[pb + lane] : (nl ? lane : 0);
       const int cs = CR + (dl ? lane : 0);

@@ -246,9 +246,11 @@ uint64_t emh_fallback_rows(emh_ctx* ctx);
  * 0 = exact kernels only (the reference "FP32 kernel alone", emeans-cuda
  * tests/contract.rs:27-37). Results are the same bits in every mode. */
 int emh_set_screen(emh_ctx* ctx, int on);
-/* Time every launch of the MFMA screen kernel (top-1 and top-k) with HIP events
- * on the context's stream while on; emh_profile_read waits, sums and resets:
- * total milliseconds, launches, and algorithmic FLOP (2 rows k d per launch). */
+/* Time every on-th launch of the MFMA screen kernel (top-1 and top-k) with HIP
+ * events on the context's stream (0: off; 1: every launch; a larger period
+ * keeps the events' own cost out of the timed work); emh_profile_read waits,
+ * sums and resets: total milliseconds, launches timed, and algorithmic FLOP
+ * (2 rows k d per timed launch). */
 int emh_profile(emh_ctx* ctx, int on);
 int emh_profile_read(emh_ctx* ctx, double* ms, uint64_t* launches, double* flop);
 
