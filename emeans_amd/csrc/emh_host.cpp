@@ -324,6 +324,23 @@ void check_flags(emh_ctx* c) {
 }
 
 // A HIP event without timing.
+// Waits until the device posts seq into *word (pinned host memory, written at
+// system scope by a kernel on c's stream): a spin, with a stream
+// synchronization after 50 ms so that a failed launch surfaces as an error.
+void wait_posted(emh_ctx* c, const uint32_t* word, uint32_t seq) {
+  const auto t0 = std::chrono::steady_clock::now();
+  for (uint32_t i = 1;; i++) {
+    if (__atomic_load_n(word, __ATOMIC_ACQUIRE) == seq) return;
+    if ((i & 1023) == 0 &&
+        std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(50)) {
+      EMH_HIP(hipStreamSynchronize(c->stream));
+      EMH_ENSURE(__atomic_load_n(word, __ATOMIC_ACQUIRE) == seq, "revival check word not posted");
+      return;
+    }
+    __builtin_ia32_pause();
+  }
+}
+
 struct Event {
   hipEvent_t e = nullptr;
   Event() { EMH_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming)); }
@@ -471,8 +488,12 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
 
   float* h_usage = (float*)c->pin_usage.get(k * 4);
   uint32_t* h_plan = (uint32_t*)c->pin_plan.get(2 * k * 4);
-  uint32_t* h_small = (uint32_t*)c->pin_small.get(2 * SW_WORDS * 4);
+  uint32_t* h_small = (uint32_t*)c->pin_small.get(3 * SW_WORDS * 4);
   uint32_t* h_small0 = h_small + SW_WORDS;
+  // The revival check's completion word, posted by the mass preview kernel.
+  uint32_t* h_seq = h_small + 2 * SW_WORDS;
+  __atomic_store_n(h_seq, 0u, __ATOMIC_RELAXED);
+  uint32_t seq_no = 0;
   uint32_t* h_order[2];
   uint32_t* h_lab[2];
   float* h_sco[2];
@@ -483,8 +504,8 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   }
   // The split kernel reads the plan where the host writes it (pinned memory
   // mapped into the device's address space): no copy between planning and
-  // the split. The next plan is written only after ev_check of the next
-  // revival, which the stream records after this split.
+  // the split. The next plan is written only after the next revival check's
+  // preview has posted its word, and that kernel runs after this split.
   uint32_t* d_plan = nullptr;
   EMH_HIP(hipHostGetDevicePointer((void**)&d_plan, h_plan, 0));
   // Likewise the revival check's masses and small-block words are written by
@@ -497,7 +518,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   // ev_order[b]: epoch order b is on the device and h_order[b] free again (copy
   // stream); ev_done[b]: the epoch that used order/labels/scores b has run
   // (main stream); ev_epoch[b]: its scores and label counts are on the host.
-  Event ev_init, ev_check, ev_order[2], ev_done[2], ev_epoch[2], ev_last, ev_posout;
+  Event ev_init, ev_order[2], ev_done[2], ev_epoch[2], ev_last, ev_posout;
 
   // Epochs alternate between two sets of order/labels/scores buffers, so the
   // copies of one epoch's run on the copy stream beside the next epoch's kernels.
@@ -567,8 +588,10 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   RandomState split_rng(cfg.seed);
   std::future<std::vector<double>> gnext =
       beside([&] { return gumbel_terms(split_rng, k); });
-  // The next block is started once the split is queued, off the GPU's path.
+  // After a revival used them, the next block is drawn on a helper once the
+  // next batch's kernels are queued, off the GPU's path.
   auto take_gumbel = [&] { return gnext.get(); };
+  bool refill = false;
   size_t n_splits = 0, step = 0;
   bool norms_stale = true;  // L2 readout: the EMA keeps the norms of the rows it moves
   std::vector<emh_epoch_stats> stats;
@@ -602,20 +625,23 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
         launch_top1(c, x, n, d, order, c0, c1, cents, cn, k, sph, lab, sco,
                     step > 0 && c0 == b);
       }
+      if (refill) {  // the next check's Gumbel terms, drawn while the GPU works
+        gnext = beside([&] { return gumbel_terms(split_rng, k); });
+        refill = false;
+      }
       const double alpha = scheduled_alpha(R.alpha0, step, R.total_steps);
       const float af = (float)alpha, df = (float)(1.0 - alpha);
       const int replace = alpha == 1.0;
       const bool check = (step + 1) % 5 == 0;  // CHECK_UNUSED_EVERY (recipe.rs:12)
       launch_scatter_count(c, b, e, lab, k, counts.u());
-      if (check) {
-        launch_mass_preview(c, mass.f(), counts.u(), k, af, df, replace, d_usage_h, d_small_h);
-        ev_check.record(c->stream);
-      }
+      if (check)
+        launch_mass_preview(c, mass.f(), counts.u(), k, af, df, replace, d_usage_h, d_small_h,
+                            d_small_h + 2 * SW_WORDS, ++seq_no);
       launch_scatter_sums(c, x, n, d, order, b, e, lab, k, sums.f(), last ? pass.f() : nullptr);
       launch_ema(c, pos.f(), mass.f(), sums.f(), counts.u(), k, d, af, df, replace,
                  sph ? nullptr : readout.f(), true, d_tally[buf]);
       if (check) {
-        ev_check.wait();
+        wait_posted(c, h_seq, seq_no);
         raise_flags(c, h_small);
         std::vector<float> usage(h_usage, h_usage + k);
         std::vector<uint32_t> plan = plan_revival(usage, R.tau, take_gumbel);
@@ -626,8 +652,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
           n_splits += np;
           norms_stale = true;
         }
-        if (!gnext.valid())
-          gnext = beside([&] { return gumbel_terms(split_rng, k); });
+        refill = !gnext.valid();  // scheduled after the next batch's launches
       }
       step++;
     }

@@ -138,6 +138,7 @@ struct emh_ctx {
   uint32_t* small = nullptr;  // SW_WORDS u32 on the device
   uint64_t fallback_total = 0;
   emh::Scratch cand, fblist, order, start, misc, knn_tmp, xnorm, bigj, chunkcnt, tickets;
+  emh::Scratch preview_ticket;  // k_mass_preview's last-block ticket (left at zero)
   // Host staging of the device loop: masses, plan, flags, epoch orders and
   // epoch labels/scores (double-buffered), results.
   emh::Pinned pin_usage, pin_plan, pin_small, pin_order[2], pin_lab[2], pin_sco[2], pin_out;
@@ -199,11 +200,13 @@ void launch_ema(emh_ctx* c, float* pos, float* usage, const float* sums, const u
                 size_t k, size_t d, float alpha, float decay, int replace, float* norms = nullptr,
                 bool clear_screen_words = false, uint32_t* tally = nullptr);
 // The masses launch_ema will leave, into out (usage untouched); with
-// small_out, also a copy of the small block's words. out and small_out may be
+// small_out, also a copy of the small block's words; with seq_out, then seq
+// into *seq_out once all of that is written. out, small_out and seq_out may be
 // pinned host memory mapped into the device's address space.
 void launch_mass_preview(emh_ctx* c, const float* usage, const uint32_t* counts, size_t k,
                          float alpha, float decay, int replace, float* out,
-                         uint32_t* small_out = nullptr);
+                         uint32_t* small_out = nullptr, uint32_t* seq_out = nullptr,
+                         uint32_t seq = 0);
 // counts = histogram of labels[0..n) (labels >= k skipped).
 void launch_hist(emh_ctx* c, const uint32_t* labels, size_t n, size_t k, uint32_t* counts);
 // Closing means: out[j] = sums[j] / counts[j] where counts[j] > 0, else pos[j].

@@ -247,17 +247,34 @@ __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __r
 
 // The masses the EMA step will leave (for the host's revival check), without
 // touching the state.
+// With seq_out, the block that takes the last ticket then posts seq there
+// (system scope, after every block's writes): a host polling pinned memory
+// sees the results as soon as they land, with no event on the stream.
 __global__ __launch_bounds__(256) void k_mass_preview(const float* __restrict__ usage,
                                                       const uint32_t* __restrict__ counts,
                                                       size_t k, float alpha, float decay,
                                                       int replace, float* __restrict__ out,
                                                       const uint32_t* __restrict__ small,
-                                                      uint32_t* __restrict__ small_out) {
+                                                      uint32_t* __restrict__ small_out,
+                                                      uint32_t* __restrict__ ticket,
+                                                      uint32_t* __restrict__ seq_out,
+                                                      uint32_t seq) {
   const size_t j = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (small_out && j < (size_t)SW_WORDS) small_out[j] = small[j];
-  if (j >= k) return;
-  float weight;
-  out[j] = ema_mass(usage[j], counts[j], alpha, decay, replace, &weight);
+  if (j < k) {
+    float weight;
+    out[j] = ema_mass(usage[j], counts[j], alpha, decay, replace, &weight);
+  }
+  if (!seq_out) return;  // uniform
+  __threadfence_system();
+  __shared__ int last;
+  if (threadIdx.x == 0) last = atomicAdd(ticket, 1u) == gridDim.x - 1;
+  __syncthreads();
+  if (last && threadIdx.x == 0) {
+    *ticket = 0;
+    __threadfence_system();
+    __hip_atomic_store(seq_out, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
 }
 
 // Label histogram of positions [0, n) (labels >= k are not counted).
@@ -413,10 +430,13 @@ void launch_ema(emh_ctx* c, float* pos, float* usage, const float* sums, const u
 }
 
 void launch_mass_preview(emh_ctx* c, const float* usage, const uint32_t* counts, size_t k,
-                         float alpha, float decay, int replace, float* out, uint32_t* small_out) {
+                         float alpha, float decay, int replace, float* out, uint32_t* small_out,
+                         uint32_t* seq_out, uint32_t seq) {
   if (k == 0) return;
+  uint32_t* ticket = seq_out ? (uint32_t*)c->preview_ticket.get_zeroed(4, c->stream) : nullptr;
   hipLaunchKernelGGL(k_mass_preview, grid1(std::max(k, (size_t)SW_WORDS), 256), dim3(256), 0,
-                     c->stream, usage, counts, k, alpha, decay, replace, out, c->small, small_out);
+                     c->stream, usage, counts, k, alpha, decay, replace, out, c->small, small_out,
+                     ticket, seq_out, seq);
   EMH_HIP(hipGetLastError());
 }
 
