@@ -344,7 +344,7 @@ constexpr int RK = 16;  // rows per block, top-k
 // barrier. Blocks whose rows have more than CCAP candidates in total take
 // further passes over the chunks.
 constexpr int CR = 32;              // rows per block
-constexpr int CCAP = 48;            // candidate slots per pass
+constexpr int CCAP = 64;            // candidate slots per pass (one chain lane each)
 constexpr int CSLOT = CR + CCAP;    // staged rows per chunk
 constexpr int CDC = 64;             // floats per chunk
 constexpr int CDC4 = CDC / 4;
