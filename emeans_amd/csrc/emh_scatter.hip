@@ -187,12 +187,25 @@ __global__ __launch_bounds__(PT) void k_prefix_chunks(size_t k, size_t nch,
   }
 }
 
+// Data row of position pos (NOROW, and the bad-id flag, when out of range).
+__device__ __forceinline__ uint32_t row_of(const uint32_t* __restrict__ ids, size_t nx,
+                                           uint32_t pos, uint32_t* __restrict__ small) {
+  const size_t r = ids ? (size_t)ids[pos] : (size_t)pos;
+  if (r >= nx) {  // a bad id adds nothing; reported at the next read
+    small[SW_BAD_ID] = 1;
+    return NOROW;
+  }
+  return (uint32_t)r;
+}
+
 // Position p of chunk c goes to rid[start[l] + (rows of label l in earlier
 // chunks) + (rows of label l earlier in this chunk)], l = labels[p].
 __global__ __launch_bounds__(256) void k_place_chunks(const uint32_t* __restrict__ labels,
                                                        size_t lo, size_t hi, size_t k,
                                                        const uint32_t* __restrict__ start,
                                                        const uint32_t* __restrict__ cnt,
+                                                       const uint32_t* __restrict__ ids, size_t nx,
+                                                       uint32_t* __restrict__ small,
                                                        uint32_t* __restrict__ rid) {
   __shared__ __attribute__((aligned(16))) uint32_t lab[CP];
   const int tid = threadIdx.x;
@@ -211,7 +224,7 @@ __global__ __launch_bounds__(256) void k_place_chunks(const uint32_t* __restrict
     rank += (uint32_t)(i < tid && q.x == l) + (uint32_t)(i + 1 < tid && q.y == l) +
             (uint32_t)(i + 2 < tid && q.z == l) + (uint32_t)(i + 3 < tid && q.w == l);
   }
-  rid[start[l] + cnt[c * k + l] + rank] = (uint32_t)p;
+  rid[start[l] + cnt[c * k + l] + rank] = row_of(ids, nx, (uint32_t)p, small);
 }
 
 // Stable placement: wave j walks positions lo..hi in order; positions with
@@ -222,6 +235,8 @@ constexpr int PW = 4;  // waves (clusters) per block: k / 4 blocks spread over t
 __global__ __launch_bounds__(64 * PW) void k_place(const uint32_t* __restrict__ labels, size_t lo,
                                                 size_t hi, size_t k,
                                                 const uint32_t* __restrict__ start,
+                                                const uint32_t* __restrict__ ids, size_t nx,
+                                                uint32_t* __restrict__ small,
                                                 uint32_t* __restrict__ rid) {
   __shared__ uint32_t lab[SEG];
   const int lane = threadIdx.x % WAVE;
@@ -262,23 +277,12 @@ __global__ __launch_bounds__(64 * PW) void k_place(const uint32_t* __restrict__ 
         if (mine) {
           const uint32_t rank = __builtin_amdgcn_mbcnt_hi(
               (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-          rid[base + rank] = (uint32_t)(s0 + p0 + u * WAVE + lane);
+          rid[base + rank] = row_of(ids, nx, (uint32_t)(s0 + p0 + u * WAVE + lane), small);
         }
         base += (uint32_t)__popcll(m);
       }
     }
   }
-}
-
-// Data row of position pos (NOROW, and the bad-id flag, when out of range).
-__device__ __forceinline__ uint32_t row_of(const uint32_t* __restrict__ ids, size_t nx,
-                                           uint32_t pos, uint32_t* __restrict__ small) {
-  const size_t r = ids ? (size_t)ids[pos] : (size_t)pos;
-  if (r >= nx) {  // a bad id adds nothing; reported at the next read
-    small[SW_BAD_ID] = 1;
-    return NOROW;
-  }
-  return (uint32_t)r;
 }
 
 // Clusters of up to SMALL rows: workgroup = cluster j; rows in order. With
@@ -287,7 +291,6 @@ __device__ __forceinline__ uint32_t row_of(const uint32_t* __restrict__ ids, siz
 constexpr int SU4 = 32;
 template <bool VEC4>
 __global__ __launch_bounds__(256) void k_sum(const float* __restrict__ x, size_t nx, size_t d,
-                                             const uint32_t* __restrict__ ids,
                                              const uint32_t* __restrict__ rid,
                                              const uint32_t* __restrict__ start, size_t k,
                                              float* __restrict__ sums, float* __restrict__ acc,
@@ -296,7 +299,7 @@ __global__ __launch_bounds__(256) void k_sum(const float* __restrict__ x, size_t
   const size_t j = blockIdx.x;
   const uint32_t b = start[j], cnt = start[j + 1] - b;
   if (cnt > (uint32_t)SMALL) return;  // k_sum_big
-  if (threadIdx.x < cnt) rows[threadIdx.x] = row_of(ids, nx, rid[b + threadIdx.x], small);
+  if (threadIdx.x < cnt) rows[threadIdx.x] = rid[b + threadIdx.x];
   __syncthreads();
   if (VEC4) {
     const size_t d4 = d / 4;
@@ -353,7 +356,6 @@ __global__ __launch_bounds__(256) void k_sum(const float* __restrict__ x, size_t
 // LDS load; thread t loads column t % BC of rows t / BC + (BT / BC) u.
 constexpr int BRP = BR + 4;  // column stride in LDS: 4-row reads stay aligned, stores 2-way
 __global__ __launch_bounds__(BT) void k_sum_big(const float* __restrict__ x, size_t nx, size_t d,
-                                                const uint32_t* __restrict__ ids,
                                                 const uint32_t* __restrict__ rid,
                                                 const uint32_t* __restrict__ start,
                                                 const uint32_t* __restrict__ bigj, int strips,
@@ -373,7 +375,7 @@ __global__ __launch_bounds__(BT) void k_sum_big(const float* __restrict__ x, siz
   const uint32_t nchunks = (cnt + BR - 1) / BR;
   auto stage = [&](uint32_t ch, int buf) {  // row ids of chunk ch
     const uint32_t i = ch * BR + tid;
-    if (tid < BR) rows[buf][tid] = i < cnt ? row_of(ids, nx, rid[b + i], small) : NOROW;
+    if (tid < BR) rows[buf][tid] = i < cnt ? rid[b + i] : NOROW;
   };
   float v[RPT];
   auto gload = [&](int buf) {
@@ -476,24 +478,24 @@ void launch_scatter_sums(emh_ctx* c, const float* x, size_t nx, size_t d, const 
     const size_t nch = (n + CP - 1) / CP;
     const uint32_t* cnt = (const uint32_t*)c->chunkcnt.get(nch * k * 4);
     hipLaunchKernelGGL(k_place_chunks, dim3((unsigned)nch), dim3(256), 0, c->stream, labels, lo,
-                       hi, k, start, cnt, rid);
+                       hi, k, start, cnt, ids, nx, c->small, rid);
     EMH_HIP(hipGetLastError());
   } else if (n > 0) {
     hipLaunchKernelGGL(k_place, grid1(k, PW), dim3(64 * PW), 0, c->stream, labels, lo, hi, k,
-                       start, rid);
+                       start, ids, nx, c->small, rid);
     EMH_HIP(hipGetLastError());
   }
   if (d % 4 == 0)
-    hipLaunchKernelGGL(k_sum<true>, dim3((unsigned)k), dim3(256), 0, c->stream, x, nx, d, ids, rid,
-                       start, k, sums, acc, c->small);
+    hipLaunchKernelGGL(k_sum<true>, dim3((unsigned)k), dim3(256), 0, c->stream, x, nx, d, rid, start,
+                       k, sums, acc, c->small);
   else
-    hipLaunchKernelGGL(k_sum<false>, dim3((unsigned)k), dim3(256), 0, c->stream, x, nx, d, ids,
-                       rid, start, k, sums, acc, c->small);
+    hipLaunchKernelGGL(k_sum<false>, dim3((unsigned)k), dim3(256), 0, c->stream, x, nx, d, rid,
+                       start, k, sums, acc, c->small);
   EMH_HIP(hipGetLastError());
   if (n > (size_t)SMALL) {
     const int strips = (int)((d + BC - 1) / BC);
     hipLaunchKernelGGL(k_sum_big, dim3((unsigned)(maxbig * strips)), dim3(BT), 0, c->stream, x,
-                       nx, d, ids, rid, start, bigj, strips, sums, acc, c->small);
+                       nx, d, rid, start, bigj, strips, sums, acc, c->small);
     EMH_HIP(hipGetLastError());
   }
 }
