@@ -702,9 +702,17 @@ __global__ __launch_bounds__(512, 1) void k_screen3(
       }
     }
     if (cs_ == nslabs - 1) {
-      // Tile done: fold its keys into the per-row lists.
+      // Tile done. Each key carries its lane-local column tag 16 a + r in its
+      // low 6 mantissa bits (the bound covers the change), so that an insert
+      // of bare floats keeps the tile's L smallest per row; the tags then
+      // give the ids, and the tile's lists join the per-row lists.
       const int tile = ct;
       const float* ns = Ns[tile & 1];
+      float tk[WN][L];
+#pragma unroll
+      for (int y = 0; y < WN; y++)
+#pragma unroll
+        for (int e = 0; e < L; e++) tk[y][e] = INFINITY;
 #pragma unroll
       for (int a = 0; a < WA; a++) {
 #pragma unroll
@@ -712,15 +720,32 @@ __global__ __launch_bounds__(512, 1) void k_screen3(
           // 32x32 accumulator layout: element (m, n) with n = lane % 32,
           // m = 8 (r / 4) + 4 (lane / 32) + r % 4.
           const int ci = wc * 128 + a * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-          const uint32_t gj = (uint32_t)(tile * TC3 + ci);
           const float nn = ns[ci];
 #pragma unroll
           for (int y = 0; y < WN; y++) {
-            float v = acc[a][y][r];
+            const float v = acc[a][y][r];
             float key = L2 ? fmaf(-2.0f, v, nn) : nn - v;  // one rounding: within E
-            if (__ballot(key < lkey[y][L - 1]) != 0ull) insert_nb<L>(lkey[y], lid[y], key, gj);
+            // NaN -> +inf (never a candidate), -inf -> -FLT_MAX (keeps its tag);
+            // a tagged +inf is a NaN, which the compare below never takes.
+            key = fmaxf(fminf(key, INFINITY), -3.4028235e38f);
+            const float tagged =
+                __uint_as_float((__float_as_uint(key) & ~63u) | (uint32_t)(16 * a + r));
+            if (__ballot(tagged < tk[y][L - 1]) != 0ull)
+              insert_key<L>(tk[y], tagged < tk[y][L - 1] ? tagged : INFINITY);
             acc[a][y][r] = 0.f;
           }
+        }
+      }
+#pragma unroll
+      for (int y = 0; y < WN; y++) {
+#pragma unroll
+        for (int e = 0; e < L; e++) {
+          const float kv = tk[y][e];
+          const uint32_t tg = __float_as_uint(kv) & 63u;
+          const int ci = wc * 128 + (int)(tg >> 4) * 32 + 8 * (int)((tg & 15u) >> 2) + 4 * h +
+                         (int)(tg & 3u);
+          const uint32_t gj = kv < INFINITY ? (uint32_t)(tile * TC3 + ci) : NONE;
+          if (__ballot(kv < lkey[y][L - 1]) != 0ull) insert_nb<L>(lkey[y], lid[y], kv, gj);
         }
       }
     }

@@ -44,6 +44,15 @@ __device__ __forceinline__ void insert(float (&key)[L], uint32_t (&id)[L], float
 // med3(key[e - 1], v, key[e]). v is first mapped to +inf when it is NaN or
 // +inf, so such a key leaves the list unchanged; equal keys stay after the
 // ones already in the list.
+// Insert v into an ascending list of L keys that keeps the L smallest (no
+// ids; v and the keys are numbers or +inf, never NaN). Branch-free.
+template <int L>
+__device__ __forceinline__ void insert_key(float (&key)[L], float v) {
+#pragma unroll
+  for (int e = L - 1; e > 0; e--) key[e] = __builtin_amdgcn_fmed3f(key[e - 1], v, key[e]);
+  key[0] = fminf(v, key[0]);
+}
+
 template <int L>
 __device__ __forceinline__ void insert_nb(float (&key)[L], uint32_t (&id)[L], float v,
                                           uint32_t j) {
@@ -94,6 +103,10 @@ __device__ __forceinline__ float screen_bound(float xn, float cmax2, float cnmax
     edot = 3.0f * g * S + (float)d * 4.7019774e-38f;  // + d 2^-124
   }
   float e = l2 ? 2.0f * edot + 2.0f * u * (cnmax + 2.0f * S) : edot;
+  // bf16 screen keys carry a 6-bit column tag in their low mantissa bits:
+  // |tagged - key| <= 63 ulp < 2^-17 |key|, with |key| <= S (IP) or
+  // cnmax + 2S (L2), plus 63 subnormal ulps (< 2^-143).
+  if (bf3) e += 7.63e-6f * (l2 ? cnmax + 2.0f * S : S) + 8.9e-44f;
   return e * 1.125f;
 }
 
