@@ -166,7 +166,7 @@ __global__ __launch_bounds__(256) void k_verify(
     int state = 0, nc = 0;
     if (rowid[tid] != NONE) {
       const float E = screen_bound(xnorm[r0 + tid], __uint_as_float(small[SW_CMAX2]),
-                                   __uint_as_float(small[SW_CNMAX]), d, l2, bf3 != 0);
+                                   __uint_as_float(small[SW_CNMAX]), d, l2, bf3 != 0, bf3 == 2);
       bool complete;
       if (KNN) {
         thr = key[kk - 1] + 2.0f * E;
@@ -422,7 +422,7 @@ __global__ __launch_bounds__(256) void k_check1(
     int cj = 0, cert = 1;
     if (vrow) {
       const float E = screen_bound(xn, __uint_as_float(small[SW_CMAX2]),
-                                   __uint_as_float(small[SW_CNMAX]), d, l2, bf3 != 0);
+                                   __uint_as_float(small[SW_CNMAX]), d, l2, bf3 != 0, bf3 == 2);
       const float thr = best + 2.0f * E;
 #pragma unroll
       for (int e = 0; e < L1; e++)
@@ -632,9 +632,10 @@ __global__ __launch_bounds__(256) void k_check1(
 void launch_verify1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
                     size_t lo, size_t n, const float* cents, const float* cnorm, size_t k, bool ip,
                     const Cand* cand, int parts, const float* xnorm, uint32_t* labels,
-                    float* scores, uint32_t* fb) {
+                    float* scores, uint32_t* fb, bool tagged) {
   const dim3 g((unsigned)((n + R1 - 1) / R1));
-  const int bf3 = c->screen != SCREEN_F32;  // the bound follows the screen's arithmetic
+  // The bound follows the screen's arithmetic: 0 f32, 1 bf16, 2 bf16 with tagged keys.
+  const int bf3 = c->screen == SCREEN_F32 ? 0 : tagged ? 2 : 1;
   if (d % 4 == 0)
     hipLaunchKernelGGL(k_check1, dim3((unsigned)((n + CR - 1) / CR)), dim3(256), 0, c->stream, x,
                        nx, (int)d, ids, lo, (int)n, cents, cnorm, ip ? 1 : 0, cand, parts, xnorm,

@@ -506,7 +506,7 @@ __global__ __launch_bounds__(256, 2) void k_screen(
 // 4 threads per row, two rows per thread for each operand).
 constexpr int TR3 = 256, TC3 = 256;
 
-template <int L, bool L2>
+template <int L, bool L2, bool TAG>
 __global__ __launch_bounds__(512, 1) void k_screen3(
     const float* __restrict__ x, size_t nx, int d, const uint32_t* __restrict__ ids, size_t lo,
     int nrows, const float* __restrict__ cents, const float* __restrict__ cnorm, int k,
@@ -701,11 +701,34 @@ __global__ __launch_bounds__(512, 1) void k_screen3(
           acc[a][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh[y], acc[a][y], 0, 0, 0);
       }
     }
-    if (cs_ == nslabs - 1) {
-      // Tile done. Each key carries its lane-local column tag 16 a + r in its
-      // low 6 mantissa bits (the bound covers the change), so that an insert
-      // of bare floats keeps the tile's L smallest per row; the tags then
-      // give the ids, and the tile's lists join the per-row lists.
+    if (!TAG && cs_ == nslabs - 1) {
+      // Tile done: fold its keys into the per-row lists.
+      const int tile = ct;
+      const float* ns = Ns[tile & 1];
+#pragma unroll
+      for (int a = 0; a < WA; a++) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          // 32x32 accumulator layout: element (m, n) with n = lane % 32,
+          // m = 8 (r / 4) + 4 (lane / 32) + r % 4.
+          const int ci = wc * 128 + a * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          const uint32_t gj = (uint32_t)(tile * TC3 + ci);
+          const float nn = ns[ci];
+#pragma unroll
+          for (int y = 0; y < WN; y++) {
+            float v = acc[a][y][r];
+            float key = L2 ? fmaf(-2.0f, v, nn) : nn - v;  // one rounding: within E
+            if (__ballot(key < lkey[y][L - 1]) != 0ull) insert_nb<L>(lkey[y], lid[y], key, gj);
+            acc[a][y][r] = 0.f;
+          }
+        }
+      }
+    }
+    if (TAG && cs_ == nslabs - 1) {
+      // Tile done, the part's only one. Each key carries its lane-local
+      // column tag 16 a + r in its low 6 mantissa bits (the bound covers the
+      // change), so that an insert of bare floats keeps the tile's L smallest
+      // per row; the tags then give the ids.
       const int tile = ct;
       const float* ns = Ns[tile & 1];
       float tk[WN][L];
@@ -878,17 +901,17 @@ void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t
   if (!words_clear)  // fallback count, cmax2, cnmax (the screen fills the maxima)
     launch_fill_u32(c, c->small, 3, 0);
   const unsigned blocks = (unsigned)(row_tiles * parts);
+  const bool tagged = big && tpp == 1;
   {
     ProfScope prof(c, 2.0 * (double)n * (double)k * (double)d);
-    if (big && ip)
-      hipLaunchKernelGGL((k_screen3<L1, false>), dim3(blocks), dim3(512), 0, c->stream, x, nx,
-                         (int)d, ids, lo, (int)n, cents, cnorm, (int)k, tpp, parts, ntiles, cand,
-                         c->small, xnorm);
-    else if (big)
-      hipLaunchKernelGGL((k_screen3<L1, true>), dim3(blocks), dim3(512), 0, c->stream, x, nx,
-                         (int)d, ids, lo, (int)n, cents, cnorm, (int)k, tpp, parts, ntiles, cand,
-                         c->small, xnorm);
-    else if (ip)
+    if (big) {
+      // One tile per part: tagged keys (the cheap fold); more: the sorted insert, which
+      // skips most keys once the lists hold good ones.
+      auto kern = ip ? (tagged ? k_screen3<L1, false, true> : k_screen3<L1, false, false>)
+                     : (tagged ? k_screen3<L1, true, true> : k_screen3<L1, true, false>);
+      hipLaunchKernelGGL(kern, dim3(blocks), dim3(512), 0, c->stream, x, nx, (int)d, ids, lo,
+                         (int)n, cents, cnorm, (int)k, tpp, parts, ntiles, cand, c->small, xnorm);
+    } else if (ip)
       launch_screen<2, L1, false, false>(c, blocks, x, nx, d, ids, lo, n, cents, cnorm, k, tpp,
                                          parts, ntiles, cand, xnorm);
     else
@@ -897,7 +920,7 @@ void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t
     if (big) EMH_HIP(hipGetLastError());
   }
   launch_verify1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, cand, parts, xnorm, labels, scores,
-                 fb);
+                 fb, tagged);
   launch_exact1(c, x, nx, d, ids, lo, n, fb, cents, cnorm, k, ip, labels, scores);
 }
 

@@ -85,7 +85,7 @@ __device__ __forceinline__ void insert_nb(float (&key)[L], uint32_t (&id)[L], fl
 //   <= 5.25 u; measured <= 4.9 u), so <= gamma(16 M) * 1.02 S (the three
 //   passes' |products| sum to <= 1.02 S); underflow: (3d + M) 2^-124.
 __device__ __forceinline__ float screen_bound(float xn, float cmax2, float cnmax, int d, bool l2,
-                                              bool bf3) {
+                                              bool bf3, bool tagged = false) {
   const float u = 5.9604645e-08f;  // 2^-24
   const float du = (float)d * u;
   const float g = du / (1.0f - du);
@@ -103,10 +103,10 @@ __device__ __forceinline__ float screen_bound(float xn, float cmax2, float cnmax
     edot = 3.0f * g * S + (float)d * 4.7019774e-38f;  // + d 2^-124
   }
   float e = l2 ? 2.0f * edot + 2.0f * u * (cnmax + 2.0f * S) : edot;
-  // bf16 screen keys carry a 6-bit column tag in their low mantissa bits:
-  // |tagged - key| <= 63 ulp < 2^-17 |key|, with |key| <= S (IP) or
-  // cnmax + 2S (L2), plus 63 subnormal ulps (< 2^-143).
-  if (bf3) e += 7.63e-6f * (l2 ? cnmax + 2.0f * S : S) + 8.9e-44f;
+  // Tagged keys (the single-tile large-tile screen) carry a 6-bit column tag
+  // in their low mantissa bits: |tagged - key| <= 63 ulp < 2^-17 |key|, with
+  // |key| <= S (IP) or cnmax + 2S (L2), plus 63 subnormal ulps (< 2^-143).
+  if (tagged) e += 7.63e-6f * (l2 ? cnmax + 2.0f * S : S) + 8.9e-44f;
   return e * 1.125f;
 }
 
@@ -137,7 +137,7 @@ __device__ __forceinline__ void merge_parts(const Cand* c, int parts, float (&ke
 void launch_verify1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
                     size_t lo, size_t n, const float* cents, const float* cnorm, size_t k, bool ip,
                     const Cand* cand, int parts, const float* xnorm, uint32_t* labels,
-                    float* scores, uint32_t* fb);
+                    float* scores, uint32_t* fb, bool tagged = false);
 void launch_verifyk(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,
                     size_t kk, const Cand* cand, int parts, const float* xnorm, uint32_t* ids,
                     float* sims, uint32_t* fb);
