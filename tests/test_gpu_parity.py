@@ -101,6 +101,21 @@ def test_top1_production_shape_with_duplicates(dev, screen, k, metric):
     assert np.all(gl < base)
 
 
+@pytest.mark.parametrize("metric", ["ip", "l2"])
+def test_top1_parts_of_several_tiles(dev, screen, metric):
+    """16,384 rows against 2,048 centroids: on 256 CUs the large-tile screen's
+    four parts span two 256-centroid tiles each, so its lists take the sorted
+    insert across tiles (single-tile parts tag their keys instead). Bit-equal
+    to the oracle."""
+    n, d, k = 16384, 256, 2048
+    x = _mix(n, d, 64, 0.6, metric == "ip", 7 * n + k)
+    c = (x[(np.arange(k) * 37) % n] * np.float32(0.95)).astype(np.float32)
+    gl, gs = _gpu_top1(dev, x, c, metric)
+    ol, osc = O.top1(x, d, c, metric)
+    assert np.array_equal(gl, ol)
+    assert gs.tobytes() == osc.tobytes()
+
+
 def _noise(i):
     i = np.asarray(i, np.uint64)
     with np.errstate(over="ignore"):
