@@ -10,22 +10,34 @@ assignment of all 200,000 rows, with the data resident in HBM.
 
 value = top-1 rows processed per second over the whole step (5 training passes
 plus the final assignment: 1.2 M rows per step), in Mrows/s. The line also
-reports train seconds, assignment Mrows/s, the MFMA screen kernel's roofline
-and the CPU baseline. The screen (the dense x.C^T contraction ahead of the
-exact f32 check) runs on the bf16 MFMA in three passes (x.c ~ xh.ch + xh.cl +
-xl.ch); its roofline is the bf16 MFMA work it issues (3 x 2 rows k d FLOP per
-launch over the HIP-event-timed duration of every 8th launch in the timed
-steps) against the 2.5 PFLOP/s dense bf16 peak, with the f32-equivalent rate (2 rows k d FLOP per launch) against the
-157.3 TFLOP/s dense f32 MFMA peak beside it. `f32_screen` repeats the step
-with the screen on v_mfma_f32_32x32x2_f32 (same bits, checked). The CPU
-baseline is the oracle's C++ restatement of the reference CPU backend
-(cpu-fused float order) running the same training and assignment on this
-host, with a bit-exact parity check.
+reports train seconds, assignment Mrows/s, the rooflines and the CPU baseline:
+
+  roofline         the dominant kernel, the MFMA screen (the dense x.C^T
+                   contraction ahead of the exact f32 check): algorithmic
+                   2 rows k d FLOP per launch over the HIP-event-timed
+                   duration of every 8th launch in the timed steps, against
+                   the 2.5 PFLOP/s dense bf16 peak of the unit it runs on (its
+                   three bf16 passes, x.c ~ xh.ch + xh.cl + xl.ch, are
+                   reported apart as the issued rate);
+  update_rooflines scatter_add and ema_update, algorithmic HBM bytes per
+                   call over their HIP-event time in two more steps with every
+                   call timed, against 8 TB/s;
+  cpu_baseline     the oracle's C++ restatement of the reference CPU backend
+                   (cpu-fused float order) running the same training and
+                   assignment on this host, median of three runs, with a
+                   bit-exact parity check;
+  other_workloads  assign-only 2M x 1024 vs k = 16,384 (IP) and knn_self k = 10
+                   on 500k x 384, data resident, with the oracle on a sample
+                   of queries.
+
+`f32_screen` repeats the step with the screen on v_mfma_f32_32x32x2_f32
+(same bits, checked).
 """
 
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -54,16 +66,52 @@ def log(*a):
 
 
 def screen_roofline(ms, launches, flop, kernel, traffic=None):
-    """The bf16 screen's roofline: the MFMA work it issues (three bf16 products
-    per multiply-add of the algorithmic 2 rows k d FLOP) over its HIP-event
-    time, against the dense bf16 peak; the f32-equivalent rate beside it."""
+    """The screen's roofline: algorithmic FLOP (2 rows k d per launch) over its
+    HIP-event time against the dense bf16 MFMA peak of the unit it runs on.
+    Beside it: the bf16 MFMA work it issues (three products per multiply-add)
+    and the ratio of the algorithmic rate to the f32 MFMA peak (above 1 when
+    the exact f32 results come faster than f32 MFMA arithmetic could give)."""
     alg = flop / (ms * 1e-3) / 1e12 if ms > 0 else 0.0
-    return {"bound": "mfma", "kernel": kernel, "achieved": 3.0 * alg, "peak": BF16_MFMA_PEAK,
-            "unit": "TFLOP/s", "frac": 3.0 * alg / BF16_MFMA_PEAK, "traffic": traffic,
+    return {"bound": "mfma", "kernel": kernel, "achieved": alg, "peak": BF16_MFMA_PEAK,
+            "unit": "TFLOP/s", "frac": alg / BF16_MFMA_PEAK, "traffic": traffic,
             "launches": launches, "avg_launch_ms": ms / max(launches, 1),
-            "flop_per_launch": 3.0 * flop / max(launches, 1),
-            "fp32_equivalent": {"achieved": alg, "peak": FP32_MFMA_PEAK, "frac": alg / FP32_MFMA_PEAK,
-                                "flop_per_launch": flop / max(launches, 1)}}
+            "flop_per_launch": flop / max(launches, 1),
+            "issued_bf16": {"achieved": 3.0 * alg, "frac": 3.0 * alg / BF16_MFMA_PEAK},
+            "vs_fp32_mfma_peak": {"peak": FP32_MFMA_PEAK, "ratio": alg / FP32_MFMA_PEAK}}
+
+
+def hbm_roofline(ms, instances, nbytes, kernels):
+    """An update op's roofline: algorithmic bytes per call over its
+    HIP-event time against the 8 TB/s HBM peak."""
+    gbs = nbytes / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
+    return {"bound": "hbm", "kernels": kernels, "achieved": gbs, "peak": HBM_PEAK, "unit": "GB/s",
+            "frac": gbs / HBM_PEAK, "calls": instances, "avg_call_ms": ms / max(instances, 1),
+            "bytes_per_call": nbytes / max(instances, 1)}
+
+
+def host_cpu():
+    """The host CPU as lscpu reports it (model, sockets, physical cores, clock)."""
+    info = {"nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0))}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        kv = {}
+        for line in out.splitlines():
+            if ":" in line:
+                a, v = line.split(":", 1)
+                kv[a.strip()] = v.strip()
+        sockets = int(kv.get("Socket(s)", "1") or 1)
+        cps = int(kv.get("Core(s) per socket", "0") or 0)
+        info.update({"model": kv.get("Model name"), "sockets": sockets,
+                     "physical_cores": sockets * cps,
+                     "threads_per_core": int(kv.get("Thread(s) per core", "1") or 1),
+                     "max_mhz": float(kv["CPU max MHz"]) if "CPU max MHz" in kv else None})
+        with open("/proc/cpuinfo") as f:
+            mhz = [float(l.split(":")[1]) for l in f if l.startswith("cpu MHz")]
+        if mhz:
+            info["cpuinfo_mhz"] = max(mhz)
+    except Exception as e:  # lscpu missing: report what Python sees
+        info["lscpu_error"] = str(e)
+    return info
 
 
 def headline(args):
@@ -98,7 +146,7 @@ def headline(args):
             log(f"warmup {i} (screen {mode}): train {tr * 1e3:.1f} ms, assign {asg * 1e3:.1f} ms, "
                 f"fallback rows {info['fallback_rows']}")
         dev.sync()
-        dev.profile(PROFILE_EVERY)
+        dev.profile(PROFILE_EVERY, "screen")
         trains, assigns = [], []
         t0 = time.perf_counter()
         for i in range(steps):
@@ -108,9 +156,19 @@ def headline(args):
         dev.sync()
         t1 = time.perf_counter()
         dev.profile(False)
-        ms, launches, flop = dev.profile_read()
+        ms, launches, flop = dev.profile_read("screen")
+        # The update ops' rooflines come from two more steps with every call
+        # timed, after the timed region (their event pairs stay out of the value).
+        dev.profile(1)
+        for _ in range(2):
+            step()
+        dev.sync()
+        dev.profile(False)
+        dev.profile_read("screen")
+        upd = {op: dev.profile_read(op) for op in ("scatter_add", "ema_update")}
         r = {"step_s": (t1 - t0) / steps, "train_s": float(np.median(trains)),
              "assign_s": float(np.median(assigns)), "ms": ms, "launches": launches, "flop": flop,
+             "update": upd,
              "cent": cent, "info": info, "labels": dev.read_u32(labels),
              "scores": dev.read_f32(scores)}
         dev.set_screen(1)
@@ -145,8 +203,14 @@ def headline(args):
         "fallback_rows_per_run": info["fallback_rows"],
         "roofline": screen_roofline(
             ms, launches, flop,
-            "k_screen (bf16 MFMA, three passes xh.ch + xh.cl + xl.ch, f32 accumulation, "
+            "k_screen3 (bf16 MFMA, three passes xh.ch + xh.cl + xl.ch, f32 accumulation, "
             "+ per-row 5-entry candidate lists per centroid part)", SCREEN_TRAFFIC_BYTES),
+        "update_rooflines": {
+            "scatter_add": hbm_roofline(*main["update"]["scatter_add"],
+                                        "k_hist_chunks + k_prefix_chunks + k_place_chunks + "
+                                        "k_sum + k_sum_big"),
+            "ema_update": hbm_roofline(*main["update"]["ema_update"], "k_ema"),
+        },
     }
     if not args.no_f32:
         f = timed(2, max(2, args.steps // 2), 1)
@@ -167,6 +231,10 @@ def headline(args):
     if not args.no_cpu:
         out["cpu_baseline"], out["parity"] = cpu_baseline(x, cfg, cent, info, gpu_labels,
                                                           gpu_scores, args)
+    if not args.no_others:
+        del xb, labels, scores, cb
+        dev.close()
+        out["other_workloads"] = other_workloads(args)
     return out
 
 
@@ -194,27 +262,37 @@ def from_host(dev, x, cfg, gpu_labels, gpu_scores):
 
 
 def cpu_baseline(x, cfg, gpu_cent, info, gpu_labels, gpu_scores, args):
+    """The oracle (the C++ restatement of the reference CPU backend, OpenMP)
+    on the same training and assignment: the median of `--cpu-runs` runs."""
     from oracle import oracle as O
 
     if args.cpu_threads:
         O.set_threads(args.cpu_threads)
     threads = O.get_threads()
     n, d, k = x.shape[0], cfg.d, cfg.k
-    t0 = time.perf_counter()
-    o = O.train(x, d, k, seed=cfg.seed)
-    t1 = time.perf_counter()
-    ol, osc = O.assign(x, d, o["centroids"], "l2")
-    t2 = time.perf_counter()
+    runs = []
+    for _ in range(max(1, args.cpu_runs)):
+        t0 = time.perf_counter()
+        o = O.train(x, d, k, seed=cfg.seed)
+        t1 = time.perf_counter()
+        ol, osc = O.assign(x, d, o["centroids"], "l2")
+        t2 = time.perf_counter()
+        runs.append((t2 - t0, t1 - t0, t2 - t1))
+    runs.sort()
+    cpu_s, train_s, assign_s = runs[len(runs) // 2]
     epochs = len(o["obj"])
-    cpu_s = t2 - t0
     base = {
         "value": (epochs * n + n) / cpu_s / 1e6,
         "unit": "Mrows/s",
         "cores": threads,
         "kind": "port",
-        "sample": "the full workload once: training (5 epochs) + assignment of all rows",
-        "train_s": t1 - t0,
-        "assign_s": t2 - t1,
+        "sample": "the full workload: training (5 epochs) + assignment of all 200,000 rows; "
+                  f"median of {len(runs)} runs",
+        "train_s": train_s,
+        "assign_s": assign_s,
+        "runs_s": [r[0] for r in runs],
+        "threads": threads,
+        "host": host_cpu(),
     }
     parity = {
         "centroids_bit_equal": bool(gpu_cent.tobytes() == o["centroids"].tobytes()),
@@ -227,6 +305,97 @@ def cpu_baseline(x, cfg, gpu_cent, info, gpu_labels, gpu_scores, args):
         "final_objective": O.mean_objective(osc, False),
     }
     return base, parity
+
+
+def other_workloads(args):
+    """Assign-only at scale (2,000,000 x 1024 unit queries vs 16,384 unit
+    centroids, IP, seed 1) and exact kNN (knn_self k = 10 on 500,000 x 384 unit
+    rows with 5% near-duplicates, seed 2), both at full size on data drawn on
+    the host (emeans_amd.synth) and resident: `--other-steps` timed runs
+    each after one warmup, the screen timed with HIP events on every launch,
+    and the oracle on a sample of the queries (bit-exact labels, scores, ids
+    and sims) as the CPU baseline."""
+    from emeans_amd import HipDevice, synth
+    from oracle import oracle as O
+
+    dev = HipDevice()
+    res = {}
+    # --- assign 2M x 1024 vs 16,384, IP
+    n, d, k = 2_000_000, 1024, 16_384
+    t = time.time()
+    q, c = synth.assign_at_scale(n, d, k, seed=1)
+    log(f"assign data: {n} x {d} and {k} centroids generated in {time.time() - t:.1f} s")
+    qb, cb = dev.bind(q), dev.upload_f32(c)
+    labels, scores = dev.zeros_u32(n), dev.zeros_f32(n)
+    dev.assign_dev(qb, n, d, cb, k, "ip", labels, scores)
+    dev.sync()
+    dev.profile(1)
+    t0 = time.perf_counter()
+    for _ in range(args.other_steps):
+        dev.assign_dev(qb, n, d, cb, k, "ip", labels, scores)
+    dev.sync()
+    step_s = (time.perf_counter() - t0) / args.other_steps
+    dev.profile(0)
+    ms, launches, flop = dev.profile_read("screen")
+    gl, gs = dev.read_u32(labels), dev.read_f32(scores)
+    g = np.random.default_rng(0)
+    sample = np.sort(g.choice(n, size=args.assign_sample, replace=False))
+    t0 = time.perf_counter()
+    ol, osc = O.assign(q[sample], d, c, "ip")
+    cpu_s = time.perf_counter() - t0
+    res["assign_2Mx1024_k16384_ip"] = {
+        "value": n / step_s / 1e6, "unit": "Mrows/s", "ms_per_run": step_s * 1e3,
+        "steps": args.other_steps,
+        "roofline": screen_roofline(ms, launches, flop, "k_screen3 (sorted-insert lists)"),
+        "cpu_baseline": {"value": len(sample) / cpu_s / 1e6, "unit": "Mrows/s",
+                         "cores": O.get_threads(), "kind": "port",
+                         "sample": f"{len(sample)} of the {n} queries against all {k} centroids"},
+        "parity": {"labels_equal": bool(np.array_equal(gl[sample], ol)),
+                   "scores_bit_equal": gs[sample].tobytes() == osc.tobytes()}}
+    log(f"assign 2M: {step_s * 1e3:.1f} ms per run")
+    del qb, cb, labels, scores, q, c
+    # --- knn_self k = 10 on 500k x 384
+    n, d, kk = 500_000, 384, 10
+    t = time.time()
+    xh, dst, src = synth.knn_near_duplicates(n, d, seed=2)
+    log(f"knn data: {n} x {d} generated in {time.time() - t:.1f} s")
+    xb = dev.bind(xh)
+    ids, sims = dev.zeros_u32(n * kk), dev.zeros_f32(n * kk)
+    dev.topk_dev(xb, n, xb, n, d, kk, True, ids, sims)
+    dev.sync()
+    dev.profile(1)
+    t0 = time.perf_counter()
+    for _ in range(args.other_steps):
+        dev.topk_dev(xb, n, xb, n, d, kk, True, ids, sims)
+    dev.sync()
+    step_s = (time.perf_counter() - t0) / args.other_steps
+    dev.profile(0)
+    ms, launches, flop = dev.profile_read("screen")
+    gi, gsm = dev.read_u32(ids).reshape(n, kk), dev.read_f32(sims).reshape(n, kk)
+    sample = np.sort(g.choice(n, size=args.knn_sample, replace=False))
+    t0 = time.perf_counter()
+    oi, osm = O.knn(xh[sample], xh, d, kk + 1, False)
+    cpu_s = time.perf_counter() - t0
+    oi, osm = oi.reshape(-1, kk + 1), osm.reshape(-1, kk + 1)
+    # exclude_self on the sample: the oracle searched kk + 1 among all rows; drop the query itself
+    wi, ws = np.empty((len(sample), kk), np.uint32), np.empty((len(sample), kk), np.float32)
+    for r, qi in enumerate(sample):
+        keep = oi[r] != qi
+        wi[r], ws[r] = oi[r][keep][:kk], osm[r][keep][:kk]
+    recall = float(np.mean((gi[dst] == src[:, None]).any(axis=1)))
+    res["knn_self_500kx384_k10"] = {
+        "value": 2.0 * n * n * d / step_s / 1e12, "unit": "TFLOP/s", "ms_per_run": step_s * 1e3,
+        "steps": args.other_steps,
+        "roofline": screen_roofline(ms, launches, flop, "k_screen (kNN, 24-entry lists)"),
+        "cpu_baseline": {"value": 2.0 * len(sample) * n * d / cpu_s / 1e12, "unit": "TFLOP/s",
+                         "cores": O.get_threads(), "kind": "port",
+                         "sample": f"{len(sample)} queries against all {n} rows"},
+        "parity": {"ids_equal": bool(np.array_equal(gi[sample], wi)),
+                   "sims_bit_equal": gsm[sample].tobytes() == ws.tobytes()},
+        "duplicates_found_as_a_neighbour": recall}
+    log(f"knn 500k: {step_s * 1e3:.1f} ms per run")
+    dev.close()
+    return res
 
 
 def knn_workload(args):
@@ -363,6 +532,14 @@ def main():
     ap.add_argument("--no-host", action="store_true",
                     help="skip the runs from host arrays (PCIe-inclusive times)")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--cpu-runs", type=int, default=3, help="CPU baseline runs (median)")
+    ap.add_argument("--no-others", action="store_true",
+                    help="skip the assign-at-scale and kNN lines of the headline run")
+    ap.add_argument("--other-steps", type=int, default=3)
+    ap.add_argument("--assign-sample", type=int, default=2000,
+                    help="queries the oracle checks at 2M x 1024 (the CPU baseline sample)")
+    ap.add_argument("--knn-sample", type=int, default=200,
+                    help="queries the oracle checks at 500k x 384 (the CPU baseline sample)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run a plain device copy of MIB MiB (HBM counter calibration)")
     ap.add_argument("--workload", choices=["headline", "knn", "assign"], default="headline",

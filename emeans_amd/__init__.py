@@ -20,8 +20,9 @@ from typing import List, Optional, Tuple
 
 import numpy as np
 
-from ._lib import (EMH_IP, EMH_L2, Config as _CConfig, EmeansHipError, EmeansHipInvalid,
-                   EpochStats as _CEpoch, TrainOut as _CTrainOut, check, lib)
+from ._lib import (EMH_IP, EMH_L2, EMH_PROF_EMA, EMH_PROF_SCATTER, EMH_PROF_SCREEN,
+                   Config as _CConfig, EmeansHipError, EmeansHipInvalid, EpochStats as _CEpoch,
+                   TrainOut as _CTrainOut, check, lib)
 
 __all__ = [
     "HipDevice", "DevBuf", "EmaStep", "Mat", "Select", "Config", "Emeans", "Trained",
@@ -260,16 +261,25 @@ class HipDevice:
                 "labels": labels}
         return cent, info
 
-    def profile(self, every):
-        """Time every `every`-th MFMA screen launch with HIP events on the
-        context's stream (0 or False: off; 1 or True: every launch)."""
-        check(lib().emh_profile(self._ctx, int(every)))
+    _PROF_OPS = {"screen": EMH_PROF_SCREEN, "scatter_add": EMH_PROF_SCATTER,
+                 "ema_update": EMH_PROF_EMA}
 
-    def profile_read(self):
-        """(total ms, launches, algorithmic FLOP) of the timed screen launches; resets."""
-        ms, n, fl = C.c_double(), C.c_uint64(), C.c_double()
-        check(lib().emh_profile_read(self._ctx, C.byref(ms), C.byref(n), C.byref(fl)))
-        return ms.value, n.value, fl.value
+    def profile(self, every, op: Optional[str] = None):
+        """Time every `every`-th instance of the MFMA screen, scatter_add and
+        ema_update (or of `op` alone) with HIP events on the context's stream
+        (0 or False: off; 1 or True: every instance)."""
+        if op is None:
+            check(lib().emh_profile(self._ctx, int(every)))
+        else:
+            check(lib().emh_profile_op(self._ctx, self._PROF_OPS[op], int(every)))
+
+    def profile_read(self, op: str = "screen"):
+        """(total ms, instances timed, algorithmic units) of op ("screen": FLOP,
+        "scatter_add" or "ema_update": HBM bytes); resets op's totals."""
+        code = self._PROF_OPS[op]
+        ms, n, u = C.c_double(), C.c_uint64(), C.c_double()
+        check(lib().emh_profile_read_op(self._ctx, code, C.byref(ms), C.byref(n), C.byref(u)))
+        return ms.value, n.value, u.value
 
     def fallback_rows(self) -> int:
         return lib().emh_fallback_rows(self._ctx)

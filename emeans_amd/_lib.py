@@ -12,6 +12,7 @@ LIB_PATH = os.path.join(HERE, "libemeans_hip.so")
 
 EMH_OK, EMH_INVALID, EMH_ERROR = 0, 1, 2
 EMH_L2, EMH_IP = 0, 1
+EMH_PROF_SCREEN, EMH_PROF_SCATTER, EMH_PROF_EMA = 0, 1, 2
 
 
 class EmeansHipError(RuntimeError):
@@ -82,7 +83,9 @@ SIGNATURES = {
     "emh_assign": (_i, [_vp, _vp, _sz, _sz, _vp, _sz, _i, _sz, _vp, _vp]),
     "emh_assign_dev": (_i, [_vp, _vp, _sz, _sz, _vp, _sz, _i, _sz, _vp, _vp]),
     "emh_profile": (_i, [_vp, _i]),
+    "emh_profile_op": (_i, [_vp, _i, _i]),
     "emh_profile_read": (_i, [_vp, C.POINTER(_d), C.POINTER(_u64), C.POINTER(_d)]),
+    "emh_profile_read_op": (_i, [_vp, _i, C.POINTER(_d), C.POINTER(_u64), C.POINTER(_d)]),
     "emh_knn": (_i, [_vp, _vp, _sz, _vp, _sz, _sz, _sz, _i, _vp, _vp]),
     "emh_dedup_neighbors": (_i, [_vp, _sz, _sz, _vp, _vp, _sz, _f, _f, _vp, _vp, _vp, _vp, _vp,
                                  C.POINTER(_sz), C.POINTER(_sz), C.POINTER(_sz)]),

@@ -18,7 +18,10 @@ CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libemeans_hip.so")
 OBJ = os.path.join(HERE, "_obj")
 SOURCES = ["emh_api.cpp", "emh_host.cpp", "emh_ops.hip", "emh_scatter.hip", "emh_screen.hip",
-           "emh_rescore.hip", "emh_verify.hip", "emh_perm.cpp"]
+           "emh_screen3.hip", "emh_screen_t1_bf3.hip", "emh_screen_t1_f32.hip",
+           "emh_screen_kn_bf3_self.hip", "emh_screen_kn_bf3_any.hip",
+           "emh_screen_kn_f32_self.hip", "emh_screen_kn_f32_any.hip", "emh_rescore.hip", "emh_verify.hip",
+           "emh_perm.cpp"]
 # Plain host C++ (no HIP), built by the system compiler.
 HOST_ONLY = {"emh_perm.cpp"}
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -48,14 +51,31 @@ def _compile(src):
     return obj, err
 
 
-def build(verbose=False):
+def _stale(src):
+    """Whether src's object is missing or older than src or any header."""
+    obj = os.path.join(OBJ, os.path.splitext(src)[0] + ".o")
+    if not os.path.exists(obj):
+        return True
+    deps = [os.path.join(CSRC, src)] + [os.path.join(CSRC, h) for h in os.listdir(CSRC)
+                                        if h.endswith(".h")]
+    deps.append(os.path.join(os.path.dirname(HERE), "include", "emeans_hip.h"))
+    t = os.path.getmtime(obj)
+    return any(os.path.getmtime(p) > t for p in deps)
+
+
+def build(verbose=False, incremental=False):
+    """Compile every source (or, with incremental, those whose object is
+    older than the source or a header) and link the library."""
     os.makedirs(OBJ, exist_ok=True)
-    with ThreadPoolExecutor(max_workers=min(len(SOURCES), 8)) as ex:
-        results = list(ex.map(_compile, SOURCES))
+    todo = [s for s in SOURCES if _stale(s)] if incremental else SOURCES
+    with ThreadPoolExecutor(max_workers=max(1, min(len(todo), os.cpu_count() or 8))) as ex:
+        results = list(ex.map(_compile, todo))
+    results += [(os.path.join(OBJ, os.path.splitext(s)[0] + ".o"), "") for s in SOURCES
+                if s not in todo]
     for _, err in results:
         if err and verbose:
             print(err, file=sys.stderr)
-    objs = [o for o, _ in results]
+    objs = [os.path.join(OBJ, os.path.splitext(s)[0] + ".o") for s in SOURCES]
     tmp = LIB + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -66,4 +86,4 @@ def build(verbose=False):
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose=True, incremental="--incremental" in sys.argv))

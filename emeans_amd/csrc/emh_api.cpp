@@ -394,6 +394,8 @@ int emh_scatter_add(emh_ctx* c, const emh_buf* x, size_t d, const emh_buf* ids, 
       EMH_ENSURE(acc->len == k * d, "acc must be k x d");
     }
     use_device(c);
+    emh::ProfScope prof(c, EMH_PROF_SCATTER, emh::scatter_bytes(hi - lo, k, d, ids, ap),
+                        emh::prof_take(c, EMH_PROF_SCATTER));
     emh::launch_scatter(c, xp, nx, d, ids ? (const uint32_t*)ids->ptr : nullptr, lo, hi, lab, k,
                         sp, cp, ap);
   });
@@ -461,6 +463,7 @@ int emh_ema_update(emh_ctx* c, emh_buf* positions, emh_buf* usage, const emh_buf
                    counts->len == k,
                "shapes");
     use_device(c);
+    emh::ProfScope prof(c, EMH_PROF_EMA, emh::ema_bytes(k, d), emh::prof_take(c, EMH_PROF_EMA));
     emh::launch_ema(c, pp, up, sp, cp, k, d, alpha, decay, replace);
   });
 }
@@ -488,29 +491,53 @@ int emh_profile(emh_ctx* c, int on) {
   return guard([&] {
     EMH_ENSURE(c, "null context");
     EMH_ENSURE(on >= 0, "profile period %d must be >= 0", on);
-    c->prof = on;
-    c->prof_count = 0;
+    for (int op = 0; op < EMH_PROF_OPS; op++) {
+      c->prof[op] = on;
+      c->prof_count[op] = 0;
+    }
+  });
+}
+
+int emh_profile_op(emh_ctx* c, int op, int on) {
+  return guard([&] {
+    EMH_ENSURE(c, "null context");
+    EMH_ENSURE(op >= 0 && op < EMH_PROF_OPS, "unknown profiled op %d", op);
+    EMH_ENSURE(on >= 0, "profile period %d must be >= 0", on);
+    c->prof[op] = on;
+    c->prof_count[op] = 0;
+  });
+}
+
+int emh_profile_read_op(emh_ctx* c, int op, double* ms, uint64_t* instances, double* units) {
+  return guard([&] {
+    EMH_ENSURE(c && ms && instances && units, "null argument");
+    EMH_ENSURE(op >= 0 && op < EMH_PROF_OPS, "unknown profiled op %d", op);
+    use_device(c);
+    EMH_HIP(hipStreamSynchronize(c->stream));
+    // Every timed segment so far goes into its op's totals; the events go
+    // back to the pool.
+    for (auto& e : c->timed) {
+      float m = 0.f;
+      EMH_HIP(hipEventElapsedTime(&m, e.a, e.b));
+      emh_ctx::ProfSum& s = c->prof_sum[e.op];
+      s.ms += m;
+      if (e.last) {
+        s.units += e.units;
+        s.instances++;
+      }
+    }
+    c->timed.clear();
+    c->ev_used = 0;
+    emh_ctx::ProfSum& s = c->prof_sum[op];
+    *ms = s.ms;
+    *instances = s.instances;
+    *units = s.units;
+    s = emh_ctx::ProfSum{};
   });
 }
 
 int emh_profile_read(emh_ctx* c, double* ms, uint64_t* launches, double* flop) {
-  return guard([&] {
-    EMH_ENSURE(c && ms && launches && flop, "null argument");
-    use_device(c);
-    EMH_HIP(hipStreamSynchronize(c->stream));
-    double t = 0.0, f = 0.0;
-    for (auto& e : c->timed) {
-      float m = 0.f;
-      EMH_HIP(hipEventElapsedTime(&m, e.a, e.b));
-      t += m;
-      f += e.flop;
-    }
-    *ms = t;
-    *launches = c->timed.size();
-    *flop = f;
-    c->timed.clear();
-    c->ev_used = 0;  // the events go back to the pool
-  });
+  return emh_profile_read_op(c, EMH_PROF_SCREEN, ms, launches, flop);
 }
 
 }  // extern "C"

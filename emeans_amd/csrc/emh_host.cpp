@@ -633,13 +633,25 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
       const float af = (float)alpha, df = (float)(1.0 - alpha);
       const int replace = alpha == 1.0;
       const bool check = (step + 1) % 5 == 0;  // CHECK_UNUSED_EVERY (recipe.rs:12)
-      launch_scatter_count(c, b, e, lab, k, counts.u());
+      // scatter_add in two segments: counts, then (after the revival check's
+      // mass preview, which needs only the counts) the ordered sums.
+      const bool tsc = prof_take(c, EMH_PROF_SCATTER);
+      {
+        ProfScope p(c, EMH_PROF_SCATTER, 0.0, tsc, false);
+        launch_scatter_count(c, b, e, lab, k, counts.u());
+      }
       if (check)
         launch_mass_preview(c, mass.f(), counts.u(), k, af, df, replace, d_usage_h, d_small_h,
                             d_small_h + 2 * SW_WORDS, ++seq_no);
-      launch_scatter_sums(c, x, n, d, order, b, e, lab, k, sums.f(), last ? pass.f() : nullptr);
-      launch_ema(c, pos.f(), mass.f(), sums.f(), counts.u(), k, d, af, df, replace,
-                 sph ? nullptr : readout.f(), true, d_tally[buf]);
+      {
+        ProfScope p(c, EMH_PROF_SCATTER, scatter_bytes(e - b, k, d, true, last), tsc);
+        launch_scatter_sums(c, x, n, d, order, b, e, lab, k, sums.f(), last ? pass.f() : nullptr);
+      }
+      {
+        ProfScope p(c, EMH_PROF_EMA, ema_bytes(k, d), prof_take(c, EMH_PROF_EMA));
+        launch_ema(c, pos.f(), mass.f(), sums.f(), counts.u(), k, d, af, df, replace,
+                   sph ? nullptr : readout.f(), true, d_tally[buf]);
+      }
       if (check) {
         wait_posted(c, h_seq, seq_no);
         raise_flags(c, h_small);

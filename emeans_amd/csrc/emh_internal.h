@@ -148,14 +148,24 @@ struct emh_ctx {
   emh::Pinned pin_stage[2];
   hipEvent_t ev_stage[3] = {nullptr, nullptr, nullptr};
   std::string name = "hip-gfx950";
-  // Screen-kernel timing (emh_profile): event pairs and the FLOP each covers.
-  int prof = 0;             // time every prof-th screen launch (0: off)
-  uint64_t prof_count = 0;  // screen launches since profiling was switched on
+  // Op timing (emh_profile): event pairs on the context stream around every
+  // prof-th instance of each timed op (EMH_PROF_*), with the algorithmic
+  // units (FLOP or bytes) each instance covers; an op of several launches
+  // records one pair per launch segment and counts once.
+  int prof[EMH_PROF_OPS] = {};               // period per op (0: off)
+  uint64_t prof_count[EMH_PROF_OPS] = {};    // instances seen since profiling was switched on
   struct Timed {
     hipEvent_t a, b;
-    double flop;
+    int op;
+    double units;  // on the instance's last segment
+    bool last;     // the instance's last segment
   };
   std::vector<Timed> timed;
+  struct ProfSum {
+    double ms = 0.0, units = 0.0;
+    uint64_t instances = 0;
+  };
+  ProfSum prof_sum[EMH_PROF_OPS];
   std::vector<hipEvent_t> ev_pool;  // events for the timing, reused across reads
   size_t ev_used = 0;
   hipEvent_t pool_event() {
@@ -172,22 +182,42 @@ namespace emh {
 
 inline dim3 grid1(size_t n, int per) { return dim3((unsigned)((n + per - 1) / per)); }
 
-// Brackets one kernel launch with events when profiling is on.
+// Whether this instance of op is timed (every prof-th instance while profiling is on).
+inline bool prof_take(emh_ctx* c, int op) {
+  return c->prof[op] && c->prof_count[op]++ % (uint64_t)c->prof[op] == 0;
+}
+
+// Brackets a segment of one op instance (one or more launches) with events
+// when `take`; `last` marks the instance's final segment, which carries its
+// algorithmic units.
 struct ProfScope {
   emh_ctx* c;
   hipEvent_t a = nullptr, b = nullptr;
-  double flop;
-  ProfScope(emh_ctx* ctx, double f) : c(ctx), flop(f) {
-    if (!c->prof || c->prof_count++ % (uint64_t)c->prof != 0) return;
+  int op;
+  double units;
+  bool last;
+  ProfScope(emh_ctx* ctx, int op_, double units_, bool take, bool last_ = true)
+      : c(ctx), op(op_), units(units_), last(last_) {
+    if (!take) return;
     a = c->pool_event();
     b = c->pool_event();
     EMH_HIP(hipEventRecord(a, c->stream));
   }
   ~ProfScope() {
-    if (!c->prof || !a) return;
-    if (hipEventRecord(b, c->stream) == hipSuccess) c->timed.push_back({a, b, flop});
+    if (!a) return;
+    if (hipEventRecord(b, c->stream) == hipSuccess) c->timed.push_back({a, b, op, units, last});
   }
 };
+
+// Algorithmic HBM bytes of one scatter_add of `rows` selected rows (row
+// reads, labels, ids when given, sums and counts written, the accumulator
+// read and written when given) and of one ema_update (positions read and
+// written, sums read, masses read and written, counts read).
+inline double scatter_bytes(size_t rows, size_t k, size_t d, bool ids, bool acc) {
+  return 4.0 * ((double)rows * (double)d + (double)rows + (ids ? (double)rows : 0.0) +
+                (double)k * (double)d + (double)k + (acc ? 2.0 * (double)k * (double)d : 0.0));
+}
+inline double ema_bytes(size_t k, size_t d) { return 4.0 * (3.0 * (double)k * (double)d + 4.0 * (double)k); }
 
 // ---- launchers (emh_ops.hip)
 void launch_fill_u32(emh_ctx* c, uint32_t* p, size_t n, uint32_t v);

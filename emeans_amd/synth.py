@@ -6,6 +6,9 @@ inputs. (The reference's own generator is crates/emeans-cluster/src/synth.rs;
 these follow the workload definitions instead.)
 """
 
+import os
+from concurrent.futures import ThreadPoolExecutor
+
 import numpy as np
 
 
@@ -47,13 +50,23 @@ def gmm_zipf(n=200_000, d=768, comps=1024, s=1.1, seed=0, chunk=50_000):
     return x, lab
 
 
-def unit_gaussian(n, d, seed, chunk=100_000):
-    """Rows i.i.d. ~N(0, I) normalised."""
-    g = np.random.default_rng(seed)
+def unit_gaussian(n, d, seed, chunk=65_536, threads=None):
+    """Rows i.i.d. ~N(0, I) normalised. Chunk i of `chunk` rows comes from its
+    own PCG64 stream (SeedSequence(seed).spawn), so the bytes do not depend on
+    how many threads fill the chunks."""
     x = np.empty((n, d), np.float32)
-    for a in range(0, n, chunk):
+    starts = list(range(0, n, chunk))
+    seqs = np.random.SeedSequence(seed).spawn(len(starts))
+
+    def fill(i):
+        a = starts[i]
         b = min(a + chunk, n)
+        g = np.random.Generator(np.random.PCG64(seqs[i]))
         x[a:b] = _unit(g.standard_normal((b - a, d), dtype=np.float32))
+
+    nt = threads or min(16, os.cpu_count() or 1)
+    with ThreadPoolExecutor(max_workers=nt) as ex:
+        list(ex.map(fill, range(len(starts))))
     return x
 
 
@@ -95,3 +108,4 @@ def nested(n=1_000_000, d=768, top=64, sub=16, s=1.3, sub_sigma=0.3, row_sigma=0
         x[a:b] = _unit(subs[lab[a:b]] + np.float32(row_sigma) *
                        g.standard_normal((b - a, d), dtype=np.float32))
     return x, lab
+

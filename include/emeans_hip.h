@@ -246,12 +246,24 @@ uint64_t emh_fallback_rows(emh_ctx* ctx);
  * 0 = exact kernels only (the reference "FP32 kernel alone", emeans-cuda
  * tests/contract.rs:27-37). Results are the same bits in every mode. */
 int emh_set_screen(emh_ctx* ctx, int on);
-/* Time every on-th launch of the MFMA screen kernel (top-1 and top-k) with HIP
- * events on the context's stream (0: off; 1: every launch; a larger period
- * keeps the events' own cost out of the timed work); emh_profile_read waits,
- * sums and resets: total milliseconds, launches timed, and algorithmic FLOP
- * (2 rows k d per timed launch). */
+/* Ops that emh_profile times. */
+#define EMH_PROF_SCREEN 0  /* the MFMA screen kernel of top-1 and top-k; units: 2 rows k d FLOP */
+#define EMH_PROF_SCATTER 1 /* scatter_add (count and ordered-sum launches); units: HBM bytes */
+#define EMH_PROF_EMA 2     /* ema_update; units: HBM bytes */
+#define EMH_PROF_OPS 3
+/* Time every on-th instance of each op above with HIP events on the
+ * context's stream (0: off; 1: every instance; a larger period keeps the
+ * events' own cost out of the timed work). No counterpart in the reference,
+ * whose CUDA backend is profiled externally (.okf/results/cuda-kernels.md);
+ * emh_profile_read_op waits, then returns and resets op's totals: milliseconds,
+ * instances timed, and the algorithmic units they cover (FLOP for the
+ * screen; bytes per the formulas rows d 4 + rows 4 (labels) [+ rows 4 (ids)]
+ * + k d 4 + k 4 [+ 2 k d 4 (acc)] for scatter_add and 3 k d 4 + 4 k 4 for
+ * ema_update). emh_profile_read is emh_profile_read_op for the screen. */
 int emh_profile(emh_ctx* ctx, int on);
+/* The same for one op (EMH_PROF_*), the others unchanged. */
+int emh_profile_op(emh_ctx* ctx, int op, int on);
+int emh_profile_read_op(emh_ctx* ctx, int op, double* ms, uint64_t* instances, double* units);
 int emh_profile_read(emh_ctx* ctx, double* ms, uint64_t* launches, double* flop);
 
 #ifdef __cplusplus
