@@ -71,6 +71,7 @@ SIGNATURES = {
     "emh_buf_ptr": (_vp, [_vp]),
     "emh_buf_len": (_sz, [_vp]),
     "emh_top1": (_i, [_vp, _vp, _sz, _vp, _sz, _sz, _vp, _vp, _sz, _i, _vp, _vp]),
+    "emh_top1_noalloc": (_i, [_vp, _vp, _sz, _vp, _sz, _sz, _vp, _vp, _sz, _i, _vp, _vp]),
     "emh_topk": (_i, [_vp, _vp, _sz, _vp, _sz, _sz, _sz, _i, _vp, _vp]),
     "emh_topk_dev": (_i, [_vp, _vp, _sz, _vp, _sz, _sz, _sz, _i, _vp, _vp]),
     "emh_scatter_add": (_i, [_vp, _vp, _sz, _vp, _sz, _sz, _vp, _sz, _vp, _vp, _vp]),

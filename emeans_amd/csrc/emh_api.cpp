@@ -3,12 +3,44 @@
 // (crates/emeans-core/src/core/cpu.rs) before anything is queued.
 
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "emh_internal.h"
 
 namespace {
 thread_local std::string g_last_error;
+
+// Device scratch of emh_top1_noalloc: one fixed block per GPU, in the code
+// object's device memory, so that the entry point allocates nothing. In host
+// code `scratch` names a host-side stand-in, never the device block: only the
+// address hipGetSymbolAddress gives (per device, kept in g_scratch) may reach
+// a kernel or a copy.
+constexpr size_t SCRATCH_BYTES = size_t(32) << 20;
+static __device__ __align__(256) char scratch[SCRATCH_BYTES];
+constexpr int SCRATCH_DEVICES = 64;
+std::mutex g_scratch_mu;
+char* g_scratch[SCRATCH_DEVICES] = {};
+
+// The device address of `scratch` on `device`, looked up once per device with
+// that device current (emh_create calls this after hipSetDevice).
+char* scratch_setup(int device) {
+  EMH_ENSURE(device >= 0 && device < SCRATCH_DEVICES, "device %d: at most %d devices", device,
+             SCRATCH_DEVICES);
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (!g_scratch[device]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      char m[256];
+      snprintf(m, sizeof m, "hipGetSymbolAddress(scratch) on device %d failed: %s", device,
+               hipGetErrorString(e));
+      throw emh::Failure(m);
+    }
+    g_scratch[device] = (char*)p;
+  }
+  return g_scratch[device];
+}
 
 template <class F>
 int guard(F&& f) {
@@ -112,8 +144,10 @@ int emh_create(int device, emh_ctx** out) {
                p.gcnArchName);
       throw emh::Failure(m);
     }
+    char* block = scratch_setup(device);
     auto* c = new emh_ctx;
     c->device = device;
+    c->scratch = block;
     c->cus = p.multiProcessorCount;
     if (const char* s = getenv("EMEANS_HIP_SCREEN")) {
       const int m = atoi(s);
@@ -289,31 +323,74 @@ void* emh_buf_ptr(const emh_buf* b) { return b ? b->ptr : nullptr; }
 size_t emh_buf_len(const emh_buf* b) { return b ? b->len : 0; }
 
 // ---------------------------------------------------------------------- ops
+}  // extern "C"
+
+namespace {
+// emh_top1's arguments, checked like the reference CPU backend's top1
+// (core/cpu.rs:77-104, assign.rs:121-147).
+struct Top1Call {
+  const float* x;
+  size_t nx;
+  const uint32_t* ids;
+  const float* cents;
+  const float* cn;
+  uint32_t* lab;
+  float* sco;
+};
+Top1Call check_top1(emh_ctx* c, const emh_buf* x, size_t d, const emh_buf* ids, size_t lo,
+                    size_t hi, const emh_buf* cents, const emh_buf* cnorm, size_t k, int metric,
+                    emh_buf* labels, emh_buf* scores) {
+  EMH_ENSURE(c, "null context");
+  EMH_ENSURE(d > 0, "d must be positive");
+  EMH_ENSURE(k > 0, "k must be positive");
+  EMH_ENSURE(metric == EMH_L2 || metric == EMH_IP, "unknown metric");
+  Top1Call t{};
+  t.x = F(x, "x");
+  t.nx = x->len / d;
+  if (ids) t.ids = U(ids, "ids");
+  check_select(ids, lo, hi, t.nx);
+  EMH_ENSURE(cents && F(cents, "centroids") && cents->len >= k * d, "centroids must be k x d");
+  t.cents = (const float*)cents->ptr;
+  if (metric == EMH_L2) {
+    EMH_ENSURE(cnorm != nullptr, "L2 top1 needs the centroid norms");
+    t.cn = F(cnorm, "cnorm");
+    EMH_ENSURE(cnorm->len >= k, "cnorm must have k entries");
+  }
+  t.lab = Um(labels, "labels");
+  t.sco = Fm(scores, "scores");
+  EMH_ENSURE(hi <= labels->len && hi <= scores->len, "outputs too short");
+  return t;
+}
+}  // namespace
+
+extern "C" {
+
 int emh_top1(emh_ctx* c, const emh_buf* x, size_t d, const emh_buf* ids, size_t lo, size_t hi,
              const emh_buf* cents, const emh_buf* cnorm, size_t k, int metric, emh_buf* labels,
              emh_buf* scores) {
   return guard([&] {
-    EMH_ENSURE(c, "null context");
-    EMH_ENSURE(d > 0, "d must be positive");
-    EMH_ENSURE(k > 0, "k must be positive");
-    EMH_ENSURE(metric == EMH_L2 || metric == EMH_IP, "unknown metric");
-    const float* xp = F(x, "x");
-    const size_t nx = x->len / d;
-    if (ids) U(ids, "ids");
-    check_select(ids, lo, hi, nx);
-    EMH_ENSURE(cents && F(cents, "centroids") && cents->len >= k * d, "centroids must be k x d");
-    const float* cn = nullptr;
-    if (metric == EMH_L2) {
-      EMH_ENSURE(cnorm != nullptr, "L2 top1 needs the centroid norms");
-      cn = F(cnorm, "cnorm");
-      EMH_ENSURE(cnorm->len >= k, "cnorm must have k entries");
-    }
-    uint32_t* lab = Um(labels, "labels");
-    float* sco = Fm(scores, "scores");
-    EMH_ENSURE(hi <= labels->len && hi <= scores->len, "outputs too short");
+    const Top1Call t = check_top1(c, x, d, ids, lo, hi, cents, cnorm, k, metric, labels, scores);
     use_device(c);
-    emh::launch_top1(c, xp, nx, d, ids ? (const uint32_t*)ids->ptr : nullptr, lo, hi,
-                     (const float*)cents->ptr, cn, k, metric == EMH_IP, lab, sco);
+    emh::launch_top1(c, t.x, t.nx, d, t.ids, lo, hi, t.cents, t.cn, k, metric == EMH_IP, t.lab,
+                     t.sco);
+  });
+}
+
+int emh_top1_noalloc(emh_ctx* c, const emh_buf* x, size_t d, const emh_buf* ids, size_t lo,
+                     size_t hi, const emh_buf* cents, const emh_buf* cnorm, size_t k, int metric,
+                     emh_buf* labels, emh_buf* scores) {
+  return guard([&] {
+    const Top1Call t = check_top1(c, x, d, ids, lo, hi, cents, cnorm, k, metric, labels, scores);
+    if (hi <= lo) return;
+    const size_t need = emh::top1_scratch_bytes(c, hi - lo, d, k);
+    EMH_ENSURE(need <= SCRATCH_BYTES,
+               "top1_noalloc: %zu rows x k = %zu x d = %zu need %zu bytes of scratch, above the "
+               "fixed %zu",
+               hi - lo, k, d, need, SCRATCH_BYTES);
+    use_device(c);
+    emh::Arena ar{c->scratch, SCRATCH_BYTES, 0};
+    emh::launch_top1(c, t.x, t.nx, d, t.ids, lo, hi, t.cents, t.cn, k, metric == EMH_IP, t.lab,
+                     t.sco, false, &ar);
   });
 }
 

@@ -78,6 +78,21 @@ struct Scratch {
   }
 };
 
+// Where an op takes its per-call device scratch: the context's growing
+// buffers (no Arena), or one fixed block carved in order, 256-byte aligned,
+// with the regions that must start at zero cleared by a fill kernel on every
+// call. Carving past the block's end throws (the callers check the size first).
+struct Arena {
+  char* base = nullptr;
+  size_t cap = 0, used = 0;
+  void* take(size_t bytes) {
+    const size_t at = (used + 255) & ~size_t(255);
+    if (at + bytes > cap) throw Invalid("scratch block too small for this call");
+    used = at + bytes;
+    return base + at;
+  }
+};
+
 // Pinned host memory that grows on demand and is reused by later calls.
 struct Pinned {
   void* ptr = nullptr;
@@ -136,6 +151,7 @@ struct emh_ctx {
   int cus = 256;
   int screen = emh::SCREEN_BF3;
   uint32_t* small = nullptr;  // SW_WORDS u32 on the device
+  char* scratch = nullptr;    // the device's fixed scratch block (emh_top1_noalloc)
   uint64_t fallback_total = 0;
   emh::Scratch cand, fblist, order, start, misc, knn_tmp, xnorm, bigj, chunkcnt, tickets;
   emh::Scratch preview_ticket;  // k_mass_preview's last-block ticket (left at zero)
@@ -267,9 +283,14 @@ void launch_scatter_sums(emh_ctx* c, const float* x, size_t nx, size_t d, const 
 // ---- emh_screen.hip (top-1 and top-k orchestration)
 // words_clear: the caller zeroed the screen's small-block words since the
 // last top-1 (launch_ema with clear_screen_words), so the fill is skipped.
+// ar: take the per-call scratch from this fixed block instead of the
+// context's buffers (no allocation; the call is not profiled).
 void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids, size_t lo, size_t hi,
                  const float* cents, const float* cnorm, size_t k, bool ip, uint32_t* labels,
-                 float* scores, bool words_clear = false);
+                 float* scores, bool words_clear = false, Arena* ar = nullptr);
+// Bytes of fixed-block scratch launch_top1 takes for a call of n rows (an
+// upper bound: each region rounded up to 256 bytes).
+size_t top1_scratch_bytes(emh_ctx* c, size_t n, size_t d, size_t k);
 
 void launch_topk(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,
                  size_t kk, bool exclude_self, uint32_t* ids, float* sims);

@@ -62,48 +62,72 @@ int choose_parts(int row_tiles, int ntiles, int cus, int per_cu = 2) {
 
 }  // namespace
 
+namespace {
+// The screen's launch geometry for n rows against k centroids.
+struct Top1Geom {
+  bool screen, big;
+  int row_tiles, ntiles, parts, tpp;
+};
+Top1Geom top1_geom(emh_ctx* c, size_t n, size_t d, size_t k) {
+  Top1Geom g{};
+  g.screen = c->screen && k >= 64 && d >= 32;
+  if (!g.screen) return g;
+  // The large-tile bf16 screen (one 512-thread block per CU) when d % 4 == 0.
+  g.big = c->screen != SCREEN_F32 && d % 4 == 0;
+  const int TR = g.big ? TR3 : 128;
+  g.row_tiles = (int)((n + TR - 1) / TR);
+  g.ntiles = (int)((k + (g.big ? TC3 : TC) - 1) / (g.big ? TC3 : TC));
+  g.parts = choose_parts(g.row_tiles, g.ntiles, c->cus, g.big ? 1 : 2);
+  g.tpp = (g.ntiles + g.parts - 1) / g.parts;
+  g.parts = (g.ntiles + g.tpp - 1) / g.tpp;
+  return g;
+}
+}  // namespace
+
+size_t top1_scratch_bytes(emh_ctx* c, size_t n, size_t d, size_t k) {
+  const Top1Geom g = top1_geom(c, n, d, k);
+  if (!g.screen) return exact1_scratch_bytes(n, d, k, false);
+  auto r = [](size_t b) { return (b + 255) & ~size_t(255); };
+  return r((size_t)g.parts * n * L1 * sizeof(Cand)) + 2 * r(n * 4) +
+         exact1_scratch_bytes(n, d, k, true);
+}
+
 void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids, size_t lo,
                  size_t hi, const float* cents, const float* cnorm, size_t k, bool ip,
-                 uint32_t* labels, float* scores, bool words_clear) {
+                 uint32_t* labels, float* scores, bool words_clear, Arena* ar) {
   if (hi <= lo) return;
   const size_t n = hi - lo;
   EMH_ENSURE(d <= 16384, "top1: d = %zu above the supported 16384", d);
   EMH_ENSURE(n < (1u << 31) && k < (1u << 31), "top1: shape too large");
-  const bool screen = c->screen && k >= 64 && d >= 32;
-  if (!screen) {
-    launch_exact1(c, x, nx, d, ids, lo, n, nullptr, cents, cnorm, k, ip, labels, scores);
+  const Top1Geom g = top1_geom(c, n, d, k);
+  if (!g.screen) {
+    launch_exact1(c, x, nx, d, ids, lo, n, nullptr, cents, cnorm, k, ip, labels, scores, ar);
     return;
   }
-  // The large-tile bf16 screen (one 512-thread block per CU) when d % 4 == 0.
-  const bool big = c->screen != SCREEN_F32 && d % 4 == 0;
-  const int TR = big ? TR3 : 128;
-  const int row_tiles = (int)((n + TR - 1) / TR);
-  const int ntiles = (int)((k + (big ? TC3 : TC) - 1) / (big ? TC3 : TC));
-  int parts = choose_parts(row_tiles, ntiles, c->cus, big ? 1 : 2);
-  const int tpp = (ntiles + parts - 1) / parts;
-  parts = (ntiles + tpp - 1) / tpp;
-  Cand* cand = (Cand*)c->cand.get((size_t)parts * n * L1 * sizeof(Cand));
-  uint32_t* fb = (uint32_t*)c->fblist.get(n * 4);
-  float* xnorm = (float*)c->xnorm.get(n * 4);
+  const int parts = g.parts, tpp = g.tpp;
+  const size_t cbytes = (size_t)parts * n * L1 * sizeof(Cand);
+  Cand* cand = (Cand*)(ar ? ar->take(cbytes) : c->cand.get(cbytes));
+  uint32_t* fb = (uint32_t*)(ar ? ar->take(n * 4) : c->fblist.get(n * 4));
+  float* xnorm = (float*)(ar ? ar->take(n * 4) : c->xnorm.get(n * 4));
   if (!words_clear)  // fallback count, cmax2, cnmax (the screen fills the maxima)
     launch_fill_u32(c, c->small, 3, 0);
-  const unsigned blocks = (unsigned)(row_tiles * parts);
-  const bool tagged = big && tpp == 1;
+  const unsigned blocks = (unsigned)(g.row_tiles * parts);
+  const bool tagged = g.big && tpp == 1;
   {
     ProfScope prof(c, EMH_PROF_SCREEN, 2.0 * (double)n * (double)k * (double)d,
-                   prof_take(c, EMH_PROF_SCREEN));
-    const ScreenArgs a{blocks, x, nx, d, ids, lo, n, cents, cnorm, k, tpp, parts, ntiles, cand,
+                   !ar && prof_take(c, EMH_PROF_SCREEN));
+    const ScreenArgs a{blocks, x, nx, d, ids, lo, n, cents, cnorm, k, tpp, parts, g.ntiles, cand,
                        xnorm};
     // One tile per part: tagged keys (the cheap fold); more: the sorted
     // insert, which skips most keys once the lists hold good ones.
-    if (big)
+    if (g.big)
       launch_screen3(c, a, ip, tagged);
     else
       launch_screen_t1(c, a, ip);
   }
   launch_verify1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, cand, parts, xnorm, labels, scores,
                  fb, tagged);
-  launch_exact1(c, x, nx, d, ids, lo, n, fb, cents, cnorm, k, ip, labels, scores);
+  launch_exact1(c, x, nx, d, ids, lo, n, fb, cents, cnorm, k, ip, labels, scores, ar);
 }
 
 void launch_topk(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,

@@ -143,9 +143,13 @@ void launch_verifyk(emh_ctx* c, const float* q, size_t m, const float* data, siz
                     float* sims, uint32_t* fb);
 // ---- emh_verify.hip: the exact scans
 // Exact scan of rows `list[0..*count)` (list != nullptr) or positions lo..lo+n.
+// ar: take the scratch from this fixed block (see Arena) instead of the context's buffers.
 void launch_exact1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
                    size_t lo, size_t n, const uint32_t* list, const float* cents,
-                   const float* cnorm, size_t k, bool ip, uint32_t* labels, float* scores);
+                   const float* cnorm, size_t k, bool ip, uint32_t* labels, float* scores,
+                   Arena* ar = nullptr);
+// Fixed-block bytes launch_exact1 takes for n rows (an upper bound).
+size_t exact1_scratch_bytes(size_t n, size_t d, size_t k, bool list);
 void launch_exactk(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,
                    size_t kk, bool exclude_self, const uint32_t* fb, uint32_t* ids, float* sims);
 

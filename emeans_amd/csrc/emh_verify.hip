@@ -576,18 +576,38 @@ __global__ __launch_bounds__(256) void k_exactk(const float* __restrict__ q, int
 
 }  // namespace
 
+size_t exact1_scratch_bytes(size_t n, size_t d, size_t k, bool list) {
+  auto r = [](size_t b) { return (b + 255) & ~size_t(255); };
+  if (list && d % 4 == 0) {
+    const size_t ngr = (n + QR - 1) / QR;
+    return r(n * 8 + ngr * 4) + r(n * 4);
+  }
+  const size_t nch = (k + CJ - 1) / CJ, ngr = (n + RG - 1) / RG;
+  return r(n * nch * sizeof(Cand)) + r(ngr * 4);
+}
+
 void launch_exact1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
                    size_t lo, size_t n, const uint32_t* list, const float* cents,
-                   const float* cnorm, size_t k, bool ip, uint32_t* labels, float* scores) {
+                   const float* cnorm, size_t k, bool ip, uint32_t* labels, float* scores,
+                   Arena* ar) {
   if (n == 0) return;
   // Both kernels read row 0 in place of a row whose id is out of range.
   EMH_ENSURE(nx > 0, "top1: a selection of %zu rows over no data rows", n);
   if (list && d % 4 == 0) {  // queued rows, few: the latency-bound scan
     const size_t ngr = (n + QR - 1) / QR;
     const size_t per = (k + QJ - 1) / QJ + (ip ? 0 : 1);
-    // Self-cleaning: the best words, then the tickets, all left at zero.
-    char* z = (char*)c->tickets.get_zeroed(n * 8 + ngr * 4, c->stream);
-    float* xnq = (float*)c->knn_tmp.get(n * 4);
+    // Self-cleaning: the best words, then the tickets, all left at zero (a
+    // fixed block is cleared on every call instead).
+    char* z;
+    float* xnq;
+    if (ar) {
+      z = (char*)ar->take(n * 8 + ngr * 4);
+      launch_fill_u32(c, (uint32_t*)z, n * 2 + ngr, 0);
+      xnq = (float*)ar->take(n * 4);
+    } else {
+      z = (char*)c->tickets.get_zeroed(n * 8 + ngr * 4, c->stream);
+      xnq = (float*)c->knn_tmp.get(n * 4);
+    }
     const unsigned g = (unsigned)std::min<size_t>(ngr * per, (size_t)2 * c->cus);
     hipLaunchKernelGGL(k_queued1, dim3(g), dim3(64), 0, c->stream, x, nx, (int)d, ids, list,
                        c->small, cents, cnorm, (int)k, ip ? 1 : 0, (unsigned long long*)z,
@@ -597,8 +617,16 @@ void launch_exact1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32
   }
   const size_t nch = (k + CJ - 1) / CJ;
   const size_t ngr = (n + RG - 1) / RG;
-  Cand* partial = (Cand*)c->knn_tmp.get(n * nch * sizeof(Cand));
-  uint32_t* tickets = (uint32_t*)c->tickets.get_zeroed(ngr * 4, c->stream);
+  Cand* partial;
+  uint32_t* tickets;
+  if (ar) {
+    partial = (Cand*)ar->take(n * nch * sizeof(Cand));
+    tickets = (uint32_t*)ar->take(ngr * 4);
+    launch_fill_u32(c, tickets, ngr, 0);
+  } else {
+    partial = (Cand*)c->knn_tmp.get(n * nch * sizeof(Cand));
+    tickets = (uint32_t*)c->tickets.get_zeroed(ngr * 4, c->stream);
+  }
   // Queued rows: the count lives on the device, so the grid covers the worst
   // case. Queued rows are few: a grid of 2 blocks per CU covers them, and
   // blocks past the device-side count exit at once.

@@ -94,6 +94,25 @@ int emh_top1(emh_ctx* ctx, const emh_buf* x, size_t d, const emh_buf* ids, size_
              const emh_buf* centroids, const emh_buf* cnorm, size_t k, int metric,
              emh_buf* labels, emh_buf* scores);
 
+/* emh_top1 that allocates nothing. No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * arguments, checks and results (the same bits) as emh_top1; the per-call
+ * scratch (screen candidate lists, the queue of rows for the exact scan, row
+ * norms, queue words) comes from one fixed 32 MiB block of device memory per
+ * GPU, held until the process ends. The screened path (k >= 64, d >= 32)
+ * takes 40 bytes per row per centroid part (1 to 8 parts, fewer as the call
+ * has more rows) plus about 21 bytes per row: some 500,000 rows per call at
+ * d % 4 == 0; with d % 4 != 0, or without the screen, 8 ceil(k / 64) bytes
+ * per row more. A call whose scratch would exceed the block fails with
+ * EMH_INVALID before anything is queued.
+ * Every call on a GPU shares that GPU's block: calls that overlap on one GPU
+ * (two streams or contexts at once) race, so serialize them. The call is not
+ * timed by emh_profile. */
+int emh_top1_noalloc(emh_ctx* ctx, const emh_buf* x, size_t d, const emh_buf* ids, size_t lo,
+                     size_t hi, const emh_buf* centroids, const emh_buf* cnorm, size_t k,
+                     int metric, emh_buf* labels, emh_buf* scores);
+
 /* Device::topk (core/mod.rs:114-124): best kk (<= 16) data rows per query by
  * inner product, best first (larger score, then lower id); with exclude_self
  * query i is data row i and is skipped; missing: id 0xFFFFFFFF, score -inf.

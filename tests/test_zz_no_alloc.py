@@ -1,0 +1,88 @@
+"""emh_top1_noalloc (top-1 with its scratch in a fixed device block, no
+allocation) against emh_top1 through the C ABI: labels and scores bit-equal,
+on two calls in a row where the second has fewer rows (the block keeps the
+first call's contents), on each top-1 path (the large-tile bf16 screen with
+queued near-tie rows, the 128 x 128 screen with d % 4 != 0 and the exact scan
+alone); and a call whose scratch exceeds the block is refused before anything
+runs."""
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from emeans_amd import _lib
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    from emeans_amd import HipDevice
+    d = HipDevice()
+    yield d
+    d.close()
+
+
+def _call(dev, fn, x, d, ids, lo, hi, cb, cn, k, metric):
+    n_out = len(ids) if ids is not None else x.shape[0]
+    lab = dev.upload_u32(np.full(n_out, 0xFFFFFFFF, np.uint32))
+    sco = dev.upload_f32(np.full(n_out, np.nan, np.float32))
+    xb = dev.bind(x)
+    idb = dev.upload_u32(ids) if ids is not None else None
+    rc = fn(dev._ctx, xb.h, d, idb.h if idb else None, lo, hi, cb.h, cn.h if cn else None, k,
+            _lib.EMH_L2 if metric == "l2" else _lib.EMH_IP, lab.h, sco.h)
+    _lib.check(rc)
+    return dev.read_u32(lab), dev.read_f32(sco)
+
+
+CASES = [
+    # (n first call, n second call, d, k, metric): large-tile screen, 128 x 128
+    # screen (d % 4 != 0), exact scan alone (k < 64)
+    (20_000, 3_000, 768, 1024, "l2"),
+    (5_000, 1_000, 99, 300, "ip"),
+    (4_000, 500, 64, 32, "l2"),
+]
+
+
+@pytest.mark.parametrize("n1,n2,d,k,metric", CASES)
+def test_noalloc_equals_top1_on_two_calls(dev, n1, n2, d, k, metric):
+    lib = _lib.lib()
+    x = O.contract_mixture(n1, d, 60, 0.3, metric == "ip", 29).reshape(n1, d)
+    c = x[(np.arange(k) * 13) % n1].copy()
+    c[k // 2:k // 2 + 16] = c[:16]  # exact duplicates in other tiles: queued rows
+    cb = dev.upload_f32(c)
+    cn = None
+    if metric == "l2":
+        cn = dev.zeros_f32(k)
+        dev.row_norms(cb, k, d, cn)
+    for n in (n1, n2):  # the second call has fewer rows
+        xs = x[:n]
+        ids = ((np.arange(n, dtype=np.uint64) * 7919 + 5) % n).astype(np.uint32)
+        lo, hi = n // 10, n - n // 8
+        ga, gs = _call(dev, lib.emh_top1_noalloc, xs, d, ids, lo, hi, cb, cn, k, metric)
+        wa, ws = _call(dev, lib.emh_top1, xs, d, ids, lo, hi, cb, cn, k, metric)
+        assert np.array_equal(ga, wa), f"n = {n}: labels differ from emh_top1"
+        assert ga[lo:hi].max() < k and np.all(ga[:lo] == 0xFFFFFFFF) and np.all(ga[hi:] == 0xFFFFFFFF)
+        assert gs.tobytes() == ws.tobytes(), f"n = {n}: scores differ from emh_top1"
+        ol = np.full(n, 0xFFFFFFFF, np.uint32)
+        osc = np.full(n, np.nan, np.float32)
+        O.top1(xs, d, c, metric, ids=ids, rows=(lo, hi), labels=ol, scores=osc)
+        assert np.array_equal(ga, ol) and gs.tobytes() == osc.tobytes(), f"n = {n}: oracle"
+
+
+def test_noalloc_refuses_a_call_beyond_its_block(dev):
+    """2,000,000 selected rows against 16,384 centroids at d = 4 (no screen):
+    the exact scan's partials alone would take 4 GB."""
+    lib = _lib.lib()
+    d, k, n = 4, 16_384, 2_000_000
+    x = np.ones((64, d), np.float32)
+    xb, cb = dev.bind(x), dev.upload_f32(np.ones((k, d), np.float32))
+    ids = dev.zeros_u32(n)
+    lab, sco = dev.zeros_u32(n), dev.zeros_f32(n)
+    rc = lib.emh_top1_noalloc(dev._ctx, xb.h, d, ids.h, 0, n, cb.h, None, k, _lib.EMH_IP, lab.h,
+                              sco.h)
+    assert rc == _lib.EMH_INVALID
+    assert b"scratch" in lib.emh_last_error()
+    assert np.all(dev.read_u32(lab, (0, 16)) == 0), "nothing ran"
