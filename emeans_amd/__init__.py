@@ -21,13 +21,14 @@ from typing import List, Optional, Tuple
 import numpy as np
 
 from ._lib import (EMH_IP, EMH_L2, EMH_PROF_EMA, EMH_PROF_SCATTER, EMH_PROF_SCREEN,
-                   Config as _CConfig, EmeansHipError, EmeansHipInvalid, EpochStats as _CEpoch,
-                   TrainOut as _CTrainOut, check, lib)
+                   Config as _CConfig, DedupConfig as _CDedupConfig,
+                   DedupInput as _CDedupInput, DedupResult as _CDedupResult, EmeansHipError,
+                   EmeansHipInvalid, EpochStats as _CEpoch, TrainOut as _CTrainOut, check, lib)
 
 __all__ = [
     "HipDevice", "DevBuf", "EmaStep", "Mat", "Select", "Config", "Emeans", "Trained",
-    "Assignment", "EpochStats", "Neighbors", "DedupConfig", "DedupResult", "knn_self", "knn",
-    "dedup", "make_assigner", "BACKEND_NAME", "EmeansHipError", "EmeansHipInvalid",
+    "Assignment", "EpochStats", "Neighbors", "DedupConfig", "DedupInput", "DedupResult",
+    "knn_self", "knn", "dedup", "dedup_with_neighbors", "make_assigner", "BACKEND_NAME", "EmeansHipError", "EmeansHipInvalid",
     "GPU_KMAX", "NONE",
 ]
 
@@ -501,10 +502,28 @@ def knn(queries, data, d: int, k: int, dev: Optional[HipDevice] = None) -> Neigh
 # ---------------------------------------------------------------------- dedup
 @dataclass
 class DedupConfig:
-    """dedup.rs:39-62 (time and burst inputs are not supported by this backend's host code)."""
+    """dedup.rs:39-62: neighbours per row, link threshold, star threshold
+    (None = sim_threshold) and the largest time gap of a link (None: similarity
+    alone decides)."""
     k: int = 10
     sim_threshold: float = 0.95
     rep_threshold: Optional[float] = None
+    max_gap_secs: Optional[float] = None
+
+    def _c(self):
+        return _CDedupConfig(self.k, self.sim_threshold, int(self.rep_threshold is not None),
+                             float(self.rep_threshold or 0.0), int(self.max_gap_secs is not None),
+                             float(self.max_gap_secs or 0.0))
+
+
+@dataclass
+class DedupInput:
+    """dedup.rs:65-76: optional per-row creation times (NaN = unknown), burst
+    ids (None = no burst; rows of one id always share a group) and
+    representative priorities (higher wins)."""
+    created_unix: Optional[np.ndarray] = None
+    burst: Optional[list] = None
+    priority: Optional[np.ndarray] = None
 
 
 @dataclass
@@ -520,31 +539,73 @@ class DedupResult:
     def n_groups(self):
         return len(self.representatives)
 
+    def anchor(self, g: int) -> int:
+        return int(self.anchors[g]) if len(self.anchors) == len(self.representatives) \
+            else int(self.representatives[g])
+
     def expand(self, rep_labels):
         rep_labels = np.asarray(rep_labels)
         assert len(rep_labels) == len(self.representatives)
         return rep_labels[self.group_of]
 
+    def gather(self, x, d: int):
+        return np.asarray(x, np.float32).reshape(-1, d)[self.representatives].reshape(-1)
 
-def dedup(x, d: int, cfg: DedupConfig = DedupConfig(), priority=None,
-          dev: Optional[HipDevice] = None) -> DedupResult:
-    """Near-duplicate groups of unit rows (dedup.rs:163-183): GPU kNN, host groups."""
-    x = _f32(x).reshape(-1)
-    if d <= 0 or x.size % d:
-        raise ValueError("x must be n x d")
+
+def _dedup_call(fn, n, input, cfg, *lead):
     if not (-1.0 <= cfg.sim_threshold <= 1.0):
         raise ValueError("sim_threshold must be in [-1, 1]")
-    n = x.size // d
-    dev = dev or make_assigner()
-    pr = None if priority is None else _f32(priority)
+    keep = []
+
+    def arr(v, dt, what):
+        if v is None:
+            return None
+        a = np.ascontiguousarray(v, dt)
+        if a.size != n:
+            raise ValueError(f"one {what} per row")
+        keep.append(a)
+        return a.ctypes.data
+
+    inp = input or DedupInput()
+    burst = None if inp.burst is None else [-1 if b is None else int(b) for b in inp.burst]
+    cin = _CDedupInput(arr(inp.created_unix, np.float64, "timestamp"),
+                       arr(burst, np.int64, "burst id"), arr(inp.priority, np.float32, "priority"))
     g = np.zeros(n, np.uint32)
     reps, anchors, sizes = (np.zeros(max(n, 1), np.uint32) for _ in range(3))
     nn = np.zeros(n, np.float32)
-    ng, lp, sc = C.c_size_t(), C.c_size_t(), C.c_size_t()
-    rep_t = cfg.sim_threshold if cfg.rep_threshold is None else cfg.rep_threshold
-    check(lib().emh_dedup(dev._ctx, _p(x), n, d, cfg.k, cfg.sim_threshold, rep_t, _p(pr),
-                          _p(g), _p(reps), _p(anchors), _p(sizes), _p(nn), C.byref(ng),
-                          C.byref(lp), C.byref(sc)))
-    m = ng.value
+    out = _CDedupResult(_p(g), _p(reps), _p(anchors), _p(sizes), _p(nn), 0, 0, 0)
+    ccfg = cfg._c()
+    check(fn(*lead, C.byref(cin), C.byref(ccfg), C.byref(out)))
+    m = out.n_groups
     return DedupResult(g, reps[:m].copy(), anchors[:m].copy(), sizes[:m].copy(), nn,
-                       lp.value, sc.value)
+                       int(out.linked_pairs), int(out.split_components))
+
+
+def dedup(x, d: int, input: Optional[DedupInput] = None, cfg: DedupConfig = DedupConfig(),
+          dev: Optional[HipDevice] = None, priority=None) -> DedupResult:
+    """Near-duplicate groups of unit rows (dedup.rs:163-183): kNN on the GPU,
+    groups on the host. `priority` is a shorthand for DedupInput(priority=...)."""
+    if input is not None and not isinstance(input, DedupInput):
+        raise TypeError("dedup(x, d, input, cfg, ...): input must be a DedupInput")
+    x = _f32(x).reshape(-1)
+    if d <= 0 or x.size % d:
+        raise ValueError("x must be n x d")
+    n = x.size // d
+    if priority is not None:
+        input = DedupInput(*(input.created_unix, input.burst) if input else (None, None), priority)
+    dev = dev or make_assigner()
+    return _dedup_call(lib().emh_dedup, n, input, cfg, dev._ctx, _p(x), n, d)
+
+
+def dedup_with_neighbors(x, d: int, nb: Neighbors, input: Optional[DedupInput] = None,
+                         cfg: DedupConfig = DedupConfig()) -> DedupResult:
+    """dedup with neighbours the caller computed (dedup.rs:186-358); host only."""
+    x = _f32(x).reshape(-1)
+    if d <= 0 or x.size % d:
+        raise ValueError("x must be n x d")
+    n = x.size // d
+    if len(nb) != n:
+        raise ValueError("neighbours must have one row per row of x")
+    ids, sims = _u32(nb.ids), _f32(nb.sims)
+    return _dedup_call(lib().emh_dedup_neighbors, n, input, cfg, _p(x), n, d, _p(ids), _p(sims),
+                       nb.k)

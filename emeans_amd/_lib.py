@@ -45,6 +45,23 @@ class TrainOut(C.Structure):
                 ("fallback_rows", C.c_uint64), ("centroids_dev", C.c_void_p)]
 
 
+class DedupConfig(C.Structure):
+    _fields_ = [("k", C.c_uint64), ("sim_threshold", C.c_float), ("has_rep_threshold", C.c_int),
+                ("rep_threshold", C.c_float), ("has_max_gap_secs", C.c_int),
+                ("max_gap_secs", C.c_double)]
+
+
+class DedupInput(C.Structure):
+    _fields_ = [("created_unix", C.c_void_p), ("burst", C.c_void_p), ("priority", C.c_void_p)]
+
+
+class DedupResult(C.Structure):
+    _fields_ = [("group_of", C.c_void_p), ("representatives", C.c_void_p),
+                ("anchors", C.c_void_p), ("sizes", C.c_void_p), ("nn_sim", C.c_void_p),
+                ("n_groups", C.c_uint64), ("linked_pairs", C.c_uint64),
+                ("split_components", C.c_uint64)]
+
+
 # name: (restype, argtypes). Every function is declared in include/emeans_hip.h.
 _vp, _sz, _i, _u32, _u64, _f, _d = (C.c_void_p, C.c_size_t, C.c_int, C.c_uint32, C.c_uint64,
                                      C.c_float, C.c_double)
@@ -88,10 +105,8 @@ SIGNATURES = {
     "emh_profile_read": (_i, [_vp, C.POINTER(_d), C.POINTER(_u64), C.POINTER(_d)]),
     "emh_profile_read_op": (_i, [_vp, _i, C.POINTER(_d), C.POINTER(_u64), C.POINTER(_d)]),
     "emh_knn": (_i, [_vp, _vp, _sz, _vp, _sz, _sz, _sz, _i, _vp, _vp]),
-    "emh_dedup_neighbors": (_i, [_vp, _sz, _sz, _vp, _vp, _sz, _f, _f, _vp, _vp, _vp, _vp, _vp,
-                                 C.POINTER(_sz), C.POINTER(_sz), C.POINTER(_sz)]),
-    "emh_dedup": (_i, [_vp, _vp, _sz, _sz, _sz, _f, _f, _vp, _vp, _vp, _vp, _vp, _vp,
-                       C.POINTER(_sz), C.POINTER(_sz), C.POINTER(_sz)]),
+    "emh_dedup_neighbors": (_i, [_vp, _sz, _sz, _vp, _vp, _sz, _vp, _vp, _vp]),
+    "emh_dedup": (_i, [_vp, _vp, _sz, _sz, _vp, _vp, _vp]),
     "emh_fallback_rows": (_u64, [_vp]),
     "emh_set_screen": (_i, [_vp, _i]),
     "emh_host_permutation": (None, [_u32, _u64, _vp]),

@@ -10,7 +10,7 @@
 //    epoch statistics run on helper threads;
 //  - assign_all / assign_on (assign.rs:785-809, core/mod.rs:249-330),
 //    knn_self / knn (emeans-cluster/src/knn.rs:17-64) and dedup
-//    (emeans-cluster/src/dedup.rs:163-358).
+//    (emeans-cluster/src/dedup.rs:163-358) with its time and burst rules.
 
 #include <algorithm>
 #include <chrono>
@@ -24,6 +24,7 @@
 #include <memory>
 #include <mutex>
 #include <set>
+#include <unordered_map>
 #include <string>
 #include <thread>
 #include <vector>
@@ -794,7 +795,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   out->fallback_rows = (uint32_t)(h_small[SW_FALLBACK_TOTAL] - h_small0[SW_FALLBACK_TOTAL]);
 }
 
-// dedup_with_neighbors (dedup.rs:186-358) for rows without timestamps or bursts.
+// dedup_with_neighbors (dedup.rs:186-358).
 float dot_seq(const float* a, const float* b, size_t d) {  // dedup.rs:158-160
   float s = 0.0f;
   for (size_t t = 0; t < d; t++) {
@@ -804,82 +805,158 @@ float dot_seq(const float* a, const float* b, size_t d) {  // dedup.rs:158-160
   return s;
 }
 
-size_t dedup_groups(const float* x, size_t n, size_t d, const uint32_t* nb_ids,
-                    const float* nb_sims, size_t kk, float sim_t, float rep_t,
-                    const float* priority, uint32_t* group_of, uint32_t* reps, uint32_t* anchors,
-                    uint32_t* sizes, size_t* linked, size_t* split_components) {
-  std::vector<uint32_t> parent(n);
-  for (size_t i = 0; i < n; i++) parent[i] = (uint32_t)i;
-  auto find = [&](uint32_t i) {
-    while (parent[i] != i) {
-      uint32_t p = parent[i];
-      parent[i] = parent[p];
-      i = p;
+// Disjoint sets whose root is always the lowest row of its set: a union
+// hangs the higher root under the lower (dedup.rs:139-155), so results do
+// not depend on the order of the unions.
+struct LowRootSets {
+  std::vector<uint32_t> up;
+  explicit LowRootSets(size_t n) : up(n) {
+    for (size_t i = 0; i < n; i++) up[i] = (uint32_t)i;
+  }
+  uint32_t root(uint32_t i) {
+    while (up[i] != i) {
+      up[i] = up[up[i]];
+      i = up[i];
     }
     return i;
+  }
+  void join(uint32_t a, uint32_t b) {
+    a = root(a);
+    b = root(b);
+    if (a != b) up[std::max(a, b)] = std::min(a, b);
+  }
+};
+
+// Rows bucketed by a key that is itself a row id (a set's lowest row): for
+// each key in ascending order, its rows in ascending order.
+struct Buckets {
+  std::vector<uint32_t> start, rows;
+  Buckets(const std::vector<uint32_t>& key, size_t n) : start(n + 1, 0), rows(n) {
+    for (size_t i = 0; i < n; i++) start[key[i] + 1]++;
+    for (size_t k = 0; k < n; k++) start[k + 1] += start[k];
+    std::vector<uint32_t> at(start.begin(), start.end() - 1);
+    for (size_t i = 0; i < n; i++) rows[at[key[i]]++] = (uint32_t)i;
+  }
+  size_t size(uint32_t k) const { return start[k + 1] - start[k]; }
+  const uint32_t* begin(uint32_t k) const { return rows.data() + start[k]; }
+  const uint32_t* end(uint32_t k) const { return rows.data() + start[k + 1]; }
+};
+
+struct DedupSide {
+  const double* t = nullptr;
+  const int64_t* burst = nullptr;
+  const float* priority = nullptr;
+  bool gap = false;
+  double max_gap = 0.0;
+};
+
+size_t dedup_groups(const float* x, size_t n, size_t d, const uint32_t* nb_ids,
+                    const float* nb_sims, size_t kk, float sim_t, float rep_t,
+                    const DedupSide& side, uint32_t* group_of, uint32_t* reps, uint32_t* anchors,
+                    uint32_t* sizes, size_t* linked, size_t* split_components) {
+  // A link or a star membership needs the two rows' times within the gap
+  // when both are known (dedup.rs:213-221).
+  auto time_ok = [&](size_t i, size_t j) {
+    if (!side.gap || !side.t || !std::isfinite(side.t[i]) || !std::isfinite(side.t[j]))
+      return true;
+    return std::fabs(side.t[i] - side.t[j]) <= side.max_gap;
   };
-  std::vector<uint32_t> degree(n, 0);
-  std::set<std::pair<uint32_t, uint32_t>> pairs;
+  auto row = [&](size_t i) { return x + i * d; };
+  // Burst units: the rows of one burst id (dedup.rs:224-233).
+  LowRootSets unit(n);
+  if (side.burst) {
+    std::unordered_map<int64_t, uint32_t> first;
+    for (size_t i = 0; i < n; i++)
+      if (side.burst[i] >= 0) unit.join(first.emplace(side.burst[i], (uint32_t)i).first->second,
+                                        (uint32_t)i);
+  }
+  std::vector<uint32_t> unit_of(n);
+  for (size_t i = 0; i < n; i++) unit_of[i] = unit.root((uint32_t)i);
+  // Components: the units, joined by the links that pass the threshold and
+  // the time rule (dedup.rs:234-254). A row's degree counts its distinct links.
+  LowRootSets comp(n);
+  for (size_t i = 0; i < n; i++) comp.join(unit_of[i], (uint32_t)i);
+  std::vector<uint64_t> links;
   for (size_t i = 0; i < n; i++)
     for (size_t t = 0; t < kk; t++) {
       const uint32_t j = nb_ids[i * kk + t];
-      if (j == 0xffffffffu || j >= n || nb_sims[i * kk + t] < sim_t) continue;
-      uint32_t a = find((uint32_t)i), b = find(j);
-      if (a != b) parent[std::max(a, b)] = std::min(a, b);  // lower root wins
-      auto key = std::make_pair(std::min<uint32_t>((uint32_t)i, j), std::max<uint32_t>((uint32_t)i, j));
-      if (pairs.insert(key).second) {
-        degree[i]++;
-        degree[j]++;
-      }
+      if (j == 0xffffffffu || j >= n || nb_sims[i * kk + t] < sim_t || !time_ok(i, j)) continue;
+      comp.join((uint32_t)i, j);
+      const uint64_t a = std::min<uint64_t>(i, j), b = std::max<uint64_t>(i, j);
+      links.push_back(a << 32 | b);
     }
-  std::map<uint32_t, std::vector<uint32_t>> members;
-  for (uint32_t i = 0; i < n; i++) members[find(i)].push_back(i);
+  std::sort(links.begin(), links.end());
+  links.erase(std::unique(links.begin(), links.end()), links.end());
+  std::vector<uint32_t> degree(n, 0);
+  for (uint64_t l : links) {
+    degree[l >> 32]++;
+    degree[l & 0xffffffffu]++;
+  }
+  std::vector<uint32_t> comp_of(n);
+  for (size_t i = 0; i < n; i++) comp_of[i] = comp.root((uint32_t)i);
+  const Buckets members(comp_of, n), units(unit_of, n);
+  // Star cover of each component (dedup.rs:263-309): the untaken row with the
+  // most links (then the lowest id) anchors a group; its own burst unit is in
+  // it whatever the similarity; every other untaken unit joins when all its
+  // rows are within rep_t of the anchor and pass the time rule.
   std::vector<std::pair<std::vector<uint32_t>, uint32_t>> groups;
   size_t split = 0;
   std::vector<char> taken(n, 0);
-  for (auto& kv : members) {
-    const auto& rows = kv.second;
-    if (rows.size() == 1) {
-      groups.push_back({rows, rows[0]});
+  std::vector<uint32_t> comp_units, order;
+  for (uint32_t c0 = 0; c0 < n; c0++) {
+    if (members.size(c0) == 0) continue;
+    if (members.size(c0) == 1) {
+      groups.push_back({{c0}, c0});
       continue;
     }
-    std::vector<uint32_t> ord(rows);
-    std::sort(ord.begin(), ord.end(), [&](uint32_t a, uint32_t b) {
+    comp_units.clear();  // the component's unit roots, ascending
+    order.assign(members.begin(c0), members.end(c0));
+    for (uint32_t r : order)
+      if (unit_of[r] == r) comp_units.push_back(r);
+    std::sort(order.begin(), order.end(), [&](uint32_t a, uint32_t b) {
       return degree[a] != degree[b] ? degree[a] > degree[b] : a < b;
     });
     const size_t before = groups.size();
-    for (uint32_t a : ord) {
-      if (taken[a]) continue;
-      taken[a] = 1;
-      std::vector<uint32_t> g{a};
-      for (uint32_t r : rows) {
-        if (taken[r]) continue;
-        if (dot_seq(x + (size_t)r * d, x + (size_t)a * d, d) >= rep_t) {
-          taken[r] = 1;
-          g.push_back(r);
+    for (uint32_t c : order) {
+      const uint32_t cu = unit_of[c];
+      if (taken[cu]) continue;
+      taken[cu] = 1;
+      std::vector<uint32_t> g(units.begin(cu), units.end(cu));
+      for (uint32_t u : comp_units) {
+        if (taken[u]) continue;
+        bool fits = true;
+        for (const uint32_t* r = units.begin(u); fits && r != units.end(u); ++r)
+          fits = time_ok(*r, c) && dot_seq(row(*r), row(c), d) >= rep_t;
+        if (fits) {
+          taken[u] = 1;
+          g.insert(g.end(), units.begin(u), units.end(u));
         }
       }
       std::sort(g.begin(), g.end());
-      groups.push_back({std::move(g), a});
+      groups.push_back({std::move(g), c});
     }
     if (groups.size() - before > 1) split++;
   }
   std::sort(groups.begin(), groups.end(),
             [](const auto& a, const auto& b) { return a.first[0] < b.first[0]; });
+  // Representatives (dedup.rs:315-340): the highest priority, then the highest
+  // mean similarity to the other members (an f64 sum in member order), then
+  // the lowest id.
   for (size_t gi = 0; gi < groups.size(); gi++) {
     const auto& g = groups[gi].first;
     anchors[gi] = groups[gi].second;
     sizes[gi] = (uint32_t)g.size();
     uint32_t rep = g[0];
-    if (g.size() > 1) {  // priority, then mean similarity, then lowest id
+    if (g.size() > 1) {
       float bp = -INFINITY;
       double bm = -INFINITY;
+      rep = 0xffffffffu;
       for (uint32_t a : g) {
         double s = 0.0;
         for (uint32_t b : g)
-          if (b != a) s += (double)dot_seq(x + (size_t)a * d, x + (size_t)b * d, d);
+          if (b != a) s += (double)dot_seq(row(a), row(b), d);
         const double mean = s / (double)(g.size() - 1);
-        const float p = priority ? priority[a] : 0.0f;
+        const float p = side.priority ? side.priority[a] : 0.0f;
         if (p > bp || (p == bp && mean > bm)) {
           bp = p;
           bm = mean;
@@ -890,7 +967,7 @@ size_t dedup_groups(const float* x, size_t n, size_t d, const uint32_t* nb_ids,
     reps[gi] = rep;
     for (uint32_t r : g) group_of[r] = (uint32_t)gi;
   }
-  *linked = pairs.size();
+  *linked = links.size();
   *split_components = split;
   return groups.size();
 }
@@ -918,6 +995,34 @@ int guard2(F&& f) {
 }  // namespace
 
 using namespace emh::host;
+
+namespace {
+// dedup_with_neighbors' argument checks (dedup.rs:193-211).
+DedupSide check_dedup(const float* x, size_t n, size_t d, const emh_dedup_input* in,
+                      const emh_dedup_config* cfg, const emh_dedup_result* out) {
+  EMH_ENSURE(d > 0, "x must be n x d");
+  EMH_ENSURE(cfg && out, "null argument");
+  EMH_ENSURE(cfg->sim_threshold >= -1.0f && cfg->sim_threshold <= 1.0f,
+             "sim_threshold must be in [-1, 1]");
+  EMH_ENSURE(n == 0 || (x && out->group_of && out->representatives && out->anchors && out->sizes),
+             "null argument");
+  DedupSide s;
+  if (in) {
+    s.t = in->created_unix;
+    s.burst = in->burst;
+    s.priority = in->priority;
+  }
+  if (s.priority)
+    for (size_t i = 0; i < n; i++)
+      EMH_ENSURE(!std::isnan(s.priority[i]), "priority must not be NaN");
+  s.gap = cfg->has_max_gap_secs != 0;
+  s.max_gap = cfg->max_gap_secs;
+  return s;
+}
+float rep_threshold(const emh_dedup_config* cfg) {
+  return cfg->has_rep_threshold ? cfg->rep_threshold : cfg->sim_threshold;
+}
+}  // namespace
 
 extern "C" {
 
@@ -1025,32 +1130,31 @@ int emh_knn(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, s
   return emh_topk(c, q, m, data, n, d, kk, exclude_self, ids, sims);
 }
 
+
 int emh_dedup_neighbors(const float* x, size_t n, size_t d, const uint32_t* nb_ids,
-                        const float* nb_sims, size_t kk, float sim_t, float rep_t,
-                        const float* priority, uint32_t* group_of, uint32_t* reps,
-                        uint32_t* anchors, uint32_t* sizes, size_t* n_groups, size_t* linked,
-                        size_t* split) {
+                        const float* nb_sims, size_t kk, const emh_dedup_input* in,
+                        const emh_dedup_config* cfg, emh_dedup_result* out) {
   return guard2([&] {
-    EMH_ENSURE(d > 0, "x must be n x d");
-    EMH_ENSURE(sim_t >= -1.0f && sim_t <= 1.0f, "sim_threshold must be in [-1, 1]");
-    if (priority)
-      for (size_t i = 0; i < n; i++) EMH_ENSURE(!std::isnan(priority[i]), "priority must not be NaN");
-    EMH_ENSURE(n == 0 || (x && nb_ids && nb_sims && group_of && reps && anchors && sizes),
-               "null argument");
+    const DedupSide s = check_dedup(x, n, d, in, cfg, out);
+    EMH_ENSURE(n == 0 || (kk > 0 && nb_ids && nb_sims), "neighbours must have one row per row of x");
     size_t lp = 0, sc = 0;
-    *n_groups = dedup_groups(x, n, d, nb_ids, nb_sims, kk, sim_t, rep_t, priority, group_of, reps,
-                             anchors, sizes, &lp, &sc);
-    *linked = lp;
-    *split = sc;
+    const size_t g = dedup_groups(x, n, d, nb_ids, nb_sims, kk, cfg->sim_threshold,
+                                  rep_threshold(cfg), s, out->group_of, out->representatives,
+                                  out->anchors, out->sizes, &lp, &sc);
+    if (out->nn_sim)
+      for (size_t i = 0; i < n; i++) out->nn_sim[i] = nb_sims[i * kk];
+    out->n_groups = g;
+    out->linked_pairs = lp;
+    out->split_components = sc;
   });
 }
 
-int emh_dedup(emh_ctx* c, const float* x, size_t n, size_t d, size_t kk, float sim_t, float rep_t,
-              const float* priority, uint32_t* group_of, uint32_t* reps, uint32_t* anchors,
-              uint32_t* sizes, float* nn_sim, size_t* n_groups, size_t* linked, size_t* split) {
+int emh_dedup(emh_ctx* c, const float* x, size_t n, size_t d, const emh_dedup_input* in,
+              const emh_dedup_config* cfg, emh_dedup_result* out) {
   return guard2([&] {
-    EMH_ENSURE(c && d > 0, "bad arguments");
-    size_t k = std::max<size_t>(std::min(kk, n > 0 ? n - 1 : 0), 1);  // dedup.rs:172
+    EMH_ENSURE(c, "null context");
+    check_dedup(x, n, d, in, cfg, out);
+    const size_t k = std::max<size_t>(std::min<size_t>(cfg->k, n > 0 ? n - 1 : 0), 1);  // dedup.rs:172
     std::vector<uint32_t> ids(n * k, 0xffffffffu);
     std::vector<float> sims(n * k, -INFINITY);
     if (n > 1) {
@@ -1058,11 +1162,8 @@ int emh_dedup(emh_ctx* c, const float* x, size_t n, size_t d, size_t kk, float s
       if (emh_topk(c, x, n, x, n, d, k, 1, ids.data(), sims.data()) != EMH_OK)
         throw emh::Failure(emh_last_error());
     }
-    if (emh_dedup_neighbors(x, n, d, ids.data(), sims.data(), k, sim_t, rep_t, priority, group_of,
-                            reps, anchors, sizes, n_groups, linked, split) != EMH_OK)
+    if (emh_dedup_neighbors(x, n, d, ids.data(), sims.data(), k, in, cfg, out) != EMH_OK)
       throw emh::Failure(emh_last_error());
-    if (nn_sim)
-      for (size_t i = 0; i < n; i++) nn_sim[i] = sims[i * k];
   });
 }
 

@@ -219,20 +219,52 @@ int emh_assign_dev(emh_ctx* ctx, const emh_buf* x, size_t n, size_t d, const emh
 int emh_knn(emh_ctx* ctx, const float* queries, size_t m, const float* data, size_t n, size_t d,
             size_t kk, int exclude_self, uint32_t* ids, float* sims);
 
-/* dedup_with_neighbors (emeans-cluster/src/dedup.rs:186-358) on the host, for
- * rows without timestamps or burst ids. Outputs: group_of[n]; representatives,
- * anchors, sizes (capacity n, *n_groups used); linked pairs; split components. */
-int emh_dedup_neighbors(const float* x, size_t n, size_t d, const uint32_t* nb_ids,
-                        const float* nb_sims, size_t kk, float sim_threshold,
-                        float rep_threshold, const float* priority, uint32_t* group_of,
-                        uint32_t* representatives, uint32_t* anchors, uint32_t* sizes,
-                        size_t* n_groups, size_t* linked_pairs, size_t* split_components);
+/* DedupConfig (emeans-cluster/src/dedup.rs:39-62). */
+typedef struct emh_dedup_config {
+  uint64_t k;                /* neighbours searched per row (10) */
+  float sim_threshold;       /* cosine that links two rows (0.95) */
+  int has_rep_threshold;     /* 0: rep_threshold = sim_threshold */
+  float rep_threshold;       /* cosine to the star's anchor needed to join it */
+  int has_max_gap_secs;      /* 0: similarity alone decides */
+  double max_gap_secs;       /* largest time gap of a link when both rows have a time */
+} emh_dedup_config;
 
-/* dedup (dedup.rs:163-183): knn_self on this context, then the host groups. */
-int emh_dedup(emh_ctx* ctx, const float* x, size_t n, size_t d, size_t kk, float sim_threshold,
-              float rep_threshold, const float* priority, uint32_t* group_of,
-              uint32_t* representatives, uint32_t* anchors, uint32_t* sizes, float* nn_sim,
-              size_t* n_groups, size_t* linked_pairs, size_t* split_components);
+/* DedupInput (dedup.rs:65-76): optional per-row side information; each
+ * pointer is NULL or has n entries. */
+typedef struct emh_dedup_input {
+  const double* created_unix; /* creation time (s); NaN = unknown */
+  const int64_t* burst;       /* burst id (the caller's interned id); < 0 = none */
+  const float* priority;      /* representative preference, higher wins; no NaN */
+} emh_dedup_input;
+
+/* DedupResult (dedup.rs:79-102): caller-allocated arrays, group_of and
+ * nn_sim with n entries (nn_sim may be NULL), representatives, anchors and
+ * sizes with capacity n; the counts are written by the call. */
+typedef struct emh_dedup_result {
+  uint32_t* group_of;
+  uint32_t* representatives;
+  uint32_t* anchors;
+  uint32_t* sizes;
+  float* nn_sim;
+  uint64_t n_groups;
+  uint64_t linked_pairs;
+  uint64_t split_components;
+} emh_dedup_result;
+
+/* dedup_with_neighbors (dedup.rs:186-358) on the host: links (cosine >=
+ * sim_threshold and, when both rows have a time and max_gap_secs is set,
+ * |t_i - t_j| <= max_gap_secs), burst units (rows of one burst id always in one
+ * group), union-find components, the star cover (a burst joins an anchor only
+ * when every one of its rows fits; the anchor's own burst is exempt) and the
+ * representatives. nb_ids / nb_sims: kk neighbours per row, as knn_self gives. */
+int emh_dedup_neighbors(const float* x, size_t n, size_t d, const uint32_t* nb_ids,
+                        const float* nb_sims, size_t kk, const emh_dedup_input* input,
+                        const emh_dedup_config* cfg, emh_dedup_result* out);
+
+/* dedup (dedup.rs:163-183): knn_self with k = min(cfg->k, n - 1) (at least 1)
+ * on this context, then the host groups. The GPU keeps at most 16 neighbours. */
+int emh_dedup(emh_ctx* ctx, const float* x, size_t n, size_t d, const emh_dedup_input* input,
+              const emh_dedup_config* cfg, emh_dedup_result* out);
 
 /* ------------------------------------------------- host replay (no device) */
 /* The seeded host-side pieces of the device loop, exported so that callers and

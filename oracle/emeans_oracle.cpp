@@ -22,7 +22,9 @@
 //   top1 / knn                         f64 brute force (non-tie labels exact) and the
 //                                      defining fma chain on small cases
 //   scatter / ema / split / norms      f64 closed forms and the reference's special cases
-//   dedup                              hand-built graphs with known groups
+//   dedup                              the reference's known-answer dedup tests
+//                                      (emeans-cluster/tests/dedup.rs:112-300) on
+//                                      their own data, and hand-built graphs
 
 #include <algorithm>
 #include <cmath>
@@ -783,9 +785,9 @@ int orc_train(const float* x, uint64_t n, const OrcTrainCfg* cfg, OrcTrainOut* o
   return 0;
 }
 
-// --- dedup (crates/emeans-cluster/src/dedup.rs:186-358), no time/burst/priority inputs
-// beyond what the caller passes. Writes group_of[n]; returns the number of groups;
-// representatives/anchors/sizes (capacity n) and linked_pairs / split_components.
+// --- dedup_with_neighbors (crates/emeans-cluster/src/dedup.rs:186-358), with the
+// reference's side inputs: created_unix (NaN = unknown) with max_gap_secs
+// (has_gap), burst ids (burst[i] < 0 = none) and priority (each may be null).
 static float dot_seq(const float* a, const float* b, size_t d) {  // dedup.rs:158-160
   float s = 0.0f;
   for (size_t t = 0; t < d; t++) {
@@ -795,36 +797,60 @@ static float dot_seq(const float* a, const float* b, size_t d) {  // dedup.rs:15
   return s;
 }
 
+namespace {
+struct OrcUnionFind {  // dedup.rs:126-156: lower root wins
+  std::vector<uint32_t> p;
+  explicit OrcUnionFind(size_t n) : p(n) {
+    for (size_t i = 0; i < n; i++) p[i] = (uint32_t)i;
+  }
+  uint32_t find(uint32_t i) {
+    while (p[i] != i) {
+      uint32_t q = p[i];
+      p[i] = p[q];
+      i = q;
+    }
+    return i;
+  }
+  void unite(uint32_t a, uint32_t b) {
+    uint32_t ra = find(a), rb = find(b);
+    if (ra != rb) p[std::max(ra, rb)] = std::min(ra, rb);
+  }
+};
+}  // namespace
+
 uint64_t orc_dedup(const float* x, uint64_t n, uint64_t d, const uint32_t* nb_ids,
                    const float* nb_sims, uint64_t kk, float sim_threshold, float rep_threshold,
-                   const float* priority, uint32_t* group_of, uint32_t* reps, uint32_t* anchors,
-                   uint32_t* sizes, uint64_t* linked_pairs, uint64_t* split_components) {
-  struct UF {
-    std::vector<uint32_t> p;
-    explicit UF(size_t n) : p(n) {
-      for (size_t i = 0; i < n; i++) p[i] = (uint32_t)i;
-    }
-    uint32_t find(uint32_t i) {
-      while (p[i] != i) {
-        uint32_t q = p[i];
-        p[i] = p[q];
-        i = q;
-      }
-      return i;
-    }
-    void unite(uint32_t a, uint32_t b) {
-      uint32_t ra = find(a), rb = find(b);
-      if (ra != rb) p[std::max(ra, rb)] = std::min(ra, rb);
-    }
+                   int has_gap, double max_gap_secs, const double* created_unix,
+                   const int64_t* burst, const float* priority, uint32_t* group_of,
+                   uint32_t* reps, uint32_t* anchors, uint32_t* sizes, uint64_t* linked_pairs,
+                   uint64_t* split_components) {
+  // time_ok (dedup.rs:213-221)
+  auto time_ok = [&](size_t i, size_t j) {
+    if (!has_gap || !created_unix) return true;
+    const double ti = created_unix[i], tj = created_unix[j];
+    if (!std::isfinite(ti) || !std::isfinite(tj)) return true;
+    return std::fabs(ti - tj) <= max_gap_secs;
   };
-  UF comp(n);
+  auto row = [&](size_t i) { return x + i * d; };
+  // Burst units (always together), then link components seeded with them (dedup.rs:224-239).
+  OrcUnionFind unit(n);
+  if (burst) {
+    std::map<int64_t, uint32_t> first;
+    for (size_t i = 0; i < n; i++) {
+      if (burst[i] < 0) continue;
+      auto it = first.emplace(burst[i], (uint32_t)i).first;
+      unit.unite(it->second, (uint32_t)i);
+    }
+  }
+  OrcUnionFind comp(n);
+  for (uint32_t i = 0; i < n; i++) comp.unite(unit.find(i), i);
   std::vector<uint32_t> degree(n, 0);
   std::set<std::pair<uint32_t, uint32_t>> pairs;
-  for (size_t i = 0; i < n; i++)
+  for (size_t i = 0; i < n; i++)  // dedup.rs:240-254
     for (size_t t = 0; t < kk; t++) {
-      uint32_t j = nb_ids[i * kk + t];
-      float s = nb_sims[i * kk + t];
-      if (j == 0xffffffffu || s < sim_threshold) continue;
+      const uint32_t j = nb_ids[i * kk + t];
+      const float s = nb_sims[i * kk + t];
+      if (j == 0xffffffffu || s < sim_threshold || !time_ok(i, j)) continue;
       comp.unite((uint32_t)i, j);
       auto key = std::make_pair((uint32_t)std::min<size_t>(i, j), (uint32_t)std::max<size_t>(i, j));
       if (pairs.insert(key).second) {
@@ -832,43 +858,59 @@ uint64_t orc_dedup(const float* x, uint64_t n, uint64_t d, const uint32_t* nb_id
         degree[j]++;
       }
     }
+  // Members of each component in row order; each row's burst unit (dedup.rs:256-261).
   std::map<uint32_t, std::vector<uint32_t>> members;
   for (uint32_t i = 0; i < n; i++) members[comp.find(i)].push_back(i);
+  std::vector<uint32_t> unit_of(n);
+  for (uint32_t i = 0; i < n; i++) unit_of[i] = unit.find(i);
+  // Star cover (dedup.rs:263-309).
   std::vector<std::pair<std::vector<uint32_t>, uint32_t>> groups;
   size_t split = 0;
   for (auto& kv : members) {
-    auto& rows = kv.second;
+    const std::vector<uint32_t>& rows = kv.second;
     if (rows.size() == 1) {
       groups.push_back({rows, rows[0]});
       continue;
     }
-    std::vector<uint32_t> ord = rows;
-    std::sort(ord.begin(), ord.end(), [&](uint32_t a, uint32_t b) {
+    std::map<uint32_t, std::vector<uint32_t>> units;
+    for (uint32_t r : rows) units[unit_of[r]].push_back(r);
+    std::vector<uint32_t> order = rows;
+    std::sort(order.begin(), order.end(), [&](uint32_t a, uint32_t b) {
       if (degree[a] != degree[b]) return degree[a] > degree[b];
       return a < b;
     });
     std::set<uint32_t> taken;
-    size_t before = groups.size();
-    for (uint32_t c : ord) {
-      if (taken.count(c)) continue;
-      taken.insert(c);
-      std::vector<uint32_t> g{c};
-      for (uint32_t r : rows) {  // units are single rows without burst ids
-        if (taken.count(r)) continue;
-        if (dot_seq(x + (size_t)r * d, x + (size_t)c * d, d) >= rep_threshold) {
-          taken.insert(r);
-          g.push_back(r);
-        }
+    const size_t before = groups.size();
+    for (uint32_t c : order) {
+      const uint32_t cu = unit_of[c];
+      if (taken.count(cu)) continue;
+      taken.insert(cu);
+      std::vector<uint32_t> g = units[cu];
+      std::vector<uint32_t> rest;
+      for (auto& u : units)
+        if (!taken.count(u.first)) rest.push_back(u.first);
+      std::vector<bool> joins;
+      for (uint32_t u : rest) {  // every row of a unit must fit the anchor
+        bool all = true;
+        for (uint32_t r : units[u])
+          all = all && time_ok(r, c) && dot_seq(row(r), row(c), d) >= rep_threshold;
+        joins.push_back(all);
       }
+      for (size_t q = 0; q < rest.size(); q++)
+        if (joins[q]) {
+          taken.insert(rest[q]);
+          g.insert(g.end(), units[rest[q]].begin(), units[rest[q]].end());
+        }
       std::sort(g.begin(), g.end());
       groups.push_back({g, c});
     }
     if (groups.size() - before > 1) split++;
   }
-  std::sort(groups.begin(), groups.end(),
-            [](const auto& a, const auto& b) { return a.first[0] < b.first[0]; });
+  std::stable_sort(groups.begin(), groups.end(),
+                   [](const auto& a, const auto& b) { return a.first[0] < b.first[0]; });
+  // Representatives: priority, then mean similarity, then lowest id (dedup.rs:315-340).
   for (size_t gi = 0; gi < groups.size(); gi++) {
-    auto& g = groups[gi].first;
+    const std::vector<uint32_t>& g = groups[gi].first;
     anchors[gi] = groups[gi].second;
     sizes[gi] = (uint32_t)g.size();
     uint32_t rep = g[0];
@@ -879,9 +921,9 @@ uint64_t orc_dedup(const float* x, uint64_t n, uint64_t d, const uint32_t* nb_id
       for (uint32_t a : g) {
         double sum = 0.0;
         for (uint32_t b : g)
-          if (b != a) sum += (double)dot_seq(x + (size_t)a * d, x + (size_t)b * d, d);
-        double mean = sum / (double)(g.size() - 1);
-        float p = priority ? priority[a] : 0.0f;
+          if (b != a) sum += (double)dot_seq(row(a), row(b), d);
+        const double mean = sum / (double)(g.size() - 1);
+        const float p = priority ? priority[a] : 0.0f;
         if (p > bp || (p == bp && mean > bm)) {
           bp = p;
           bm = mean;

@@ -53,8 +53,9 @@ def _load():
         "orc_set_threads": (None, [i32]),
         "orc_get_threads": (i32, []),
         "orc_train": (i32, [_f32p, u64, vp, vp]),
-        "orc_dedup": (u64, [_f32p, u64, u64, _u32p, _f32p, u64, C.c_float, C.c_float, vp,
-                            _u32p, _u32p, _u32p, _u32p, C.POINTER(u64), C.POINTER(u64)]),
+        "orc_dedup": (u64, [_f32p, u64, u64, _u32p, _f32p, u64, C.c_float, C.c_float, i32, f64,
+                            vp, vp, vp, _u32p, _u32p, _u32p, _u32p, C.POINTER(u64),
+                            C.POINTER(u64)]),
         "orc_contract_mixture": (None, [u64, u64, u64, f64, i32, u32, _f32p]),
         "orc_common_mixture": (None, [u64, u64, u64, C.c_float, i32, u32, _f32p]),
     }
@@ -281,7 +282,10 @@ def mean_objective(scores, spherical):
 
 
 # -------------------------------------------------------------------- dedup
-def dedup(x, d, nb_ids, nb_sims, kk, sim_threshold, rep_threshold=None, priority=None):
+def dedup(x, d, nb_ids, nb_sims, kk, sim_threshold, rep_threshold=None, priority=None,
+          created_unix=None, max_gap_secs=None, burst=None):
+    """dedup_with_neighbors (dedup.rs:186-358). burst: one id per row, negative
+    (or None entries) for rows without one; created_unix: NaN = unknown."""
     x = np.ascontiguousarray(x, np.float32)
     n = x.size // d
     group_of = np.zeros(n, np.uint32)
@@ -290,10 +294,14 @@ def dedup(x, d, nb_ids, nb_sims, kk, sim_threshold, rep_threshold=None, priority
     sizes = np.zeros(n, np.uint32)
     lp, sc = C.c_uint64(), C.c_uint64()
     pr = None if priority is None else np.ascontiguousarray(priority, np.float32)
+    tm = None if created_unix is None else np.ascontiguousarray(created_unix, np.float64)
+    bu = None if burst is None else np.array([-1 if b is None else b for b in burst], np.int64)
     g = lib.orc_dedup(x, n, d, np.ascontiguousarray(nb_ids, np.uint32),
                       np.ascontiguousarray(nb_sims, np.float32), kk, float(sim_threshold),
-                      float(sim_threshold if rep_threshold is None else rep_threshold), _ptr(pr),
-                      group_of, reps, anchors, sizes, C.byref(lp), C.byref(sc))
+                      float(sim_threshold if rep_threshold is None else rep_threshold),
+                      int(max_gap_secs is not None), float(max_gap_secs or 0.0), _ptr(tm),
+                      _ptr(bu), _ptr(pr), group_of, reps, anchors, sizes, C.byref(lp),
+                      C.byref(sc))
     return {"group_of": group_of, "representatives": reps[:g], "anchors": anchors[:g],
             "sizes": sizes[:g], "linked_pairs": lp.value, "split_components": sc.value}
 

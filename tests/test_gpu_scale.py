@@ -81,7 +81,7 @@ def test_knn_self_and_dedup_500k_x_384(dev):
     # The injected duplicates sit above the threshold: each one's source is a neighbour.
     assert np.mean((gi[dst] == src[:, None]).any(axis=1)) > 0.999
     # dedup through the full path (kNN on the GPU from host rows, groups on the host).
-    r = dedup(xh, d, DedupConfig(k=kk, sim_threshold=0.97), dev=dev)
+    r = dedup(xh, d, cfg=DedupConfig(k=kk, sim_threshold=0.97), dev=dev)
     assert np.array_equal(r.nn_sim, gsm[:, 0]), "dedup's kNN differs from topk_dev's"
     want = O.dedup(xh, d, gi.reshape(-1), gsm.reshape(-1), kk, 0.97)
     assert np.array_equal(r.group_of, want["group_of"])

@@ -117,7 +117,7 @@ def test_knn_self_and_dedup(dev):
     nb = knn_self(x, 96, 10, dev)
     oi, osims = O.knn(x, x, 96, 10, True)
     assert np.array_equal(nb.ids, oi) and nb.sims.tobytes() == osims.tobytes()
-    r = dedup(x, 96, DedupConfig(k=10, sim_threshold=0.97), dev=dev)
+    r = dedup(x, 96, cfg=DedupConfig(k=10, sim_threshold=0.97), dev=dev)
     want = O.dedup(x, 96, oi, osims, 10, 0.97)
     assert np.array_equal(r.group_of, want["group_of"])
     assert np.array_equal(r.representatives, want["representatives"])
@@ -153,3 +153,40 @@ def test_assign_host_buffers_in_chunks(dev, metric):
     ol, osc = O.assign(x, d, c, metric)
     assert np.array_equal(gl, ol)
     assert gs.tobytes() == osc.tobytes()
+
+
+def test_dedup_bursts_time_gap_priority(dev):
+    """dedup with every side input on the GPU's kNN: the reference's nested
+    data (6,000 x 128) plus 300 bursts of perturbed copies one second apart
+    (synth.rs:215-248), burst ids on each source and its copies, creation times
+    (5% unknown) under a one-minute gap, and random priorities. The whole result
+    equals the oracle's grouping of the same neighbours, and the groups are the
+    injected bursts."""
+    from emeans_amd import DedupConfig, DedupInput, dedup
+
+    from .ref_synth import nested, with_bursts
+    d = 128
+    x, _, _ = nested(n=6000, d=d, n_broad=8, sub_range=(2, 4), seed=21)
+    wx, truth, created = with_bursts(x, d, 300, (1, 6), 0.143, 5)
+    n = wx.shape[0]
+    g = np.random.default_rng(3)
+    created[g.choice(n, n // 20, replace=False)] = np.nan
+    counts = np.bincount(truth, minlength=n)
+    burst = [int(truth[i]) if counts[truth[i]] > 1 else None for i in range(n)]
+    pr = g.random(n).astype(np.float32)
+    inp = DedupInput(created_unix=created, burst=burst, priority=pr)
+    cfg = DedupConfig(k=10, sim_threshold=0.95, max_gap_secs=60.0)
+    r = dedup(wx, d, inp, cfg, dev=dev)
+    ids, sims = O.knn(wx, wx, d, 10, True)
+    assert np.array_equal(r.nn_sim, sims.reshape(n, 10)[:, 0])
+    want = O.dedup(wx, d, ids, sims, 10, 0.95, priority=pr, created_unix=created,
+                   max_gap_secs=60.0, burst=burst)
+    assert np.array_equal(r.group_of, want["group_of"])
+    assert np.array_equal(r.representatives, want["representatives"])
+    assert np.array_equal(r.anchors, want["anchors"])
+    assert np.array_equal(r.sizes, want["sizes"])
+    assert r.linked_pairs == want["linked_pairs"]
+    assert r.split_components == want["split_components"]
+    assert r.n_groups() == x.shape[0]
+    pairs = set(zip(truth.tolist(), r.group_of.tolist()))
+    assert len(pairs) == r.n_groups(), "groups differ from the injected bursts"

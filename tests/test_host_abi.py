@@ -138,6 +138,9 @@ def test_host_revival_plan_and_pairwise_sum_match_the_oracle(lib):
 
 
 def test_dedup_neighbors_matches_the_oracle(lib):
+    """The host grouping with every side input: priorities, creation times
+    (some unknown) under a time gap, and burst ids, against the oracle."""
+    from emeans_amd import DedupConfig, DedupInput, Neighbors, dedup_with_neighbors
     g = np.random.default_rng(11)
     n, d, kk = 400, 16, 5
     x = g.standard_normal((n, d)).astype(np.float32)
@@ -147,33 +150,54 @@ def test_dedup_neighbors_matches_the_oracle(lib):
     x /= np.linalg.norm(x, axis=1, keepdims=True)
     ids, sims = O.knn(x, x, d, kk, True)
     pr = g.random(n).astype(np.float32)
-    for priority in (None, pr):
-        want = O.dedup(x, d, ids, sims, kk, 0.97, priority=priority)
-        group_of, reps, anchors, sizes = (np.zeros(n, np.uint32) for _ in range(4))
-        ng, lp, sc = C.c_size_t(), C.c_size_t(), C.c_size_t()
-        rc = lib.emh_dedup_neighbors(
-            x.ctypes.data, n, d, ids.ctypes.data, sims.ctypes.data, kk, 0.97, 0.97,
-            None if priority is None else priority.ctypes.data, group_of.ctypes.data,
-            reps.ctypes.data, anchors.ctypes.data, sizes.ctypes.data, C.byref(ng), C.byref(lp),
-            C.byref(sc))
-        assert rc == _lib.EMH_OK
-        assert group_of.tolist() == want["group_of"].tolist()
-        assert reps[: ng.value].tolist() == want["representatives"].tolist()
-        assert anchors[: ng.value].tolist() == want["anchors"].tolist()
-        assert sizes[: ng.value].tolist() == want["sizes"].tolist()
-        assert (lp.value, sc.value) == (want["linked_pairs"], want["split_components"])
-        assert ng.value < n  # the injected duplicates merged
+    t = g.uniform(0, 600, n)
+    t[g.choice(n, 40, replace=False)] = np.nan
+    burst = [None] * n
+    for b, rows in enumerate(np.array_split(g.choice(n, 90, replace=False), 30)):
+        for r in rows:
+            burst[r] = b
+    cases = [(DedupInput(), DedupConfig(sim_threshold=0.97)),
+             (DedupInput(priority=pr), DedupConfig(sim_threshold=0.97)),
+             (DedupInput(created_unix=t), DedupConfig(sim_threshold=0.97, max_gap_secs=120.0)),
+             (DedupInput(burst=burst, priority=pr),
+              DedupConfig(sim_threshold=0.97, rep_threshold=0.98)),
+             (DedupInput(created_unix=t, burst=burst),
+              DedupConfig(sim_threshold=0.96, max_gap_secs=200.0))]
+    for inp, cfg in cases:
+        want = O.dedup(x, d, ids, sims, kk, cfg.sim_threshold, cfg.rep_threshold,
+                       priority=inp.priority, created_unix=inp.created_unix,
+                       max_gap_secs=cfg.max_gap_secs, burst=inp.burst)
+        r = dedup_with_neighbors(x, d, Neighbors(kk, ids, sims), inp, cfg)
+        assert r.group_of.tolist() == want["group_of"].tolist()
+        assert r.representatives.tolist() == want["representatives"].tolist()
+        assert r.anchors.tolist() == want["anchors"].tolist()
+        assert r.sizes.tolist() == want["sizes"].tolist()
+        assert (r.linked_pairs, r.split_components) == (want["linked_pairs"],
+                                                        want["split_components"])
+        assert r.n_groups() < n  # the injected duplicates merged
+        if inp.burst is not None:  # rows of one burst share a group
+            for b in range(30):
+                rows = [i for i in range(n) if burst[i] == b]
+                assert len(set(r.group_of[rows].tolist())) == 1
 
 
 def test_dedup_neighbors_rejects_bad_arguments(lib):
+    from emeans_amd import DedupConfig, DedupInput, EmeansHipInvalid, Neighbors, \
+        dedup_with_neighbors
+    from emeans_amd._lib import DedupConfig as CCfg, DedupInput as CIn, DedupResult as COut
     x = np.zeros((2, 4), np.float32)
     ids = np.zeros(2, np.uint32)
     sims = np.zeros(2, np.float32)
     out = [np.zeros(2, np.uint32) for _ in range(4)]
-    ng, lp, sc = C.c_size_t(7), C.c_size_t(), C.c_size_t()
-    rc = lib.emh_dedup_neighbors(x.ctypes.data, 2, 4, ids.ctypes.data, sims.ctypes.data, 1, 1.5,
-                                 1.5, None, *[o.ctypes.data for o in out], C.byref(ng),
-                                 C.byref(lp), C.byref(sc))
+    res = COut(*[o.ctypes.data for o in out], None, 7, 0, 0)
+    cfg = CCfg(10, 1.5, 0, 0.0, 0, 0.0)
+    rc = lib.emh_dedup_neighbors(x.ctypes.data, 2, 4, ids.ctypes.data, sims.ctypes.data, 1,
+                                 C.byref(CIn()), C.byref(cfg), C.byref(res))
     assert rc == _lib.EMH_INVALID
     assert b"sim_threshold" in lib.emh_last_error()
-    assert ng.value == 7, "no out-parameter is written on failure"
+    assert res.n_groups == 7, "no out-parameter is written on failure"
+    nb = Neighbors(1, ids, sims)
+    with pytest.raises(EmeansHipInvalid, match="priority"):
+        dedup_with_neighbors(x, 4, nb, DedupInput(priority=np.array([0, np.nan], np.float32)))
+    with pytest.raises(ValueError, match="one timestamp per row"):
+        dedup_with_neighbors(x, 4, nb, DedupInput(created_unix=np.zeros(3)), DedupConfig())
