@@ -23,7 +23,8 @@ import numpy as np
 from ._lib import (EMH_IP, EMH_L2, EMH_PROF_EMA, EMH_PROF_SCATTER, EMH_PROF_SCREEN,
                    Config as _CConfig, DedupConfig as _CDedupConfig,
                    DedupInput as _CDedupInput, DedupResult as _CDedupResult, EmeansHipError,
-                   EmeansHipInvalid, EpochStats as _CEpoch, TrainOut as _CTrainOut, check, lib)
+                   EmeansHipInvalid, EpochStats as _CEpoch, TrainInit as _CTrainInit,
+                   TrainOut as _CTrainOut, check, lib)
 
 __all__ = [
     "HipDevice", "DevBuf", "EmaStep", "Mat", "Select", "Config", "Emeans", "Trained",
@@ -241,9 +242,12 @@ class HipDevice:
         check(lib().emh_assign_dev(self._ctx, x.h, n, d, centroids.h, k, _metric(metric), chunk,
                                    labels.h, scores.h))
 
-    def train_dev(self, x: DevBuf, n: int, config: "Config", centroids_out: Optional[DevBuf] = None):
+    def train_dev(self, x: DevBuf, n: int, config: "Config", centroids_out: Optional[DevBuf] = None,
+                  init=None, state=None):
         """Emeans::train on data already bound to the device; returns (centroids, info).
-        With centroids_out (a k*d f32 buffer) the centroids also stay on the device."""
+        init: initial centroids (k*d host array or DevBuf; train_from); state:
+        (positions, usage) EMA state (train_resume). With centroids_out (a k*d
+        f32 buffer) the centroids also stay on the device."""
         k, d = config.k, config.d
         cent = np.empty(k * d, np.float32)
         pos = np.empty(k * d, np.float32)
@@ -253,7 +257,9 @@ class HipDevice:
         out = _CTrainOut(_p(cent), _p(pos), _p(usage), _p(labels), C.addressof(stats), 64)
         out.centroids_dev = centroids_out.h if centroids_out is not None else None
         ccfg = config._c()
-        check(lib().emh_train_dev(self._ctx, x.h, n, C.byref(ccfg), C.byref(out)))
+        cin, keep = _train_init(k, d, init, state)
+        check(lib().emh_train_dev(self._ctx, x.h, n, C.byref(ccfg), cin, C.byref(out)))
+        del keep
         info = {"stats": [EpochStats(stats[e].obj, stats[e].time, stats[e].imbalance_factor,
                                      int(stats[e].nsplit)) for e in range(out.n_epochs)],
                 "n_splits": int(out.n_splits), "batch_size": int(out.batch_size),
@@ -290,6 +296,27 @@ class HipDevice:
         check (default), 2 = f32 MFMA screen + exact check, 0 or False = the
         exact kernels alone. Every mode gives the same bits."""
         check(lib().emh_set_screen(self._ctx, int(mode)))
+
+
+def _train_init(k, d, init, state):
+    """The emh_train_init of a run (or None) and the arrays it points into."""
+    if init is None and state is None:
+        return None, []
+    if init is not None and state is not None:
+        raise ValueError("give initial centroids or EMA state, not both")
+    if isinstance(init, DevBuf):
+        return C.byref(_CTrainInit(None, init.h, None, None)), [init]
+    if init is not None:
+        c = _f32(init).reshape(-1)
+        if c.size != k * d:
+            raise ValueError("init centroids must be k x d")
+        return C.byref(_CTrainInit(_p(c), None, None, None)), [c]
+    pos, usage = (_f32(v).reshape(-1) for v in state)
+    if pos.size != k * d:
+        raise ValueError("positions must be k x d")
+    if usage.size != k:
+        raise ValueError("usage must have k entries")
+    return C.byref(_CTrainInit(None, None, _p(pos), _p(usage))), [pos, usage]
 
 
 def make_assigner(backend: str = BACKEND_NAME, device: int = 0) -> HipDevice:
@@ -395,20 +422,36 @@ class Emeans:
         return np.sort(keep[: m * self.config.k])
 
     def train(self, x) -> Trained:
+        """Sample k initial centroids, train, close with exact means (model.rs:700-703)."""
+        return self.train_from(x, None)
+
+    def train_from(self, x, init=None) -> Trained:
+        """train with given initial centroids (k x d; model.rs:705-736)."""
         self._require_ok()
         try:
-            return self._train(x)
+            return self._train(x, init=init)
         except Exception:
             self.failed = True
             raise
 
-    def _train(self, x) -> Trained:
+    def train_resume(self, x) -> Trained:
+        """Continue from the saved EMA state on x, new or grown data (model.rs:739-749)."""
+        self._require_ok()
+        if self._usage is None:
+            raise RuntimeError("no EMA state to resume from")
+        try:
+            return self._train(x, state=(self._positions, self._usage))
+        except Exception:
+            self.failed = True
+            raise
+
+    def _train(self, x, init=None, state=None) -> Trained:
         cfg = self.config
         x = _f32(x).reshape(-1)
         if x.size % cfg.d:
             raise ValueError("x must be n x d")
         n = x.size // cfg.d
-        keep = self.training_subset(n)
+        keep = self.training_subset(n) if state is None else None  # resume: all rows
         xs = x if keep is None else x.reshape(n, cfg.d)[keep].reshape(-1)
         m = xs.size // cfg.d
         k, d = cfg.k, cfg.d
@@ -419,7 +462,9 @@ class Emeans:
         stats = (_CEpoch * 64)()
         out = _CTrainOut(_p(cent), _p(pos), _p(usage), _p(labels), C.addressof(stats), 64)
         ccfg = cfg._c()
-        check(lib().emh_train(self.dev._ctx, _p(xs), m, C.byref(ccfg), C.byref(out)))
+        cin, hold = _train_init(k, d, init, state)
+        check(lib().emh_train(self.dev._ctx, _p(xs), m, C.byref(ccfg), cin, C.byref(out)))
+        del hold
         self._centroids, self._positions, self._usage = cent, pos, usage
         self._stats = [EpochStats(stats[e].obj, stats[e].time, stats[e].imbalance_factor,
                                   int(stats[e].nsplit)) for e in range(out.n_epochs)]

@@ -45,6 +45,11 @@ class TrainOut(C.Structure):
                 ("fallback_rows", C.c_uint64), ("centroids_dev", C.c_void_p)]
 
 
+class TrainInit(C.Structure):
+    _fields_ = [("centroids", C.c_void_p), ("centroids_dev", C.c_void_p),
+                ("positions", C.c_void_p), ("usage", C.c_void_p)]
+
+
 class DedupConfig(C.Structure):
     _fields_ = [("k", C.c_uint64), ("sim_threshold", C.c_float), ("has_rep_threshold", C.c_int),
                 ("rep_threshold", C.c_float), ("has_max_gap_secs", C.c_int),
@@ -96,8 +101,8 @@ SIGNATURES = {
     "emh_normalize_rows": (_i, [_vp, _vp, _sz, _sz, _vp]),
     "emh_split": (_i, [_vp, _vp, _vp, _vp, _sz, _sz]),
     "emh_ema_update": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _f, _f, _i]),
-    "emh_train": (_i, [_vp, _vp, _sz, _vp, _vp]),
-    "emh_train_dev": (_i, [_vp, _vp, _sz, _vp, _vp]),
+    "emh_train": (_i, [_vp, _vp, _sz, _vp, _vp, _vp]),
+    "emh_train_dev": (_i, [_vp, _vp, _sz, _vp, _vp, _vp]),
     "emh_assign": (_i, [_vp, _vp, _sz, _sz, _vp, _sz, _i, _sz, _vp, _vp]),
     "emh_assign_dev": (_i, [_vp, _vp, _sz, _sz, _vp, _sz, _i, _sz, _vp, _vp]),
     "emh_profile": (_i, [_vp, _i]),

@@ -450,6 +450,25 @@ void copy_async(emh_ctx* c, void* dst, const void* src, size_t bytes, hipMemcpyK
   if (bytes) EMH_HIP(hipMemcpyAsync(dst, src, bytes, kind, c->stream));
 }
 
+// The start's arguments (model.rs:306-336): one kind of start, the right
+// shapes, masses finite and >= 0.
+void check_init(const emh_config* cfg, const emh_train_init* init) {
+  if (!init) return;
+  const int kinds = (init->centroids != nullptr) + (init->centroids_dev != nullptr) +
+                    (init->positions != nullptr);
+  EMH_ENSURE(kinds <= 1, "give initial centroids or EMA state, not both");
+  EMH_ENSURE(!init->usage || init->positions, "usage comes with positions");
+  if (init->centroids_dev)
+    EMH_ENSURE(init->centroids_dev->kind == 0 && init->centroids_dev->len == cfg->k * cfg->d,
+               "init centroids must be k x d");
+  if (init->positions) {
+    EMH_ENSURE(init->usage, "positions need their usage (k masses)");
+    for (size_t j = 0; j < cfg->k; j++)
+      EMH_ENSURE(std::isfinite(init->usage[j]) && init->usage[j] >= 0.0f,
+                 "usage must be finite and >= 0");
+  }
+}
+
 void check_cfg(size_t n, const emh_config* cfg, const emh_train_out* out) {
   EMH_ENSURE(cfg && out && out->centroids, "null argument");
   EMH_ENSURE(!out->centroids_dev ||
@@ -478,7 +497,7 @@ void check_cfg(size_t n, const emh_config* cfg, const emh_train_out* out) {
 // wait for them on a helper thread; the next epoch's order is drawn on
 // another and copied in from a pinned buffer.
 void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
-               emh_train_out* out) {
+               const emh_train_init* init, emh_train_out* out) {
   const auto t_start = std::chrono::steady_clock::now();
   const size_t k = cfg.k, d = cfg.d;
   const bool sph = cfg.spherical != 0;
@@ -556,24 +575,37 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   // The first epoch's order is drawn while the initial centroids are (model.rs:783-784).
   std::future<void> next = beside([&] { fill_order(0); });
 
-  // Initial centroids: the rows permutation(n)[..k] (model.rs:786-797),
-  // normalized when spherical (model.rs:306-315), masses INIT_USAGE (recipe.rs:14).
-  if (n == k) {
-    EMH_HIP(hipMemcpyAsync(pos.p, x, k * d * 4, hipMemcpyDeviceToDevice, c->stream));
+  // The start (model.rs:772-797): saved EMA state as it is (begin_with_state);
+  // else initial centroids, given (begin) or the rows permutation(n)[..k],
+  // normalized when spherical (model.rs:306-316), masses INIT_USAGE
+  // (recipe.rs:14).
+  const bool resume = init && init->positions;
+  if (resume) {
+    h2d(c, pos.p, init->positions, k * d * 4);
+    h2d(c, mass.p, init->usage, k * 4);
   } else {
-    RandomState::permutation_into(cfg.seed, n, h_order[1]);  // unused until epoch 1
-    copy_async(c, init_ids.p, h_order[1], k * 4, hipMemcpyHostToDevice);
-    launch_gather_rows(c, x, n, d, init_ids.u(), k, pos.f());
-  }
-  if (sph) {
-    launch_normalize_rows(c, pos.f(), k, d, readout.f());
-    EMH_HIP(hipMemcpyAsync(pos.p, readout.p, k * d * 4, hipMemcpyDeviceToDevice, c->stream));
+    if (init && init->centroids) {
+      h2d(c, pos.p, init->centroids, k * d * 4);
+    } else if (init && init->centroids_dev) {
+      EMH_HIP(hipMemcpyAsync(pos.p, init->centroids_dev->ptr, k * d * 4, hipMemcpyDeviceToDevice,
+                             c->stream));
+    } else if (n == k) {
+      EMH_HIP(hipMemcpyAsync(pos.p, x, k * d * 4, hipMemcpyDeviceToDevice, c->stream));
+    } else {
+      RandomState::permutation_into(cfg.seed, n, h_order[1]);  // unused until epoch 1
+      copy_async(c, init_ids.p, h_order[1], k * 4, hipMemcpyHostToDevice);
+      launch_gather_rows(c, x, n, d, init_ids.u(), k, pos.f());
+    }
+    if (sph) {
+      launch_normalize_rows(c, pos.f(), k, d, readout.f());
+      EMH_HIP(hipMemcpyAsync(pos.p, readout.p, k * d * 4, hipMemcpyDeviceToDevice, c->stream));
+    }
+    const float init_usage = 1.0f / 65536.0f;
+    uint32_t init_bits;
+    std::memcpy(&init_bits, &init_usage, 4);
+    launch_fill_u32(c, mass.u(), k, init_bits);
   }
   launch_check_finite(c, pos.f(), k * d, c->small + SW_BAD_INIT);
-  const float init_usage = 1.0f / 65536.0f;
-  uint32_t init_bits;
-  std::memcpy(&init_bits, &init_usage, 4);
-  launch_fill_u32(c, mass.u(), k, init_bits);
   launch_fill_u32(c, pass.u(), k * d, 0);
   copy_async(c, h_small0, c->small, SW_WORDS * 4, hipMemcpyDeviceToHost);
   ev_order[1].record(c->stream);  // the initial ids are out of h_order[1]
@@ -1027,24 +1059,27 @@ float rep_threshold(const emh_dedup_config* cfg) {
 extern "C" {
 
 int emh_train_dev(emh_ctx* c, const emh_buf* x, size_t n, const emh_config* cfg,
-                  emh_train_out* out) {
+                  const emh_train_init* init, emh_train_out* out) {
   return guard2([&] {
     EMH_ENSURE(c && x && x->kind == 0, "x must be an f32 buffer");
     check_cfg(n, cfg, out);
+    check_init(cfg, init);
     EMH_ENSURE(x->len == n * cfg->d, "x must be n x d");
     EMH_HIP(hipSetDevice(c->device));
-    train_dev(c, (const float*)x->ptr, n, *cfg, out);
+    train_dev(c, (const float*)x->ptr, n, *cfg, init, out);
   });
 }
 
-int emh_train(emh_ctx* c, const float* x, size_t n, const emh_config* cfg, emh_train_out* out) {
+int emh_train(emh_ctx* c, const float* x, size_t n, const emh_config* cfg,
+              const emh_train_init* init, emh_train_out* out) {
   return guard2([&] {
     EMH_ENSURE(c && x, "null argument");
     check_cfg(n, cfg, out);
+    check_init(cfg, init);
     EMH_HIP(hipSetDevice(c->device));
     Buf xd(c, n * cfg->d * 4);  // Device::bind: the data set goes to the device once
     upload(c, xd.p, x, n * cfg->d * 4);
-    train_dev(c, xd.f(), n, *cfg, out);
+    train_dev(c, xd.f(), n, *cfg, init, out);
   });
 }
 

@@ -193,14 +193,31 @@ typedef struct emh_train_out {
   emh_buf* centroids_dev; /* optional: the centroids also land in this k*d f32 buffer */
 } emh_train_out;
 
-/* Emeans::train (model.rs:700-811) driving the device loop core::train::run
- * (core/train.rs:60-303) on this context: sampled initial centroids, the
- * seeded epoch permutations and revival draws on the host, every batch op on
- * the device. x is n*d host floats, copied to the device once. */
-int emh_train(emh_ctx* ctx, const float* x, size_t n, const emh_config* cfg, emh_train_out* out);
+/* The start of a training run (the Job's positions and usage,
+ * core/train.rs:33-58). All NULL: k sampled rows (Emeans::train,
+ * model.rs:786-797). centroids or centroids_dev (k x d, host or device): given
+ * initial centroids, normalized when spherical, masses 2^-16 (train_from ->
+ * begin, model.rs:705-736, 306-316). positions (k x d) with usage (k), host:
+ * saved EMA state taken as it is (train_resume -> begin_with_state,
+ * model.rs:739-749, 318-336); masses must be finite and >= 0. Initial
+ * centroids and positions must be finite. */
+typedef struct emh_train_init {
+  const float* centroids;
+  const emh_buf* centroids_dev;
+  const float* positions;
+  const float* usage;
+} emh_train_init;
+
+/* Emeans::train / train_from / train_resume (model.rs:700-811) driving the
+ * device loop core::train::run (core/train.rs:60-303) on this context: the
+ * start given by init (NULL: sampled centroids), the seeded epoch
+ * permutations and revival draws on the host, every batch op on the device.
+ * x is n*d host floats, copied to the device once. */
+int emh_train(emh_ctx* ctx, const float* x, size_t n, const emh_config* cfg,
+              const emh_train_init* init, emh_train_out* out);
 /* The same with the data already on the device (x: n*d f32 buffer). */
 int emh_train_dev(emh_ctx* ctx, const emh_buf* x, size_t n, const emh_config* cfg,
-                  emh_train_out* out);
+                  const emh_train_init* init, emh_train_out* out);
 
 /* Emeans::assign (model.rs:898-919) -> assign_all (assign.rs:785-809) ->
  * assign_on (core/mod.rs:249-330) on this context: labels/scores of every row

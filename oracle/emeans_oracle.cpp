@@ -672,23 +672,41 @@ struct OrcTrainOut {
   uint64_t total_steps;
 };
 
-int orc_train(const float* x, uint64_t n, const OrcTrainCfg* cfg, OrcTrainOut* out) {
+// Emeans::train_rows (model.rs:772-811) from its three starts: init == null
+// and positions == null: k sampled rows (train); init: given centroids
+// (train_from -> begin, model.rs:306-316); positions + usage: saved EMA state
+// (train_resume -> begin_with_state, model.rs:318-336). Returns 0, or 1 for
+// bad shapes, 2 for state the reference refuses (non-finite centroids or
+// positions, masses not finite and >= 0).
+int orc_train_from(const float* x, uint64_t n, const OrcTrainCfg* cfg, const float* init,
+                   const float* positions, const float* usage_in, OrcTrainOut* out) {
   const size_t k = cfg->k, d = cfg->d;
   if (n < k || d == 0 || k == 0) return 1;
   const bool sph = cfg->spherical != 0;
   const bool ip = sph;
-  // Initial centroids: model.rs:789-796.
   std::vector<float> pos(k * d);
-  if (n == k) {
-    std::memcpy(pos.data(), x, k * d * 4);
-  } else {
-    std::vector<uint32_t> perm(n);
-    RandomState(cfg->seed).permutation(n, perm.data());
-    for (size_t j = 0; j < k; j++) std::memcpy(&pos[j * d], x + (size_t)perm[j] * d, d * 4);
-  }
-  if (sph)
-    for (size_t j = 0; j < k; j++) normalize_row(&pos[j * d], d);  // model.rs:311-314
   std::vector<float> usage(k, INIT_USAGE);
+  if (positions) {
+    if (!usage_in) return 1;
+    std::memcpy(pos.data(), positions, k * d * 4);
+    std::memcpy(usage.data(), usage_in, k * 4);
+    for (size_t j = 0; j < k; j++)
+      if (!std::isfinite(usage[j]) || usage[j] < 0.0f) return 2;
+  } else {
+    if (init) {
+      std::memcpy(pos.data(), init, k * d * 4);
+    } else if (n == k) {  // model.rs:789-796
+      std::memcpy(pos.data(), x, k * d * 4);
+    } else {
+      std::vector<uint32_t> perm(n);
+      RandomState(cfg->seed).permutation(n, perm.data());
+      for (size_t j = 0; j < k; j++) std::memcpy(&pos[j * d], x + (size_t)perm[j] * d, d * 4);
+    }
+    if (sph)
+      for (size_t j = 0; j < k; j++) normalize_row(&pos[j * d], d);  // model.rs:311-314
+  }
+  for (size_t i = 0; i < k * d; i++)
+    if (!std::isfinite(pos[i])) return 2;  // model.rs:349-352
   // Recipe (recipe.rs:200-254).
   int law = orc_resolve_law(cfg->batch_law, d);
   size_t bsz;
@@ -783,6 +801,10 @@ int orc_train(const float* x, uint64_t n, const OrcTrainCfg* cfg, OrcTrainOut* o
   out->alpha0 = alpha0;
   out->total_steps = total_steps;
   return 0;
+}
+
+int orc_train(const float* x, uint64_t n, const OrcTrainCfg* cfg, OrcTrainOut* out) {
+  return orc_train_from(x, n, cfg, nullptr, nullptr, nullptr, out);
 }
 
 // --- dedup_with_neighbors (crates/emeans-cluster/src/dedup.rs:186-358), with the

@@ -53,6 +53,7 @@ def _load():
         "orc_set_threads": (None, [i32]),
         "orc_get_threads": (i32, []),
         "orc_train": (i32, [_f32p, u64, vp, vp]),
+        "orc_train_from": (i32, [_f32p, u64, vp, vp, vp, vp, vp]),
         "orc_dedup": (u64, [_f32p, u64, u64, _u32p, _f32p, u64, C.c_float, C.c_float, i32, f64,
                             vp, vp, vp, _u32p, _u32p, _u32p, _u32p, C.POINTER(u64),
                             C.POINTER(u64)]),
@@ -237,8 +238,11 @@ class _Out(C.Structure):
 
 
 def train(x, d, k, nepochs=5.0, batch_size=None, alpha0=None, batch_law="auto", seed=1234,
-          spherical=False, unused_threshold=None, assignment_chunk_size=None):
-    """Emeans::train on the CPU device loop (model.rs:700-811, core/train.rs:60-303)."""
+          spherical=False, unused_threshold=None, assignment_chunk_size=None, init=None,
+          positions=None, usage=None):
+    """Emeans::train on the CPU device loop (model.rs:700-811, core/train.rs:60-303);
+    with init, train_from (model.rs:705-736); with positions and usage,
+    train_resume (model.rs:739-749)."""
     x = np.ascontiguousarray(x, np.float32)
     n = x.size // d
     cfg = _Cfg(k, d, float(nepochs), batch_size or 0, int(alpha0 is not None),
@@ -247,19 +251,23 @@ def train(x, d, k, nepochs=5.0, batch_size=None, alpha0=None, batch_law="auto", 
                assignment_chunk_size or 0)
     cent = np.zeros(k * d, np.float32)
     pos = np.zeros(k * d, np.float32)
-    usage = np.zeros(k, np.float32)
+    us = np.zeros(k, np.float32)
     labels = np.zeros(n, np.int32)
     obj = np.zeros(64, np.float64)
     imb = np.zeros(64, np.float64)
     nsp = np.zeros(64, np.uint64)
-    out = _Out(_ptr(cent), _ptr(pos), _ptr(usage), _ptr(labels), _ptr(obj), _ptr(imb),
+    out = _Out(_ptr(cent), _ptr(pos), _ptr(us), _ptr(labels), _ptr(obj), _ptr(imb),
                _ptr(nsp), 0, 0, 0, 0.0, 0)
-    rc = lib.orc_train(x, n, C.addressof(cfg), C.addressof(out))
+    keep = [None if v is None else np.ascontiguousarray(v, np.float32).reshape(-1)
+            for v in (init, positions, usage)]
+    rc = lib.orc_train_from(x, n, C.addressof(cfg), *[_ptr(v) for v in keep], C.addressof(out))
+    if rc == 2:
+        raise ValueError("oracle train: initial state not finite, or masses not finite and >= 0")
     if rc != 0:
         raise ValueError("oracle train: bad arguments")
     e = out.n_epochs
     return {
-        "centroids": cent, "positions": pos, "usage": usage, "labels": labels,
+        "centroids": cent, "positions": pos, "usage": us, "labels": labels,
         "obj": obj[:e].copy(), "imbalance": imb[:e].copy(), "nsplit": nsp[:e].astype(int),
         "n_splits": out.n_splits, "batch_size": out.batch_size, "alpha0": out.alpha0,
         "total_steps": out.total_steps,

@@ -28,14 +28,18 @@ def dev():
     d.close()
 
 
-def _train_both(dev, x, cfg):
+def _train_both(dev, x, cfg, init=None):
     from emeans_amd import Emeans
     m = Emeans(cfg, dev)
-    t = m.train(x)
-    o = O.train(x, cfg.d, cfg.k, nepochs=cfg.nepochs, batch_size=cfg.batch_size,
-                alpha0=cfg.alpha0, batch_law=cfg.batch_law, seed=cfg.seed,
-                spherical=cfg.spherical, unused_threshold=cfg.unused_threshold)
+    t = m.train_from(x, init)
+    o = _oracle_train(x, cfg, init=init)
     return m, t, o
+
+
+def _oracle_train(x, cfg, **start):
+    return O.train(x, cfg.d, cfg.k, nepochs=cfg.nepochs, batch_size=cfg.batch_size,
+                   alpha0=cfg.alpha0, batch_law=cfg.batch_law, seed=cfg.seed,
+                   spherical=cfg.spherical, unused_threshold=cfg.unused_threshold, **start)
 
 
 def _assert_same_run(m, t, o, tag):
@@ -190,3 +194,69 @@ def test_dedup_bursts_time_gap_priority(dev):
     assert r.n_groups() == x.shape[0]
     pairs = set(zip(truth.tolist(), r.group_of.tolist()))
     assert len(pairs) == r.n_groups(), "groups differ from the injected bursts"
+
+
+@pytest.mark.parametrize("spherical", [False, True])
+def test_train_from_given_centroids(dev, spherical):
+    """train_from (model.rs:705-736): given initial centroids, normalized when
+    spherical; a quarter of them far from every row, so revival splits run."""
+    from emeans_amd import Config, synth
+    n, d, k = 30_000, 128, 256
+    if spherical:
+        x, _ = synth.blobs_spherical(n, d, 200, 0.2, seed=13)
+    else:
+        x, _ = synth.gmm_zipf(n=n, d=d, comps=300, s=1.1, seed=13)
+    g = np.random.default_rng(2)
+    init = (x[g.choice(n, k, replace=False)] * np.float32(1.7)).astype(np.float32)
+    init[k - k // 4:] += np.float32(50.0)
+    cfg = Config(d=d, k=k, seed=21, spherical=spherical)
+    m, t, o = _train_both(dev, x, cfg, init=init)
+    _assert_same_run(m, t, o, f"train_from sph={spherical}")
+    assert sum(s.nsplit for s in m.iteration_stats()) >= k // 4
+
+
+def test_train_resume_on_grown_data(dev):
+    """train_resume (model.rs:739-749): train, then continue two epochs from the
+    EMA state on the data grown by a fifth; both runs bit-equal to the oracle's,
+    and the same resume through train_dev with the state given explicitly and
+    the initial centroids from a device buffer."""
+    from emeans_amd import Config, Emeans, synth
+    x, _ = synth.gmm_zipf(n=60_000, d=192, comps=600, s=1.1, seed=17)
+    x1 = x[:50_000]
+    cfg = Config(d=192, k=512, seed=5)
+    m, t, o = _train_both(dev, x1, cfg)
+    _assert_same_run(m, t, o, "first run")
+    cfg.nepochs = 2.0
+    t2 = m.train_resume(x)
+    o2 = _oracle_train(x, cfg, positions=o["positions"], usage=o["usage"])
+    _assert_same_run(m, t2, o2, "resume on grown data")
+    assert len(m.iteration_stats()) == 2
+    # The same on the device entry point, state given explicitly.
+    xb = dev.bind(x)
+    cent, info = dev.train_dev(xb, x.shape[0], cfg, state=(o["positions"], o["usage"]))
+    assert cent.tobytes() == o2["centroids"].tobytes()
+    assert info["positions"].tobytes() == o2["positions"].tobytes()
+    # train_from with the initial centroids in a device buffer.
+    init = x[::117][:512].copy()
+    cb = dev.upload_f32(init)
+    cent, info = dev.train_dev(xb, x.shape[0], cfg, init=cb)
+    o3 = _oracle_train(x, cfg, init=init)
+    assert cent.tobytes() == o3["centroids"].tobytes()
+    assert [s.obj for s in info["stats"]] == o3["obj"].tolist()
+
+
+def test_train_start_refuses_bad_state(dev):
+    from emeans_amd import Config, EmeansHipInvalid
+    x = O.common_mixture(2000, 16, 8, 0.5, False, 1).reshape(2000, 16)
+    xb = dev.bind(x)
+    cfg = Config(d=16, k=8)
+    pos = x[:8].copy()
+    with pytest.raises(EmeansHipInvalid, match="usage must be finite"):
+        dev.train_dev(xb, 2000, cfg, state=(pos, np.full(8, -1.0, np.float32)))
+    bad = pos.copy()
+    bad[3, 2] = np.nan
+    with pytest.raises(EmeansHipInvalid, match="finite"):
+        dev.train_dev(xb, 2000, cfg, init=bad)
+    # the context still works afterwards
+    cent, _ = dev.train_dev(xb, 2000, cfg, init=pos)
+    assert cent.tobytes() == _oracle_train(x, cfg, init=pos)["centroids"].tobytes()
