@@ -20,6 +20,7 @@ from typing import List, Optional, Tuple
 
 import numpy as np
 
+from . import model_file
 from ._lib import (EMH_IP, EMH_L2, EMH_PROF_EMA, EMH_PROF_SCATTER, EMH_PROF_SCREEN,
                    Config as _CConfig, DedupConfig as _CDedupConfig,
                    DedupInput as _CDedupInput, DedupResult as _CDedupResult, EmeansHipError,
@@ -319,6 +320,16 @@ def _train_init(k, d, init, state):
     return C.byref(_CTrainInit(None, None, _p(pos), _p(usage))), [pos, usage]
 
 
+def _epoch_rows(n, cfg):
+    """Recipe::resolve's epoch rows for n rows (emh_host_recipe, no device)."""
+    b, a0, ne, tot = C.c_uint64(), C.c_double(), C.c_uint64(), C.c_uint64()
+    rows = np.zeros(64, np.uint64)
+    ccfg = cfg._c()
+    check(lib().emh_host_recipe(n, C.byref(ccfg), C.byref(b), C.byref(a0), _p(rows), 64,
+                                C.byref(ne), C.byref(tot)))
+    return [int(r) for r in rows[:ne.value]]
+
+
 def make_assigner(backend: str = BACKEND_NAME, device: int = 0) -> HipDevice:
     """make_assigner(Backend::Custom{name: "hip"}) (backend.rs:170-178)."""
     if backend != BACKEND_NAME:
@@ -398,7 +409,7 @@ class Emeans:
         if config.unused_threshold is not None and config.unused_threshold < 0:
             raise ValueError("unused_threshold must be >= 0 (0 disables revival)")
         self.config = config
-        self.dev = assigner or make_assigner()
+        self._dev = assigner  # made on first use when not given
         self._centroids = None
         self._positions = None
         self._usage = None
@@ -407,6 +418,12 @@ class Emeans:
         self._recipe = {}
         self.failed = False
         self.fallback_rows = 0
+
+    @property
+    def dev(self) -> HipDevice:
+        if self._dev is None:
+            self._dev = make_assigner()
+        return self._dev
 
     def _require_ok(self):
         if self.failed:
@@ -469,8 +486,8 @@ class Emeans:
         self._stats = [EpochStats(stats[e].obj, stats[e].time, stats[e].imbalance_factor,
                                   int(stats[e].nsplit)) for e in range(out.n_epochs)]
         self._n_splits = int(out.n_splits)
-        self._recipe = {"batch_size": int(out.batch_size), "alpha0": out.alpha0,
-                        "total_steps": int(out.total_steps)}
+        self._recipe = model_file.recipe_dict(cfg, m, int(out.batch_size), out.alpha0,
+                                              _epoch_rows(m, cfg), self.dev.name())
         self.fallback_rows = int(out.fallback_rows)
         lab = labels if cfg.capture_assignments else None
         if lab is not None and keep is not None:
@@ -504,6 +521,45 @@ class Emeans:
 
     def recipe(self):
         return dict(self._recipe)
+
+    # -- model files (io.rs:72-186)
+    def to_bytes(self) -> bytes:
+        """The model file's bytes (io.rs:92-121)."""
+        self._require_ok()
+        st = [(s.obj, s.time, s.imbalance_factor, s.nsplit) for s in self._stats]
+        return model_file.to_bytes(self.config, self._recipe or None, self._n_splits, st,
+                                   self._centroids, self._positions,
+                                   self._usage if self._usage is not None else [])
+
+    def save(self, path):
+        """Write the model file to a temporary file, then rename it over path (io.rs:74-88)."""
+        import os
+        b = self.to_bytes()
+        tmp = os.path.splitext(str(path))[0] + ".tmp"
+        with open(tmp, "wb") as f:
+            f.write(b)
+            f.flush()
+            os.fsync(f.fileno())
+        os.replace(tmp, path)
+
+    @classmethod
+    def from_bytes_with(cls, b, assigner: Optional[HipDevice] = None) -> "Emeans":
+        """A model from the bytes of to_bytes or a model file (io.rs:137-186)."""
+        header, cent, pos, usage = model_file.from_bytes(b)
+        c = header["config"]
+        cfg = Config(**c)
+        m = cls(cfg, assigner)
+        m._recipe = header["recipe"] or {}
+        m._n_splits = int(header["n_splits"])
+        m._stats = [EpochStats(s["obj"], s["time"], s["imbalance_factor"], int(s["nsplit"]))
+                    for s in header["iteration_stats"]]
+        m._centroids, m._positions, m._usage = cent, pos, usage
+        return m
+
+    @classmethod
+    def load_with(cls, path, assigner: Optional[HipDevice] = None) -> "Emeans":
+        with open(path, "rb") as f:
+            return cls.from_bytes_with(f.read(), assigner)
 
 
 # ------------------------------------------------------------------------ kNN

@@ -56,6 +56,27 @@ def _assert_same_run(m, t, o, tag):
     assert t.centroids.tobytes() == o["centroids"].tobytes(), f"{tag}: centroids"
 
 
+def _assert_same_model_file(dev, m, o, cfg, x):
+    """The HIP-trained model's file (io.rs:72-186) equals the one the oracle's
+    run makes, byte for byte. Two header fields are not the trajectory's and
+    come from the HIP run on both sides: the backend name (recipe.backend, the
+    assigner's name) and each epoch's wall-clock time. Then the file loads
+    back to the same model and the same assignment."""
+    from emeans_amd import Emeans, _epoch_rows, model_file as MF
+    hb = m.to_bytes()
+    n = x.shape[0]
+    rec = MF.recipe_dict(cfg, n, o["batch_size"], o["alpha0"], _epoch_rows(n, cfg), dev.name())
+    times = [s.time for s in m.iteration_stats()]
+    stats = [(ob, t, im, int(ns)) for ob, t, im, ns in zip(o["obj"], times, o["imbalance"],
+                                                           o["nsplit"])]
+    ob = MF.to_bytes(cfg, rec, o["n_splits"], stats, o["centroids"], o["positions"], o["usage"])
+    assert hb == ob, "model file differs from the oracle-trained one"
+    back = Emeans.from_bytes_with(hb, dev)
+    assert back.to_bytes() == hb
+    a, b = m.assign(x), back.assign(x)
+    assert np.array_equal(a.labels, b.labels) and a.scores.tobytes() == b.scores.tobytes()
+
+
 def test_faiss_fixture_runs(dev):
     """The five faiss NumpyEmeans runs: GPU == oracle bit for bit, and faiss within tolerance."""
     from emeans_amd import Config
@@ -84,6 +105,7 @@ def test_spherical_blobs_config(dev):
     cfg = Config(d=64, k=32, spherical=True, seed=7)
     m, t, o = _train_both(dev, x, cfg)
     _assert_same_run(m, t, o, "blobs")
+    _assert_same_model_file(dev, m, o, cfg, x)
     a = m.assign(x)
     ol, osc = O.assign(x, 64, t.centroids, "ip")
     assert np.array_equal(a.labels, ol) and a.scores.tobytes() == osc.tobytes()
@@ -108,6 +130,7 @@ def test_headline_config_bit_exact(dev):
     cfg = Config(d=768, k=1024, seed=0)
     m, t, o = _train_both(dev, x, cfg)
     _assert_same_run(m, t, o, "headline")
+    _assert_same_model_file(dev, m, o, cfg, x)
     a = m.assign(x)
     ol, osc = O.assign(x, 768, t.centroids, "l2")
     assert np.array_equal(a.labels, ol) and a.scores.tobytes() == osc.tobytes()
