@@ -30,7 +30,8 @@ from ._lib import (EMH_IP, EMH_L2, EMH_PROF_EMA, EMH_PROF_SCATTER, EMH_PROF_SCRE
 __all__ = [
     "HipDevice", "DevBuf", "EmaStep", "Mat", "Select", "Config", "Emeans", "Trained",
     "Assignment", "EpochStats", "Neighbors", "DedupConfig", "DedupInput", "DedupResult",
-    "knn_self", "knn", "dedup", "dedup_with_neighbors", "make_assigner", "BACKEND_NAME", "EmeansHipError", "EmeansHipInvalid",
+    "knn_self", "knn", "dedup", "dedup_with_neighbors", "make_assigner", "available_backends",
+    "Backend", "BACKEND_NAME", "EmeansHipError", "EmeansHipInvalid",
     "GPU_KMAX", "NONE",
 ]
 
@@ -330,11 +331,53 @@ def _epoch_rows(n, cfg):
     return [int(r) for r in rows[:ne.value]]
 
 
-def make_assigner(backend: str = BACKEND_NAME, device: int = 0) -> HipDevice:
-    """make_assigner(Backend::Custom{name: "hip"}) (backend.rs:170-178)."""
-    if backend != BACKEND_NAME:
-        raise ValueError(f"unknown backend {backend!r} (this package provides {BACKEND_NAME!r})")
+class Backend:
+    """The backend names of this package, as emeans_cluster::Backend gives
+    them (backend.rs:41-102): NAMES lists what from_str accepts for help
+    texts; "hip-gfx950" is an alias of "hip"."""
+    NAMES = (BACKEND_NAME,)
+    _ALIASES = {"hip": BACKEND_NAME, "hip-gfx950": BACKEND_NAME}
+
+    def __init__(self, name: str = BACKEND_NAME):
+        self._name = Backend.from_str(name)._name if name != BACKEND_NAME else name
+
+    @staticmethod
+    def from_str(s: str) -> "Backend":
+        if s not in Backend._ALIASES:
+            raise ValueError(f"unknown backend {s!r} ({', '.join(Backend.NAMES)})")
+        b = Backend.__new__(Backend)
+        b._name = Backend._ALIASES[s]
+        return b
+
+    def name(self) -> str:
+        return self._name
+
+    def __eq__(self, other):
+        return isinstance(other, Backend) and other._name == self._name
+
+    def __repr__(self):
+        return f"Backend({self._name!r})"
+
+
+def make_assigner(backend=BACKEND_NAME, device: int = 0) -> HipDevice:
+    """make_assigner (backend.rs:106-114) for the "hip" backend: builds the
+    gfx950 engine; fails when the library or a gfx950 device is missing."""
+    b = backend if isinstance(backend, Backend) else Backend.from_str(backend)
+    assert b.name() == BACKEND_NAME
     return HipDevice(device)
+
+
+def available_backends():
+    """available_backends (bindings/common/src/lib.rs:131-137): the names of
+    Backend.NAMES whose make_assigner succeeds on this machine."""
+    out = []
+    for n in Backend.NAMES:
+        try:
+            make_assigner(n).close()
+            out.append(n)
+        except (EmeansHipError, EmeansHipInvalid, OSError):
+            pass
+    return out
 
 
 # ---------------------------------------------------------------------- model

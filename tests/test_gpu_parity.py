@@ -396,3 +396,13 @@ def test_topk_production_duplicates(dev, screen):
     gi, gs = dev.topk(q, data, d, 16, False)
     oi, osims = O.knn(q, data, d, 16, False)
     assert np.array_equal(gi, oi) and gs.tobytes() == osims.tobytes()
+
+
+def test_backend_is_available_by_name():
+    """available_backends lists "hip" on a gfx950 machine; make_assigner builds
+    it from either name (backend.rs:84-114)."""
+    from emeans_amd import Backend, available_backends, make_assigner
+    assert available_backends() == ["hip"]
+    d = make_assigner(Backend.from_str("hip-gfx950"))
+    assert d.name() == "hip-gfx950"
+    d.close()

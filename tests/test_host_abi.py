@@ -201,3 +201,19 @@ def test_dedup_neighbors_rejects_bad_arguments(lib):
         dedup_with_neighbors(x, 4, nb, DedupInput(priority=np.array([0, np.nan], np.float32)))
     with pytest.raises(ValueError, match="one timestamp per row"):
         dedup_with_neighbors(x, 4, nb, DedupInput(created_unix=np.zeros(3)), DedupConfig())
+
+
+def test_backend_names_and_availability():
+    """The "hip" name as emeans_cluster::Backend would list it (backend.rs:41-102)
+    and available_backends (bindings/common/src/lib.rs:131-137): names whose
+    make_assigner succeeds; none on a machine without a gfx950 device."""
+    from emeans_amd import Backend, EmeansHipError, available_backends, make_assigner
+    assert Backend.NAMES == ("hip",)
+    assert Backend.from_str("hip") == Backend.from_str("hip-gfx950")
+    assert Backend.from_str("hip-gfx950").name() == "hip"
+    with pytest.raises(ValueError, match=r"unknown backend 'cuda' \(hip\)"):
+        Backend.from_str("cuda")
+    if not os.path.exists("/dev/kfd"):
+        assert available_backends() == []
+        with pytest.raises(EmeansHipError):
+            make_assigner(Backend.from_str("hip"))
