@@ -290,6 +290,35 @@ class HipDevice:
         check(lib().emh_profile_read_op(self._ctx, code, C.byref(ms), C.byref(n), C.byref(u)))
         return ms.value, n.value, u.value
 
+    SCREEN_VARIANTS = {0: "none", 1: "big_tagged", 2: "big_sorted", 3: "small_bf16",
+                       4: "small_f32"}
+
+    def screen_margin(self, x: Mat, sel: Select, centroids: DevBuf, cnorm: Optional[DevBuf],
+                      k: int, metric) -> dict:
+        """The screen of top1 on these arguments, measured instead of checked:
+        which screen ran, and max |screen key - exact key| / E over its lists."""
+        from ._lib import ScreenReport
+        r = ScreenReport()
+        check(lib().emh_screen_margin(self._ctx, x.dev.h, x.d, sel.ids.h if sel.ids else None,
+                                      sel.rows[0], sel.rows[1], centroids.h,
+                                      cnorm.h if cnorm else None, k, _metric(metric),
+                                      C.byref(r)))
+        return self._report(r)
+
+    def screen_margin_topk(self, q: DevBuf, m: int, data: DevBuf, n: int, d: int,
+                           exclude_self: bool) -> dict:
+        """The same for the kNN screen (16-neighbour lists) of topk_dev."""
+        from ._lib import ScreenReport
+        r = ScreenReport()
+        check(lib().emh_screen_margin_topk(self._ctx, q.h, m, data.h, n, d, int(exclude_self),
+                                           C.byref(r)))
+        return self._report(r)
+
+    def _report(self, r):
+        return {"variant": self.SCREEN_VARIANTS[r.variant], "parts": r.parts,
+                "tiles_per_part": r.tiles_per_part, "pairs": int(r.pairs), "over": int(r.over),
+                "max_ratio": r.max_ratio, "max_dot_ratio": r.max_dot_ratio}
+
     def fallback_rows(self) -> int:
         return lib().emh_fallback_rows(self._ctx)
 

@@ -45,6 +45,12 @@ class TrainOut(C.Structure):
                 ("fallback_rows", C.c_uint64), ("centroids_dev", C.c_void_p)]
 
 
+class ScreenReport(C.Structure):
+    _fields_ = [("variant", C.c_int), ("parts", C.c_int), ("tiles_per_part", C.c_int),
+                ("pairs", C.c_uint64), ("over", C.c_uint64), ("max_ratio", C.c_double),
+                ("max_dot_ratio", C.c_double)]
+
+
 class TrainInit(C.Structure):
     _fields_ = [("centroids", C.c_void_p), ("centroids_dev", C.c_void_p),
                 ("positions", C.c_void_p), ("usage", C.c_void_p)]
@@ -113,6 +119,8 @@ SIGNATURES = {
     "emh_dedup_neighbors": (_i, [_vp, _sz, _sz, _vp, _vp, _sz, _vp, _vp, _vp]),
     "emh_dedup": (_i, [_vp, _vp, _sz, _sz, _vp, _vp, _vp]),
     "emh_fallback_rows": (_u64, [_vp]),
+    "emh_screen_margin": (_i, [_vp, _vp, _sz, _vp, _sz, _sz, _vp, _vp, _sz, _i, _vp]),
+    "emh_screen_margin_topk": (_i, [_vp, _vp, _sz, _vp, _sz, _sz, _i, _vp]),
     "emh_set_screen": (_i, [_vp, _i]),
     "emh_host_permutation": (None, [_u32, _u64, _vp]),
     "emh_host_random_sample": (_d, [_u32, _u64]),

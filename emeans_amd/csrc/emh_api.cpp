@@ -394,6 +394,38 @@ int emh_top1_noalloc(emh_ctx* c, const emh_buf* x, size_t d, const emh_buf* ids,
   });
 }
 
+int emh_screen_margin(emh_ctx* c, const emh_buf* x, size_t d, const emh_buf* ids, size_t lo,
+                      size_t hi, const emh_buf* cents, const emh_buf* cnorm, size_t k, int metric,
+                      emh_screen_report* out) {
+  return guard([&] {
+    EMH_ENSURE(out, "null argument");
+    // Only the screen's lists are touched: labels and scores need no buffers.
+    emh_buf none_u{nullptr, hi, 1, false}, none_f{nullptr, hi, 0, false};
+    const Top1Call t = check_top1(c, x, d, ids, lo, hi, cents, cnorm, k, metric, &none_u, &none_f);
+    use_device(c);
+    emh_screen_report r{};
+    emh::screen_margin_top1(c, t.x, t.nx, d, t.ids, lo, hi, t.cents, t.cn, k, metric == EMH_IP,
+                            &r);
+    *out = r;
+  });
+}
+
+int emh_screen_margin_topk(emh_ctx* c, const emh_buf* q, size_t m, const emh_buf* data, size_t n,
+                           size_t d, int exclude_self, emh_screen_report* out) {
+  return guard([&] {
+    EMH_ENSURE(c && out, "null argument");
+    EMH_ENSURE(d > 0, "d must be positive");
+    EMH_ENSURE(!exclude_self || m == n, "exclude_self needs queries == data");
+    const float* qp = F(q, "queries");
+    const float* dp = F(data, "data");
+    EMH_ENSURE(q->len >= m * d && data->len >= n * d, "queries m x d, data n x d");
+    use_device(c);
+    emh_screen_report r{};
+    emh::launch_topk(c, qp, m, dp, n, d, 16, exclude_self != 0, nullptr, nullptr, &r);
+    *out = r;
+  });
+}
+
 int emh_topk_dev(emh_ctx* c, const emh_buf* q, size_t m, const emh_buf* data, size_t n, size_t d,
                  size_t kk, int exclude_self, emh_buf* ids, emh_buf* sims) {
   return guard([&] {

@@ -292,7 +292,14 @@ void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t
 // upper bound: each region rounded up to 256 bytes).
 size_t top1_scratch_bytes(emh_ctx* c, size_t n, size_t d, size_t k);
 
+// With rep, the screen runs and its lists are measured (launch_margin) instead
+// of checked: nothing is written to ids or sims.
 void launch_topk(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,
-                 size_t kk, bool exclude_self, uint32_t* ids, float* sims);
+                 size_t kk, bool exclude_self, uint32_t* ids, float* sims,
+                 emh_screen_report* rep = nullptr);
+// The screen stage of a top-1 call, its lists measured instead of checked.
+void screen_margin_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
+                        size_t lo, size_t hi, const float* cents, const float* cnorm, size_t k,
+                        bool ip, emh_screen_report* out);
 
 }  // namespace emh

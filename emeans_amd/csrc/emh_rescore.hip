@@ -13,6 +13,8 @@
 // candidate) pair runs a chain, reading the row and the candidate from global
 // memory with PF float4 loads of each in flight.
 
+#include <cstring>
+
 #include "emh_select.h"
 
 namespace emh {
@@ -627,7 +629,81 @@ __global__ __launch_bounds__(256) void k_check1(
   }
 }
 
+// One thread per list entry: the entry's exact key (the check's fma chain
+// over t = 0..d-1 from +0; IP -dot, L2 cnorm - 2 dot) against its screen key.
+// out[0]: entries measured; out[1]: entries beyond E; out[2]: the largest
+// |screen key - exact key| / E; out[3]: the largest dot error over the bound's
+// dot term, after the allowances that are IEEE rounding (L2: one rounding of
+// each key) or the tag (tagged keys): max(0, |dk| - u(|ks| + |ke|) - 2^-17 |ks|)
+// / ((2 for L2) edot). Ratios are f32 bits (>= 0, so their bits order as the
+// values). Entries with a non-finite key or bound are not measured (their rows
+// go to the exact scan).
+__global__ __launch_bounds__(256) void k_margin(
+    const float* __restrict__ x, size_t nx, int d, const uint32_t* __restrict__ ids, size_t lo,
+    size_t nrows, const float* __restrict__ cents, const float* __restrict__ cnorm, int ip,
+    const Cand* __restrict__ cand, int per_row, const float* __restrict__ xnorm,
+    const uint32_t* __restrict__ small, int bound, unsigned long long* __restrict__ out) {
+  const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= nrows * (size_t)per_row) return;
+  const size_t r = e / (size_t)per_row;
+  const Cand cd = cand[e];
+  if (cd.id == NONE || !isfinite(cd.key)) return;
+  const size_t p = lo + r;
+  const size_t xi = ids ? (size_t)ids[p] : p;
+  if (xi >= nx) return;
+  const float* xr = x + xi * (size_t)d;
+  const float* cr = cents + (size_t)cd.id * d;
+  float acc = 0.f;
+  for (int t = 0; t < d; t++) acc = fmaf(xr[t], cr[t], acc);
+  const float kx = ip ? -acc : cnorm[cd.id] - 2.0f * acc;
+  float edot = 0.f;
+  const float E = screen_bound(xnorm[r], __uint_as_float(small[SW_CMAX2]),
+                               __uint_as_float(small[SW_CNMAX]), d, !ip, bound != 0, bound == 2,
+                               &edot);
+  if (!isfinite(kx) || !isfinite(E) || !(E > 0.f) || !(edot > 0.f)) return;
+  const float dk = fabsf(cd.key - kx);
+  const float ratio = dk / E;
+  const float u = 5.9604645e-08f;
+  const float allow = (ip ? 0.f : 1.0000002f * u * (fabsf(cd.key) + fabsf(kx))) +
+                      (bound == 2 ? 7.63e-6f * fabsf(cd.key) + 8.9e-44f : 0.f);
+  const float dot_ratio = fmaxf(dk - allow, 0.f) / ((ip ? 1.0f : 2.0f) * edot);
+  atomicAdd(&out[0], 1ull);
+  if (ratio > 1.0f) atomicAdd(&out[1], 1ull);
+  atomicMax(&out[2], (unsigned long long)__float_as_uint(ratio));
+  atomicMax(&out[3], (unsigned long long)__float_as_uint(dot_ratio));
+}
+
 }  // namespace
+
+void launch_margin(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
+                   size_t lo, size_t n, const float* cents, const float* cnorm, bool ip,
+                   const Cand* cand, int parts, int L, const float* xnorm, int bound,
+                   emh_screen_report* rep) {
+  unsigned long long* w = nullptr;
+  EMH_HIP(hipMalloc(&w, 4 * sizeof(unsigned long long)));
+  unsigned long long h[4] = {0, 0, 0, 0};
+  try {
+    EMH_HIP(hipMemcpyAsync(w, h, sizeof h, hipMemcpyHostToDevice, c->stream));
+    const size_t total = n * (size_t)parts * L;
+    hipLaunchKernelGGL(k_margin, grid1(total, 256), dim3(256), 0, c->stream, x, nx, (int)d, ids,
+                       lo, n, cents, cnorm, ip ? 1 : 0, cand, parts * L, xnorm, c->small, bound,
+                       w);
+    EMH_HIP(hipGetLastError());
+    EMH_HIP(hipMemcpyAsync(h, w, sizeof h, hipMemcpyDeviceToHost, c->stream));
+    EMH_HIP(hipStreamSynchronize(c->stream));
+  } catch (...) {
+    (void)hipFree(w);
+    throw;
+  }
+  EMH_HIP(hipFree(w));
+  uint32_t bits[2] = {(uint32_t)h[2], (uint32_t)h[3]};
+  float mr[2];
+  std::memcpy(mr, bits, 8);
+  rep->pairs = h[0];
+  rep->over = h[1];
+  rep->max_ratio = mr[0];
+  rep->max_dot_ratio = mr[1];
+}
 
 void launch_verify1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
                     size_t lo, size_t n, const float* cents, const float* cnorm, size_t k, bool ip,

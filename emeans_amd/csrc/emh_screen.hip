@@ -92,6 +92,49 @@ size_t top1_scratch_bytes(emh_ctx* c, size_t n, size_t d, size_t k) {
          exact1_scratch_bytes(n, d, k, true);
 }
 
+namespace {
+// The screen stage of a top-1 call: its lists, their parts, the rows' |x|^2,
+// the check's queue and the arithmetic the check's bound must follow.
+struct Top1Screen {
+  Top1Geom g;
+  Cand* cand = nullptr;
+  uint32_t* fb = nullptr;
+  float* xnorm = nullptr;
+  bool tagged = false;
+};
+
+Top1Screen screen_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
+                       size_t lo, size_t n, const float* cents, const float* cnorm, size_t k,
+                       bool ip, bool words_clear, Arena* ar) {
+  Top1Screen s;
+  s.g = top1_geom(c, n, d, k);
+  if (!s.g.screen) return s;
+  const Top1Geom& g = s.g;
+  const size_t cbytes = (size_t)g.parts * n * L1 * sizeof(Cand);
+  s.cand = (Cand*)(ar ? ar->take(cbytes) : c->cand.get(cbytes));
+  s.fb = (uint32_t*)(ar ? ar->take(n * 4) : c->fblist.get(n * 4));
+  s.xnorm = (float*)(ar ? ar->take(n * 4) : c->xnorm.get(n * 4));
+  if (!words_clear)  // fallback count, cmax2, cnmax (the screen fills the maxima)
+    launch_fill_u32(c, c->small, 3, 0);
+  const unsigned blocks = (unsigned)(g.row_tiles * g.parts);
+  s.tagged = g.big && g.tpp == 1;
+  ProfScope prof(c, EMH_PROF_SCREEN, 2.0 * (double)n * (double)k * (double)d,
+                 !ar && prof_take(c, EMH_PROF_SCREEN));
+  const ScreenArgs a{blocks, x, nx, d, ids, lo, n, cents, cnorm, k, g.tpp, g.parts, g.ntiles,
+                     s.cand, s.xnorm};
+  // One tile per part: tagged keys (the cheap fold); more: the sorted
+  // insert, which skips most keys once the lists hold good ones.
+  if (g.big)
+    launch_screen3(c, a, ip, s.tagged);
+  else
+    launch_screen_t1(c, a, ip);
+  return s;
+}
+
+// The check's bound arithmetic: 0 f32 screen, 1 bf16, 2 bf16 with tagged keys.
+int bound_kind(emh_ctx* c, bool tagged) { return c->screen == SCREEN_F32 ? 0 : tagged ? 2 : 1; }
+}  // namespace
+
 void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids, size_t lo,
                  size_t hi, const float* cents, const float* cnorm, size_t k, bool ip,
                  uint32_t* labels, float* scores, bool words_clear, Arena* ar) {
@@ -99,39 +142,35 @@ void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t
   const size_t n = hi - lo;
   EMH_ENSURE(d <= 16384, "top1: d = %zu above the supported 16384", d);
   EMH_ENSURE(n < (1u << 31) && k < (1u << 31), "top1: shape too large");
-  const Top1Geom g = top1_geom(c, n, d, k);
-  if (!g.screen) {
+  const Top1Screen s = screen_top1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, words_clear, ar);
+  if (!s.g.screen) {
     launch_exact1(c, x, nx, d, ids, lo, n, nullptr, cents, cnorm, k, ip, labels, scores, ar);
     return;
   }
-  const int parts = g.parts, tpp = g.tpp;
-  const size_t cbytes = (size_t)parts * n * L1 * sizeof(Cand);
-  Cand* cand = (Cand*)(ar ? ar->take(cbytes) : c->cand.get(cbytes));
-  uint32_t* fb = (uint32_t*)(ar ? ar->take(n * 4) : c->fblist.get(n * 4));
-  float* xnorm = (float*)(ar ? ar->take(n * 4) : c->xnorm.get(n * 4));
-  if (!words_clear)  // fallback count, cmax2, cnmax (the screen fills the maxima)
-    launch_fill_u32(c, c->small, 3, 0);
-  const unsigned blocks = (unsigned)(g.row_tiles * parts);
-  const bool tagged = g.big && tpp == 1;
-  {
-    ProfScope prof(c, EMH_PROF_SCREEN, 2.0 * (double)n * (double)k * (double)d,
-                   !ar && prof_take(c, EMH_PROF_SCREEN));
-    const ScreenArgs a{blocks, x, nx, d, ids, lo, n, cents, cnorm, k, tpp, parts, g.ntiles, cand,
-                       xnorm};
-    // One tile per part: tagged keys (the cheap fold); more: the sorted
-    // insert, which skips most keys once the lists hold good ones.
-    if (g.big)
-      launch_screen3(c, a, ip, tagged);
-    else
-      launch_screen_t1(c, a, ip);
-  }
-  launch_verify1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, cand, parts, xnorm, labels, scores,
-                 fb, tagged);
-  launch_exact1(c, x, nx, d, ids, lo, n, fb, cents, cnorm, k, ip, labels, scores, ar);
+  launch_verify1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, s.cand, s.g.parts, s.xnorm, labels,
+                 scores, s.fb, s.tagged);
+  launch_exact1(c, x, nx, d, ids, lo, n, s.fb, cents, cnorm, k, ip, labels, scores, ar);
+}
+
+void screen_margin_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
+                        size_t lo, size_t hi, const float* cents, const float* cnorm, size_t k,
+                        bool ip, emh_screen_report* out) {
+  *out = emh_screen_report{};
+  if (hi <= lo) return;
+  const size_t n = hi - lo;
+  EMH_ENSURE(d <= 16384 && n < (1u << 31) && k < (1u << 31), "top1: shape too large");
+  const Top1Screen s = screen_top1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, false, nullptr);
+  if (!s.g.screen) return;  // variant 0: no screen, nothing to measure
+  out->variant = s.g.big ? (s.tagged ? EMH_SCREEN_BIG_TAGGED : EMH_SCREEN_BIG_SORTED)
+                         : (c->screen == SCREEN_F32 ? EMH_SCREEN_SMALL_F32 : EMH_SCREEN_SMALL_BF16);
+  out->parts = s.g.parts;
+  out->tiles_per_part = s.g.tpp;
+  launch_margin(c, x, nx, d, ids, lo, n, cents, cnorm, ip, s.cand, s.g.parts, L1, s.xnorm,
+                bound_kind(c, s.tagged), out);
 }
 
 void launch_topk(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,
-                 size_t kk, bool exclude_self, uint32_t* ids, float* sims) {
+                 size_t kk, bool exclude_self, uint32_t* ids, float* sims, emh_screen_report* rep) {
   if (m == 0) return;
   EMH_ENSURE(kk >= 1 && kk <= (size_t)KMAX, "topk: kk = %zu must be in 1..16", kk);
   EMH_ENSURE(d <= 16384, "topk: d = %zu above the supported 16384", d);
@@ -157,6 +196,16 @@ void launch_topk(emh_ctx* c, const float* q, size_t m, const float* data, size_t
     parts = 1;
     launch_fill_u32(c, (uint32_t*)cand, m * LK * 2, NONE);  // empty lists
     launch_fill_u32(c, (uint32_t*)xnorm, m, 0);
+  }
+  if (rep) {  // the diagnostic: measure the lists, change nothing
+    *rep = emh_screen_report{};
+    if (n == 0) return;
+    rep->variant = c->screen == SCREEN_F32 ? EMH_SCREEN_SMALL_F32 : EMH_SCREEN_SMALL_BF16;
+    rep->parts = parts;
+    rep->tiles_per_part = tpp;
+    launch_margin(c, q, m, d, nullptr, 0, m, data, nullptr, true, cand, parts, LK, xnorm,
+                  c->screen != SCREEN_F32 ? 1 : 0, rep);
+    return;
   }
   launch_verifyk(c, q, m, data, n, d, kk, cand, parts, xnorm, ids, sims, fb);
   launch_exactk(c, q, m, data, n, d, kk, exclude_self, fb, ids, sims);

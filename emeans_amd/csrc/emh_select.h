@@ -75,7 +75,8 @@ __device__ __forceinline__ void insert_nb(float (&key)[L], uint32_t (&id)[L], fl
 // Terms of |dot' - dot|, with S >= sum_t |x_t c_t|:
 //   the check's fma chain: gamma_d S;
 //   f32 screen: the MFMA's sum in any order, taken at 2 gamma_d S, with a
-//   denormal-flush floor of d 2^-124;
+//   denormal-flush floor of d 2^-124, and 2^-126 sqrt(d) (|x| + cmax) for
+//   elements below 2^-126 that the MFMA may take as zero;
 //   bf16 screen (bf3): the split (x ~ xh + xl, c ~ ch + cl, the xl.cl product
 //   dropped): <= 3.05 * 2^-16 S, plus 2^-133 per element in the bf16
 //   subnormal range, <= 2^-133 sqrt(d) (|x| + cmax) for the three products;
@@ -84,12 +85,19 @@ __device__ __forceinline__ void insert_nb(float (&key)[L], uint32_t (&id)[L], fl
 //   2^-26 grid relative to the largest term, then rounds the sum once:
 //   <= 5.25 u; measured <= 4.9 u), so <= gamma(16 M) * 1.02 S (the three
 //   passes' |products| sum to <= 1.02 S); underflow: (3d + M) 2^-124.
+// With edot_out, also the bound's dot term (unscaled, before the L2 key and
+// tag allowances): the part that rests on the split and the MFMA model.
 __device__ __forceinline__ float screen_bound(float xn, float cmax2, float cnmax, int d, bool l2,
-                                              bool bf3, bool tagged = false) {
+                                              bool bf3, bool tagged = false,
+                                              float* edot_out = nullptr) {
   const float u = 5.9604645e-08f;  // 2^-24
   const float du = (float)d * u;
   const float g = du / (1.0f - du);
-  const float xa = sqrtf(xn) * (1.0f + g), ca = sqrtf(cmax2) * (1.0f + g);
+  // A square or a partial sum in the subnormal range loses at most 2^-150, so
+  // the true squared norm is at most the computed one plus d 2^-149 (a row or
+  // centroid whose |.|^2 underflows still gets a bound that covers its dots).
+  const float uf = (float)d * 1.4012985e-45f;  // d 2^-149
+  const float xa = sqrtf(xn + uf) * (1.0f + g), ca = sqrtf(cmax2 + uf) * (1.0f + g);
   const float S = xa * ca;
   float edot;
   if (bf3) {
@@ -100,8 +108,10 @@ __device__ __forceinline__ float screen_bound(float xn, float cmax2, float cnmax
            + 9.1835e-41f * sqrtf((float)d) * (xa + ca)   // 2^-133
            + (float)(3 * d + (int)m) * 4.7019774e-38f;   // 2^-124
   } else {
-    edot = 3.0f * g * S + (float)d * 4.7019774e-38f;  // + d 2^-124
+    edot = 3.0f * g * S + (float)d * 4.7019774e-38f   // + d 2^-124
+           + 1.1754944e-38f * sqrtf((float)d) * (xa + ca);  // inputs below 2^-126 taken as 0
   }
+  if (edot_out) *edot_out = edot;
   float e = l2 ? 2.0f * edot + 2.0f * u * (cnmax + 2.0f * S) : edot;
   // Tagged keys (the single-tile large-tile screen) carry a 6-bit column tag
   // in their low mantissa bits: |tagged - key| <= 63 ulp < 2^-17 |key|, with
@@ -141,6 +151,15 @@ void launch_verify1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint3
 void launch_verifyk(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,
                     size_t kk, const Cand* cand, int parts, const float* xnorm, uint32_t* ids,
                     float* sims, uint32_t* fb);
+// Re-score every entry of the screen's lists (rows lo..lo+n, parts x L
+// entries each, laid out [row][part][L]) with the check's exact key and fill
+// rep's pair count, pairs beyond the bound and max |screen key - exact key| / E
+// (E from the row's |x|^2 and the call's bound words; bound as in
+// launch_verify1). Waits for the result.
+void launch_margin(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
+                   size_t lo, size_t n, const float* cents, const float* cnorm, bool ip,
+                   const Cand* cand, int parts, int L, const float* xnorm, int bound,
+                   emh_screen_report* rep);
 // ---- emh_verify.hip: the exact scans
 // Exact scan of rows `list[0..*count)` (list != nullptr) or positions lo..lo+n.
 // ar: take the scratch from this fixed block (see Arena) instead of the context's buffers.

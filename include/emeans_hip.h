@@ -306,6 +306,33 @@ uint64_t emh_host_plan_revival(const float* usage, uint64_t k, double tau, uint3
 float emh_host_numpy_sum_f32(const float* a, uint64_t n);
 
 /* ------------------------------------------------------------ diagnostics */
+/* Which screen a top-1 or top-k call ran (emh_screen_report.variant). */
+#define EMH_SCREEN_NONE 0        /* no screen: k < 64, d < 32 or emh_set_screen(ctx, 0) */
+#define EMH_SCREEN_BIG_TAGGED 1  /* large-tile bf16 screen, one tile per part, tagged keys */
+#define EMH_SCREEN_BIG_SORTED 2  /* large-tile bf16 screen, several tiles per part */
+#define EMH_SCREEN_SMALL_BF16 3  /* 128 x 128 bf16 screen (d % 4 != 0, and kNN) */
+#define EMH_SCREEN_SMALL_F32 4   /* 128 x 128 f32 screen (emh_set_screen(ctx, 2)) */
+typedef struct emh_screen_report {
+  int variant;          /* EMH_SCREEN_* */
+  int parts;            /* centroid (or data row) parts per row tile */
+  int tiles_per_part;
+  uint64_t pairs;       /* list entries re-scored */
+  uint64_t over;        /* entries whose |screen key - exact key| exceeded the bound E */
+  double max_ratio;     /* max |screen key - exact key| / E over the entries */
+  double max_dot_ratio; /* max dot error / the bound's dot term (split + MFMA model), after
+                           the allowances that are IEEE rounding of the keys or the tag */
+} emh_screen_report;
+/* Diagnostics of the screen's exactness argument (no counterpart in the
+ * reference): run the screen of emh_top1 (or of emh_topk_dev) on the same
+ * arguments, then re-score every entry of its candidate lists with the exact
+ * fma-chain key the check uses and report how far the screen's key was from
+ * it, relative to the per-row bound E the check trusts. Writes no labels,
+ * scores, ids or sims; waits for the device. */
+int emh_screen_margin(emh_ctx* ctx, const emh_buf* x, size_t d, const emh_buf* ids, size_t lo,
+                      size_t hi, const emh_buf* centroids, const emh_buf* cnorm, size_t k,
+                      int metric, emh_screen_report* out);
+int emh_screen_margin_topk(emh_ctx* ctx, const emh_buf* queries, size_t m, const emh_buf* data,
+                           size_t n, size_t d, int exclude_self, emh_screen_report* out);
 /* Rows the exact top-1 / top-k kernels rescanned since the context was made
  * (the screen's misses; EMEANS_CUDA_SCREEN_STATS analogue, emeans-cuda lib.rs:278-287). */
 uint64_t emh_fallback_rows(emh_ctx* ctx);

@@ -406,3 +406,28 @@ def test_backend_is_available_by_name():
     d = make_assigner(Backend.from_str("hip-gfx950"))
     assert d.name() == "hip-gfx950"
     d.close()
+
+
+@pytest.mark.parametrize("metric", ["ip", "l2"])
+def test_screen_tiny_rows_finite_bound(dev, screen, metric):
+    """Rows whose squared norm underflows f32 (scales 1e-40 .. 1e-20, elements
+    in the f32 and bf16 subnormal ranges) against centroids up to 5e17, the
+    largest scale whose |c|^2 is finite at d = 768, so the screen's bound stays
+    finite and the check decides these rows: bit-equal to the oracle in both
+    screen arithmetics."""
+    n, d, k = 2048, 768, 256
+    base = _mix(n, d, 16, 0.2, True, 41)
+    cb = _mix(k, d, 16, 0.2, True, 42)
+    if metric == "ip":
+        xs = np.array([1e-40, 1e-38, 1e-36, 1e-30, 1e-20, 1.0], np.float64)
+        cs = np.array([5e17, 1e3, 1.0], np.float64)
+    else:
+        xs = np.array([1e-40, 1e-38, 1e-30, 1e-20, 1.0], np.float64)
+        cs = np.array([1e-18, 1.0, 1e12], np.float64)
+    x = (base * xs[np.arange(n) % len(xs)][:, None]).astype(np.float32)
+    c = (cb * cs[np.arange(k) % len(cs)][:, None]).astype(np.float32)
+    gl, gs = _gpu_top1(dev, x, c, metric)
+    ol, osc = O.top1(x, d, c, metric)
+    bad = np.nonzero(gl != ol)[0]
+    assert bad.size == 0, f"{bad.size} labels differ, rows {bad[:8]} (scales {xs[bad[:8] % len(xs)]})"
+    assert gs.tobytes() == osc.tobytes()
