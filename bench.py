@@ -506,6 +506,75 @@ def assign_workload(args):
     return out
 
 
+def autok_workload(args):
+    """C5's GPU work (auto_cluster + Hierarchy::add on 1,000,000 x 768 nested
+    unit rows, 64 Zipf(1.3) top groups of 16 sub-groups, seed 3): the level-1
+    sweep of auto_cluster over the first 900,000 rows (k = 2 .. 40, four
+    k-means++ restarts each: 156 spherical e-means fits with their
+    assignments, scored by internal_scores, the k chosen by the silhouette;
+    auto.rs:457-542), then the add of the last 100,000 rows at the top level
+    (incremental.rs:306-360: 11% new rows call for the EMA update: assign the
+    new rows, then resume the model from its EMA state for one epoch on all
+    rows). The data stay bound on one context. CPU baseline: the oracle's fit
+    at the median k on the same 900,000 rows."""
+    from emeans_amd import Config, HipDevice, auto, synth
+    from oracle import oracle as O
+
+    n_all, n, d = 1_000_000, 900_000, 768
+    t = time.time()
+    x_all, _ = synth.nested(n=n_all, d=d, seed=3)
+    x = x_all[:n]
+    log(f"autok data: {n_all} x {d} generated in {time.time() - t:.1f} s")
+    dev = HipDevice()
+    xb = dev.bind(x)
+    cfg = auto.AutoConfig(restarts=args.autok_restarts, seed=3)
+    ks = list(range(cfg.k1_range[0], cfg.k1_range[1] + 1))
+    auto.fit(dev, x, xb, 8, 1.0, 1, None)  # warm the kernels up
+    dev.sync()
+    tm = {}
+    t0 = time.perf_counter()
+    out, _ = auto.sweep(dev, x, xb, ks, cfg, salt=0, timing=tm)
+    dev.sync()
+    sweep_s = time.perf_counter() - t0
+    scores = [s for s, _ in out]
+    pick = auto.select(scores, cfg, False)
+    lvl1 = out[pick][1]
+    log(f"autok: level-1 sweep {sweep_s:.2f} s ({tm['fits']} fits), k1 = {ks[pick]}")
+    # Hierarchy::add of the last 100,000 rows at the top level.
+    xa = dev.bind(x_all)
+    xn = dev.bind(x_all[n:])
+    cb = dev.upload_f32(lvl1.centroids)
+    lab, sco = dev.zeros_u32(n_all - n), dev.zeros_f32(n_all - n)
+    dev.sync()
+    t0 = time.perf_counter()
+    dev.assign_dev(xn, n_all - n, d, cb, lvl1.k, "ip", lab, sco)
+    dev.sync()
+    t1 = time.perf_counter()
+    c1 = Config(d=d, k=lvl1.k, spherical=True, nepochs=1.0, seed=lvl1.seed,
+                capture_assignments=False)
+    dev.train_dev(xa, n_all, c1, state=(lvl1.positions, lvl1.usage))
+    dev.sync()
+    t2 = time.perf_counter()
+    # CPU baseline: the oracle's fit (train_from + assign) at the median k.
+    kc = ks[len(ks) // 2]
+    init = x[dev.kmeans_pp(xb, n, d, kc, 7)]
+    c0 = time.perf_counter()
+    o = O.train(x, d, kc, spherical=True, seed=7, init=init)
+    O.assign(x, d, o["centroids"], "ip")
+    cpu_fit_s = time.perf_counter() - c0
+    gpu_fit_s = tm["fit_s"] / max(tm["fits"], 1)
+    dev.close()
+    return {"value": tm["fits"] / sweep_s, "unit": "fits/s", "sweep_s": sweep_s,
+            "fits": tm["fits"], "ms_per_fit": gpu_fit_s * 1e3,
+            "kmeans_pp_s": tm["kmeans_pp_s"], "internal_scores_s": tm["scores_s"],
+            "k1": ks[pick], "level1": [vars(s) for s in scores],
+            "add": {"assign_100k_s": t1 - t0, "resume_1M_1epoch_s": t2 - t1},
+            "cpu_baseline": {"value": 1.0 / cpu_fit_s, "unit": "fits/s", "cores": O.get_threads(),
+                             "kind": "port", "fit_s": cpu_fit_s,
+                             "sample": f"one fit (k = {kc}: train_from k-means++ rows, 5 epochs, "
+                                       f"then assign) on the same {n} rows"}}
+
+
 def copy_probe(mib):
     """A plain device-to-device copy of `mib` MiB, three times: the known-size
     kernel that calibrates the HBM byte counters (FETCH_SIZE, WRITE_SIZE)."""
@@ -542,7 +611,9 @@ def main():
                     help="queries the oracle checks at 500k x 384 (the CPU baseline sample)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run a plain device copy of MIB MiB (HBM counter calibration)")
-    ap.add_argument("--workload", choices=["headline", "knn", "assign"], default="headline",
+    ap.add_argument("--autok-restarts", type=int, default=4)
+    ap.add_argument("--workload", choices=["headline", "knn", "assign", "autok"],
+                    default="headline",
                     help="headline: train + assign 200k x 768 (the metric); knn: knn_self "
                          "500k x 384; assign: 2M x 1024 vs k = 16384")
     ap.add_argument("--knn-n", type=int, default=500_000)
@@ -558,7 +629,8 @@ def main():
         sys.exit("--steps must be >= 1")
     if args.copy_probe:
         copy_probe(args.copy_probe)
-    out = {"headline": headline, "knn": knn_workload, "assign": assign_workload}[args.workload](args)
+    out = {"headline": headline, "knn": knn_workload, "assign": assign_workload,
+           "autok": autok_workload}[args.workload](args)
     print(json.dumps(out), flush=True)
 
 

@@ -290,6 +290,25 @@ class HipDevice:
         check(lib().emh_profile_read_op(self._ctx, code, C.byref(ms), C.byref(n), C.byref(u)))
         return ms.value, n.value, u.value
 
+    def kmeans_pp(self, x: DevBuf, n: int, d: int, kmax: int, seed: int) -> np.ndarray:
+        """kmeans_pp (emeans-cluster/src/auto.rs:401-455) on rows resident on the device."""
+        picks = np.zeros(max(kmax, 1), np.uint32)
+        m = C.c_size_t()
+        check(lib().emh_kmeans_pp(self._ctx, x.h, n, d, kmax, seed & 0xFFFFFFFF, _p(picks),
+                                  C.byref(m)))
+        return picks[:m.value].copy()
+
+    def internal_scores(self, x: DevBuf, n: int, d: int, labels: DevBuf, k: int) -> dict:
+        """internal_scores (emeans-cluster/src/metrics.rs:113-268) on the device."""
+        from ._lib import Internal
+        r = Internal()
+        sizes = np.zeros(k, np.uint64)
+        check(lib().emh_internal_scores(self._ctx, x.h, n, d, labels.h, k, C.byref(r),
+                                        _p(sizes)))
+        return {"k_eff": int(r.k_eff), "silhouette": r.silhouette,
+                "calinski_harabasz": r.calinski_harabasz, "davies_bouldin": r.davies_bouldin,
+                "objective": r.objective, "sizes": sizes.astype(np.int64)}
+
     SCREEN_VARIANTS = {0: "none", 1: "big_tagged", 2: "big_sorted", 3: "small_bf16",
                        4: "small_f32"}
 
@@ -462,10 +481,11 @@ class Assignment:
     scores: np.ndarray
 
     def mean_objective(self, spherical: bool) -> float:
-        """Mean squared distance, or mean of 2 - 2 cos (model.rs:127-141)."""
+        """Mean squared distance, or mean of 2 - 2 cos (model.rs:127-141): an
+        f64 sum in row order."""
         s = self.scores.astype(np.float64)
         v = 2.0 - 2.0 * s if spherical else s
-        return float(np.add.reduce(v, dtype=np.float64) / max(len(v), 1))
+        return float(np.cumsum(v)[-1] / len(v)) if len(v) else 0.0
 
 
 class Emeans:

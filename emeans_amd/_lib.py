@@ -51,6 +51,12 @@ class ScreenReport(C.Structure):
                 ("max_dot_ratio", C.c_double)]
 
 
+class Internal(C.Structure):
+    _fields_ = [("k_eff", C.c_uint64), ("silhouette", C.c_double),
+                ("calinski_harabasz", C.c_double), ("davies_bouldin", C.c_double),
+                ("objective", C.c_double)]
+
+
 class TrainInit(C.Structure):
     _fields_ = [("centroids", C.c_void_p), ("centroids_dev", C.c_void_p),
                 ("positions", C.c_void_p), ("usage", C.c_void_p)]
@@ -119,6 +125,8 @@ SIGNATURES = {
     "emh_dedup_neighbors": (_i, [_vp, _sz, _sz, _vp, _vp, _sz, _vp, _vp, _vp]),
     "emh_dedup": (_i, [_vp, _vp, _sz, _sz, _vp, _vp, _vp]),
     "emh_fallback_rows": (_u64, [_vp]),
+    "emh_kmeans_pp": (_i, [_vp, _vp, _sz, _sz, _sz, _u32, _vp, C.POINTER(_sz)]),
+    "emh_internal_scores": (_i, [_vp, _vp, _sz, _sz, _vp, _sz, _vp, _vp]),
     "emh_screen_margin": (_i, [_vp, _vp, _sz, _vp, _sz, _sz, _vp, _vp, _sz, _i, _vp]),
     "emh_screen_margin_topk": (_i, [_vp, _vp, _sz, _vp, _sz, _sz, _i, _vp]),
     "emh_set_screen": (_i, [_vp, _i]),

@@ -1,0 +1,171 @@
+"""The sweep pattern of automatic k (emeans-cluster/src/auto.rs) on the gfx950
+backend: many spherical e-means models trained and scored on one context with
+the data bound once.
+
+  seed_for   auto.rs:343-349  the seed of each (salt, k, restart)
+  fit        auto.rs:351-375  train_from k-means++ rows (or train), then assign
+  sweep      auto.rs:457-510  every k of a list, best of `restarts`, scored by
+                              internal_scores (on the device)
+  select     auto.rs:513-542  the chosen k of a sweep
+  kmeans_pp  auto.rs:401-455  on the device (HipDevice.kmeans_pp)
+
+Two-level auto_cluster and Hierarchy (auto.rs:1001-1101, incremental.rs) are
+callers of these: a level-1 sweep, then a level-2 sweep inside each group;
+Hierarchy::add assigns new rows and, by its policy, resumes the models from
+their EMA state (Emeans.train_resume).
+"""
+
+import time
+from dataclasses import dataclass, field
+from typing import List, Optional, Tuple
+
+import numpy as np
+
+from . import Config, HipDevice
+
+
+@dataclass
+class AutoConfig:
+    """The AutoConfig fields the sweeps read (auto.rs:99-175), with its defaults."""
+    k1_range: Tuple[int, int] = (2, 40)
+    k2_max: int = 20
+    criterion1: str = "silhouette"
+    criterion2: str = "davies_bouldin"
+    level1_tolerance: float = 0.0
+    level2_tolerance: float = 0.05
+    min_cluster_size: int = 20
+    max_cluster_size: int = 200
+    restarts: int = 4
+    nepochs: float = 5.0
+    init: str = "kmeans_plus_plus"  # or "random_rows"
+    seed: int = 1234
+
+
+@dataclass
+class KScore:
+    """Scores of one k in a sweep (auto.rs:178-192)."""
+    k: int
+    k_eff: int
+    silhouette: float
+    calinski_harabasz: float
+    davies_bouldin: float
+    objective: float
+    browsable: float
+    seconds: float
+
+
+@dataclass
+class Fitted:
+    """One fitted model of a sweep: its centroids and assignment (device buffers)."""
+    k: int
+    seed: int
+    centroids: np.ndarray
+    labels: object  # DevBuf, u32 n
+    scores: object  # DevBuf, f32 n
+    objective: float
+    positions: np.ndarray = None  # EMA state, for a later resume
+    usage: np.ndarray = None
+
+
+def criterion_value(crit: str, s: KScore) -> float:
+    """Criterion::value (auto.rs:53-60): the criterion as higher-is-better."""
+    if crit == "silhouette":
+        return s.silhouette
+    if crit == "calinski_harabasz":
+        return s.calinski_harabasz
+    if crit == "davies_bouldin":
+        return -s.davies_bouldin
+    raise ValueError(f"unknown criterion {crit!r}")
+
+
+def seed_for(cfg: AutoConfig, salt: int, k: int, restart: int) -> int:
+    """u32 wrapping arithmetic of auto.rs:343-349."""
+    m = 0xFFFFFFFF
+    return (cfg.seed + ((salt * 7919) & m) + ((k * 131) & m) + ((restart * 1_000_003) & m)) & m
+
+
+def fit(dev: HipDevice, x: np.ndarray, xb, k: int, nepochs: float, seed: int,
+        init_rows: Optional[np.ndarray]) -> Fitted:
+    """auto.rs:351-375: one spherical e-means model (capture off) from the
+    first k k-means++ rows (or k sampled rows), then the assignment of every row."""
+    n, d = x.shape
+    c = Config(d=d, k=k, spherical=True, nepochs=nepochs, seed=seed, capture_assignments=False)
+    if init_rows is not None:
+        if len(init_rows) < k:
+            raise ValueError("need k init rows")
+        init = x[np.asarray(init_rows[:k], np.int64)]
+    else:
+        init = None
+    cb = dev.zeros_f32(k * d)
+    cent, info = dev.train_dev(xb, n, c, centroids_out=cb, init=init)
+    labels, scores = dev.zeros_u32(n), dev.zeros_f32(n)
+    dev.assign_dev(xb, n, d, cb, k, "ip", labels, scores)
+    s = dev.read_f32(scores).astype(np.float64)
+    obj = float(np.cumsum(2.0 - 2.0 * s)[-1] / n)  # Assignment::mean_objective(true)
+    return Fitted(k, seed, cent, labels, scores, obj, info["positions"], info["usage"])
+
+
+def browsable(sizes, cfg: AutoConfig) -> float:
+    """auto.rs:377-384: the fraction of rows in clusters of browsable size."""
+    sizes = np.asarray(sizes, np.int64)
+    ok = sizes[(sizes >= cfg.min_cluster_size) & (sizes <= cfg.max_cluster_size)].sum()
+    return float(ok) / float(max(int(sizes.sum()), 1))
+
+
+def sweep(dev: HipDevice, x: np.ndarray, xb, ks: List[int], cfg: AutoConfig, salt: int,
+          verbose: bool = False, timing: Optional[dict] = None):
+    """auto.rs:457-510: for every k, the best (lowest objective) of
+    cfg.restarts fits, each seeded by its restart's k-means++ rows (one
+    seeding per restart, up to the largest k); scored by internal_scores.
+    Returns [(KScore, Fitted)] and the k-means++ picks of each restart."""
+    n, d = x.shape
+    tm = timing if timing is not None else {}
+    for key in ("kmeans_pp_s", "fit_s", "scores_s"):
+        tm.setdefault(key, 0.0)
+    tm.setdefault("fits", 0)
+    kmax = max(ks) if ks else 1
+    t0 = time.perf_counter()
+    inits = [dev.kmeans_pp(xb, n, d, kmax, seed_for(cfg, salt, 0, r))
+             if cfg.init == "kmeans_plus_plus" else None for r in range(max(cfg.restarts, 1))]
+    tm["kmeans_pp_s"] += time.perf_counter() - t0
+    out = []
+    for k in ks:
+        t = time.perf_counter()
+        best = None
+        for r, rows in enumerate(inits):
+            f = fit(dev, x, xb, k, cfg.nepochs, seed_for(cfg, salt, k, r), rows)
+            tm["fits"] += 1
+            if best is None or f.objective < best.objective:
+                best = f
+        t1 = time.perf_counter()
+        tm["fit_s"] += t1 - t
+        i = dev.internal_scores(xb, n, d, best.labels, k)
+        tm["scores_s"] += time.perf_counter() - t1
+        s = KScore(k, i["k_eff"], i["silhouette"], i["calinski_harabasz"], i["davies_bouldin"],
+                   i["objective"], browsable(i["sizes"], cfg), time.perf_counter() - t)
+        if verbose:
+            print(f"  k={k:3} k_eff={s.k_eff:3} sil={s.silhouette:.4f} "
+                  f"ch={s.calinski_harabasz:.1f} db={s.davies_bouldin:.3f} "
+                  f"obj={s.objective:.4f} browsable={s.browsable:.2f} ({s.seconds:.2f}s)")
+        out.append((s, best))
+    return out, inits
+
+
+def select(scores: List[KScore], cfg: AutoConfig, prefer_browsable: bool) -> int:
+    """auto.rs:513-542: among the k within the tolerance of the best criterion,
+    the smallest k (level 1), or the most browsable then the smaller k (level 2)."""
+    crit = cfg.criterion2 if prefer_browsable else cfg.criterion1
+    v = [criterion_value(crit, s) for s in scores]
+    best = max(v) if v else float("-inf")
+    tol = cfg.level2_tolerance if prefer_browsable else cfg.level1_tolerance
+    floor = best - tol * abs(best)
+    cands = [i for i in range(len(scores)) if v[i] >= floor]
+    if prefer_browsable:
+        # max_by: browsable (total order), then the smaller k; the last of equal maxima
+        top = cands[0]
+        for i in cands[1:]:
+            a, b = scores[i], scores[top]
+            if (a.browsable, -a.k) >= (b.browsable, -b.k):
+                top = i
+        return top
+    return min(cands, key=lambda i: scores[i].k)

@@ -185,7 +185,8 @@ int emh_destroy(emh_ctx* c) {
       s->release();
     for (emh::Pinned* s : {&c->pin_usage, &c->pin_plan, &c->pin_small, &c->pin_order[0],
                            &c->pin_order[1], &c->pin_lab[0], &c->pin_lab[1], &c->pin_sco[0],
-                           &c->pin_sco[1], &c->pin_out, &c->pin_stage[0], &c->pin_stage[1]})
+                           &c->pin_sco[1], &c->pin_out, &c->pin_stage[0], &c->pin_stage[1],
+                           &c->pin_aux})
       s->release();
     if (c->small) (void)hipFree(c->small);
     for (hipEvent_t e : c->ev_pool) (void)hipEventDestroy(e);

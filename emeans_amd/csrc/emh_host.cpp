@@ -1004,6 +1004,177 @@ size_t dedup_groups(const float* x, size_t n, size_t d, const uint32_t* nb_ids,
   return groups.size();
 }
 
+// ------------------------------------------------------------- auto-k pieces
+// kmeans_pp (emeans-cluster/src/auto.rs:401-455) on rows resident on the
+// device: each pick's row dots raise every row's best cosine on the device
+// (k_pp_best); the D^2 weights, their f64 sum and the draw run here in row
+// order, as the reference's.
+std::vector<uint32_t> kmeans_pp_dev(emh_ctx* c, const float* x, size_t n, size_t d, size_t kmax,
+                                    uint32_t seed) {
+  kmax = std::min(kmax, n);
+  std::vector<uint32_t> picks;
+  if (kmax == 0) return picks;
+  RandomState rng(seed);
+  size_t last = (size_t)rng.interval(n - 1);
+  picks.push_back((uint32_t)last);
+  Buf best(c, n * 4);
+  launch_fill_u32(c, best.u(), n, 0xff800000u);  // -inf
+  float* hb = (float*)c->pin_aux.get(n * 4);
+  std::vector<double> w(n);
+  std::vector<char> picked(n, 0);
+  picked[last] = 1;
+  while (picks.size() < kmax) {
+    launch_pp_best(c, x, n, d, last, best.f());
+    copy_async(c, hb, best.p, n * 4, hipMemcpyDeviceToHost);
+    EMH_HIP(hipStreamSynchronize(c->stream));
+    double total = 0.0;
+    for (size_t i = 0; i < n; i++) {
+      const double dist = std::fmax(1.0 - (double)hb[i], 0.0);
+      w[i] = dist * dist;
+      total += w[i];
+    }
+    size_t next = 0;
+    if (total > 0.0) {
+      double u = rng.random_sample() * total;
+      size_t j = n - 1;
+      for (size_t i = 0; i < n; i++) {
+        if (u < w[i]) {
+          j = i;
+          break;
+        }
+        u -= w[i];
+      }
+      if (w[j] == 0.0) {  // rounding landed on a zero weight: the last of the largest
+        size_t m = 0;
+        for (size_t i = 1; i < n; i++)
+          if (!(w[i] < w[m])) m = i;
+        j = m;
+      }
+      next = j;
+    } else {  // every row coincides with a pick: the first unpicked row
+      while (next < n && picked[next]) next++;
+      if (next == n) next = 0;
+    }
+    picks.push_back((uint32_t)next);
+    picked[next] = 1;
+    last = next;
+  }
+  return picks;
+}
+
+// internal_scores (emeans-cluster/src/metrics.rs:113-268) of labels (n, on
+// the device, < k) on unit rows resident on the device. The cluster sums and
+// every row's terms come from the device; the row-order f64 sums, the
+// Calinski-Harabasz dispersions and the Davies-Bouldin ratios run here.
+void internal_scores_dev(emh_ctx* c, const float* x, size_t n, size_t d, const uint32_t* labels_d,
+                         size_t k, emh_internal* out, uint64_t* sizes_out) {
+  std::vector<uint32_t> lab(n);
+  copy_async(c, lab.data(), labels_d, n * 4, hipMemcpyDeviceToHost);
+  EMH_HIP(hipStreamSynchronize(c->stream));
+  std::vector<uint64_t> sizes(k, 0);
+  for (size_t i = 0; i < n; i++) {
+    EMH_ENSURE(lab[i] < k, "label out of range");
+    sizes[lab[i]]++;
+  }
+  std::vector<uint32_t> live, slot(k, 0xffffffffu);
+  for (size_t j = 0; j < k; j++)
+    if (sizes[j] > 0) {
+      slot[j] = (uint32_t)live.size();
+      live.push_back((uint32_t)j);
+    }
+  const size_t ke = live.size();
+  // Rows grouped by cluster, in row order within each (a stable counting sort).
+  std::vector<uint32_t> start(ke + 1, 0), rid(n), own(n);
+  for (size_t s = 0; s < ke; s++) start[s + 1] = start[s] + (uint32_t)sizes[live[s]];
+  {
+    std::vector<uint32_t> at(start.begin(), start.end() - 1);
+    for (size_t i = 0; i < n; i++) {
+      own[i] = slot[lab[i]];
+      rid[at[own[i]]++] = (uint32_t)i;
+    }
+  }
+  Buf rid_d(c, n * 4), start_d(c, (ke + 1) * 4), own_d(c, n * 4), sums_d(c, ke * d * 8),
+      s32_d(c, ke * d * 4), size_d(c, ke * 8), sq_d(c, ke * 8), g_d(c, n * ke * 4),
+      xx_d(c, n * 8), sil_d(c, n * 8), obj_d(c, n * 8), dist_d(c, n * 8);
+  h2d(c, rid_d.p, rid.data(), n * 4);
+  h2d(c, start_d.p, start.data(), (ke + 1) * 4);
+  h2d(c, own_d.p, own.data(), n * 4);
+  std::vector<double> sums(ke * d), sq(ke, 0.0), size(ke);
+  if (ke > 0) launch_sum64(c, x, d, rid_d.u(), start_d.u(), ke, (double*)sums_d.p);
+  d2h(c, sums.data(), sums_d.p, ke * d * 8);
+  std::vector<float> s32(ke * d);
+  for (size_t s = 0; s < ke; s++) {
+    size[s] = (double)sizes[live[s]];
+    for (size_t t = 0; t < d; t++) {
+      const double v = sums[s * d + t];
+      s32[s * d + t] = (float)v;
+      sq[s] += v * v;
+    }
+  }
+  h2d(c, s32_d.p, s32.data(), ke * d * 4);
+  h2d(c, size_d.p, size.data(), ke * 8);
+  h2d(c, sq_d.p, sq.data(), ke * 8);
+  std::vector<double> xx(n), sil(n), obj(n), dist(n);
+  if (n > 0) {
+    if (ke > 0) {
+      launch_row_dots(c, x, n, d, s32_d.f(), ke, g_d.f(), (double*)xx_d.p);
+      launch_iscore_terms(c, n, ke, g_d.f(), (double*)xx_d.p, own_d.u(), (double*)size_d.p,
+                          (double*)sq_d.p, (double*)sil_d.p, (double*)obj_d.p, (double*)dist_d.p);
+    }
+    d2h(c, xx.data(), xx_d.p, n * 8);
+    d2h(c, sil.data(), sil_d.p, n * 8);
+    d2h(c, obj.data(), obj_d.p, n * 8);
+    d2h(c, dist.data(), dist_d.p, n * 8);
+  }
+  double sil_sum = 0.0, obj_sum = 0.0, total_xx = 0.0;
+  std::vector<double> scatter(ke, 0.0);
+  for (size_t i = 0; i < n; i++) {
+    sil_sum += sil[i];
+    obj_sum += obj[i];
+    scatter[own[i]] += dist[i];
+  }
+  for (size_t i = 0; i < n; i++) total_xx += xx[i];
+  const double nf = (double)std::max<size_t>(n, 1);
+  double wsum = 0.0;
+  for (size_t s = 0; s < ke; s++) wsum += sq[s] / size[s];
+  const double within = total_xx - wsum;
+  std::vector<double> grand(d, 0.0);
+  for (size_t s = 0; s < ke; s++)
+    for (size_t t = 0; t < d; t++) grand[t] += sums[s * d + t];
+  double gsq = 0.0;
+  for (size_t t = 0; t < d; t++) gsq += grand[t] * grand[t];
+  const double between = (total_xx - gsq / nf) - within;
+  out->calinski_harabasz = (ke < 2 || n <= ke || within <= 0.0)
+                               ? 0.0
+                               : (between / (double)(ke - 1)) / (within / (double)(n - ke));
+  double db = 0.0;
+  if (ke >= 2) {
+    double acc = 0.0;
+    for (size_t a = 0; a < ke; a++) {
+      double worst = 0.0;
+      for (size_t b = 0; b < ke; b++) {
+        if (b == a) continue;
+        double m2 = 0.0;
+        for (size_t t = 0; t < d; t++) {
+          const double p = sums[a * d + t] / size[a], q = sums[b * d + t] / size[b];
+          m2 += (p - q) * (p - q);
+        }
+        const double m = std::sqrt(m2);
+        const double r = m > 0.0 ? (scatter[a] / size[a] + scatter[b] / size[b]) / m : INFINITY;
+        worst = std::fmax(worst, r);
+      }
+      acc += worst;
+    }
+    db = acc / (double)ke;
+  }
+  out->k_eff = ke;
+  out->silhouette = sil_sum / nf;
+  out->davies_bouldin = db;
+  out->objective = obj_sum / nf;
+  if (sizes_out)
+    for (size_t j = 0; j < k; j++) sizes_out[j] = sizes[j];
+}
+
 }  // namespace host
 }  // namespace emh
 
@@ -1199,6 +1370,34 @@ int emh_dedup(emh_ctx* c, const float* x, size_t n, size_t d, const emh_dedup_in
     }
     if (emh_dedup_neighbors(x, n, d, ids.data(), sims.data(), k, in, cfg, out) != EMH_OK)
       throw emh::Failure(emh_last_error());
+  });
+}
+
+int emh_kmeans_pp(emh_ctx* c, const emh_buf* x, size_t n, size_t d, size_t kmax, uint32_t seed,
+                  uint32_t* picks, size_t* n_picks) {
+  return guard2([&] {
+    EMH_ENSURE(c && x && x->kind == 0 && picks && n_picks, "null argument");
+    EMH_ENSURE(d > 0 && x->len >= n * d, "x must be n x d");
+    EMH_ENSURE(n < (1ull << 32), "kmeans_pp: too many rows");
+    EMH_HIP(hipSetDevice(c->device));
+    const std::vector<uint32_t> p = kmeans_pp_dev(c, (const float*)x->ptr, n, d, kmax, seed);
+    std::memcpy(picks, p.data(), p.size() * 4);
+    *n_picks = p.size();
+  });
+}
+
+int emh_internal_scores(emh_ctx* c, const emh_buf* x, size_t n, size_t d, const emh_buf* labels,
+                        size_t k, emh_internal* out, uint64_t* sizes) {
+  return guard2([&] {
+    EMH_ENSURE(c && x && labels && out, "null argument");
+    EMH_ENSURE(x->kind == 0 && labels->kind == 1, "x f32, labels u32");
+    EMH_ENSURE(d > 0 && x->len >= n * d, "x must be n x d");
+    EMH_ENSURE(labels->len >= n, "one label per row");
+    EMH_ENSURE(k > 0 && n < (1ull << 32), "bad shape");
+    EMH_HIP(hipSetDevice(c->device));
+    emh_internal r{};
+    internal_scores_dev(c, (const float*)x->ptr, n, d, (const uint32_t*)labels->ptr, k, &r, sizes);
+    *out = r;
   });
 }
 

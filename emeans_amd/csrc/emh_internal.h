@@ -162,6 +162,7 @@ struct emh_ctx {
   // pinned halves, each with the event of the last copy that read it, and the
   // event the context stream waits on for the whole upload.
   emh::Pinned pin_stage[2];
+  emh::Pinned pin_aux;  // kmeans_pp's best cosines on the way to the host
   hipEvent_t ev_stage[3] = {nullptr, nullptr, nullptr};
   std::string name = "hip-gfx950";
   // Op timing (emh_profile): event pairs on the context stream around every
@@ -279,6 +280,20 @@ void launch_scatter_count(emh_ctx* c, size_t lo, size_t hi, const uint32_t* labe
 void launch_scatter_sums(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
                          size_t lo, size_t hi, const uint32_t* labels, size_t k, float* sums,
                          float* acc);
+
+// ---- emh_autok.hip (kmeans_pp and internal_scores of the automatic-k callers)
+// best[i] = max(best[i], dot(x[i], x[last])), the dot in sequence without fma.
+void launch_pp_best(emh_ctx* c, const float* x, size_t n, size_t d, size_t last, float* best);
+// sums[s][t] = f64 sum over rows rid[start[s] .. start[s + 1]) of x[row][t], in order.
+void launch_sum64(emh_ctx* c, const float* x, size_t d, const uint32_t* rid,
+                  const uint32_t* start, size_t ke, double* sums);
+// g[i][s] = fma chain of x[i] . sums32[s] (i < n, s < ke); xx[i] = f64 sum of squares.
+void launch_row_dots(emh_ctx* c, const float* x, size_t n, size_t d, const float* sums32,
+                     size_t ke, float* g, double* xx);
+// Per-row silhouette, objective and distance terms (metrics.rs:158-184).
+void launch_iscore_terms(emh_ctx* c, size_t n, size_t ke, const float* g, const double* xx,
+                         const uint32_t* own, const double* size, const double* sq, double* sil,
+                         double* obj, double* dist);
 
 // ---- emh_screen.hip (top-1 and top-k orchestration)
 // words_clear: the caller zeroed the screen's small-block words since the

@@ -92,9 +92,11 @@ def knn_near_duplicates(n=500_000, d=384, frac=0.05, noise=0.01, seed=2):
 
 
 def nested(n=1_000_000, d=768, top=64, sub=16, s=1.3, sub_sigma=0.3, row_sigma=0.05, seed=3,
-           chunk=100_000):
+           chunk=65_536, threads=None):
     """Two-level mixture: top centers (Zipf(s) weights), sub-centers = center +
-    N(0, sub_sigma^2) renormalised, rows = sub-center + N(0, row_sigma^2) renormalised."""
+    N(0, sub_sigma^2) renormalised, rows = sub-center + N(0, row_sigma^2)
+    renormalised. Returns the rows and each row's sub-center (top * sub + j).
+    Row chunks draw their noise from their own PCG64 streams."""
     g = np.random.default_rng(seed)
     centers = _unit(g.standard_normal((top, d), dtype=np.float32))
     subs = centers[:, None, :] + np.float32(sub_sigma) * g.standard_normal((top, sub, d),
@@ -103,9 +105,16 @@ def nested(n=1_000_000, d=768, top=64, sub=16, s=1.3, sub_sigma=0.3, row_sigma=0
     t = g.choice(top, size=n, p=zipf_weights(top, s))
     lab = t * sub + g.integers(0, sub, size=n)
     x = np.empty((n, d), np.float32)
-    for a in range(0, n, chunk):
-        b = min(a + chunk, n)
-        x[a:b] = _unit(subs[lab[a:b]] + np.float32(row_sigma) *
-                       g.standard_normal((b - a, d), dtype=np.float32))
-    return x, lab
+    starts = list(range(0, n, chunk))
+    seqs = np.random.SeedSequence(int(g.integers(1 << 31))).spawn(len(starts))
 
+    def fill(i):
+        a = starts[i]
+        b = min(a + chunk, n)
+        gc = np.random.Generator(np.random.PCG64(seqs[i]))
+        x[a:b] = _unit(subs[lab[a:b]] + np.float32(row_sigma) *
+                       gc.standard_normal((b - a, d), dtype=np.float32))
+
+    with ThreadPoolExecutor(max_workers=threads or min(16, os.cpu_count() or 1)) as ex:
+        list(ex.map(fill, range(len(starts))))
+    return x, lab

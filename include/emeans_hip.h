@@ -283,6 +283,30 @@ int emh_dedup_neighbors(const float* x, size_t n, size_t d, const uint32_t* nb_i
 int emh_dedup(emh_ctx* ctx, const float* x, size_t n, size_t d, const emh_dedup_input* input,
               const emh_dedup_config* cfg, emh_dedup_result* out);
 
+/* --------------------------------------------- the automatic-k callers */
+/* kmeans_pp (emeans-cluster/src/auto.rs:401-455): k-means++ seeding with the
+ * cosine distance 1 - x.y on the rows of x (n x d f32 buffer, unit rows):
+ * min(kmax, n) row ids in pick order (picks has kmax entries), the same as the
+ * reference's for the same seed. */
+int emh_kmeans_pp(emh_ctx* ctx, const emh_buf* x, size_t n, size_t d, size_t kmax,
+                  uint32_t seed, uint32_t* picks, size_t* n_picks);
+
+/* Internal (emeans-cluster/src/metrics.rs:95-111). */
+typedef struct emh_internal {
+  uint64_t k_eff;             /* non-empty clusters */
+  double silhouette;          /* mean cosine-distance silhouette */
+  double calinski_harabasz;
+  double davies_bouldin;
+  double objective;           /* mean 2 - 2 cos to the normalized cluster mean */
+} emh_internal;
+/* internal_scores (metrics.rs:113-268) of labels (n entries < k, u32
+ * buffer) on the unit rows of x (n x d f32 buffer); sizes (k, may be NULL)
+ * gets the rows per label. The reference takes the row-by-cluster-sum dots
+ * from the gemm crate; here each is one fma chain over the columns in order
+ * (the scores agree with scikit-learn's within the reference's 1e-5). */
+int emh_internal_scores(emh_ctx* ctx, const emh_buf* x, size_t n, size_t d, const emh_buf* labels,
+                        size_t k, emh_internal* out, uint64_t* sizes);
+
 /* ------------------------------------------------- host replay (no device) */
 /* The seeded host-side pieces of the device loop, exported so that callers and
  * tests can check them without a GPU. They never touch the device. */

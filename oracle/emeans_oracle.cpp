@@ -962,6 +962,177 @@ uint64_t orc_dedup(const float* x, uint64_t n, uint64_t d, const uint32_t* nb_id
   return groups.size();
 }
 
+// --- kmeans_pp (crates/emeans-cluster/src/auto.rs:401-455): k-means++ seeding
+// with the cosine distance 1 - x.y; kmax row ids in pick order. The dots are
+// dedup.rs's order: rounded products added in sequence (no fma).
+uint64_t orc_kmeans_pp(const float* x, uint64_t n, uint64_t d, uint64_t kmax, uint32_t seed,
+                       uint32_t* picks) {
+  kmax = std::min(kmax, n);
+  if (kmax == 0) return 0;
+  RandomState rng(seed);
+  const size_t first = (size_t)rng.random_interval(n - 1);
+  std::vector<uint32_t> pk{(uint32_t)first};
+  std::vector<float> best(n, -INFINITY);
+  std::vector<double> w(n);
+  size_t last = first;
+  while (pk.size() < kmax) {
+    const float* c = x + last * d;
+    for (size_t i = 0; i < n; i++) {
+      const float s = dot_seq(x + i * d, c, d);
+      if (s > best[i]) best[i] = s;
+    }
+    double total = 0.0;
+    for (size_t i = 0; i < n; i++) {
+      const double dist = std::fmax(1.0 - (double)best[i], 0.0);  // f64::max
+      w[i] = dist * dist;
+      total += w[i];
+    }
+    size_t next;
+    if (total > 0.0) {
+      double u = rng.random_sample() * total;
+      size_t j = n - 1;
+      for (size_t i = 0; i < n; i++) {
+        if (u < w[i]) {
+          j = i;
+          break;
+        }
+        u -= w[i];
+      }
+      if (w[j] == 0.0) {  // the farthest row; the last of equal maxima (Iterator::max_by)
+        size_t m = 0;
+        for (size_t i = 1; i < n; i++)
+          if (!(w[i] < w[m])) m = i;
+        j = m;
+      }
+      next = j;
+    } else {
+      next = 0;
+      for (size_t i = 0; i < n; i++)
+        if (std::find(pk.begin(), pk.end(), (uint32_t)i) == pk.end()) {
+          next = i;
+          break;
+        }
+    }
+    pk.push_back((uint32_t)next);
+    last = next;
+  }
+  std::memcpy(picks, pk.data(), pk.size() * 4);
+  return pk.size();
+}
+
+// --- internal_scores (crates/emeans-cluster/src/metrics.rs:113-268): cosine
+// silhouette, Calinski-Harabasz, Davies-Bouldin and the spherical objective of
+// `labels` (< k) on unit rows. The row-by-cluster-sum dots come from the
+// `gemm` crate in the reference; here they are one fma chain each over t in
+// order. Everything else keeps the reference's f64 order, with its parallel
+// sums taken in index order. out: silhouette, CH, DB, objective; sizes k.
+int orc_internal_scores(const float* x, uint64_t n, uint64_t d, const uint32_t* labels,
+                        uint64_t k, double* out, uint64_t* sizes_out, uint64_t* k_eff_out) {
+  for (size_t i = 0; i < n; i++)
+    if (labels[i] >= k) return 1;
+  std::vector<uint64_t> sizes(k, 0);
+  std::vector<double> sums(k * d, 0.0);
+  for (size_t i = 0; i < n; i++) {
+    sizes[labels[i]]++;
+    double* s = &sums[labels[i] * d];
+    for (size_t t = 0; t < d; t++) s[t] += (double)x[i * d + t];
+  }
+  std::vector<size_t> live;
+  for (size_t j = 0; j < k; j++)
+    if (sizes[j] > 0) live.push_back(j);
+  const size_t ke = live.size();
+  std::vector<float> sums32(ke * d);
+  std::vector<double> sq(ke, 0.0);
+  std::vector<size_t> slot(k, SIZE_MAX);
+  for (size_t s = 0; s < ke; s++) {
+    slot[live[s]] = s;
+    for (size_t t = 0; t < d; t++) {
+      const double v = sums[live[s] * d + t];
+      sums32[s * d + t] = (float)v;
+      sq[s] += v * v;
+    }
+  }
+  std::vector<double> xx(n);
+  for (size_t i = 0; i < n; i++) {
+    double a = 0.0;
+    for (size_t t = 0; t < d; t++) a += (double)x[i * d + t] * (double)x[i * d + t];
+    xx[i] = a;
+  }
+  double sil_sum = 0.0, obj_sum = 0.0;
+  std::vector<double> scatter(ke, 0.0);
+  std::vector<float> g(ke);
+  for (size_t i = 0; i < n; i++) {
+    for (size_t s = 0; s < ke; s++) {
+      float acc = 0.0f;
+      for (size_t t = 0; t < d; t++) acc = std::fma(x[i * d + t], sums32[s * d + t], acc);
+      g[s] = acc;
+    }
+    const size_t own = slot[labels[i]];
+    const double na = (double)sizes[live[own]];
+    const double dot_own = (double)g[own];
+    const double dist = std::sqrt(std::fmax(xx[i] - 2.0 * dot_own / na + sq[own] / (na * na), 0.0));
+    const double cos_c = dot_own / std::fmax(std::sqrt(sq[own]), 1e-30);
+    const double obj = 2.0 - 2.0 * cos_c;
+    double sil = 0.0;
+    if (!(ke < 2 || na < 2.0)) {
+      const double a = 1.0 - (dot_own - xx[i]) / (na - 1.0);
+      double b = INFINITY;
+      for (size_t s = 0; s < ke; s++)
+        if (s != own) b = std::fmin(b, 1.0 - (double)g[s] / (double)sizes[live[s]]);
+      const double m = std::fmax(a, b);
+      sil = m > 0.0 ? (b - a) / m : 0.0;
+    }
+    sil_sum += sil;
+    obj_sum += obj;
+    scatter[own] += dist;
+  }
+  const double nf = (double)std::max<uint64_t>(n, 1);
+  double total_xx = 0.0;
+  for (size_t i = 0; i < n; i++) total_xx += xx[i];
+  double wsum = 0.0;
+  for (size_t s = 0; s < ke; s++) wsum += sq[s] / (double)sizes[live[s]];
+  const double within = total_xx - wsum;
+  std::vector<double> grand(d, 0.0);
+  for (size_t s = 0; s < ke; s++)
+    for (size_t t = 0; t < d; t++) grand[t] += sums[live[s] * d + t];
+  double gsq = 0.0;
+  for (size_t t = 0; t < d; t++) gsq += grand[t] * grand[t];
+  const double total = total_xx - gsq / nf;
+  const double between = total - within;
+  const double ch = (ke < 2 || n <= ke || within <= 0.0)
+                        ? 0.0
+                        : (between / (double)(ke - 1)) / (within / (double)(n - ke));
+  double db = 0.0;
+  if (ke >= 2) {
+    double acc = 0.0;
+    for (size_t a = 0; a < ke; a++) {
+      double worst = 0.0;
+      for (size_t b = 0; b < ke; b++) {
+        if (b == a) continue;
+        double m2 = 0.0;
+        for (size_t t = 0; t < d; t++) {
+          const double p = sums[live[a] * d + t] / (double)sizes[live[a]];
+          const double q = sums[live[b] * d + t] / (double)sizes[live[b]];
+          m2 += (p - q) * (p - q);
+        }
+        const double m = std::sqrt(m2);
+        const double sa = scatter[a] / (double)sizes[live[a]], sb = scatter[b] / (double)sizes[live[b]];
+        const double r = m > 0.0 ? (sa + sb) / m : INFINITY;
+        worst = std::fmax(worst, r);
+      }
+      acc += worst;
+    }
+    db = acc / (double)ke;
+  }
+  out[0] = sil_sum / nf;
+  out[1] = ch;
+  out[2] = db;
+  out[3] = obj_sum / nf;
+  for (size_t j = 0; j < k; j++) sizes_out[j] = sizes[j];
+  *k_eff_out = ke;
+  return 0;
+}
+
 // --- Test-data generators of the reference's own tests.
 // core/contract.rs:40-60 (`mixture`): Box-Muller over MT19937 random_sample, f64.
 void orc_contract_mixture(uint64_t n, uint64_t d, uint64_t centers, double sigma, int unit,

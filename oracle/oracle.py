@@ -54,6 +54,9 @@ def _load():
         "orc_get_threads": (i32, []),
         "orc_train": (i32, [_f32p, u64, vp, vp]),
         "orc_train_from": (i32, [_f32p, u64, vp, vp, vp, vp, vp]),
+        "orc_kmeans_pp": (u64, [_f32p, u64, u64, u64, u32, _u32p]),
+        "orc_internal_scores": (i32, [_f32p, u64, u64, _u32p, u64, _f64p,
+                                      np.ctypeslib.ndpointer(np.uint64), C.POINTER(u64)]),
         "orc_dedup": (u64, [_f32p, u64, u64, _u32p, _f32p, u64, C.c_float, C.c_float, i32, f64,
                             vp, vp, vp, _u32p, _u32p, _u32p, _u32p, C.POINTER(u64),
                             C.POINTER(u64)]),
@@ -312,6 +315,31 @@ def dedup(x, d, nb_ids, nb_sims, kk, sim_threshold, rep_threshold=None, priority
                       C.byref(sc))
     return {"group_of": group_of, "representatives": reps[:g], "anchors": anchors[:g],
             "sizes": sizes[:g], "linked_pairs": lp.value, "split_components": sc.value}
+
+
+# ----------------------------------------------------------------- auto-k
+def kmeans_pp(x, d, kmax, seed):
+    """kmeans_pp (emeans-cluster/src/auto.rs:401-455): kmax row ids in pick order."""
+    x = np.ascontiguousarray(x, np.float32)
+    n = x.size // d
+    picks = np.zeros(max(min(kmax, n), 1), np.uint32)
+    m = lib.orc_kmeans_pp(x, n, d, kmax, seed & 0xFFFFFFFF, picks)
+    return picks[:m]
+
+
+def internal_scores(x, d, labels, k):
+    """internal_scores (emeans-cluster/src/metrics.rs:113-268), fma-chain dots."""
+    x = np.ascontiguousarray(x, np.float32)
+    n = x.size // d
+    out = np.zeros(4, np.float64)
+    sizes = np.zeros(k, np.uint64)
+    ke = C.c_uint64()
+    rc = lib.orc_internal_scores(x, n, d, np.ascontiguousarray(labels, np.uint32), k, out, sizes,
+                                 C.byref(ke))
+    if rc != 0:
+        raise ValueError("label out of range")
+    return {"k_eff": ke.value, "silhouette": out[0], "calinski_harabasz": out[1],
+            "davies_bouldin": out[2], "objective": out[3], "sizes": sizes.astype(np.int64)}
 
 
 # --------------------------------------------------------------- generators
