@@ -70,10 +70,15 @@ struct Top1Geom {
 };
 Top1Geom top1_geom(emh_ctx* c, size_t n, size_t d, size_t k) {
   Top1Geom g{};
-  g.screen = c->screen && k >= 64 && d >= 32;
+  // The screen for any k >= 2 with d >= 32: below that, and for k = 1, the
+  // exact scan is as fast. (At small k the exact scan's items leave most
+  // lanes idle: 900,000 rows against 40 centroids took 10x the screen's time.)
+  g.screen = c->screen && k >= 2 && d >= 32;
   if (!g.screen) return g;
-  // The large-tile bf16 screen (one 512-thread block per CU) when d % 4 == 0.
-  g.big = c->screen != SCREEN_F32 && d % 4 == 0;
+  // The large-tile bf16 screen (one 512-thread block per CU, 256-centroid
+  // tiles) when d % 4 == 0 and k >= 64; smaller k fill a 128-centroid tile
+  // better.
+  g.big = c->screen != SCREEN_F32 && d % 4 == 0 && k >= 64;
   const int TR = g.big ? TR3 : 128;
   g.row_tiles = (int)((n + TR - 1) / TR);
   g.ntiles = (int)((k + (g.big ? TC3 : TC) - 1) / (g.big ? TC3 : TC));

@@ -100,7 +100,7 @@ int emh_top1(emh_ctx* ctx, const emh_buf* x, size_t d, const emh_buf* ids, size_
  * arguments, checks and results (the same bits) as emh_top1; the per-call
  * scratch (screen candidate lists, the queue of rows for the exact scan, row
  * norms, queue words) comes from one fixed 32 MiB block of device memory per
- * GPU, held until the process ends. The screened path (k >= 64, d >= 32)
+ * GPU, held until the process ends. The screened path (k >= 2, d >= 32)
  * takes 40 bytes per row per centroid part (1 to 8 parts, fewer as the call
  * has more rows) plus about 21 bytes per row: some 500,000 rows per call at
  * d % 4 == 0; with d % 4 != 0, or without the screen, 8 ceil(k / 64) bytes
@@ -331,7 +331,7 @@ float emh_host_numpy_sum_f32(const float* a, uint64_t n);
 
 /* ------------------------------------------------------------ diagnostics */
 /* Which screen a top-1 or top-k call ran (emh_screen_report.variant). */
-#define EMH_SCREEN_NONE 0        /* no screen: k < 64, d < 32 or emh_set_screen(ctx, 0) */
+#define EMH_SCREEN_NONE 0        /* no screen: k < 2, d < 32 or emh_set_screen(ctx, 0) */
 #define EMH_SCREEN_BIG_TAGGED 1  /* large-tile bf16 screen, one tile per part, tagged keys */
 #define EMH_SCREEN_BIG_SORTED 2  /* large-tile bf16 screen, several tiles per part */
 #define EMH_SCREEN_SMALL_BF16 3  /* 128 x 128 bf16 screen (d % 4 != 0, and kNN) */

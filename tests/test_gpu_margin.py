@@ -171,6 +171,25 @@ def test_margin_tagged_and_sorted_lists(dev, metric):
         assert (r["tiles_per_part"] == 1) == (want == "big_tagged")
 
 
+@pytest.mark.parametrize("mode", [1, 2], ids=["bf16x3", "f32"])
+@pytest.mark.parametrize("k", [2, 21, 63])
+def test_margin_small_k(dev, mode, k):
+    """Small k on the 128 x 128 screen (one partly filled tile) at d = 768,
+    crowded near ties included."""
+    n, d = 4096, 768
+    c = _mix(k, d, k, 0.0, True, 40 + k)
+    if k > 2:
+        c[1] = (c[0].astype(np.float64) * (1.0 + 1e-6 * _noise(np.arange(d)))).astype(np.float32)
+    x = _mix(n, d, k, 0.3, True, 50 + k)
+    dev.set_screen(mode)
+    try:
+        for metric in ("ip", "l2"):
+            want = "small_f32" if mode == 2 else "small_bf16"
+            _margin(dev, x, c, metric, f"small k={k} {metric} screen={mode}", want)
+    finally:
+        dev.set_screen(1)
+
+
 def test_margin_no_screen_below_32_dims(dev):
     x = _mix(1000, 13, 8, 0.5, False, 3)
     r = _margin(dev, x, x[:100].copy(), "l2", "d=13", "none")

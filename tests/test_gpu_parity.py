@@ -116,6 +116,24 @@ def test_top1_parts_of_several_tiles(dev, screen, metric):
     assert gs.tobytes() == osc.tobytes()
 
 
+@pytest.mark.parametrize("k", [2, 3, 21, 40, 63])
+@pytest.mark.parametrize("d", [768, 99, 32])
+@pytest.mark.parametrize("metric", ["ip", "l2"])
+def test_top1_small_k(dev, screen, k, d, metric):
+    """Small k (the automatic-k sweeps' k = 2 .. 40) on the 128 x 128 screen
+    with one partly filled centroid tile: an exact duplicate pair, a near pair
+    within 1e-6 and rows on the bisector of two centroids."""
+    n = 6000
+    x = _mix(n, d, 9, 0.4, metric == "ip", 11 * k + d)
+    c = (x[(np.arange(k) * 101) % n] * np.float32(0.97)).astype(np.float32)
+    if k >= 3:
+        c[k - 1] = c[0]  # the lower id wins
+        c[1] = (c[0].astype(np.float64) * (1.0 + 1e-6 * _noise(np.arange(d)))).astype(np.float32)
+    mid = (0.5 * (c[0].astype(np.float64) + c[k // 2])).astype(np.float32)
+    x[::7] = mid
+    _check_top1(dev, x, c, metric, f"small k={k} d={d} {metric}")
+
+
 def _noise(i):
     i = np.asarray(i, np.uint64)
     with np.errstate(over="ignore"):

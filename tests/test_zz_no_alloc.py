@@ -39,10 +39,11 @@ def _call(dev, fn, x, d, ids, lo, hi, cb, cn, k, metric):
 
 CASES = [
     # (n first call, n second call, d, k, metric): large-tile screen, 128 x 128
-    # screen (d % 4 != 0), exact scan alone (k < 64)
+    # screen (d % 4 != 0), 128 x 128 screen at small k, exact scan alone (d < 32)
     (20_000, 3_000, 768, 1024, "l2"),
     (5_000, 1_000, 99, 300, "ip"),
     (4_000, 500, 64, 32, "l2"),
+    (4_000, 500, 24, 40, "ip"),
 ]
 
 
