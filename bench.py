@@ -50,11 +50,12 @@ FP32_MFMA_PEAK = 157.3  # TFLOP/s, MI355X dense
 BF16_MFMA_PEAK = 2500.0  # TFLOP/s, MI355X dense
 HBM_PEAK = 8000.0       # GB/s
 METRIC = "train s & assign Mrows/s at 200k×768 k=1024 FP32; % of FP32 MFMA peak"
-# HBM bytes per k_screen launch over this workload's launch mix (calibrated
+# HBM bytes per screen launch over this workload's launch mix (calibrated
 # FETCH_SIZE + WRITE_SIZE from two rocprofv3 --pmc passes of this script, with
 # a plain copy kernel of known size as the scale;
-# profiles/k_screen_train_assign_200kx768_k1024_hbm_traffic.md).
-SCREEN_TRAFFIC_BYTES = 108.4e6
+# profiles/k_screen_train_assign_200kx768_k1024_hbm_traffic.md). None until
+# measured for the current screen.
+SCREEN_TRAFFIC_BYTES = None
 # The screen's roofline times every PROFILE_EVERY-th launch of the timed steps
 # with HIP events (an event pair between two kernels costs the stream a few
 # microseconds; on every launch that was ~5 % of the headline step).
@@ -203,8 +204,9 @@ def headline(args):
         "fallback_rows_per_run": info["fallback_rows"],
         "roofline": screen_roofline(
             ms, launches, flop,
-            "k_screen3 (bf16 MFMA, three passes xh.ch + xh.cl + xl.ch, f32 accumulation, "
-            "+ per-row 5-entry candidate lists per centroid part)", SCREEN_TRAFFIC_BYTES),
+            "k_screen4 (bf16 MFMA, three passes xh.ch + xh.cl + xl.ch on operands split "
+            "ahead of time, f32 accumulation, LDS-DMA ring; per-row candidate lists within "
+            "the bound of each lane's best)", SCREEN_TRAFFIC_BYTES),
         "update_rooflines": {
             "scatter_add": hbm_roofline(*main["update"]["scatter_add"],
                                         "k_hist_chunks + k_prefix_chunks + k_place_chunks + "

@@ -18,7 +18,7 @@ CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libemeans_hip.so")
 OBJ = os.path.join(HERE, "_obj")
 SOURCES = ["emh_api.cpp", "emh_host.cpp", "emh_ops.hip", "emh_scatter.hip", "emh_screen.hip",
-           "emh_screen3.hip", "emh_screen_t1_bf3.hip", "emh_screen_t1_f32.hip",
+           "emh_screen3.hip", "emh_screen4.hip", "emh_screen_t1_bf3.hip", "emh_screen_t1_f32.hip",
            "emh_screen_kn_bf3_self.hip", "emh_screen_kn_bf3_any.hip",
            "emh_screen_kn_f32_self.hip", "emh_screen_kn_f32_any.hip", "emh_rescore.hip",
            "emh_verify.hip", "emh_autok.hip",

@@ -546,6 +546,18 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
       sco1(c, n * 4), pos(c, k * d * 4), mass(c, k * 4),
       readout(c, (sph ? k * d : k) * 4), sums(c, k * d * 4), counts(c, k * 4),
       pass(c, k * d * 4), tally0(c, k * 4), tally1(c, k * 4), init_ids(c, k * 4);
+  // When the batches take the split-operand screen, every row's bf16 halves
+  // once (slab-major, with |x|^2): each batch then gathers its rows' halves
+  // by id instead of splitting them again.
+  SplitRows pre_rows{};
+  const SplitRows* pre = nullptr;
+  if (split_screen(c, d, k) && n < (1u << 25)) {
+    pre_rows = SplitRows{c->xpre.get(halves_bytes(n, d)), (float*)c->xpre_norm.get(n * 4), n,
+                         n * 128};
+    launch_halves(c, x, n, d, nullptr, 0, n, (void*)pre_rows.xs, (float*)pre_rows.xn, nullptr,
+                  nullptr);
+    pre = &pre_rows;
+  }
   uint32_t* d_order[2] = {order0.u(), order1.u()};
   uint32_t* d_lab[2] = {lab0.u(), lab1.u()};
   // The epoch's label counts, tallied batch by batch by the EMA launches: the
@@ -656,7 +668,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
         const size_t c1 = std::min(c0 + chunk, e);
         // After the first step the previous EMA cleared the screen's words.
         launch_top1(c, x, n, d, order, c0, c1, cents, cn, k, sph, lab, sco,
-                    step > 0 && c0 == b);
+                    step > 0 && c0 == b, nullptr, pre);
       }
       if (refill) {  // the next check's Gumbel terms, drawn while the GPU works
         gnext = beside([&] { return gumbel_terms(split_rng, k); });

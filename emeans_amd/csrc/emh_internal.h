@@ -154,6 +154,8 @@ struct emh_ctx {
   char* scratch = nullptr;    // the device's fixed scratch block (emh_top1_noalloc)
   uint64_t fallback_total = 0;
   emh::Scratch cand, fblist, order, start, misc, knn_tmp, xnorm, bigj, chunkcnt, tickets;
+  emh::Scratch xsplit, csplit, csplit_norm, csplit_part;  // split-operand screen: a call's rows, centroids
+  emh::Scratch xpre, xpre_norm;              // a training run's rows, split once
   emh::Scratch preview_ticket;  // k_mass_preview's last-block ticket (left at zero)
   // Host staging of the device loop: masses, plan, flags, epoch orders and
   // epoch labels/scores (double-buffered), results.
@@ -300,9 +302,32 @@ void launch_iscore_terms(emh_ctx* c, size_t n, size_t ke, const float* g, const 
 // last top-1 (launch_ema with clear_screen_words), so the fill is skipped.
 // ar: take the per-call scratch from this fixed block instead of the
 // context's buffers (no allocation; the call is not profiled).
+// Rows split into bf16 halves ahead of the calls (launch_halves over all nx
+// rows of x, slab-major with slab stride `slab` bytes), with their |x|^2:
+// the screen gathers them by id instead of splitting each call's selection.
+struct SplitRows {
+  const void* xs;
+  const float* xn;
+  size_t nx, slab;
+};
+// pre: x's rows already split (used when the call takes the split-operand
+// screen; see split_screen).
 void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids, size_t lo, size_t hi,
                  const float* cents, const float* cnorm, size_t k, bool ip, uint32_t* labels,
-                 float* scores, bool words_clear = false, Arena* ar = nullptr);
+                 float* scores, bool words_clear = false, Arena* ar = nullptr,
+                 const SplitRows* pre = nullptr);
+// Whether top-1 calls with d dimensions and k centroids take the
+// split-operand screen (k_screen4), whose rows a caller may split ahead.
+bool split_screen(emh_ctx* c, size_t d, size_t k);
+// Split rows of x (n rows, or ids[lo..lo+n)) into bf16 halves in out,
+// slab-major, with their |x|^2 in norm; with part, each of the
+// halves_blocks(n) blocks leaves the largest |x|^2 of its rows and the
+// largest cnorm in part[2 b], part[2 b + 1] (emh_screen4.hip). Bytes of out:
+// halves_bytes(n, d).
+void launch_halves(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids, size_t lo,
+                   size_t n, void* out, float* norm, const float* cnorm, uint32_t* part);
+inline size_t halves_bytes(size_t n, size_t d) { return n * ((d + 31) / 32) * 128; }
+inline size_t halves_blocks(size_t n) { return (n + 7) / 8; }
 // Bytes of fixed-block scratch launch_top1 takes for a call of n rows (an
 // upper bound: each region rounded up to 256 bytes).
 size_t top1_scratch_bytes(emh_ctx* c, size_t n, size_t d, size_t k);

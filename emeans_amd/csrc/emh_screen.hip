@@ -63,18 +63,32 @@ int choose_parts(int row_tiles, int ntiles, int cus, int per_cu = 2) {
 }  // namespace
 
 namespace {
-// The screen's launch geometry for n rows against k centroids.
+// The screen's launch geometry for n rows against k centroids. split: the
+// call may take the split-operand screen (k_screen4: bf16 arithmetic, k >= 64
+// and at most MAX_PARTS tiles of 256 centroids, one tile per part with
+// tagged keys; any d >= 32). Otherwise (and for the no-allocation entry, which
+// has no room to split a selection) the large-tile screen that splits its
+// slabs itself (k_screen3, d % 4 == 0, k >= 64) or the 128 x 128 screens.
 struct Top1Geom {
-  bool screen, big;
+  bool screen, big, split;
   int row_tiles, ntiles, parts, tpp;
 };
-Top1Geom top1_geom(emh_ctx* c, size_t n, size_t d, size_t k) {
+Top1Geom top1_geom(emh_ctx* c, size_t n, size_t d, size_t k, bool split) {
   Top1Geom g{};
   // The screen for any k >= 2 with d >= 32: below that, and for k = 1, the
   // exact scan is as fast. (At small k the exact scan's items leave most
   // lanes idle: 900,000 rows against 40 centroids took 10x the screen's time.)
   g.screen = c->screen && k >= 2 && d >= 32;
   if (!g.screen) return g;
+  const int nt3 = (int)((k + TC3 - 1) / TC3);
+  // (k_screen4 addresses a slab's rows with 32-bit offsets: fewer than 2^25 rows.)
+  if (split && c->screen != SCREEN_F32 && k >= 64 && nt3 <= MAX_PARTS && n < (1u << 25)) {
+    g.big = g.split = true;
+    g.row_tiles = (int)((n + TR3 - 1) / TR3);
+    g.ntiles = g.parts = nt3;
+    g.tpp = 1;
+    return g;
+  }
   // The large-tile bf16 screen (one 512-thread block per CU, 256-centroid
   // tiles) when d % 4 == 0 and k >= 64; smaller k fill a 128-centroid tile
   // better.
@@ -89,8 +103,10 @@ Top1Geom top1_geom(emh_ctx* c, size_t n, size_t d, size_t k) {
 }
 }  // namespace
 
+bool split_screen(emh_ctx* c, size_t d, size_t k) { return top1_geom(c, 1, d, k, true).split; }
+
 size_t top1_scratch_bytes(emh_ctx* c, size_t n, size_t d, size_t k) {
-  const Top1Geom g = top1_geom(c, n, d, k);
+  const Top1Geom g = top1_geom(c, n, d, k, false);
   if (!g.screen) return exact1_scratch_bytes(n, d, k, false);
   auto r = [](size_t b) { return (b + 255) & ~size_t(255); };
   return r((size_t)g.parts * n * L1 * sizeof(Cand)) + 2 * r(n * 4) +
@@ -110,19 +126,49 @@ struct Top1Screen {
 
 Top1Screen screen_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
                        size_t lo, size_t n, const float* cents, const float* cnorm, size_t k,
-                       bool ip, bool words_clear, Arena* ar) {
+                       bool ip, bool words_clear, Arena* ar, const SplitRows* pre) {
   Top1Screen s;
-  s.g = top1_geom(c, n, d, k);
+  s.g = top1_geom(c, n, d, k, !ar);
   if (!s.g.screen) return s;
   const Top1Geom& g = s.g;
   const size_t cbytes = (size_t)g.parts * n * L1 * sizeof(Cand);
   s.cand = (Cand*)(ar ? ar->take(cbytes) : c->cand.get(cbytes));
   s.fb = (uint32_t*)(ar ? ar->take(n * 4) : c->fblist.get(n * 4));
   s.xnorm = (float*)(ar ? ar->take(n * 4) : c->xnorm.get(n * 4));
-  if (!words_clear)  // fallback count, cmax2, cnmax (the screen fills the maxima)
+  if (!words_clear)  // fallback count, cmax2, cnmax (the screen or the split fills the maxima)
     launch_fill_u32(c, c->small, 3, 0);
   const unsigned blocks = (unsigned)(g.row_tiles * g.parts);
   s.tagged = g.big && g.tpp == 1;
+  if (g.split) {
+    // The centroids' halves and the bound's centroid maxima, then the rows'
+    // halves (the caller's, split ahead, or this selection's).
+    void* cs = c->csplit.get(halves_bytes(k, d));
+    uint32_t* part = (uint32_t*)c->csplit_part.get(halves_blocks(k) * 8);
+    launch_halves(c, cents, k, d, nullptr, 0, k, cs, (float*)c->csplit_norm.get(k * 4),
+                  ip ? nullptr : cnorm, part);
+    Screen4Args a{blocks,   nullptr,  0,      nullptr, 0,       d,       nullptr,
+                  0,        n,        cs,     k * 128, cnorm,   k,       1,
+                  g.parts,  g.ntiles, s.cand, s.xnorm, part,    (int)halves_blocks(k)};
+    if (pre) {
+      a.xs = pre->xs;
+      a.xslab = pre->slab;
+      a.xn = pre->xn;
+      a.nx = pre->nx;
+      a.ids = ids;
+      a.lo = lo;
+    } else {
+      void* xs = c->xsplit.get(halves_bytes(n, d));
+      launch_halves(c, x, nx, d, ids, lo, n, xs, s.xnorm, nullptr, nullptr);
+      a.xs = xs;
+      a.xslab = n * 128;
+      a.xn = s.xnorm;
+      a.nx = n;
+    }
+    ProfScope prof(c, EMH_PROF_SCREEN, 2.0 * (double)n * (double)k * (double)d,
+                   prof_take(c, EMH_PROF_SCREEN));
+    launch_screen4(c, a, ip, true);
+    return s;
+  }
   ProfScope prof(c, EMH_PROF_SCREEN, 2.0 * (double)n * (double)k * (double)d,
                  !ar && prof_take(c, EMH_PROF_SCREEN));
   const ScreenArgs a{blocks, x, nx, d, ids, lo, n, cents, cnorm, k, g.tpp, g.parts, g.ntiles,
@@ -142,12 +188,14 @@ int bound_kind(emh_ctx* c, bool tagged) { return c->screen == SCREEN_F32 ? 0 : t
 
 void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids, size_t lo,
                  size_t hi, const float* cents, const float* cnorm, size_t k, bool ip,
-                 uint32_t* labels, float* scores, bool words_clear, Arena* ar) {
+                 uint32_t* labels, float* scores, bool words_clear, Arena* ar,
+                 const SplitRows* pre) {
   if (hi <= lo) return;
   const size_t n = hi - lo;
   EMH_ENSURE(d <= 16384, "top1: d = %zu above the supported 16384", d);
   EMH_ENSURE(n < (1u << 31) && k < (1u << 31), "top1: shape too large");
-  const Top1Screen s = screen_top1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, words_clear, ar);
+  const Top1Screen s =
+      screen_top1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, words_clear, ar, pre);
   if (!s.g.screen) {
     launch_exact1(c, x, nx, d, ids, lo, n, nullptr, cents, cnorm, k, ip, labels, scores, ar);
     return;
@@ -164,7 +212,8 @@ void screen_margin_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const u
   if (hi <= lo) return;
   const size_t n = hi - lo;
   EMH_ENSURE(d <= 16384 && n < (1u << 31) && k < (1u << 31), "top1: shape too large");
-  const Top1Screen s = screen_top1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, false, nullptr);
+  const Top1Screen s =
+      screen_top1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, false, nullptr, nullptr);
   if (!s.g.screen) return;  // variant 0: no screen, nothing to measure
   out->variant = s.g.big ? (s.tagged ? EMH_SCREEN_BIG_TAGGED : EMH_SCREEN_BIG_SORTED)
                          : (c->screen == SCREEN_F32 ? EMH_SCREEN_SMALL_F32 : EMH_SCREEN_SMALL_BF16);

@@ -828,6 +828,29 @@ struct ScreenArgs {
 // The large-tile bf16 top-1 screen (emh_screen3.hip): d % 4 == 0; tagged keys
 // when every part is one tile.
 void launch_screen3(emh_ctx* c, const ScreenArgs& a, bool ip, bool tagged);
+
+// Operands of the large-tile screen over split rows and centroids (emh_screen4.hip):
+// xs, cs hold d32 = ceil(d / 32) slabs of 128 bytes per row, slab-major (slab
+// j of row r at j * slab stride + 128 r); xn the rows' |x|^2.
+struct Screen4Args {
+  unsigned blocks;
+  const void* xs;
+  size_t xslab;
+  const float* xn;
+  size_t nx, d;
+  const uint32_t* ids;
+  size_t lo, n;
+  const void* cs;
+  size_t cslab;
+  const float* cnorm;
+  size_t k;
+  int tpp, parts, ntiles;
+  Cand* cand;
+  float* xnorm;
+  const uint32_t* part;  // the centroid split's per-block maxima (launch_halves' part)
+  int nparts;
+};
+void launch_screen4(emh_ctx* c, const Screen4Args& a, bool ip, bool tagged);
 // The 128 x 128 top-1 screen (emh_screen_t1_{bf3,f32}.hip) and the kNN screen
 // (emh_screen_kn_{bf3,f32}_{self,any}.hip), in bf16 three-pass or f32 MFMA arithmetic.
 void launch_screen_t1_bf3(emh_ctx* c, const ScreenArgs& a, bool ip);

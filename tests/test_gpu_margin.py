@@ -13,9 +13,10 @@ can reach 1/1.125 on rows where that allowance dominates E.) Inputs are
 adversarial: crowds of centroids within 1e-6,
 exact duplicates, rows at scales 1e3 .. 1e-15, rows in the bf16 subnormal
 range, centroids up to 5e17 (1e34 overflows the bound's |c|^2 and sends every
-row to the exact scan), d from 36 to 2500 (d % 4 != 0 takes the 128 x 128
-screen; d < 32 runs no screen), both screen arithmetics, tagged single-tile
-lists and sorted many-tile lists, and the kNN screen's 24-entry lists. They
+row to the exact scan), d from 36 to 2500 (d < 32 runs no screen), both
+screen arithmetics, the split-operand screen's filtered single-tile lists
+(k <= 2048), the sorted many-tile lists of larger k, the 128 x 128 screen of
+small k, and the kNN screen's 24-entry lists. They
 also pin which screen variant ran, whatever the CU count. With
 EMEANS_MARGIN_OUT set, each case's report is appended to that file (JSON lines).
 """
@@ -115,7 +116,7 @@ def test_margin_near_tie_crowds(dev, mode, metric, d):
     x = (rows * scale[:, None]).astype(np.float32)
     dev.set_screen(mode)
     try:
-        want = "small_f32" if mode == 2 else ("big_tagged" if d % 4 == 0 else "small_bf16")
+        want = "small_f32" if mode == 2 else "big_tagged"
         _margin(dev, x, c, metric, f"crowds d={d} {metric} screen={mode}", want)
     finally:
         dev.set_screen(1)
@@ -159,8 +160,9 @@ def _args(dev, x, c):
 
 @pytest.mark.parametrize("metric", ["ip", "l2"])
 def test_margin_tagged_and_sorted_lists(dev, metric):
-    """16,384 rows: k = 1024 gives parts of one 256-centroid tile (tagged keys),
-    k = 4096 parts of several tiles (sorted insert): both measured, and the
+    """16,384 rows: k = 1024 takes the split-operand screen (parts of one
+    256-centroid tile, tagged keys), k = 4096 the screen that splits its own
+    slabs with parts of several tiles (sorted insert): both measured, and the
     variant each ran is the one expected."""
     from emeans_amd import HipDevice
     n, d = 16384, 256

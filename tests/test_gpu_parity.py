@@ -101,13 +101,15 @@ def test_top1_production_shape_with_duplicates(dev, screen, k, metric):
     assert np.all(gl < base)
 
 
+@pytest.mark.parametrize("n,k", [(16384, 2048), (8192, 4096)])
 @pytest.mark.parametrize("metric", ["ip", "l2"])
-def test_top1_parts_of_several_tiles(dev, screen, metric):
-    """16,384 rows against 2,048 centroids: on 256 CUs the large-tile screen's
-    four parts span two 256-centroid tiles each, so its lists take the sorted
-    insert across tiles (single-tile parts tag their keys instead). Bit-equal
-    to the oracle."""
-    n, d, k = 16384, 256, 2048
+def test_top1_parts_of_several_tiles(dev, screen, n, k, metric):
+    """2,048 centroids: the split-operand screen's eight single-tile parts
+    (tagged keys); 4,096 centroids (16 tiles, more than eight parts): the
+    large-tile screen that splits its own slabs, on 256 CUs eight parts of two
+    tiles each, so its lists take the sorted insert across tiles. Bit-equal to
+    the oracle."""
+    d = 256
     x = _mix(n, d, 64, 0.6, metric == "ip", 7 * n + k)
     c = (x[(np.arange(k) * 37) % n] * np.float32(0.95)).astype(np.float32)
     gl, gs = _gpu_top1(dev, x, c, metric)
