@@ -619,6 +619,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   }
   launch_check_finite(c, pos.f(), k * d, c->small + SW_BAD_INIT);
   launch_fill_u32(c, pass.u(), k * d, 0);
+  launch_fill_u32(c, counts.u(), k, 0);  // each EMA leaves them at zero for the next batch
   copy_async(c, h_small0, c->small, SW_WORDS * 4, hipMemcpyDeviceToHost);
   ev_order[1].record(c->stream);  // the initial ids are out of h_order[1]
   ev_init.record(c->stream);
@@ -683,7 +684,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
       const bool tsc = prof_take(c, EMH_PROF_SCATTER);
       {
         ProfScope p(c, EMH_PROF_SCATTER, 0.0, tsc, false);
-        launch_scatter_count(c, b, e, lab, k, counts.u());
+        launch_scatter_count(c, b, e, lab, k, counts.u(), true);
       }
       if (check)
         launch_mass_preview(c, mass.f(), counts.u(), k, af, df, replace, d_usage_h, d_small_h,
@@ -695,7 +696,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
       {
         ProfScope p(c, EMH_PROF_EMA, ema_bytes(k, d), prof_take(c, EMH_PROF_EMA));
         launch_ema(c, pos.f(), mass.f(), sums.f(), counts.u(), k, d, af, df, replace,
-                   sph ? nullptr : readout.f(), true, d_tally[buf]);
+                   sph ? nullptr : readout.f(), true, d_tally[buf], true);
       }
       if (check) {
         wait_posted(c, h_seq, seq_no);

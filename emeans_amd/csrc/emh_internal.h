@@ -244,10 +244,13 @@ void launch_row_norms(emh_ctx* c, const float* m, size_t rows, size_t d, float* 
 void launch_normalize_rows(emh_ctx* c, const float* src, size_t rows, size_t d, float* dst);
 // With clear_screen_words, also zeroes the small-block words launch_top1
 // clears before its screen (the fallback count and the bound maxima), so the
-// next top-1 may skip that fill. With tally, also adds counts into it.
+// next top-1 may skip that fill. With tally, also adds counts into it. With
+// zero_counts, leaves counts at zero once read (the next batch's
+// launch_scatter_count adds into them).
 void launch_ema(emh_ctx* c, float* pos, float* usage, const float* sums, const uint32_t* counts,
                 size_t k, size_t d, float alpha, float decay, int replace, float* norms = nullptr,
-                bool clear_screen_words = false, uint32_t* tally = nullptr);
+                bool clear_screen_words = false, uint32_t* tally = nullptr,
+                bool zero_counts = false);
 // The masses launch_ema will leave, into out (usage untouched); with
 // small_out, also a copy of the small block's words; with seq_out, then seq
 // into *seq_out once all of that is written. out, small_out and seq_out may be
@@ -277,8 +280,10 @@ void launch_scatter(emh_ctx* c, const float* x, size_t nx, size_t d, const uint3
                     float* acc);
 // The same in two halves: counts (and the cluster offsets), then the ordered
 // sums; the caller may queue work that needs only the counts in between.
+// counts_zero: counts holds zeros on entry (launch_ema with zero_counts left
+// them so), which saves a fill.
 void launch_scatter_count(emh_ctx* c, size_t lo, size_t hi, const uint32_t* labels, size_t k,
-                          uint32_t* counts);
+                          uint32_t* counts, bool counts_zero = false);
 void launch_scatter_sums(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
                          size_t lo, size_t hi, const uint32_t* labels, size_t k, float* sums,
                          float* acc);

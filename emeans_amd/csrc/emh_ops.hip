@@ -152,11 +152,12 @@ constexpr int ECH = 1024;  // dimensions per LDS pass
 constexpr int EU = 16;    // elements per thread whose loads are in flight together
 __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __restrict__ usage,
                                              const float* __restrict__ sums,
-                                             const uint32_t* __restrict__ counts, size_t k,
+                                             const uint32_t* counts, size_t k,
                                              size_t d, float alpha, float decay, int replace,
                                              float* __restrict__ norms,
                                              uint32_t* __restrict__ clear3,
-                                             uint32_t* __restrict__ tally) {
+                                             uint32_t* __restrict__ tally,
+                                             uint32_t* zero_counts) {  // counts itself, or null
   // EC rows of min(d, ECH) + 4 floats (norms only)
   extern __shared__ __attribute__((aligned(16))) float sq[];
   __shared__ float wgt[EC], cntf[EC];
@@ -166,6 +167,7 @@ __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __r
   if (clear3 && blockIdx.x == 0 && tid < 3) clear3[tid] = 0;
   if (tid < nc) {
     const uint32_t cnt = counts[j0 + tid];
+    if (zero_counts) zero_counts[j0 + tid] = 0;  // the same array: read above, this thread only
     if (tally) tally[j0 + tid] += cnt;
     float weight;
     usage[j0 + tid] = ema_mass(usage[j0 + tid], cnt, alpha, decay, replace, &weight);
@@ -420,12 +422,12 @@ void launch_normalize_rows(emh_ctx* c, const float* src, size_t rows, size_t d, 
 
 void launch_ema(emh_ctx* c, float* pos, float* usage, const float* sums, const uint32_t* counts,
                 size_t k, size_t d, float alpha, float decay, int replace, float* norms,
-                bool clear_screen_words, uint32_t* tally) {
+                bool clear_screen_words, uint32_t* tally, bool zero_counts) {
   if (k == 0) return;
   const size_t lds = norms ? (size_t)EC * (std::min(d, (size_t)ECH) + 4) * sizeof(float) : 0;
   hipLaunchKernelGGL(k_ema, grid1(k, EC), dim3(256), lds, c->stream, pos, usage, sums, counts, k,
                      d, alpha, decay, replace, norms, clear_screen_words ? c->small : nullptr,
-                     tally);
+                     tally, zero_counts ? const_cast<uint32_t*>(counts) : nullptr);
   EMH_HIP(hipGetLastError());
 }
 

@@ -5,21 +5,21 @@
 //   1. count:  labels -> counts (integer atomics; exact in any order); the
 //              last workgroup to finish scans the counts into start offsets
 //              and lists the clusters too large for the per-column path. For
-//              k up to KCH the counts are per-chunk LDS histograms of CP
-//              positions, prefixed per label over the chunks by one workgroup
-//              (a thread per label);
+//              k up to KCH the counts come from per-chunk LDS histograms of
+//              CP positions, kept per chunk and added to the totals;
 //   2. place:  each position's rank among the earlier positions of its label
-//              (chunked: the earlier chunks' prefix plus a scan of its own
-//              chunk in LDS; else one wave per cluster walking the labels with
-//              ballots), so each cluster's positions land in order at its
-//              start offset;
-//   3. sum:    clusters of up to SMALL rows: a workgroup per cluster, a
-//              thread per four columns (d % 4 == 0; else per column) adds the
-//              rows in order with SU4 (SU) row loads in flight;
-//   4. sum_big larger clusters: a workgroup per (cluster, 32-column strip);
-//              eight threads per column load the next 256 rows into LDS while
-//              one lane per column adds the current 256 in order, so a long
-//              chain waits on adds, not on memory.
+//              (chunked: the sum of its label's earlier chunk histograms plus
+//              a scan of its own chunk in LDS; else one wave per cluster
+//              walking the labels with ballots), so each cluster's positions
+//              land in order at its start offset;
+//   3. sums (one launch, k_sums): clusters of up to SMALL rows: a
+//              workgroup per cluster, a thread per four columns (d % 4 == 0;
+//              else per column) adds the rows in order with SU4 (SU) row loads
+//              in flight; larger clusters, beside them: a workgroup per
+//              (cluster, 32-column strip); eight threads per column load the
+//              next 128 rows into LDS while one lane per column adds the
+//              current 128 in order, so a long chain waits on adds, not on
+//              memory.
 // HBM-bound: reads rows*d*4 bytes of rows (gathered by id) plus labels/ids,
 // writes k*d*4 of sums (+ k*d*4 read/write of acc).
 
@@ -32,7 +32,7 @@ constexpr int WAVE = 64;
 constexpr uint32_t NOROW = 0xffffffffu;
 constexpr int SMALL = 128;  // largest cluster the per-column path takes
 constexpr int SU = 32;      // row loads in flight per thread on that path
-constexpr int BR = 256;     // rows per chunk on the large-cluster path
+constexpr int BR = 128;     // rows per chunk on the large-cluster path
 constexpr int BC = 32;      // columns per large-cluster workgroup
 constexpr int BT = 256;     // threads per large-cluster workgroup (BT / BC per column)
 
@@ -84,7 +84,12 @@ __global__ __launch_bounds__(256) void k_count(const uint32_t* __restrict__ labe
     const uint32_t cj = __hip_atomic_load(&counts[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     start[j] = run;
     run += cj;
-    if (cj > (uint32_t)SMALL) bigj[atomicAdd(&nbig, 1u)] = (uint32_t)j;
+    if (cj > (uint32_t)SMALL) {
+      const uint32_t i = atomicAdd(&nbig, 1u);
+      bigj[3 * i] = (uint32_t)j;
+      bigj[3 * i + 1] = run - cj;
+      bigj[3 * i + 2] = cj;
+    }
   }
   if (tid == 255) start[k] = part[255];
   __syncthreads();
@@ -98,12 +103,21 @@ __global__ __launch_bounds__(256) void k_count(const uint32_t* __restrict__ labe
 constexpr int CP = 256;
 constexpr int KCH = 8192;  // LDS histogram of one chunk
 
-// Chunk c's label histogram (LDS atomics) goes to cnt[c][0..k).
-__global__ __launch_bounds__(256) void k_hist_chunks(const uint32_t* __restrict__ labels,
-                                                      size_t lo, size_t hi, size_t k,
-                                                      uint32_t* __restrict__ cnt,
-                                                      uint32_t* __restrict__ small) {
+// Chunk c's label histogram (LDS atomics) goes to cnt[c][0..k) and is added
+// to the totals counts[0..k) (zero on entry);
+// the last workgroup to finish scans the totals into start[0..k] and lists
+// the clusters above SMALL rows.
+__global__ __launch_bounds__(256) void k_hist_total(const uint32_t* __restrict__ labels, size_t lo,
+                                                    size_t hi, size_t k,
+                                                    uint32_t* __restrict__ cnt,
+                                                    uint32_t* __restrict__ counts,
+                                                    uint32_t* __restrict__ start,
+                                                    uint32_t* __restrict__ bigj,
+                                                    uint32_t* __restrict__ small) {
   __shared__ uint32_t h[KCH];
+  __shared__ uint32_t part[256];
+  __shared__ uint32_t nbig;
+  __shared__ int last;
   const int tid = threadIdx.x;
   const size_t c = blockIdx.x;
   for (size_t j = tid; j < k; j += 256) h[j] = 0;
@@ -117,73 +131,60 @@ __global__ __launch_bounds__(256) void k_hist_chunks(const uint32_t* __restrict_
       small[SW_BAD_LABEL] = 1;
   }
   __syncthreads();
-  for (size_t j = tid; j < k; j += 256) cnt[c * k + j] = h[j];
-}
-
-// One workgroup of 1024 threads, 1024 labels at a time: thread j turns label
-// j's column of chunk counts into its exclusive prefix over the chunks (in
-// place; the column's loads all in flight at once) and its total; the totals
-// are scanned (shuffles within each wave, LDS across waves, a running carry
-// across label groups) into start offsets, and the clusters above SMALL rows
-// are listed.
-constexpr int PMC = 32;  // chunk counts per thread in flight
-constexpr int PT = 1024;
-__global__ __launch_bounds__(PT) void k_prefix_chunks(size_t k, size_t nch,
-                                                       uint32_t* __restrict__ cnt,
-                                                       uint32_t* __restrict__ counts,
-                                                       uint32_t* __restrict__ start,
-                                                       uint32_t* __restrict__ bigj,
-                                                       uint32_t* __restrict__ small) {
-  __shared__ uint32_t part[PT / 64];
-  __shared__ uint32_t nbig, carry_s;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  for (size_t j = tid; j < k; j += 256) {
+    const uint32_t v = h[j];
+    cnt[c * k + j] = v;
+    if (v) atomicAdd(&counts[j], v);
+  }
+  __threadfence();  // this workgroup's counts are visible before its ticket
+  __syncthreads();
   if (tid == 0) {
+    const uint32_t t = atomicAdd(&small[SW_TICKET], 1u);
+    last = t == gridDim.x - 1;
     nbig = 0;
-    carry_s = 0;
   }
   __syncthreads();
-  for (size_t j0 = 0; j0 < k; j0 += PT) {
-    const size_t j = j0 + tid;
-    uint32_t s = 0;
-    if (j < k) {
-      for (size_t cc0 = 0; cc0 < nch; cc0 += PMC) {
-        uint32_t v[PMC];
+  if (!last) return;
+  __threadfence();
+  // Thread t scans the run [t*per, (t+1)*per) of the totals (per <= KCH / 256),
+  // its loads all in flight at once and kept for the second pass.
+  constexpr int PERMAX = KCH / 256;
+  const size_t per = (k + 255) / 256;
+  const size_t a = min(k, (size_t)tid * per), b = min(k, a + per);
+  uint32_t tv[PERMAX];
 #pragma unroll
-        for (int u = 0; u < PMC; u++) v[u] = cc0 + u < nch ? cnt[(cc0 + u) * k + j] : 0u;
+  for (int u = 0; u < PERMAX; u++)
+    tv[u] = a + u < b ? __hip_atomic_load(&counts[a + u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                      : 0u;
+  uint32_t sacc = 0;
 #pragma unroll
-        for (int u = 0; u < PMC; u++)
-          if (cc0 + u < nch) {
-            cnt[(cc0 + u) * k + j] = s;
-            s += v[u];
-          }
-      }
-      counts[j] = s;
-    }
-    uint32_t x = s;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint32_t y = __shfl_up(x, o, 64);
-      if (lane >= o) x += y;
-    }
-    if (lane == 63) part[w] = x;
+  for (int u = 0; u < PERMAX; u++) sacc += tv[u];
+  part[tid] = sacc;
+  __syncthreads();
+  for (int o = 1; o < 256; o <<= 1) {  // Hillis-Steele inclusive scan of the run totals
+    const uint32_t add = tid >= o ? part[tid - o] : 0u;
     __syncthreads();
-    uint32_t run = carry_s + x - s;
-    for (int i = 0; i < w; i++) run += part[i];
-    if (j < k) {
-      start[j] = run;
-      if (s > (uint32_t)SMALL) bigj[atomicAdd(&nbig, 1u)] = (uint32_t)j;
-    }
-    __syncthreads();
-    if (tid == 0) {
-      uint32_t tot = 0;
-      for (int i = 0; i < PT / 64; i++) tot += part[i];
-      carry_s += tot;
-    }
+    part[tid] += add;
     __syncthreads();
   }
+  uint32_t run = part[tid] - sacc;
+#pragma unroll
+  for (int u = 0; u < PERMAX; u++) {
+    if (a + u >= b) break;
+    start[a + u] = run;
+    run += tv[u];
+    if (tv[u] > (uint32_t)SMALL) {
+      const uint32_t i = atomicAdd(&nbig, 1u);
+      bigj[3 * i] = (uint32_t)(a + u);
+      bigj[3 * i + 1] = run - tv[u];
+      bigj[3 * i + 2] = tv[u];
+    }
+  }
+  if (tid == 255) start[k] = part[255];
+  __syncthreads();
   if (tid == 0) {
-    start[k] = carry_s;
     small[SW_NBIG] = nbig;
+    small[SW_TICKET] = 0;  // ready for the next call
   }
 }
 
@@ -199,14 +200,15 @@ __device__ __forceinline__ uint32_t row_of(const uint32_t* __restrict__ ids, siz
 }
 
 // Position p of chunk c goes to rid[start[l] + (rows of label l in earlier
-// chunks) + (rows of label l earlier in this chunk)], l = labels[p].
-__global__ __launch_bounds__(256) void k_place_chunks(const uint32_t* __restrict__ labels,
-                                                       size_t lo, size_t hi, size_t k,
-                                                       const uint32_t* __restrict__ start,
-                                                       const uint32_t* __restrict__ cnt,
-                                                       const uint32_t* __restrict__ ids, size_t nx,
-                                                       uint32_t* __restrict__ small,
-                                                       uint32_t* __restrict__ rid) {
+// chunks: the sum of the chunk histograms cnt[c'][l], c' < c, loads in flight
+// together) + (rows of label l earlier in this chunk)], l = labels[p].
+__global__ __launch_bounds__(256) void k_place_sum(const uint32_t* __restrict__ labels,
+                                                    size_t lo, size_t hi, size_t k,
+                                                    const uint32_t* __restrict__ start,
+                                                    const uint32_t* __restrict__ cnt,
+                                                    const uint32_t* __restrict__ ids, size_t nx,
+                                                    uint32_t* __restrict__ small,
+                                                    uint32_t* __restrict__ rid) {
   __shared__ __attribute__((aligned(16))) uint32_t lab[CP];
   const int tid = threadIdx.x;
   const size_t c = blockIdx.x;
@@ -215,6 +217,14 @@ __global__ __launch_bounds__(256) void k_place_chunks(const uint32_t* __restrict
   lab[tid] = l;
   __syncthreads();
   if (l >= k) return;
+  uint32_t pre = 0;
+  for (size_t c0 = 0; c0 < c; c0 += 64) {
+    uint32_t v[64];
+#pragma unroll
+    for (int u = 0; u < 64; u++) v[u] = c0 + u < c ? cnt[(c0 + u) * k + l] : 0u;
+#pragma unroll
+    for (int u = 0; u < 64; u++) pre += v[u];
+  }
   uint32_t rank = 0;
   const uint4* l4 = reinterpret_cast<const uint4*>(lab);
 #pragma unroll 8
@@ -224,7 +234,7 @@ __global__ __launch_bounds__(256) void k_place_chunks(const uint32_t* __restrict
     rank += (uint32_t)(i < tid && q.x == l) + (uint32_t)(i + 1 < tid && q.y == l) +
             (uint32_t)(i + 2 < tid && q.z == l) + (uint32_t)(i + 3 < tid && q.w == l);
   }
-  rid[start[l] + cnt[c * k + l] + rank] = row_of(ids, nx, (uint32_t)p, small);
+  rid[start[l] + pre + rank] = row_of(ids, nx, (uint32_t)p, small);
 }
 
 // Stable placement: wave j walks positions lo..hi in order; positions with
@@ -285,22 +295,15 @@ __global__ __launch_bounds__(64 * PW) void k_place(const uint32_t* __restrict__ 
   }
 }
 
-// Clusters of up to SMALL rows: workgroup = cluster j; rows in order. With
-// VEC4 a thread adds four columns (16-byte loads, SU4 rows in flight), else
-// one column (SU rows in flight).
+// Cluster j's sum of the rows rows[0..cnt) (LDS, in order; NOROW adds
+// nothing) into sums[j] (and acc[j] += it), by the workgroup's 256 threads.
+// With VEC4 a thread adds four columns (16-byte loads, SU4 rows in flight),
+// else one column (SU rows in flight).
 constexpr int SU4 = 32;
 template <bool VEC4>
-__global__ __launch_bounds__(256) void k_sum(const float* __restrict__ x, size_t nx, size_t d,
-                                             const uint32_t* __restrict__ rid,
-                                             const uint32_t* __restrict__ start, size_t k,
-                                             float* __restrict__ sums, float* __restrict__ acc,
-                                             uint32_t* __restrict__ small) {
-  __shared__ uint32_t rows[SMALL];
-  const size_t j = blockIdx.x;
-  const uint32_t b = start[j], cnt = start[j + 1] - b;
-  if (cnt > (uint32_t)SMALL) return;  // k_sum_big
-  if (threadIdx.x < cnt) rows[threadIdx.x] = rid[b + threadIdx.x];
-  __syncthreads();
+__device__ __forceinline__ void sum_rows(const float* __restrict__ x, size_t d,
+                                         const uint32_t* rows, uint32_t cnt, size_t j,
+                                         float* __restrict__ sums, float* __restrict__ acc) {
   if (VEC4) {
     const size_t d4 = d / 4;
     for (size_t c4 = threadIdx.x; c4 < d4; c4 += blockDim.x) {
@@ -350,25 +353,20 @@ __global__ __launch_bounds__(256) void k_sum(const float* __restrict__ x, size_t
   }
 }
 
-// Clusters with more than SMALL rows (listed by k_count): workgroup =
-// (listed cluster, strip of BC columns). Chunks of BR rows are double-buffered
-// in LDS, column-major (stride BRP) so that a column's lane reads four rows per
+// Clusters with more than SMALL rows (listed as (cluster, offset of its
+// positions in rid, count) by the count kernels): workgroup = (listed
+// cluster bi, strip of BC columns). Chunks of BR rows are double-buffered in
+// LDS, column-major (stride BRP) so that a column's lane reads four rows per
 // LDS load; thread t loads column t % BC of rows t / BC + (BT / BC) u.
 constexpr int BRP = BR + 4;  // column stride in LDS: 4-row reads stay aligned, stores 2-way
-__global__ __launch_bounds__(BT) void k_sum_big(const float* __restrict__ x, size_t nx, size_t d,
-                                                const uint32_t* __restrict__ rid,
-                                                const uint32_t* __restrict__ start,
-                                                const uint32_t* __restrict__ bigj, int strips,
-                                                float* __restrict__ sums, float* __restrict__ acc,
-                                                uint32_t* __restrict__ small) {
+__device__ __forceinline__ void sum_big(int bi, int strip, const float* __restrict__ x, size_t d,
+                                        const uint32_t* __restrict__ rid,
+                                        const uint32_t* __restrict__ bigj,
+                                        float* __restrict__ sums, float* __restrict__ acc,
+                                        float (*vals)[BC * BRP], uint32_t (*rows)[BR]) {
   constexpr int RPT = BR * BC / BT;  // rows loaded per thread per chunk
   constexpr int RS = BT / BC;        // row stride between a thread's loads
-  __shared__ __attribute__((aligned(16))) float vals[2][BC * BRP];
-  __shared__ uint32_t rows[2][BR];
-  const int bi = blockIdx.x / strips, strip = blockIdx.x % strips;
-  if (bi >= (int)small[SW_NBIG]) return;
-  const uint32_t j = bigj[bi];
-  const uint32_t b = start[j], cnt = start[j + 1] - b;
+  const uint32_t j = bigj[3 * bi], b = bigj[3 * bi + 1], cnt = bigj[3 * bi + 2];
   const int tid = threadIdx.x, c = tid % BC, r0 = tid / BC;
   const size_t col = (size_t)strip * BC + c;
   const bool colok = col < d;
@@ -428,6 +426,36 @@ __global__ __launch_bounds__(BT) void k_sum_big(const float* __restrict__ x, siz
   }
 }
 
+// All the sums in one launch: workgroups [0, nbb) take (large cluster,
+// strip) work (nbb = listed-cluster slots x strips; one past the clusters
+// the count listed exits), the rest cluster j = blockIdx.x - nbb of up to
+// SMALL rows. The large clusters' long in-order chains then run beside the
+// small clusters' sums instead of after them.
+template <bool VEC4>
+__global__ __launch_bounds__(BT) void k_sums(const float* __restrict__ x, size_t nx, size_t d,
+                                             const uint32_t* __restrict__ rid,
+                                             const uint32_t* __restrict__ start, size_t k,
+                                             const uint32_t* __restrict__ bigj, int strips,
+                                             int nbb, float* __restrict__ sums,
+                                             float* __restrict__ acc,
+                                             uint32_t* __restrict__ small) {
+  __shared__ __attribute__((aligned(16))) float vals[2][BC * BRP];
+  __shared__ uint32_t rows[2][BR];
+  static_assert(BR >= SMALL, "the small path's rows fit one row-id buffer");
+  if ((int)blockIdx.x < nbb) {
+    const int bi = blockIdx.x / strips, strip = blockIdx.x % strips;
+    if (bi >= (int)small[SW_NBIG]) return;
+    sum_big(bi, strip, x, d, rid, bigj, sums, acc, vals, rows);
+    return;
+  }
+  const size_t j = blockIdx.x - nbb;
+  const uint32_t b = start[j], cnt = start[j + 1] - b;
+  if (cnt > (uint32_t)SMALL) return;  // a large cluster: done above
+  if (threadIdx.x < cnt) rows[0][threadIdx.x] = rid[b + threadIdx.x];
+  __syncthreads();
+  sum_rows<VEC4>(x, d, rows[0], cnt, j, sums, acc);
+}
+
 }  // namespace
 
 // The chunked path when the chunk histograms fit LDS and the last
@@ -438,20 +466,18 @@ static bool chunked(size_t n, size_t k) {
 }
 
 void launch_scatter_count(emh_ctx* c, size_t lo, size_t hi, const uint32_t* labels, size_t k,
-                          uint32_t* counts) {
+                          uint32_t* counts, bool counts_zero) {
   const size_t n = hi > lo ? hi - lo : 0;
   uint32_t* start = (uint32_t*)c->start.get((k + 1) * 4);
   // Clusters above SMALL rows: at most n / (SMALL + 1) of them.
   const size_t maxbig = std::min(k, n / (SMALL + 1) + 1);
-  uint32_t* bigj = (uint32_t*)c->bigj.get(maxbig * 4);
+  uint32_t* bigj = (uint32_t*)c->bigj.get(maxbig * 12);
   if (chunked(n, k)) {
     const size_t nch = (n + CP - 1) / CP;
     uint32_t* cnt = (uint32_t*)c->chunkcnt.get(nch * k * 4);
-    hipLaunchKernelGGL(k_hist_chunks, dim3((unsigned)nch), dim3(256), 0, c->stream, labels, lo,
-                       hi, k, cnt, c->small);
-    EMH_HIP(hipGetLastError());
-    hipLaunchKernelGGL(k_prefix_chunks, dim3(1), dim3(PT), 0, c->stream, k, nch, cnt, counts,
-                       start, bigj, c->small);
+    if (!counts_zero) launch_fill_u32(c, counts, k, 0);
+    hipLaunchKernelGGL(k_hist_total, dim3((unsigned)nch), dim3(256), 0, c->stream, labels, lo,
+                       hi, k, cnt, counts, start, bigj, c->small);
     EMH_HIP(hipGetLastError());
     return;
   }
@@ -473,37 +499,30 @@ void launch_scatter_sums(emh_ctx* c, const float* x, size_t nx, size_t d, const 
   uint32_t* start = (uint32_t*)c->start.get((k + 1) * 4);
   uint32_t* rid = (uint32_t*)c->order.get(std::max<size_t>(n, 1) * 4);
   const size_t maxbig = std::min(k, n / (SMALL + 1) + 1);
-  uint32_t* bigj = (uint32_t*)c->bigj.get(maxbig * 4);
+  uint32_t* bigj = (uint32_t*)c->bigj.get(maxbig * 12);
+  const int strips = (int)((d + BC - 1) / BC);
   if (chunked(n, k)) {
     const size_t nch = (n + CP - 1) / CP;
     const uint32_t* cnt = (const uint32_t*)c->chunkcnt.get(nch * k * 4);
-    hipLaunchKernelGGL(k_place_chunks, dim3((unsigned)nch), dim3(256), 0, c->stream, labels, lo,
-                       hi, k, start, cnt, ids, nx, c->small, rid);
+    hipLaunchKernelGGL(k_place_sum, dim3((unsigned)nch), dim3(256), 0, c->stream, labels, lo, hi,
+                       k, start, cnt, ids, nx, c->small, rid);
     EMH_HIP(hipGetLastError());
   } else if (n > 0) {
     hipLaunchKernelGGL(k_place, grid1(k, PW), dim3(64 * PW), 0, c->stream, labels, lo, hi, k,
                        start, ids, nx, c->small, rid);
     EMH_HIP(hipGetLastError());
   }
-  if (d % 4 == 0)
-    hipLaunchKernelGGL(k_sum<true>, dim3((unsigned)k), dim3(256), 0, c->stream, x, nx, d, rid, start,
-                       k, sums, acc, c->small);
-  else
-    hipLaunchKernelGGL(k_sum<false>, dim3((unsigned)k), dim3(256), 0, c->stream, x, nx, d, rid,
-                       start, k, sums, acc, c->small);
+  const int nbb = n > (size_t)SMALL ? (int)(maxbig * strips) : 0;
+  auto kern = d % 4 == 0 ? k_sums<true> : k_sums<false>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)(nbb + k)), dim3(BT), 0, c->stream, x, nx, d, rid, start,
+                     k, bigj, strips, nbb, sums, acc, c->small);
   EMH_HIP(hipGetLastError());
-  if (n > (size_t)SMALL) {
-    const int strips = (int)((d + BC - 1) / BC);
-    hipLaunchKernelGGL(k_sum_big, dim3((unsigned)(maxbig * strips)), dim3(BT), 0, c->stream, x,
-                       nx, d, rid, start, bigj, strips, sums, acc, c->small);
-    EMH_HIP(hipGetLastError());
-  }
 }
 
 void launch_scatter(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids, size_t lo,
                     size_t hi, const uint32_t* labels, size_t k, float* sums, uint32_t* counts,
                     float* acc) {
-  launch_scatter_count(c, lo, hi, labels, k, counts);
+  launch_scatter_count(c, lo, hi, labels, k, counts, false);
   launch_scatter_sums(c, x, nx, d, ids, lo, hi, labels, k, sums, acc);
 }
 

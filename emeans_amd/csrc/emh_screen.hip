@@ -166,7 +166,7 @@ Top1Screen screen_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const ui
     }
     ProfScope prof(c, EMH_PROF_SCREEN, 2.0 * (double)n * (double)k * (double)d,
                    prof_take(c, EMH_PROF_SCREEN));
-    launch_screen4(c, a, ip, true);
+    launch_screen4(c, a, ip);
     return s;
   }
   ProfScope prof(c, EMH_PROF_SCREEN, 2.0 * (double)n * (double)k * (double)d,

@@ -48,29 +48,30 @@ __device__ __forceinline__ void wait_vm() {
 // waits and barriers), where the compiler, unable to tell the ring's stages
 // apart across loop iterations, would wait for every DMA in flight before
 // each read. (Other loads the compiler waits for stay correct: DMAs it does
-// not count only make its vmcnt waits stricter.)
+// not count only make its vmcnt waits stricter.) M0 is saved and restored
+// around the DMA, so no value the compiler keeps there is disturbed.
 __device__ __forceinline__ uint32_t lds_addr(const void* lds) {
   return __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds);
 }
-__device__ __forceinline__ void dma16(const void* g, void* lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :
-               : "v"(g), "s"(lds_addr(lds))
-               : "memory", "m0");
-}
-// The same from a wave-uniform base plus a 32-bit per-lane byte offset.
+// From a wave-uniform base plus a 32-bit per-lane byte offset.
 __device__ __forceinline__ void dma16o(const void* base, uint32_t off, void* lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-               :
-               : "v"(off), "s"(base), "s"(lds_addr(lds))
-               : "memory", "m0");
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(off), "s"(base), "s"(lds_addr(lds))
+      : "memory");
 }
 __device__ __forceinline__ void dma4(const void* g, void* lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
-               :
-               : "v"(g), "s"(lds_addr(lds))
-               : "memory", "m0");
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\t"
+      "global_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(g), "s"(lds_addr(lds))
+      : "memory");
 }
 
 // Chunks of a slab row: 4 kk + (0, 1) the hi halves of dimensions 16 kk +
@@ -181,7 +182,7 @@ using StageNo = std::integral_constant<int, I>;
 // s % 2. Step s waits for its own DMAs, passes a barrier (every wave's DMAs of
 // step s are in, and every wave is done with stage (s + 1) % 2), then runs
 // its MFMAs while it issues the DMAs of step s + 1 into the other stage.
-template <int L, bool L2, bool TAG, int NW>
+template <int L, bool L2, int NW>
 __global__ __launch_bounds__(NW * 64, 1) void k_screen4(
     const char* __restrict__ xs, size_t xslab, const float* __restrict__ xn, size_t nx, int d,
     const uint32_t* __restrict__ ids, size_t lo, int nrows, const char* __restrict__ cs,
@@ -277,17 +278,8 @@ __global__ __launch_bounds__(NW * 64, 1) void k_screen4(
     al[a] = *reinterpret_cast<const v8bf*>(p + ol);
   };
 
-  float lkey[WN][L];  // per-row lists (tagged keys: filled by the fold after the loop)
+  float lkey[WN][L];  // per-row lists, filled by the fold after the loop
   uint32_t lid[WN][L];
-  if (!TAG) {
-#pragma unroll
-    for (int y = 0; y < WN; y++)
-#pragma unroll
-      for (int e = 0; e < L; e++) {
-        lkey[y][e] = INFINITY;
-        lid[y][e] = NONE;
-      }
-  }
   v16f acc[WA][WN];
 #pragma unroll
   for (int a = 0; a < WA; a++)
@@ -296,7 +288,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_screen4(
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[a][y][r] = 0.f;
 
-  // The folds keep, per lane and row, the L smallest keys of the lane's
+  // The fold keeps, per lane and row, the L smallest keys of the lane's
   // columns among those within its own smallest key m plus twice the bound
   // E' >= E the check uses (screen_bound on the same inputs, with a margin
   // for its own rounding and for the tags' 63 ulps). The check settles a row
@@ -335,64 +327,11 @@ __global__ __launch_bounds__(NW * 64, 1) void k_screen4(
         const size_t id = ids ? (size_t)ids[p] : p;
         xv = xn[id < nx ? id : 0];
       }
-      thr_e[y] = 2.0f * 1.0078125f * screen_bound(xv, cm2, cnm, d, L2, true, TAG);
+      thr_e[y] = 2.0f * 1.0078125f * screen_bound(xv, cm2, cnm, d, L2, true, true);
     }
   }
   auto threshold = [&](float m, int y) __attribute__((always_inline)) {
     return m + thr_e[y] + fabsf(m) * 1.52587890625e-05f + 1e-42f;  // + 2^-16 |m|: the tags
-  };
-  // A finished tile of a part of several tiles: the sorted insert, with the
-  // running minimum over the part's tiles so far (a lower minimum only
-  // narrows the window, and keys outside it stay outside). The tile's norms
-  // landed with its first slab, at least one barrier ago.
-  float mrun[WN];
-#pragma unroll
-  for (int y = 0; y < WN; y++) mrun[y] = INFINITY;
-  auto fold_sorted = [&](int tile) __attribute__((always_inline)) {
-    const float* ns = Ns[tile & 3];
-    // Keys into the accumulators; the lane's minimum per row.
-#pragma unroll
-    for (int a = 0; a < WA; a++) {
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        // 32x32 accumulator layout: element (m, n) with n = lane % 32,
-        // m = 8 (r / 4) + 4 (lane / 32) + r % 4; r = 4 q + e.
-        const int c0 = wc * 128 + a * 32 + 8 * q + 4 * h;
-        const float4 n4 = L2 ? *reinterpret_cast<const float4*>(ns + c0) : make_float4(0, 0, 0, 0);
-        const float nv[4] = {n4.x, n4.y, n4.z, n4.w};
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const int r = 4 * q + e;
-          const float nn = tile * TC3 + c0 + e < k ? nv[e] : INFINITY;
-#pragma unroll
-          for (int y = 0; y < WN; y++) {
-            const float v = acc[a][y][r];
-            const float key = L2 ? fmaf(-2.0f, v, nn) : nn - v;  // one rounding: within E
-            acc[a][y][r] = key;
-            mrun[y] = fminf(mrun[y], key);
-          }
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);  // one centroid block's accumulators at a time
-    }
-    float thr[WN];
-#pragma unroll
-    for (int y = 0; y < WN; y++) thr[y] = threshold(mrun[y], y);
-#pragma unroll
-    for (int a = 0; a < WA; a++) {
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const uint32_t gj = (uint32_t)(tile * TC3 + wc * 128 + a * 32 + 8 * (r >> 2) + 4 * h + (r & 3));
-#pragma unroll
-        for (int y = 0; y < WN; y++) {
-          const float key = acc[a][y][r];
-          if (__ballot(key <= thr[y]) != 0ull)
-            insert_nb<L>(lkey[y], lid[y], key <= thr[y] ? key : INFINITY, gj);
-          acc[a][y][r] = 0.f;
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
   };
   // A part of one tile: each key carries its lane-local column tag 16 a + r
   // in its low 6 mantissa bits (the bound covers the change), so that an
@@ -484,7 +423,6 @@ __global__ __launch_bounds__(NW * 64, 1) void k_screen4(
   read_rows(s0, 0, r0);
 #pragma unroll
   for (int a = 0; a < WA; a++) read_cent(s0, 0, a);
-  int ct = t0, cj = 0;  // compute cursor (sorted lists)
   // One step s (a 32-dimension slab in stage s % 2, two MFMA steps), as
   // groups of 3 WN MFMAs (one centroid block each) with the fences keeping
   // each group's other work after it:
@@ -525,17 +463,13 @@ __global__ __launch_bounds__(NW * 64, 1) void k_screen4(
       if (a == WA - 1) advance();
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (!TAG && ++cj == d32) {
-      cj = 0;
-      fold_sorted(ct++);
-    }
   };
   for (int st = 0; st < nsteps; st += 2) {
     step(StageNo<0>{});
     if (st + 1 < nsteps) step(StageNo<1>{});
   }
   wait_vm<0>();  // the DMAs past the last step have landed (the merge reuses stages)
-  if (TAG) fold_tagged(t0);  // tagged keys: one tile per part
+  fold_tagged(t0);
 
   // The rows' |x|^2 for the check (the split's sums).
   if (part == 0 && xn != xnorm && tid < TR3) {

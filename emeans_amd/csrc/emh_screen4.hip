@@ -6,11 +6,12 @@
 
 namespace emh {
 
-void launch_screen4(emh_ctx* c, const Screen4Args& a, bool ip, bool tagged) {
-  // The kernel addresses a slab's rows with 32-bit byte offsets (128 per row).
+void launch_screen4(emh_ctx* c, const Screen4Args& a, bool ip) {
+  // The kernel addresses a slab's rows with 32-bit byte offsets (128 per row)
+  // and keeps one tile per part.
   EMH_ENSURE(a.nx < (1u << 25) && a.k < (1u << 25), "screen: more than 2^25 rows or centroids");
-  auto kern = ip ? (tagged ? k_screen4<L1, false, true, 8> : k_screen4<L1, false, false, 8>)
-                 : (tagged ? k_screen4<L1, true, true, 8> : k_screen4<L1, true, false, 8>);
+  EMH_ENSURE(a.tpp == 1 && a.parts == a.ntiles, "screen: one tile per part");
+  auto kern = ip ? k_screen4<L1, false, 8> : k_screen4<L1, true, 8>;
   hipLaunchKernelGGL(kern, dim3(a.blocks), dim3(512), 0, c->stream, (const char*)a.xs, a.xslab,
                      a.xn, a.nx, (int)a.d, a.ids, a.lo, (int)a.n, (const char*)a.cs, a.cslab,
                      a.cnorm, (int)a.k, a.tpp, a.parts, a.ntiles, a.cand, a.xnorm, a.part,

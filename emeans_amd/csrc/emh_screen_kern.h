@@ -850,7 +850,7 @@ struct Screen4Args {
   const uint32_t* part;  // the centroid split's per-block maxima (launch_halves' part)
   int nparts;
 };
-void launch_screen4(emh_ctx* c, const Screen4Args& a, bool ip, bool tagged);
+void launch_screen4(emh_ctx* c, const Screen4Args& a, bool ip);
 // The 128 x 128 top-1 screen (emh_screen_t1_{bf3,f32}.hip) and the kNN screen
 // (emh_screen_kn_{bf3,f32}_{self,any}.hip), in bf16 three-pass or f32 MFMA arithmetic.
 void launch_screen_t1_bf3(emh_ctx* c, const ScreenArgs& a, bool ip);

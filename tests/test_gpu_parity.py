@@ -324,13 +324,13 @@ def test_scatter_ema_split(dev, n, d, k):
     assert dev.read_f32(u).tobytes() == wu.tobytes()
 
 
-@pytest.mark.parametrize("d,k", [(200, 96), (768, 96), (64, 9000)])
+@pytest.mark.parametrize("d,k", [(200, 96), (768, 96), (64, 4096), (64, 9000)])
 def test_scatter_skewed_clusters(dev, d, k):
     """Skewed cluster sizes (the Zipf case of training): clusters of several
     thousand rows, sizes at the edges of the per-column path (127..129, 256,
     257 rows), a single row and empty clusters; rows gathered by id; with acc.
-    k = 9000 takes the placement path for more clusters than the chunk
-    histograms hold."""
+    k = 96 and 4096 take the counting sort with chunk histograms; k = 9000
+    the placement path for more clusters than the chunk histograms hold."""
     from emeans_amd import Mat, Select
     n = 20000
     g = np.random.default_rng(d)
@@ -356,6 +356,29 @@ def test_scatter_skewed_clusters(dev, d, k):
     # Without ids (rows are positions) and without acc.
     dev.scatter_add(Mat(xb, d), Select(None, (0, n)), lb, k, sums, counts, None)
     os_, oc = O.scatter_add(x[:n], d, labels, k)
+    assert np.array_equal(dev.read_u32(counts), oc)
+    assert dev.read_f32(sums).tobytes() == os_.tobytes()
+
+
+@pytest.mark.parametrize("k", [96, 4096])
+def test_scatter_label_out_of_range_fails(dev, k):
+    """A label >= k (an index out of the sums in core/cpu.rs:118-143, which
+    panics) fails at the next wait, as every error the kernels record, with
+    few clusters (k = 96) and many (k = 4096); the next call runs as usual."""
+    from emeans_amd import Mat, Select
+    n, d = 20000, 64
+    g = np.random.default_rng(k)
+    x = g.standard_normal((n, d)).astype(np.float32)
+    labels = g.integers(0, k, n).astype(np.uint32)
+    bad = labels.copy()
+    bad[n // 2] = k + 3
+    xb = dev.bind(x)
+    sums, counts = dev.zeros_f32(k * d), dev.zeros_u32(k)
+    with pytest.raises(Exception, match="label out of range"):
+        dev.scatter_add(Mat(xb, d), Select(None, (0, n)), dev.upload_u32(bad), k, sums, counts, None)
+        dev.read_u32(counts)
+    dev.scatter_add(Mat(xb, d), Select(None, (0, n)), dev.upload_u32(labels), k, sums, counts, None)
+    os_, oc = O.scatter_add(x, d, labels, k)
     assert np.array_equal(dev.read_u32(counts), oc)
     assert dev.read_f32(sums).tobytes() == os_.tobytes()
 
