@@ -53,9 +53,10 @@ METRIC = "train s & assign Mrows/s at 200k×768 k=1024 FP32; % of FP32 MFMA peak
 # HBM bytes per screen launch over this workload's launch mix (calibrated
 # FETCH_SIZE + WRITE_SIZE from two rocprofv3 --pmc passes of this script, with
 # a plain copy kernel of known size as the scale;
-# profiles/k_screen_train_assign_200kx768_k1024_hbm_traffic.md). None until
-# measured for the current screen.
-SCREEN_TRAFFIC_BYTES = None
+# profiles/k_screen_train_assign_200kx768_k1024_hbm_traffic.md): 88.7 MB per
+# 16,384-row batch launch (50.3 MB of split rows, the centroids once per XCD),
+# 332 MB per 65,536-row assignment chunk, 45 MB per epoch-tail batch.
+SCREEN_TRAFFIC_BYTES = 95.4e6
 # The screen's roofline times every PROFILE_EVERY-th launch of the timed steps
 # with HIP events (an event pair between two kernels costs the stream a few
 # microseconds; on every launch that was ~5 % of the headline step).
@@ -209,8 +210,8 @@ def headline(args):
             "the bound of each lane's best)", SCREEN_TRAFFIC_BYTES),
         "update_rooflines": {
             "scatter_add": hbm_roofline(*main["update"]["scatter_add"],
-                                        "k_hist_chunks + k_prefix_chunks + k_place_chunks + "
-                                        "k_sum + k_sum_big"),
+                                        "k_hist_total + k_place_sum + k_sums (chunked "
+                                        "counting sort, ordered per-cluster sums)"),
             "ema_update": hbm_roofline(*main["update"]["ema_update"], "k_ema"),
         },
     }
