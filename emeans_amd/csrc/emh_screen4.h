@@ -106,58 +106,94 @@ __device__ __forceinline__ void load32(const float* p, int col, int d, float (&v
 // order: the screen bound's input). With part: block b writes the largest
 // |x|^2 of its rows and, with cnorm, the largest cnorm[g] (f32 bits; a NaN or
 // negative value wins) to part[2 b], part[2 b + 1]: the bound's centroid
-// inputs, which the screen reduces (no atomics on one word). 32 lanes per
-// row, lane j takes slabs j, j + 32, ...; block b takes rows 8 b .. 8 b + 7.
+// inputs, which the screen reduces (no atomics on one word).
+// Block b takes rows 8 b .. 8 b + 7, two per wave. A wave reads a row in
+// 256-dimension segments, 16 contiguous bytes per lane (one 1 KB run per
+// load instruction), and lane l writes the hi and lo quads of its four
+// dimensions (8 bytes each) into slab 8 s + l / 8: eight lanes fill one
+// slab row, so each store instruction covers eight whole 128-byte lines.
 template <bool VEC4>
 __global__ __launch_bounds__(256) void k_halves(const float* __restrict__ x, size_t nx, int d,
                                                 const uint32_t* __restrict__ ids, size_t lo,
-                                                size_t n, uint4* __restrict__ out,
+                                                size_t n, char* __restrict__ out,
                                                 float* __restrict__ norm,
                                                 const float* __restrict__ cnorm,
                                                 uint32_t* __restrict__ part) {
-  const int j0 = threadIdx.x & 31;
-  const int d32 = (d + 31) >> 5;
-  const size_t g = (size_t)blockIdx.x * 8 + (threadIdx.x >> 5);
-  const bool valid = g < n;
-  size_t id = 0;
-  if (valid) {
-    id = ids ? (size_t)ids[lo + g] : lo + g;
-    if (id >= nx) id = 0;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int d32 = (d + 31) >> 5, nseg = (d32 + 7) >> 3;
+  const int js = lane >> 3, c4 = lane & 7;
+  // Quad c4 of a slab row holds dimensions 4 c4 .. 4 c4 + 3: 8-dimension
+  // chunk c8 = c4 / 2 of MFMA step kk = c8 / 2, whose hi half sits in chunk
+  // 4 kk + c8 % 2 and lo half two chunks later.
+  const int c8 = c4 >> 1;
+  const int hoff = 16 * (4 * (c8 >> 1) + (c8 & 1)) + 8 * (c4 & 1);
+  size_t g[2];
+  bool valid[2];
+  const float* xr[2];
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    g[i] = (size_t)blockIdx.x * 8 + 2 * w + i;
+    valid[i] = g[i] < n;
+    size_t id = 0;
+    if (valid[i]) {
+      id = ids ? (size_t)ids[lo + g[i]] : lo + g[i];
+      if (id >= nx) id = 0;
+    }
+    xr[i] = x + id * (size_t)d;
   }
-  const float* xr = x + id * (size_t)d;
-  float sq = 0.f;
-  for (int j = j0; j < d32; j += 32) {
-    float v[32];
-    load32<VEC4>(xr, 32 * j, d, v);
-    v8bf hi[4], lw[4];
+  float sq[2] = {0.f, 0.f};
+#pragma unroll 3
+  for (int s = 0; s < nseg; s++) {
+    const int j = 8 * s + js;
+    if (j >= d32) break;
+    const int col = 32 * j + 4 * c4;
+    float4 v[2];
 #pragma unroll
-    for (int c = 0; c < 4; c++)
-      split8(make_float4(v[8 * c], v[8 * c + 1], v[8 * c + 2], v[8 * c + 3]),
-             make_float4(v[8 * c + 4], v[8 * c + 5], v[8 * c + 6], v[8 * c + 7]), hi[c], lw[c]);
+    for (int i = 0; i < 2; i++) {
+      if (VEC4) {
+        v[i] = col < d ? *reinterpret_cast<const float4*>(xr[i] + col) : make_float4(0.f, 0.f, 0.f, 0.f);
+      } else {
+        v[i].x = col < d ? xr[i][col] : 0.f;
+        v[i].y = col + 1 < d ? xr[i][col + 1] : 0.f;
+        v[i].z = col + 2 < d ? xr[i][col + 2] : 0.f;
+        v[i].w = col + 3 < d ? xr[i][col + 3] : 0.f;
+      }
+    }
 #pragma unroll
-    for (int e = 0; e < 32; e++) sq = fmaf(v[e], v[e], sq);
-    if (valid) {
-      uint4* o = out + ((size_t)j * n + g) * 8;
+    for (int i = 0; i < 2; i++) {
+      const float e[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+      v4bf hi, lw;
 #pragma unroll
-      for (int kk = 0; kk < 2; kk++) {
-        o[4 * kk] = __builtin_bit_cast(uint4, hi[2 * kk]);
-        o[4 * kk + 1] = __builtin_bit_cast(uint4, hi[2 * kk + 1]);
-        o[4 * kk + 2] = __builtin_bit_cast(uint4, lw[2 * kk]);
-        o[4 * kk + 3] = __builtin_bit_cast(uint4, lw[2 * kk + 1]);
+      for (int t = 0; t < 4; t++) {
+        const __bf16 h = (__bf16)e[t];
+        hi[t] = h;
+        lw[t] = (__bf16)(e[t] - (float)h);
+        sq[i] = fmaf(e[t], e[t], sq[i]);
+      }
+      if (valid[i]) {
+        char* o = out + ((size_t)j * n + g[i]) * SLAB_BYTES + hoff;
+        *reinterpret_cast<uint2*>(o) = __builtin_bit_cast(uint2, hi);
+        *reinterpret_cast<uint2*>(o + 32) = __builtin_bit_cast(uint2, lw);
       }
     }
   }
 #pragma unroll
-  for (int m = 16; m > 0; m >>= 1) sq += __shfl_xor(sq, m, 32);
-  if (valid && j0 == 0) norm[g] = sq;
+  for (int i = 0; i < 2; i++) {
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) sq[i] += __shfl_xor(sq[i], m, 64);
+    if (valid[i] && lane == 0) norm[g[i]] = sq[i];
+  }
   if (part) {
-    uint32_t ma = valid ? __float_as_uint(sq) : 0u;
-    uint32_t mb = valid && cnorm ? __float_as_uint(cnorm[g]) : 0u;
-    ma = max(ma, (uint32_t)__shfl_xor((int)ma, 32, 64));  // lanes 0, 32 hold their rows' values
-    mb = max(mb, (uint32_t)__shfl_xor((int)mb, 32, 64));
+    uint32_t ma = 0u, mb = 0u;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      if (valid[i]) {
+        ma = max(ma, __float_as_uint(sq[i]));
+        if (cnorm) mb = max(mb, __float_as_uint(cnorm[g[i]]));
+      }
+    }
     __shared__ uint32_t red[2][4];
-    const int w = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) {
+    if (lane == 0) {
       red[0][w] = ma;
       red[1][w] = mb;
     }

@@ -25,7 +25,7 @@ void launch_halves(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32
   EMH_ENSURE(d >= 1 && n < (1u << 31), "halves: shape out of range");
   auto kern = d % 4 == 0 ? k_halves<true> : k_halves<false>;
   hipLaunchKernelGGL(kern, dim3((unsigned)halves_blocks(n)), dim3(256), 0, c->stream, x, nx,
-                     (int)d, ids, lo, n, (uint4*)out, norm, cnorm, part);
+                     (int)d, ids, lo, n, (char*)out, norm, cnorm, part);
   EMH_HIP(hipGetLastError());
 }
 
