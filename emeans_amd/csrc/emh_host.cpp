@@ -558,6 +558,16 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
                   nullptr);
     pre = &pre_rows;
   }
+  // L2 batches on the split-operand screen keep the centroids split for the
+  // run: a full split after each row-norms readout (the first batch, and
+  // after a revival moved rows), then the EMA rewrites the rows it moves.
+  const bool keep_csplit = pre && !sph;
+  void* tsplit = keep_csplit ? c->tsplit.get(halves_bytes(k, d)) : nullptr;
+  uint32_t* tpart_h = keep_csplit
+                          ? (uint32_t*)c->tsplit_part.get((halves_blocks(k) + ema_blocks(k)) * 8)
+                          : nullptr;
+  uint32_t* tpart_e = keep_csplit ? tpart_h + 2 * halves_blocks(k) : nullptr;
+  SplitCents pcents{tsplit, tpart_h, (int)halves_blocks(k)};
   uint32_t* d_order[2] = {order0.u(), order1.u()};
   uint32_t* d_lab[2] = {lab0.u(), lab1.u()};
   // The epoch's label counts, tallied batch by batch by the EMA launches: the
@@ -662,6 +672,12 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
       } else if (norms_stale) {
         launch_row_norms(c, pos.f(), k, d, readout.f());
         norms_stale = false;
+        if (keep_csplit) {
+          launch_halves(c, pos.f(), k, d, nullptr, 0, k, tsplit, (float*)c->csplit_norm.get(k * 4),
+                        readout.f(), tpart_h);
+          pcents.part = tpart_h;
+          pcents.nparts = (int)halves_blocks(k);
+        }
       }
       const float* cents = sph ? readout.f() : pos.f();
       const float* cn = sph ? nullptr : readout.f();
@@ -669,7 +685,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
         const size_t c1 = std::min(c0 + chunk, e);
         // After the first step the previous EMA cleared the screen's words.
         launch_top1(c, x, n, d, order, c0, c1, cents, cn, k, sph, lab, sco,
-                    step > 0 && c0 == b, nullptr, pre);
+                    step > 0 && c0 == b, nullptr, pre, keep_csplit ? &pcents : nullptr);
       }
       if (refill) {  // the next check's Gumbel terms, drawn while the GPU works
         gnext = beside([&] { return gumbel_terms(split_rng, k); });
@@ -696,7 +712,11 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
       {
         ProfScope p(c, EMH_PROF_EMA, ema_bytes(k, d), prof_take(c, EMH_PROF_EMA));
         launch_ema(c, pos.f(), mass.f(), sums.f(), counts.u(), k, d, af, df, replace,
-                   sph ? nullptr : readout.f(), true, d_tally[buf], true);
+                   sph ? nullptr : readout.f(), true, d_tally[buf], true, tsplit, tpart_e);
+        if (keep_csplit) {
+          pcents.part = tpart_e;
+          pcents.nparts = (int)ema_blocks(k);
+        }
       }
       if (check) {
         wait_posted(c, h_seq, seq_no);

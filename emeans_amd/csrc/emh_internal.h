@@ -156,6 +156,7 @@ struct emh_ctx {
   emh::Scratch cand, fblist, order, start, misc, knn_tmp, xnorm, bigj, chunkcnt, tickets;
   emh::Scratch xsplit, csplit, csplit_norm, csplit_part;  // split-operand screen: a call's rows, centroids
   emh::Scratch xpre, xpre_norm;              // a training run's rows, split once
+  emh::Scratch tsplit, tsplit_part;          // a training run's centroids, kept split by the EMA
   emh::Scratch preview_ticket;  // k_mass_preview's last-block ticket (left at zero)
   // Host staging of the device loop: masses, plan, flags, epoch orders and
   // epoch labels/scores (double-buffered), results.
@@ -246,11 +247,15 @@ void launch_normalize_rows(emh_ctx* c, const float* src, size_t rows, size_t d, 
 // clears before its screen (the fallback count and the bound maxima), so the
 // next top-1 may skip that fill. With tally, also adds counts into it. With
 // zero_counts, leaves counts at zero once read (the next batch's
-// launch_scatter_count adds into them).
+// launch_scatter_count adds into them). With csplit (norms needed), also
+// rewrites the bf16 halves (launch_halves' layout, k rows) of the rows it
+// moves and leaves the bound's centroid maxima of its ema_blocks(k) blocks in
+// cpart, as launch_halves' part does.
 void launch_ema(emh_ctx* c, float* pos, float* usage, const float* sums, const uint32_t* counts,
                 size_t k, size_t d, float alpha, float decay, int replace, float* norms = nullptr,
                 bool clear_screen_words = false, uint32_t* tally = nullptr,
-                bool zero_counts = false);
+                bool zero_counts = false, void* csplit = nullptr, uint32_t* cpart = nullptr);
+size_t ema_blocks(size_t k);
 // The masses launch_ema will leave, into out (usage untouched); with
 // small_out, also a copy of the small block's words; with seq_out, then seq
 // into *seq_out once all of that is written. out, small_out and seq_out may be
@@ -315,12 +320,20 @@ struct SplitRows {
   const float* xn;
   size_t nx, slab;
 };
-// pre: x's rows already split (used when the call takes the split-operand
-// screen; see split_screen).
+// Centroids split ahead of the call (launch_halves over the k centroids, or
+// launch_ema's csplit for the rows it moved), with the bound's centroid
+// maxima in nparts (max |c|^2, max cnorm) pairs.
+struct SplitCents {
+  const void* cs;
+  const uint32_t* part;
+  int nparts;
+};
+// pre: x's rows already split, pc: the centroids (used when the call takes
+// the split-operand screen; see split_screen).
 void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids, size_t lo, size_t hi,
                  const float* cents, const float* cnorm, size_t k, bool ip, uint32_t* labels,
                  float* scores, bool words_clear = false, Arena* ar = nullptr,
-                 const SplitRows* pre = nullptr);
+                 const SplitRows* pre = nullptr, const SplitCents* pc = nullptr);
 // Whether top-1 calls with d dimensions and k centroids take the
 // split-operand screen (k_screen4), whose rows a caller may split ahead.
 bool split_screen(emh_ctx* c, size_t d, size_t k);

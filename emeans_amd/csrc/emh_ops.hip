@@ -10,6 +10,7 @@
 // so one wave owns a row: its lanes square the elements in parallel into LDS
 // and one lane adds them in order.
 
+#include "emh_halves.h"
 #include "emh_internal.h"
 
 namespace emh {
@@ -141,6 +142,11 @@ __device__ __forceinline__ float ema_mass(float u, uint32_t cnt, float alpha, fl
 
 // With norms != nullptr, also the squared norm of every updated row (the next
 // batch's L2 readout, assign.rs:150-155); rows without members keep theirs.
+// With csplit (norms too), also the bf16 halves of every updated row in the
+// split-operand layout of k rows (emh_halves.h), so the next batch's screen
+// need not split the centroids again (rows without members keep theirs), and
+// cpart[2 b] = cpart[2 b + 1] = the largest norms[] of block b's rows (f32
+// bits; a NaN wins): the bound's centroid maxima, as k_halves leaves them.
 // Workgroup = EC clusters: the 256 threads update the clusters' positions
 // element by element, then lane c of the first wave adds cluster c's rounded
 // squares in order from LDS (rows padded by four floats so the EC lanes read
@@ -157,8 +163,11 @@ __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __r
                                              float* __restrict__ norms,
                                              uint32_t* __restrict__ clear3,
                                              uint32_t* __restrict__ tally,
-                                             uint32_t* zero_counts) {  // counts itself, or null
-  // EC rows of min(d, ECH) + 4 floats (norms only)
+                                             uint32_t* zero_counts,  // counts itself, or null
+                                             char* __restrict__ csplit,
+                                             uint32_t* __restrict__ cpart) {
+  // EC rows of min(d, ECH) + 4 floats (norms only): the rounded squares;
+  // with csplit, then as many for the values.
   extern __shared__ __attribute__((aligned(16))) float sq[];
   __shared__ float wgt[EC], cntf[EC];
   const int tid = threadIdx.x;
@@ -176,6 +185,7 @@ __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __r
   }
   __syncthreads();
   const int seg = (int)min(d, (size_t)ECH), row = seg + 4;  // rows stay 16-byte aligned
+  float* vs = sq + EC * row;
   // Thread layout of the update: TPC threads per cluster, thread q of cluster
   // c takes dimensions q, q + TPC, ...
   const int c = tid / TPC, q = tid % TPC;
@@ -210,11 +220,32 @@ __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __r
           }
           p[t] = v;
           if (norms) sq[c * row + t] = v * v;
+          if (csplit) vs[c * row + t] = v;
         }
       }
     }
     if (!norms) continue;
     __syncthreads();
+    if (csplit && tid >= WAVE) {
+      // Waves 1-3 write the halves of the pass's dimensions (c0 is a
+      // multiple of 32; the last slab's dimensions past d are zero) while
+      // lanes of wave 0 run the chains.
+      const int nq = (((int)len + 31) & ~31) >> 2;  // quads in the pass
+      for (int e = tid - WAVE; e < EC * nq; e += 256 - WAVE) {
+        const int cc = e / nq, t = 4 * (e % nq);
+        if (cc >= nc || wgt[cc] < 0.0f) continue;
+        const float* vr = vs + cc * row;
+        const float4 v4 = make_float4(t < len ? vr[t] : 0.0f, t + 1 < len ? vr[t + 1] : 0.0f,
+                                      t + 2 < len ? vr[t + 2] : 0.0f,
+                                      t + 3 < len ? vr[t + 3] : 0.0f);
+        uint2 hi, lw;
+        split_quad(v4, hi, lw);
+        const size_t col = c0 + (size_t)t;
+        char* o = csplit + ((col >> 5) * k + j0 + cc) * SLAB_BYTES + quad_hi_offset((int)(col & 31) >> 2);
+        *reinterpret_cast<uint2*>(o) = hi;
+        *reinterpret_cast<uint2*>(o + 32) = lw;
+      }
+    }
     if (tid < nc && wgt[tid] >= 0.0f) {
       // Adds in order; the next 16 squares' LDS reads are in flight while the
       // current 16 are added.
@@ -245,6 +276,16 @@ __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __r
     __syncthreads();
   }
   if (norms && tid < nc && wgt[tid] >= 0.0f) norms[j0 + tid] = nrm;
+  if (cpart && tid < WAVE) {
+    uint32_t m = 0u;
+    if (tid < nc) m = __float_as_uint(wgt[tid] >= 0.0f ? nrm : norms[j0 + tid]);
+#pragma unroll
+    for (int o = 1; o < EC; o <<= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o, WAVE));
+    if (tid == 0) {
+      cpart[2 * blockIdx.x] = m;
+      cpart[2 * blockIdx.x + 1] = m;
+    }
+  }
 }
 
 // The masses the EMA step will leave (for the host's revival check), without
@@ -422,14 +463,21 @@ void launch_normalize_rows(emh_ctx* c, const float* src, size_t rows, size_t d, 
 
 void launch_ema(emh_ctx* c, float* pos, float* usage, const float* sums, const uint32_t* counts,
                 size_t k, size_t d, float alpha, float decay, int replace, float* norms,
-                bool clear_screen_words, uint32_t* tally, bool zero_counts) {
+                bool clear_screen_words, uint32_t* tally, bool zero_counts, void* csplit,
+                uint32_t* cpart) {
   if (k == 0) return;
-  const size_t lds = norms ? (size_t)EC * (std::min(d, (size_t)ECH) + 4) * sizeof(float) : 0;
+  EMH_ENSURE(!csplit || (norms && cpart), "ema: the centroid halves need the norms and maxima");
+  const size_t lds = norms ? (size_t)EC * (std::min(d, (size_t)ECH) + 4) * sizeof(float) *
+                                 (csplit ? 2 : 1)
+                           : 0;
   hipLaunchKernelGGL(k_ema, grid1(k, EC), dim3(256), lds, c->stream, pos, usage, sums, counts, k,
                      d, alpha, decay, replace, norms, clear_screen_words ? c->small : nullptr,
-                     tally, zero_counts ? const_cast<uint32_t*>(counts) : nullptr);
+                     tally, zero_counts ? const_cast<uint32_t*>(counts) : nullptr,
+                     (char*)csplit, cpart);
   EMH_HIP(hipGetLastError());
 }
+
+size_t ema_blocks(size_t k) { return (k + EC - 1) / EC; }
 
 void launch_mass_preview(emh_ctx* c, const float* usage, const uint32_t* counts, size_t k,
                          float alpha, float decay, int replace, float* out, uint32_t* small_out,

@@ -126,7 +126,8 @@ struct Top1Screen {
 
 Top1Screen screen_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
                        size_t lo, size_t n, const float* cents, const float* cnorm, size_t k,
-                       bool ip, bool words_clear, Arena* ar, const SplitRows* pre) {
+                       bool ip, bool words_clear, Arena* ar, const SplitRows* pre,
+                       const SplitCents* pc) {
   Top1Screen s;
   s.g = top1_geom(c, n, d, k, !ar);
   if (!s.g.screen) return s;
@@ -140,15 +141,28 @@ Top1Screen screen_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const ui
   const unsigned blocks = (unsigned)(g.row_tiles * g.parts);
   s.tagged = g.big && g.tpp == 1;
   if (g.split) {
-    // The centroids' halves and the bound's centroid maxima, then the rows'
-    // halves (the caller's, split ahead, or this selection's).
-    void* cs = c->csplit.get(halves_bytes(k, d));
-    uint32_t* part = (uint32_t*)c->csplit_part.get(halves_blocks(k) * 8);
-    launch_halves(c, cents, k, d, nullptr, 0, k, cs, (float*)c->csplit_norm.get(k * 4),
-                  ip ? nullptr : cnorm, part);
+    // The centroids' halves and the bound's centroid maxima (the caller's,
+    // split ahead, or split here), then the rows' halves (the caller's, or
+    // this selection's).
+    const void* cs;
+    const uint32_t* part;
+    int nparts;
+    if (pc) {
+      cs = pc->cs;
+      part = pc->part;
+      nparts = pc->nparts;
+    } else {
+      void* cw = c->csplit.get(halves_bytes(k, d));
+      uint32_t* pw = (uint32_t*)c->csplit_part.get(halves_blocks(k) * 8);
+      launch_halves(c, cents, k, d, nullptr, 0, k, cw, (float*)c->csplit_norm.get(k * 4),
+                    ip ? nullptr : cnorm, pw);
+      cs = cw;
+      part = pw;
+      nparts = (int)halves_blocks(k);
+    }
     Screen4Args a{blocks,   nullptr,  0,      nullptr, 0,       d,       nullptr,
                   0,        n,        cs,     k * 128, cnorm,   k,       1,
-                  g.parts,  g.ntiles, s.cand, s.xnorm, part,    (int)halves_blocks(k)};
+                  g.parts,  g.ntiles, s.cand, s.xnorm, part,    nparts};
     if (pre) {
       a.xs = pre->xs;
       a.xslab = pre->slab;
@@ -189,13 +203,13 @@ int bound_kind(emh_ctx* c, bool tagged) { return c->screen == SCREEN_F32 ? 0 : t
 void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids, size_t lo,
                  size_t hi, const float* cents, const float* cnorm, size_t k, bool ip,
                  uint32_t* labels, float* scores, bool words_clear, Arena* ar,
-                 const SplitRows* pre) {
+                 const SplitRows* pre, const SplitCents* pc) {
   if (hi <= lo) return;
   const size_t n = hi - lo;
   EMH_ENSURE(d <= 16384, "top1: d = %zu above the supported 16384", d);
   EMH_ENSURE(n < (1u << 31) && k < (1u << 31), "top1: shape too large");
   const Top1Screen s =
-      screen_top1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, words_clear, ar, pre);
+      screen_top1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, words_clear, ar, pre, pc);
   if (!s.g.screen) {
     launch_exact1(c, x, nx, d, ids, lo, n, nullptr, cents, cnorm, k, ip, labels, scores, ar);
     return;
@@ -213,7 +227,7 @@ void screen_margin_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const u
   const size_t n = hi - lo;
   EMH_ENSURE(d <= 16384 && n < (1u << 31) && k < (1u << 31), "top1: shape too large");
   const Top1Screen s =
-      screen_top1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, false, nullptr, nullptr);
+      screen_top1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, false, nullptr, nullptr, nullptr);
   if (!s.g.screen) return;  // variant 0: no screen, nothing to measure
   out->variant = s.g.big ? (s.tagged ? EMH_SCREEN_BIG_TAGGED : EMH_SCREEN_BIG_SORTED)
                          : (c->screen == SCREEN_F32 ? EMH_SCREEN_SMALL_F32 : EMH_SCREEN_SMALL_BF16);

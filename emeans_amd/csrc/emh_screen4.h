@@ -24,12 +24,12 @@
 
 #include <type_traits>
 
+#include "emh_halves.h"
 #include "emh_screen_kern.h"
 
 namespace emh {
 namespace {
 
-constexpr int SLAB_BYTES = 128;            // one row's 32 dimensions (one cache line)
 constexpr int S4_HALF = TR3 * SLAB_BYTES;  // one operand's slab in LDS: 32 KB
 constexpr int S4_STAGE = 2 * S4_HALF;      // rows and centroids: 64 KB
 
@@ -122,11 +122,7 @@ __global__ __launch_bounds__(256) void k_halves(const float* __restrict__ x, siz
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int d32 = (d + 31) >> 5, nseg = (d32 + 7) >> 3;
   const int js = lane >> 3, c4 = lane & 7;
-  // Quad c4 of a slab row holds dimensions 4 c4 .. 4 c4 + 3: 8-dimension
-  // chunk c8 = c4 / 2 of MFMA step kk = c8 / 2, whose hi half sits in chunk
-  // 4 kk + c8 % 2 and lo half two chunks later.
-  const int c8 = c4 >> 1;
-  const int hoff = 16 * (4 * (c8 >> 1) + (c8 & 1)) + 8 * (c4 & 1);
+  const int hoff = quad_hi_offset(c4);
   size_t g[2];
   bool valid[2];
   const float* xr[2];
@@ -161,19 +157,16 @@ __global__ __launch_bounds__(256) void k_halves(const float* __restrict__ x, siz
     }
 #pragma unroll
     for (int i = 0; i < 2; i++) {
-      const float e[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
-      v4bf hi, lw;
-#pragma unroll
-      for (int t = 0; t < 4; t++) {
-        const __bf16 h = (__bf16)e[t];
-        hi[t] = h;
-        lw[t] = (__bf16)(e[t] - (float)h);
-        sq[i] = fmaf(e[t], e[t], sq[i]);
-      }
+      sq[i] = fmaf(v[i].x, v[i].x, sq[i]);
+      sq[i] = fmaf(v[i].y, v[i].y, sq[i]);
+      sq[i] = fmaf(v[i].z, v[i].z, sq[i]);
+      sq[i] = fmaf(v[i].w, v[i].w, sq[i]);
+      uint2 hi, lw;
+      split_quad(v[i], hi, lw);
       if (valid[i]) {
         char* o = out + ((size_t)j * n + g[i]) * SLAB_BYTES + hoff;
-        *reinterpret_cast<uint2*>(o) = __builtin_bit_cast(uint2, hi);
-        *reinterpret_cast<uint2*>(o + 32) = __builtin_bit_cast(uint2, lw);
+        *reinterpret_cast<uint2*>(o) = hi;
+        *reinterpret_cast<uint2*>(o + 32) = lw;
       }
     }
   }

@@ -18,7 +18,6 @@ constexpr int LDK = BK + 4;  // f32 screen: padded LDS row (floats), conflict-fr
 
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
-typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
 
 // Work item of block `bid` of `nb`: blocks are dealt round-robin to the 8 XCDs
 // (consecutive ids land on different XCDs), so number each XCD's blocks
