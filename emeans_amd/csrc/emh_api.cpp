@@ -182,7 +182,7 @@ int emh_destroy(emh_ctx* c) {
     for (emh::Scratch* s : {&c->cand, &c->fblist, &c->order, &c->start, &c->misc, &c->knn_tmp,
                             &c->xnorm, &c->bigj, &c->chunkcnt, &c->tickets,
                             &c->preview_ticket, &c->xsplit, &c->csplit, &c->csplit_norm, &c->csplit_part,
-                            &c->xpre, &c->xpre_norm, &c->tsplit, &c->tsplit_part})
+                            &c->xpre, &c->xpre_norm, &c->tsplit, &c->tsplit_part, &c->tally_cnt})
       s->release();
     for (emh::Pinned* s : {&c->pin_usage, &c->pin_plan, &c->pin_small, &c->pin_order[0],
                            &c->pin_order[1], &c->pin_lab[0], &c->pin_lab[1], &c->pin_sco[0],

@@ -568,6 +568,14 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
                           : nullptr;
   uint32_t* tpart_e = keep_csplit ? tpart_h + 2 * halves_blocks(k) : nullptr;
   SplitCents pcents{tsplit, tpart_h, (int)halves_blocks(k)};
+  // When the batches' top-1 runs the screen with d % 4 == 0, the check and
+  // the queued-row scan tally the labels they write (counts and the chunk
+  // histograms of the counting sort), so scatter_add needs no count launch;
+  // the EMA clears both for the next batch.
+  const bool tally = top1_screens(c, d, k) && d % 4 == 0 && scatter_tallied(bsz, k);
+  uint32_t* tcnt =
+      tally ? (uint32_t*)c->tally_cnt.get(scatter_chunks(bsz) * k * 4) : nullptr;
+  if (tally) launch_fill_u32(c, tcnt, scatter_chunks(bsz) * k, 0);
   uint32_t* d_order[2] = {order0.u(), order1.u()};
   uint32_t* d_lab[2] = {lab0.u(), lab1.u()};
   // The epoch's label counts, tallied batch by batch by the EMA launches: the
@@ -681,11 +689,13 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
       }
       const float* cents = sph ? readout.f() : pos.f();
       const float* cn = sph ? nullptr : readout.f();
+      const LabelTally tl{tcnt, counts.u(), b};
       for (size_t c0 = b; c0 < e; c0 += chunk) {
         const size_t c1 = std::min(c0 + chunk, e);
         // After the first step the previous EMA cleared the screen's words.
         launch_top1(c, x, n, d, order, c0, c1, cents, cn, k, sph, lab, sco,
-                    step > 0 && c0 == b, nullptr, pre, keep_csplit ? &pcents : nullptr);
+                    step > 0 && c0 == b, nullptr, pre, keep_csplit ? &pcents : nullptr,
+                    tally ? &tl : nullptr);
       }
       if (refill) {  // the next check's Gumbel terms, drawn while the GPU works
         gnext = beside([&] { return gumbel_terms(split_rng, k); });
@@ -698,7 +708,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
       // scatter_add in two segments: counts, then (after the revival check's
       // mass preview, which needs only the counts) the ordered sums.
       const bool tsc = prof_take(c, EMH_PROF_SCATTER);
-      {
+      if (!tally) {
         ProfScope p(c, EMH_PROF_SCATTER, 0.0, tsc, false);
         launch_scatter_count(c, b, e, lab, k, counts.u(), true);
       }
@@ -707,12 +717,14 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
                             d_small_h + 2 * SW_WORDS, ++seq_no);
       {
         ProfScope p(c, EMH_PROF_SCATTER, scatter_bytes(e - b, k, d, true, last), tsc);
-        launch_scatter_sums(c, x, n, d, order, b, e, lab, k, sums.f(), last ? pass.f() : nullptr);
+        launch_scatter_sums(c, x, n, d, order, b, e, lab, k, sums.f(), last ? pass.f() : nullptr,
+                            tally ? counts.u() : nullptr, tcnt);
       }
       {
         ProfScope p(c, EMH_PROF_EMA, ema_bytes(k, d), prof_take(c, EMH_PROF_EMA));
         launch_ema(c, pos.f(), mass.f(), sums.f(), counts.u(), k, d, af, df, replace,
-                   sph ? nullptr : readout.f(), true, d_tally[buf], true, tsplit, tpart_e);
+                   sph ? nullptr : readout.f(), true, d_tally[buf], true, tsplit, tpart_e, tcnt,
+                   tally ? scatter_chunks(e - b) * k : 0);
         if (keep_csplit) {
           pcents.part = tpart_e;
           pcents.nparts = (int)ema_blocks(k);

@@ -157,6 +157,7 @@ struct emh_ctx {
   emh::Scratch xsplit, csplit, csplit_norm, csplit_part;  // split-operand screen: a call's rows, centroids
   emh::Scratch xpre, xpre_norm;              // a training run's rows, split once
   emh::Scratch tsplit, tsplit_part;          // a training run's centroids, kept split by the EMA
+  emh::Scratch tally_cnt;                    // a training run's label tally (chunk histograms)
   emh::Scratch preview_ticket;  // k_mass_preview's last-block ticket (left at zero)
   // Host staging of the device loop: masses, plan, flags, epoch orders and
   // epoch labels/scores (double-buffered), results.
@@ -250,11 +251,13 @@ void launch_normalize_rows(emh_ctx* c, const float* src, size_t rows, size_t d, 
 // launch_scatter_count adds into them). With csplit (norms needed), also
 // rewrites the bf16 halves (launch_halves' layout, k rows) of the rows it
 // moves and leaves the bound's centroid maxima of its ema_blocks(k) blocks in
-// cpart, as launch_halves' part does.
+// cpart, as launch_halves' part does. With zero_words, also clears
+// zero_words[0..nzero) (a tally's chunk histograms).
 void launch_ema(emh_ctx* c, float* pos, float* usage, const float* sums, const uint32_t* counts,
                 size_t k, size_t d, float alpha, float decay, int replace, float* norms = nullptr,
                 bool clear_screen_words = false, uint32_t* tally = nullptr,
-                bool zero_counts = false, void* csplit = nullptr, uint32_t* cpart = nullptr);
+                bool zero_counts = false, void* csplit = nullptr, uint32_t* cpart = nullptr,
+                uint32_t* zero_words = nullptr, size_t nzero = 0);
 size_t ema_blocks(size_t k);
 // The masses launch_ema will leave, into out (usage untouched); with
 // small_out, also a copy of the small block's words; with seq_out, then seq
@@ -289,9 +292,14 @@ void launch_scatter(emh_ctx* c, const float* x, size_t nx, size_t d, const uint3
 // them so), which saves a fill.
 void launch_scatter_count(emh_ctx* c, size_t lo, size_t hi, const uint32_t* labels, size_t k,
                           uint32_t* counts, bool counts_zero = false);
+// counts_tallied: the labels' counts and chunk histograms come from the
+// top-1 call that wrote them (LabelTally with cnt = tally_cnt), and
+// launch_scatter_count was not called; the placement then scans the counts
+// itself. Needs scatter_tallied(hi - lo, k).
 void launch_scatter_sums(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
                          size_t lo, size_t hi, const uint32_t* labels, size_t k, float* sums,
-                         float* acc);
+                         float* acc, const uint32_t* counts_tallied = nullptr,
+                         const uint32_t* tally_cnt = nullptr);
 
 // ---- emh_autok.hip (kmeans_pp and internal_scores of the automatic-k callers)
 // best[i] = max(best[i], dot(x[i], x[last])), the dot in sequence without fma.
@@ -320,6 +328,21 @@ struct SplitRows {
   const float* xn;
   size_t nx, slab;
 };
+// Positions per chunk of scatter_add's chunked counting sort.
+constexpr int TALLY_CP = 256;
+// The labels a top-1 call writes, tallied for the scatter_add of the same
+// positions that follows it (launch_scatter_sums with tallied): for each
+// labelled position p, cnt[((p - lo) / TALLY_CP) k + label] and counts[label]
+// grow by one. Both must be zero on entry (launch_ema clears them).
+struct LabelTally {
+  uint32_t* cnt;
+  uint32_t* counts;
+  size_t lo;
+};
+// Whether a scatter_add of n positions with k labels can take tallied labels
+// (the chunked path), and its chunk count.
+bool scatter_tallied(size_t n, size_t k);
+inline size_t scatter_chunks(size_t n) { return (n + TALLY_CP - 1) / TALLY_CP; }
 // Centroids split ahead of the call (launch_halves over the k centroids, or
 // launch_ema's csplit for the rows it moved), with the bound's centroid
 // maxima in nparts (max |c|^2, max cnorm) pairs.
@@ -330,13 +353,19 @@ struct SplitCents {
 };
 // pre: x's rows already split, pc: the centroids (used when the call takes
 // the split-operand screen; see split_screen).
+// tally: tally the labels (see LabelTally; the call must take the screen with
+// d % 4 == 0, where the check and the queued-row scan write every label).
 void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids, size_t lo, size_t hi,
                  const float* cents, const float* cnorm, size_t k, bool ip, uint32_t* labels,
                  float* scores, bool words_clear = false, Arena* ar = nullptr,
-                 const SplitRows* pre = nullptr, const SplitCents* pc = nullptr);
+                 const SplitRows* pre = nullptr, const SplitCents* pc = nullptr,
+                 const LabelTally* tally = nullptr);
 // Whether top-1 calls with d dimensions and k centroids take the
 // split-operand screen (k_screen4), whose rows a caller may split ahead.
 bool split_screen(emh_ctx* c, size_t d, size_t k);
+// Whether top-1 calls with d dimensions and k centroids run a screen (and so
+// the check and the queued-row scan).
+bool top1_screens(emh_ctx* c, size_t d, size_t k);
 // Split rows of x (n rows, or ids[lo..lo+n)) into bf16 halves in out,
 // slab-major, with their |x|^2 in norm; with part, each of the
 // halves_blocks(n) blocks leaves the largest |x|^2 of its rows and the

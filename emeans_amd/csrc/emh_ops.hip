@@ -165,7 +165,8 @@ __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __r
                                              uint32_t* __restrict__ tally,
                                              uint32_t* zero_counts,  // counts itself, or null
                                              char* __restrict__ csplit,
-                                             uint32_t* __restrict__ cpart) {
+                                             uint32_t* __restrict__ cpart,
+                                             uint32_t* __restrict__ zero_words, size_t nzero) {
   // EC rows of min(d, ECH) + 4 floats (norms only): the rounded squares;
   // with csplit, then as many for the values.
   extern __shared__ __attribute__((aligned(16))) float sq[];
@@ -174,6 +175,8 @@ __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __r
   const size_t j0 = (size_t)blockIdx.x * EC;
   const int nc = (int)min((size_t)EC, k - j0);
   if (clear3 && blockIdx.x == 0 && tid < 3) clear3[tid] = 0;
+  for (size_t i = (size_t)blockIdx.x * 256 + tid; i < nzero; i += (size_t)gridDim.x * 256)
+    zero_words[i] = 0;
   if (tid < nc) {
     const uint32_t cnt = counts[j0 + tid];
     if (zero_counts) zero_counts[j0 + tid] = 0;  // the same array: read above, this thread only
@@ -464,7 +467,7 @@ void launch_normalize_rows(emh_ctx* c, const float* src, size_t rows, size_t d, 
 void launch_ema(emh_ctx* c, float* pos, float* usage, const float* sums, const uint32_t* counts,
                 size_t k, size_t d, float alpha, float decay, int replace, float* norms,
                 bool clear_screen_words, uint32_t* tally, bool zero_counts, void* csplit,
-                uint32_t* cpart) {
+                uint32_t* cpart, uint32_t* zero_words, size_t nzero) {
   if (k == 0) return;
   EMH_ENSURE(!csplit || (norms && cpart), "ema: the centroid halves need the norms and maxima");
   const size_t lds = norms ? (size_t)EC * (std::min(d, (size_t)ECH) + 4) * sizeof(float) *
@@ -473,7 +476,7 @@ void launch_ema(emh_ctx* c, float* pos, float* usage, const float* sums, const u
   hipLaunchKernelGGL(k_ema, grid1(k, EC), dim3(256), lds, c->stream, pos, usage, sums, counts, k,
                      d, alpha, decay, replace, norms, clear_screen_words ? c->small : nullptr,
                      tally, zero_counts ? const_cast<uint32_t*>(counts) : nullptr,
-                     (char*)csplit, cpart);
+                     (char*)csplit, cpart, zero_words, zero_words ? nzero : 0);
   EMH_HIP(hipGetLastError());
 }
 

@@ -371,7 +371,8 @@ __global__ __launch_bounds__(256) void k_check1(
     int nrows, const float* __restrict__ cents, const float* __restrict__ cnorm, int ip,
     const Cand* __restrict__ cand, int parts, const float* __restrict__ xnorm,
     uint32_t* __restrict__ labels, float* __restrict__ scores, uint32_t* __restrict__ fb,
-    uint32_t* __restrict__ small, int bf3) {
+    uint32_t* __restrict__ small, int bf3, uint32_t* __restrict__ tcnt,
+    uint32_t* __restrict__ tcounts, size_t tlo, int tk) {
   __shared__ v4f stage[2][CSLOT * CDP4];
   __shared__ uint32_t xrow[CR];  // x row of each settled row, NONE otherwise
   __shared__ int rcnt[CR], roff[CR + 1], rset[CR];
@@ -601,6 +602,7 @@ __global__ __launch_bounds__(256) void k_check1(
     __syncthreads();
   }
   // One thread per settled row picks the exact best (ties to the lower id).
+  uint32_t mylab = NONE;
   if (tid < rows && rset[tid]) {
     const int a = roff[tid], b = roff[tid + 1];
     float bk = INFINITY;
@@ -626,6 +628,29 @@ __global__ __launch_bounds__(256) void k_check1(
     const size_t p = lo + (size_t)(r0 + tid);
     labels[p] = bid;
     scores[p] = ip ? -bk : fmaxf(rnorm[tid] + bk, 0.0f);
+    mylab = bid;
+  }
+  if (tcnt) {
+    // The tally: the block's rows lie in one chunk of TALLY_CP positions (lo
+    // - tlo is a multiple of it), so the first row of each label adds the
+    // label's rows in the block, one atomic per (block, label) on each word.
+    __shared__ uint32_t tl[CR];
+    if (tid < CR) tl[tid] = mylab;
+    __syncthreads();
+    if (tid < CR && mylab != NONE) {
+      uint32_t cntl = 0;
+      bool first = true;
+      for (int j = 0; j < CR; j++) {
+        const bool same = tl[j] == mylab;
+        cntl += same;
+        first = first && !(same && j < tid);
+      }
+      if (first) {
+        const size_t ch = (lo - tlo + (size_t)r0) / TALLY_CP;
+        atomicAdd(&tcnt[ch * (size_t)tk + mylab], cntl);
+        atomicAdd(&tcounts[mylab], cntl);
+      }
+    }
   }
 }
 
@@ -708,14 +733,18 @@ void launch_margin(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32
 void launch_verify1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
                     size_t lo, size_t n, const float* cents, const float* cnorm, size_t k, bool ip,
                     const Cand* cand, int parts, const float* xnorm, uint32_t* labels,
-                    float* scores, uint32_t* fb, bool tagged) {
+                    float* scores, uint32_t* fb, bool tagged, const LabelTally* tally) {
   const dim3 g((unsigned)((n + R1 - 1) / R1));
   // The bound follows the screen's arithmetic: 0 f32, 1 bf16, 2 bf16 with tagged keys.
   const int bf3 = c->screen == SCREEN_F32 ? 0 : tagged ? 2 : 1;
+  static_assert(TALLY_CP % CR == 0, "a check block's rows lie in one tally chunk");
+  EMH_ENSURE(!tally || (d % 4 == 0 && lo >= tally->lo && (lo - tally->lo) % TALLY_CP == 0),
+             "check: a tally needs d %% 4 == 0 and chunk-aligned positions");
   if (d % 4 == 0)
     hipLaunchKernelGGL(k_check1, dim3((unsigned)((n + CR - 1) / CR)), dim3(256), 0, c->stream, x,
                        nx, (int)d, ids, lo, (int)n, cents, cnorm, ip ? 1 : 0, cand, parts, xnorm,
-                       labels, scores, fb, c->small, bf3);
+                       labels, scores, fb, c->small, bf3, tally ? tally->cnt : nullptr,
+                       tally ? tally->counts : nullptr, tally ? tally->lo : 0, (int)k);
   else
     hipLaunchKernelGGL((k_verify<L1, R1, false, false>), g, dim3(256), 0, c->stream, x, nx,
                        (int)d, ids, lo, (int)n, cents, cnorm, (int)k, ip ? 1 : 0, 1, cand, parts,

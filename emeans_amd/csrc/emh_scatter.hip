@@ -100,7 +100,7 @@ __global__ __launch_bounds__(256) void k_count(const uint32_t* __restrict__ labe
 }
 
 // ---- chunked count and placement (k <= KCH): positions in chunks of CP.
-constexpr int CP = 256;
+constexpr int CP = TALLY_CP;
 constexpr int KCH = 8192;  // LDS histogram of one chunk
 
 // Chunk c's label histogram (LDS atomics) goes to cnt[c][0..k) and is added
@@ -235,6 +235,97 @@ __global__ __launch_bounds__(256) void k_place_sum(const uint32_t* __restrict__ 
             (uint32_t)(i + 2 < tid && q.z == l) + (uint32_t)(i + 3 < tid && q.w == l);
   }
   rid[start[l] + pre + rank] = row_of(ids, nx, (uint32_t)p, small);
+}
+
+// k_place_sum for tallied labels (the top-1 call counted them: counts and the
+// chunk histograms cnt are complete, and no k_hist_total ran): every block
+// scans the counts into start offsets in LDS itself, and block 0 also writes
+// them to start[0..k] with the list of clusters above SMALL rows, for the
+// sums that follow.
+__global__ __launch_bounds__(256) void k_place_scan(const uint32_t* __restrict__ labels,
+                                                     size_t lo, size_t hi, size_t k,
+                                                     const uint32_t* __restrict__ counts,
+                                                     const uint32_t* __restrict__ cnt,
+                                                     const uint32_t* __restrict__ ids, size_t nx,
+                                                     uint32_t* __restrict__ small,
+                                                     uint32_t* __restrict__ start,
+                                                     uint32_t* __restrict__ bigj,
+                                                     uint32_t* __restrict__ rid) {
+  __shared__ uint32_t st[KCH];
+  __shared__ uint32_t wsum[4];
+  __shared__ __attribute__((aligned(16))) uint32_t lab[CP];
+  __shared__ uint32_t nbig;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const size_t c = blockIdx.x;
+  const size_t p = lo + c * CP + tid;
+  const uint32_t l = p < hi ? labels[p] : 0xffffffffu;
+  const uint32_t row = l < k ? row_of(ids, nx, (uint32_t)p, small) : NOROW;
+  lab[tid] = l;
+  // Rows of label l in earlier chunks (loads in flight with the scan's).
+  uint32_t pre = 0;
+  if (l < k) {
+    for (size_t c0 = 0; c0 < c; c0 += 64) {
+      uint32_t v[64];
+#pragma unroll
+      for (int u = 0; u < 64; u++) v[u] = c0 + u < c ? cnt[(c0 + u) * k + l] : 0u;
+#pragma unroll
+      for (int u = 0; u < 64; u++) pre += v[u];
+    }
+  }
+  // Thread t scans the run [t per, (t + 1) per) of the counts.
+  constexpr int PERMAX = KCH / 256;
+  const size_t per = (k + 255) / 256;
+  const size_t a = min(k, (size_t)tid * per), b = min(k, a + per);
+  uint32_t tv[PERMAX];
+#pragma unroll
+  for (int u = 0; u < PERMAX; u++) tv[u] = a + u < b ? counts[a + u] : 0u;
+  uint32_t sacc = 0;
+#pragma unroll
+  for (int u = 0; u < PERMAX; u++) sacc += tv[u];
+  // Inclusive scan of the run totals: within each wave by shuffles, then
+  // the earlier waves' totals.
+  uint32_t inc = sacc;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t t = (uint32_t)__shfl_up((int)inc, o, 64);
+    if (lane >= o) inc += t;
+  }
+  if (lane == 63) wsum[w] = inc;
+  if (tid == 0) nbig = 0;
+  __syncthreads();
+  for (int i = 0; i < w; i++) inc += wsum[i];
+  uint32_t run = inc - sacc;
+#pragma unroll
+  for (int u = 0; u < PERMAX; u++) {
+    if (a + u >= b) break;
+    st[a + u] = run;
+    if (c == 0) {
+      start[a + u] = run;
+      if (tv[u] > (uint32_t)SMALL) {
+        const uint32_t i = atomicAdd(&nbig, 1u);
+        bigj[3 * i] = (uint32_t)(a + u);
+        bigj[3 * i + 1] = run;
+        bigj[3 * i + 2] = tv[u];
+      }
+    }
+    run += tv[u];
+  }
+  __syncthreads();
+  if (c == 0 && tid == 0) {
+    start[k] = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    small[SW_NBIG] = nbig;
+  }
+  if (l >= k) return;
+  uint32_t rank = 0;
+  const uint4* l4 = reinterpret_cast<const uint4*>(lab);
+#pragma unroll 8
+  for (int i4 = 0; i4 < CP / 4; i4++) {
+    const uint4 q = l4[i4];
+    const int i = 4 * i4;
+    rank += (uint32_t)(i < tid && q.x == l) + (uint32_t)(i + 1 < tid && q.y == l) +
+            (uint32_t)(i + 2 < tid && q.z == l) + (uint32_t)(i + 3 < tid && q.w == l);
+  }
+  rid[st[l] + pre + rank] = row;
 }
 
 // Stable placement: wave j walks positions lo..hi in order; positions with
@@ -465,6 +556,8 @@ static bool chunked(size_t n, size_t k) {
   return n > 0 && k <= (size_t)KCH && nch <= 256;
 }
 
+bool scatter_tallied(size_t n, size_t k) { return chunked(n, k); }
+
 void launch_scatter_count(emh_ctx* c, size_t lo, size_t hi, const uint32_t* labels, size_t k,
                           uint32_t* counts, bool counts_zero) {
   const size_t n = hi > lo ? hi - lo : 0;
@@ -494,14 +587,20 @@ void launch_scatter_count(emh_ctx* c, size_t lo, size_t hi, const uint32_t* labe
 
 void launch_scatter_sums(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
                          size_t lo, size_t hi, const uint32_t* labels, size_t k, float* sums,
-                         float* acc) {
+                         float* acc, const uint32_t* counts_tallied, const uint32_t* tally_cnt) {
   const size_t n = hi > lo ? hi - lo : 0;
   uint32_t* start = (uint32_t*)c->start.get((k + 1) * 4);
   uint32_t* rid = (uint32_t*)c->order.get(std::max<size_t>(n, 1) * 4);
   const size_t maxbig = std::min(k, n / (SMALL + 1) + 1);
   uint32_t* bigj = (uint32_t*)c->bigj.get(maxbig * 12);
   const int strips = (int)((d + BC - 1) / BC);
-  if (chunked(n, k)) {
+  if (counts_tallied) {
+    EMH_ENSURE(chunked(n, k) && tally_cnt, "scatter: tallied labels need the chunked path");
+    hipLaunchKernelGGL(k_place_scan, dim3((unsigned)scatter_chunks(n)), dim3(256), 0, c->stream,
+                       labels, lo, hi, k, counts_tallied, tally_cnt, ids, nx, c->small, start,
+                       bigj, rid);
+    EMH_HIP(hipGetLastError());
+  } else if (chunked(n, k)) {
     const size_t nch = (n + CP - 1) / CP;
     const uint32_t* cnt = (const uint32_t*)c->chunkcnt.get(nch * k * 4);
     hipLaunchKernelGGL(k_place_sum, dim3((unsigned)nch), dim3(256), 0, c->stream, labels, lo, hi,

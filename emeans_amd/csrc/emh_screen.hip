@@ -104,6 +104,7 @@ Top1Geom top1_geom(emh_ctx* c, size_t n, size_t d, size_t k, bool split) {
 }  // namespace
 
 bool split_screen(emh_ctx* c, size_t d, size_t k) { return top1_geom(c, 1, d, k, true).split; }
+bool top1_screens(emh_ctx* c, size_t d, size_t k) { return top1_geom(c, 1, d, k, false).screen; }
 
 size_t top1_scratch_bytes(emh_ctx* c, size_t n, size_t d, size_t k) {
   const Top1Geom g = top1_geom(c, n, d, k, false);
@@ -203,20 +204,22 @@ int bound_kind(emh_ctx* c, bool tagged) { return c->screen == SCREEN_F32 ? 0 : t
 void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids, size_t lo,
                  size_t hi, const float* cents, const float* cnorm, size_t k, bool ip,
                  uint32_t* labels, float* scores, bool words_clear, Arena* ar,
-                 const SplitRows* pre, const SplitCents* pc) {
+                 const SplitRows* pre, const SplitCents* pc, const LabelTally* tally) {
   if (hi <= lo) return;
   const size_t n = hi - lo;
   EMH_ENSURE(d <= 16384, "top1: d = %zu above the supported 16384", d);
   EMH_ENSURE(n < (1u << 31) && k < (1u << 31), "top1: shape too large");
   const Top1Screen s =
       screen_top1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, words_clear, ar, pre, pc);
+  EMH_ENSURE(!tally || (s.g.screen && d % 4 == 0),
+             "top1: labels are tallied only on the screen with d %% 4 == 0");
   if (!s.g.screen) {
     launch_exact1(c, x, nx, d, ids, lo, n, nullptr, cents, cnorm, k, ip, labels, scores, ar);
     return;
   }
   launch_verify1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, s.cand, s.g.parts, s.xnorm, labels,
-                 scores, s.fb, s.tagged);
-  launch_exact1(c, x, nx, d, ids, lo, n, s.fb, cents, cnorm, k, ip, labels, scores, ar);
+                 scores, s.fb, s.tagged, tally);
+  launch_exact1(c, x, nx, d, ids, lo, n, s.fb, cents, cnorm, k, ip, labels, scores, ar, tally);
 }
 
 void screen_margin_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,

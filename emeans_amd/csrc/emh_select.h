@@ -147,7 +147,8 @@ __device__ __forceinline__ void merge_parts(const Cand* c, int parts, float (&ke
 void launch_verify1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
                     size_t lo, size_t n, const float* cents, const float* cnorm, size_t k, bool ip,
                     const Cand* cand, int parts, const float* xnorm, uint32_t* labels,
-                    float* scores, uint32_t* fb, bool tagged = false);
+                    float* scores, uint32_t* fb, bool tagged = false,
+                    const LabelTally* tally = nullptr);
 void launch_verifyk(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,
                     size_t kk, const Cand* cand, int parts, const float* xnorm, uint32_t* ids,
                     float* sims, uint32_t* fb);
@@ -166,7 +167,7 @@ void launch_margin(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32
 void launch_exact1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
                    size_t lo, size_t n, const uint32_t* list, const float* cents,
                    const float* cnorm, size_t k, bool ip, uint32_t* labels, float* scores,
-                   Arena* ar = nullptr);
+                   Arena* ar = nullptr, const LabelTally* tally = nullptr);
 // Fixed-block bytes launch_exact1 takes for n rows (an upper bound).
 size_t exact1_scratch_bytes(size_t n, size_t d, size_t k, bool list);
 void launch_exactk(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,

@@ -336,7 +336,8 @@ __global__ __launch_bounds__(64) void k_queued1(
     const uint32_t* __restrict__ list, uint32_t* __restrict__ small,
     const float* __restrict__ cents, const float* __restrict__ cnorm, int k, int ip,
     unsigned long long* __restrict__ best, uint32_t* __restrict__ tickets,
-    float* __restrict__ xnq, uint32_t* __restrict__ labels, float* __restrict__ scores) {
+    float* __restrict__ xnq, uint32_t* __restrict__ labels, float* __restrict__ scores,
+    uint32_t* __restrict__ tcnt, uint32_t* __restrict__ tcounts, size_t tlo) {
   typedef float v4f __attribute__((ext_vector_type(4)));
   __shared__ v4f cs[QU * QJ];
   __shared__ v4f xs[QU * QR];
@@ -444,6 +445,10 @@ __global__ __launch_bounds__(64) void k_queued1(
           const size_t p = list[f];
           labels[p] = bid;
           scores[p] = ip ? -bk : fmaxf(xnq[f] + bk, 0.0f);
+          if (tcnt) {  // the tally (few rows: one atomic each)
+            atomicAdd(&tcnt[((p - tlo) / TALLY_CP) * (size_t)k + bid], 1u);
+            atomicAdd(&tcounts[bid], 1u);
+          }
         }
       }
       if (lane == 0) tickets[g] = 0;
@@ -589,8 +594,9 @@ size_t exact1_scratch_bytes(size_t n, size_t d, size_t k, bool list) {
 void launch_exact1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
                    size_t lo, size_t n, const uint32_t* list, const float* cents,
                    const float* cnorm, size_t k, bool ip, uint32_t* labels, float* scores,
-                   Arena* ar) {
+                   Arena* ar, const LabelTally* tally) {
   if (n == 0) return;
+  EMH_ENSURE(!tally || (list && d % 4 == 0), "exact: a tally needs the queued-row scan");
   // Both kernels read row 0 in place of a row whose id is out of range.
   EMH_ENSURE(nx > 0, "top1: a selection of %zu rows over no data rows", n);
   if (list && d % 4 == 0) {  // queued rows, few: the latency-bound scan
@@ -611,7 +617,9 @@ void launch_exact1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32
     const unsigned g = (unsigned)std::min<size_t>(ngr * per, (size_t)2 * c->cus);
     hipLaunchKernelGGL(k_queued1, dim3(g), dim3(64), 0, c->stream, x, nx, (int)d, ids, list,
                        c->small, cents, cnorm, (int)k, ip ? 1 : 0, (unsigned long long*)z,
-                       (uint32_t*)(z + n * 8), xnq, labels, scores);
+                       (uint32_t*)(z + n * 8), xnq, labels, scores,
+                       tally ? tally->cnt : nullptr, tally ? tally->counts : nullptr,
+                       tally ? tally->lo : 0);
     EMH_HIP(hipGetLastError());
     return;
   }
