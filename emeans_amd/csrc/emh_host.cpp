@@ -573,9 +573,9 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   // histograms of the counting sort), so scatter_add needs no count launch;
   // the EMA clears both for the next batch.
   const bool tally = top1_screens(c, d, k) && d % 4 == 0 && scatter_tallied(bsz, k);
-  uint32_t* tcnt =
-      tally ? (uint32_t*)c->tally_cnt.get(scatter_chunks(bsz) * k * 4) : nullptr;
-  if (tally) launch_fill_u32(c, tcnt, scatter_chunks(bsz) * k, 0);
+  const size_t tstride = tally_stride(bsz);
+  uint32_t* tcnt = tally ? (uint32_t*)c->tally_cnt.get(tstride * k * 4) : nullptr;
+  if (tally) launch_fill_u32(c, tcnt, tstride * k, 0);
   uint32_t* d_order[2] = {order0.u(), order1.u()};
   uint32_t* d_lab[2] = {lab0.u(), lab1.u()};
   // The epoch's label counts, tallied batch by batch by the EMA launches: the
@@ -689,7 +689,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
       }
       const float* cents = sph ? readout.f() : pos.f();
       const float* cn = sph ? nullptr : readout.f();
-      const LabelTally tl{tcnt, counts.u(), b};
+      const LabelTally tl{tcnt, counts.u(), b, tstride};
       for (size_t c0 = b; c0 < e; c0 += chunk) {
         const size_t c1 = std::min(c0 + chunk, e);
         // After the first step the previous EMA cleared the screen's words.
@@ -718,13 +718,13 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
       {
         ProfScope p(c, EMH_PROF_SCATTER, scatter_bytes(e - b, k, d, true, last), tsc);
         launch_scatter_sums(c, x, n, d, order, b, e, lab, k, sums.f(), last ? pass.f() : nullptr,
-                            tally ? counts.u() : nullptr, tcnt);
+                            tally ? counts.u() : nullptr, tcnt, tstride);
       }
       {
         ProfScope p(c, EMH_PROF_EMA, ema_bytes(k, d), prof_take(c, EMH_PROF_EMA));
         launch_ema(c, pos.f(), mass.f(), sums.f(), counts.u(), k, d, af, df, replace,
                    sph ? nullptr : readout.f(), true, d_tally[buf], true, tsplit, tpart_e, tcnt,
-                   tally ? scatter_chunks(e - b) * k : 0);
+                   tally ? tstride * k : 0);
         if (keep_csplit) {
           pcents.part = tpart_e;
           pcents.nparts = (int)ema_blocks(k);

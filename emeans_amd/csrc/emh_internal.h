@@ -293,13 +293,14 @@ void launch_scatter(emh_ctx* c, const float* x, size_t nx, size_t d, const uint3
 void launch_scatter_count(emh_ctx* c, size_t lo, size_t hi, const uint32_t* labels, size_t k,
                           uint32_t* counts, bool counts_zero = false);
 // counts_tallied: the labels' counts and chunk histograms come from the
-// top-1 call that wrote them (LabelTally with cnt = tally_cnt), and
+// top-1 call that wrote them (LabelTally with cnt = tally_cnt, stride =
+// tally_stride), and
 // launch_scatter_count was not called; the placement then scans the counts
 // itself. Needs scatter_tallied(hi - lo, k).
 void launch_scatter_sums(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
                          size_t lo, size_t hi, const uint32_t* labels, size_t k, float* sums,
                          float* acc, const uint32_t* counts_tallied = nullptr,
-                         const uint32_t* tally_cnt = nullptr);
+                         const uint32_t* tally_cnt = nullptr, size_t tally_stride = 0);
 
 // ---- emh_autok.hip (kmeans_pp and internal_scores of the automatic-k callers)
 // best[i] = max(best[i], dot(x[i], x[last])), the dot in sequence without fma.
@@ -332,17 +333,21 @@ struct SplitRows {
 constexpr int TALLY_CP = 256;
 // The labels a top-1 call writes, tallied for the scatter_add of the same
 // positions that follows it (launch_scatter_sums with tallied): for each
-// labelled position p, cnt[((p - lo) / TALLY_CP) k + label] and counts[label]
-// grow by one. Both must be zero on entry (launch_ema clears them).
+// labelled position p, cnt[label stride + (p - lo) / TALLY_CP] and
+// counts[label] grow by one (label-major chunk histograms: a label's chunks
+// are contiguous, stride = tally_stride(positions)). Both must be zero on
+// entry (launch_ema clears them), and every position must get a label (ids
+// in range).
 struct LabelTally {
   uint32_t* cnt;
   uint32_t* counts;
-  size_t lo;
+  size_t lo, stride;
 };
 // Whether a scatter_add of n positions with k labels can take tallied labels
 // (the chunked path), and its chunk count.
 bool scatter_tallied(size_t n, size_t k);
 inline size_t scatter_chunks(size_t n) { return (n + TALLY_CP - 1) / TALLY_CP; }
+inline size_t tally_stride(size_t n) { return (scatter_chunks(n) + 3) & ~(size_t)3; }
 // Centroids split ahead of the call (launch_halves over the k centroids, or
 // launch_ema's csplit for the rows it moved), with the bound's centroid
 // maxima in nparts (max |c|^2, max cnorm) pairs.

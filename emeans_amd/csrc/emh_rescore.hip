@@ -372,7 +372,7 @@ __global__ __launch_bounds__(256) void k_check1(
     const Cand* __restrict__ cand, int parts, const float* __restrict__ xnorm,
     uint32_t* __restrict__ labels, float* __restrict__ scores, uint32_t* __restrict__ fb,
     uint32_t* __restrict__ small, int bf3, uint32_t* __restrict__ tcnt,
-    uint32_t* __restrict__ tcounts, size_t tlo, int tk) {
+    uint32_t* __restrict__ tcounts, size_t tlo, size_t tstride) {
   __shared__ v4f stage[2][CSLOT * CDP4];
   __shared__ uint32_t xrow[CR];  // x row of each settled row, NONE otherwise
   __shared__ int rcnt[CR], roff[CR + 1], rset[CR];
@@ -647,7 +647,7 @@ __global__ __launch_bounds__(256) void k_check1(
       }
       if (first) {
         const size_t ch = (lo - tlo + (size_t)r0) / TALLY_CP;
-        atomicAdd(&tcnt[ch * (size_t)tk + mylab], cntl);
+        atomicAdd(&tcnt[(size_t)mylab * tstride + ch], cntl);
         atomicAdd(&tcounts[mylab], cntl);
       }
     }
@@ -744,7 +744,8 @@ void launch_verify1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint3
     hipLaunchKernelGGL(k_check1, dim3((unsigned)((n + CR - 1) / CR)), dim3(256), 0, c->stream, x,
                        nx, (int)d, ids, lo, (int)n, cents, cnorm, ip ? 1 : 0, cand, parts, xnorm,
                        labels, scores, fb, c->small, bf3, tally ? tally->cnt : nullptr,
-                       tally ? tally->counts : nullptr, tally ? tally->lo : 0, (int)k);
+                       tally ? tally->counts : nullptr, tally ? tally->lo : 0,
+                       tally ? tally->stride : 0);
   else
     hipLaunchKernelGGL((k_verify<L1, R1, false, false>), g, dim3(256), 0, c->stream, x, nx,
                        (int)d, ids, lo, (int)n, cents, cnorm, (int)k, ip ? 1 : 0, 1, cand, parts,

@@ -238,7 +238,8 @@ __global__ __launch_bounds__(256) void k_place_sum(const uint32_t* __restrict__ 
 }
 
 // k_place_sum for tallied labels (the top-1 call counted them: counts and the
-// chunk histograms cnt are complete, and no k_hist_total ran): every block
+// label-major chunk histograms cnt[label stride + chunk] are complete, and no
+// k_hist_total ran; a label's earlier chunks are one contiguous run): every block
 // scans the counts into start offsets in LDS itself, and block 0 also writes
 // them to start[0..k] with the list of clusters above SMALL rows, for the
 // sums that follow.
@@ -246,6 +247,7 @@ __global__ __launch_bounds__(256) void k_place_scan(const uint32_t* __restrict__
                                                      size_t lo, size_t hi, size_t k,
                                                      const uint32_t* __restrict__ counts,
                                                      const uint32_t* __restrict__ cnt,
+                                                     size_t stride,
                                                      const uint32_t* __restrict__ ids, size_t nx,
                                                      uint32_t* __restrict__ small,
                                                      uint32_t* __restrict__ start,
@@ -261,15 +263,22 @@ __global__ __launch_bounds__(256) void k_place_scan(const uint32_t* __restrict__
   const uint32_t l = p < hi ? labels[p] : 0xffffffffu;
   const uint32_t row = l < k ? row_of(ids, nx, (uint32_t)p, small) : NOROW;
   lab[tid] = l;
-  // Rows of label l in earlier chunks (loads in flight with the scan's).
+  // Rows of label l in earlier chunks: 16-byte loads of the label's run
+  // (stride is a multiple of 4), in flight with the scan's.
   uint32_t pre = 0;
   if (l < k) {
-    for (size_t c0 = 0; c0 < c; c0 += 64) {
-      uint32_t v[64];
+    const uint4* run4 = reinterpret_cast<const uint4*>(cnt + (size_t)l * stride);
+    const int n4 = (int)((c + 3) >> 2);
+    for (int q0 = 0; q0 < n4; q0 += 16) {
+      uint4 v[16];
 #pragma unroll
-      for (int u = 0; u < 64; u++) v[u] = c0 + u < c ? cnt[(c0 + u) * k + l] : 0u;
+      for (int u = 0; u < 16; u++) v[u] = q0 + u < n4 ? run4[q0 + u] : make_uint4(0, 0, 0, 0);
 #pragma unroll
-      for (int u = 0; u < 64; u++) pre += v[u];
+      for (int u = 0; u < 16; u++) {
+        const size_t e = 4 * (size_t)(q0 + u);
+        pre += (e < c ? v[u].x : 0u) + (e + 1 < c ? v[u].y : 0u) + (e + 2 < c ? v[u].z : 0u) +
+               (e + 3 < c ? v[u].w : 0u);
+      }
     }
   }
   // Thread t scans the run [t per, (t + 1) per) of the counts.
@@ -587,7 +596,8 @@ void launch_scatter_count(emh_ctx* c, size_t lo, size_t hi, const uint32_t* labe
 
 void launch_scatter_sums(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
                          size_t lo, size_t hi, const uint32_t* labels, size_t k, float* sums,
-                         float* acc, const uint32_t* counts_tallied, const uint32_t* tally_cnt) {
+                         float* acc, const uint32_t* counts_tallied, const uint32_t* tally_cnt,
+                         size_t tally_stride) {
   const size_t n = hi > lo ? hi - lo : 0;
   uint32_t* start = (uint32_t*)c->start.get((k + 1) * 4);
   uint32_t* rid = (uint32_t*)c->order.get(std::max<size_t>(n, 1) * 4);
@@ -595,10 +605,12 @@ void launch_scatter_sums(emh_ctx* c, const float* x, size_t nx, size_t d, const 
   uint32_t* bigj = (uint32_t*)c->bigj.get(maxbig * 12);
   const int strips = (int)((d + BC - 1) / BC);
   if (counts_tallied) {
-    EMH_ENSURE(chunked(n, k) && tally_cnt, "scatter: tallied labels need the chunked path");
+    EMH_ENSURE(chunked(n, k) && tally_cnt && tally_stride % 4 == 0 &&
+                   tally_stride >= scatter_chunks(n),
+               "scatter: tallied labels need the chunked path");
     hipLaunchKernelGGL(k_place_scan, dim3((unsigned)scatter_chunks(n)), dim3(256), 0, c->stream,
-                       labels, lo, hi, k, counts_tallied, tally_cnt, ids, nx, c->small, start,
-                       bigj, rid);
+                       labels, lo, hi, k, counts_tallied, tally_cnt, tally_stride, ids, nx,
+                       c->small, start, bigj, rid);
     EMH_HIP(hipGetLastError());
   } else if (chunked(n, k)) {
     const size_t nch = (n + CP - 1) / CP;

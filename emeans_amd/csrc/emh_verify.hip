@@ -337,7 +337,7 @@ __global__ __launch_bounds__(64) void k_queued1(
     const float* __restrict__ cents, const float* __restrict__ cnorm, int k, int ip,
     unsigned long long* __restrict__ best, uint32_t* __restrict__ tickets,
     float* __restrict__ xnq, uint32_t* __restrict__ labels, float* __restrict__ scores,
-    uint32_t* __restrict__ tcnt, uint32_t* __restrict__ tcounts, size_t tlo) {
+    uint32_t* __restrict__ tcnt, uint32_t* __restrict__ tcounts, size_t tlo, size_t tstride) {
   typedef float v4f __attribute__((ext_vector_type(4)));
   __shared__ v4f cs[QU * QJ];
   __shared__ v4f xs[QU * QR];
@@ -446,7 +446,7 @@ __global__ __launch_bounds__(64) void k_queued1(
           labels[p] = bid;
           scores[p] = ip ? -bk : fmaxf(xnq[f] + bk, 0.0f);
           if (tcnt) {  // the tally (few rows: one atomic each)
-            atomicAdd(&tcnt[((p - tlo) / TALLY_CP) * (size_t)k + bid], 1u);
+            atomicAdd(&tcnt[(size_t)bid * tstride + (p - tlo) / TALLY_CP], 1u);
             atomicAdd(&tcounts[bid], 1u);
           }
         }
@@ -619,7 +619,7 @@ void launch_exact1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32
                        c->small, cents, cnorm, (int)k, ip ? 1 : 0, (unsigned long long*)z,
                        (uint32_t*)(z + n * 8), xnq, labels, scores,
                        tally ? tally->cnt : nullptr, tally ? tally->counts : nullptr,
-                       tally ? tally->lo : 0);
+                       tally ? tally->lo : 0, tally ? tally->stride : 0);
     EMH_HIP(hipGetLastError());
     return;
   }
