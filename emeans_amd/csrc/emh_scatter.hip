@@ -455,56 +455,85 @@ __device__ __forceinline__ void sum_rows(const float* __restrict__ x, size_t d,
 
 // Clusters with more than SMALL rows (listed as (cluster, offset of its
 // positions in rid, count) by the count kernels): workgroup = (listed
-// cluster bi, strip of BC columns). Chunks of BR rows are double-buffered in
-// LDS, column-major (stride BRP) so that a column's lane reads four rows per
-// LDS load; thread t loads column t % BC of rows t / BC + (BT / BC) u.
-constexpr int BRP = BR + 4;  // column stride in LDS: 4-row reads stay aligned, stores 2-way
+// cluster bi, strip of BC columns). Lane c < BC of wave 0 adds column c's
+// rows in order, four per LDS read, from column-major chunks of BR rows
+// (stride BRP) double-buffered in LDS; thread t loads rows RPT (t / BC) ..
+// + RPT - 1 of each chunk in column t % BC. The loads run ahead of the adds
+// in a software pipeline, so that the long chain of a large cluster waits on
+// its adds rather than on memory: at step ch the values of chunk ch + 3 are
+// loaded into one of three register sets (their row ids read from LDS), the
+// values of chunk ch + 1 (loaded two steps before) go to LDS, and wave 0 adds
+// chunk ch. Row ids come in blocks of IDB, loaded into registers one block
+// ahead and stored to LDS four steps before their first use.
+constexpr int BRP = BR + 4;          // column stride in LDS: 4-row accesses stay aligned
+constexpr int RPT = BR * BC / BT;    // rows loaded per thread per chunk (16)
+constexpr int IDB = 512;             // row ids per LDS block (four chunks)
+constexpr int IDT = IDB / BT;        // ids loaded per thread per block
+static_assert(IDB == 4 * BR && IDB % BT == 0 && RPT % 4 == 0, "pipeline shape");
 __device__ __forceinline__ void sum_big(int bi, int strip, const float* __restrict__ x, size_t d,
                                         const uint32_t* __restrict__ rid,
                                         const uint32_t* __restrict__ bigj,
                                         float* __restrict__ sums, float* __restrict__ acc,
-                                        float (*vals)[BC * BRP], uint32_t (*rows)[BR]) {
-  constexpr int RPT = BR * BC / BT;  // rows loaded per thread per chunk
-  constexpr int RS = BT / BC;        // row stride between a thread's loads
+                                        float (*vals)[BC * BRP], uint32_t (*idl)[IDB]) {
   const uint32_t j = bigj[3 * bi], b = bigj[3 * bi + 1], cnt = bigj[3 * bi + 2];
-  const int tid = threadIdx.x, c = tid % BC, r0 = tid / BC;
+  const int tid = threadIdx.x, c = tid % BC, g = tid / BC;
   const size_t col = (size_t)strip * BC + c;
   const bool colok = col < d;
-  const uint32_t nchunks = (cnt + BR - 1) / BR;
-  auto stage = [&](uint32_t ch, int buf) {  // row ids of chunk ch
-    const uint32_t i = ch * BR + tid;
-    if (tid < BR) rows[buf][tid] = i < cnt ? rid[b + i] : NOROW;
-  };
-  float v[RPT];
-  auto gload = [&](int buf) {
+  const float* xc = x + (colok ? col : 0);
+  const uint32_t nch = (cnt + BR - 1) / BR;
+  const uint32_t nblk = (cnt + IDB - 1) / IDB;
+  uint32_t inext[IDT];
+  // Loads are unconditional and nothing reads their results before the
+  // step that needs them (ids past the cluster, and rows that add nothing,
+  // are masked when stored), so that the compiler's waits come only where
+  // the values are used.
+  auto id_load = [&](uint32_t m) {
 #pragma unroll
-    for (int u = 0; u < RPT; u++) {
-      const uint32_t r = rows[buf][r0 + RS * u];
-      v[u] = (r != NOROW && colok) ? x[(size_t)r * d + col] : 0.0f;
+    for (int e = 0; e < IDT; e++) inext[e] = rid[b + min(m * IDB + tid + BT * e, cnt - 1)];
+  };
+  auto id_store = [&](uint32_t m) {
+#pragma unroll
+    for (int e = 0; e < IDT; e++) {
+      const uint32_t i = m * IDB + tid + BT * e;
+      idl[m & 1][tid + BT * e] = m < nblk && i < cnt ? inext[e] : NOROW;
     }
   };
-  auto lstore = [&](int buf) {
+  float v0[RPT], v1[RPT], v2[RPT];
+  auto dload = [&](uint32_t ch, float (&v)[RPT]) -> uint32_t {  // returns the rows' mask
+    const uint32_t* il = idl[(ch / 4) & 1] + (ch % 4) * BR + g * RPT;
+    const bool live = ch < nch;
+    uint32_t mk = 0;
 #pragma unroll
-    for (int u = 0; u < RPT; u++) vals[buf][c * BRP + r0 + RS * u] = v[u];
+    for (int u = 0; u < RPT; u++) {
+      const uint32_t ri = il[u];
+      const bool ok = live && ri != NOROW && colok;
+      v[u] = xc[(size_t)(ok ? ri : 0u) * d];
+      mk |= (uint32_t)ok << u;
+    }
+    return mk;
   };
-  stage(0, 0);
-  __syncthreads();
-  gload(0);
-  lstore(0);
-  if (nchunks > 1) stage(1, 1);
-  __syncthreads();
-  float s = 0.0f;
-  for (uint32_t ch = 0; ch < nchunks; ch++) {
-    const int cur = ch & 1, nxt = cur ^ 1;
-    if (ch + 1 < nchunks) gload(nxt);  // in flight while the current chunk is added
-    if (tid < BC) {  // rows in order; 32 rows of LDS reads in flight
-      const uint32_t len = min((uint32_t)BR, cnt - ch * BR);
-      const float* vc = vals[cur] + tid * BRP;
-      uint32_t i = 0;
-      for (; i + 32 <= len; i += 32) {
-        float4 q[8];
+  auto dstore = [&](uint32_t ch, const float (&v)[RPT], uint32_t mk) {
+    if (ch >= nch) return;
+    float* vb = vals[ch & 1] + c * BRP + g * RPT;
+    auto m = [&](int u) { return (mk >> u) & 1u ? v[u] : 0.0f; };
 #pragma unroll
-        for (int u = 0; u < 8; u++) q[u] = *reinterpret_cast<const float4*>(vc + i + 4 * u);
+    for (int u = 0; u < RPT; u += 4)
+      *reinterpret_cast<float4*>(vb + u) = make_float4(m(u), m(u + 1), m(u + 2), m(u + 3));
+  };
+  float s = 0.0f;
+  auto add = [&](uint32_t ch) {
+    if (tid >= BC || ch >= nch) return;
+    const uint32_t len = min((uint32_t)BR, cnt - ch * BR);
+    const float* vc = vals[ch & 1] + tid * BRP;
+    uint32_t i = 0;
+    if (len >= 32) {  // the next 32 rows' LDS reads in flight while 32 are added
+      float4 q[8], nq[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) q[u] = *reinterpret_cast<const float4*>(vc + 4 * u);
+      for (; i + 32 <= len; i += 32) {
+        const uint32_t in = i + 64 <= len ? i + 32 : i;  // the last group reloads itself
+#pragma unroll
+        for (int u = 0; u < 8; u++) nq[u] = *reinterpret_cast<const float4*>(vc + in + 4 * u);
 #pragma unroll
         for (int u = 0; u < 8; u++) {
           s = s + q[u].x;
@@ -512,13 +541,39 @@ __device__ __forceinline__ void sum_big(int bi, int strip, const float* __restri
           s = s + q[u].z;
           s = s + q[u].w;
         }
+#pragma unroll
+        for (int u = 0; u < 8; u++) q[u] = nq[u];
       }
-      for (; i < len; i++) s = s + vc[i];
     }
-    __syncthreads();  // the current chunk's values and row ids are consumed
-    if (ch + 1 < nchunks) lstore(nxt);
-    if (ch + 2 < nchunks) stage(ch + 2, cur);
+    for (; i < len; i++) s = s + vc[i];
+  };
+  // One step of the pipeline (see above); VL holds chunk ch + 3's loads,
+  // VS chunk ch + 1's values.
+  auto step = [&](uint32_t ch, float (&VL)[RPT], uint32_t& ML, const float (&VS)[RPT],
+                  uint32_t MS) __attribute__((always_inline)) {
+    ML = dload(ch + 3, VL);
+    add(ch);
+    __syncthreads();  // chunk ch - 1's buffer is free; chunk ch + 3's ids were read
+    dstore(ch + 1, VS, MS);
+    if (ch % 4 == 0) {  // block ch / 4 + 1's ids to LDS (its first chunk loads next step)
+      id_store(ch / 4 + 1);
+      id_load(ch / 4 + 2);
+    }
     __syncthreads();
+  };
+  // Prologue: id block 0 in LDS, block 1 in registers; chunks 0-2 loaded,
+  // chunk 0 stored.
+  id_load(0);
+  id_store(0);
+  id_load(1);
+  __syncthreads();
+  uint32_t m0 = dload(0, v0), m1 = dload(1, v1), m2 = dload(2, v2);
+  dstore(0, v0, m0);
+  __syncthreads();
+  for (uint32_t ch = 0; ch < nch; ch += 3) {
+    step(ch, v0, m0, v1, m1);
+    step(ch + 1, v1, m1, v2, m2);
+    step(ch + 2, v2, m2, v0, m0);
   }
   if (tid < BC && colok) {
     sums[(size_t)j * d + col] = s;
@@ -540,20 +595,20 @@ __global__ __launch_bounds__(BT) void k_sums(const float* __restrict__ x, size_t
                                              float* __restrict__ acc,
                                              uint32_t* __restrict__ small) {
   __shared__ __attribute__((aligned(16))) float vals[2][BC * BRP];
-  __shared__ uint32_t rows[2][BR];
-  static_assert(BR >= SMALL, "the small path's rows fit one row-id buffer");
+  __shared__ uint32_t idl[2][IDB];
+  static_assert(IDB >= SMALL, "the small path's rows fit one row-id buffer");
   if ((int)blockIdx.x < nbb) {
     const int bi = blockIdx.x / strips, strip = blockIdx.x % strips;
     if (bi >= (int)small[SW_NBIG]) return;
-    sum_big(bi, strip, x, d, rid, bigj, sums, acc, vals, rows);
+    sum_big(bi, strip, x, d, rid, bigj, sums, acc, vals, idl);
     return;
   }
   const size_t j = blockIdx.x - nbb;
   const uint32_t b = start[j], cnt = start[j + 1] - b;
   if (cnt > (uint32_t)SMALL) return;  // a large cluster: done above
-  if (threadIdx.x < cnt) rows[0][threadIdx.x] = rid[b + threadIdx.x];
+  if (threadIdx.x < cnt) idl[0][threadIdx.x] = rid[b + threadIdx.x];
   __syncthreads();
-  sum_rows<VEC4>(x, d, rows[0], cnt, j, sums, acc);
+  sum_rows<VEC4>(x, d, idl[0], cnt, j, sums, acc);
 }
 
 }  // namespace
