@@ -35,6 +35,7 @@ constexpr int SU = 32;      // row loads in flight per thread on that path
 constexpr int BR = 128;     // rows per chunk on the large-cluster path
 constexpr int BC = 32;      // columns per large-cluster workgroup
 constexpr int BT = 256;     // threads per large-cluster workgroup (BT / BC per column)
+constexpr int BIG_SLOTS = 32;  // large-cluster workgroup slots per strip
 
 // Counts, then (last workgroup) exclusive scan into start[0..k] and the list
 // of clusters with more than SMALL rows.
@@ -395,11 +396,12 @@ __global__ __launch_bounds__(64 * PW) void k_place(const uint32_t* __restrict__ 
   }
 }
 
-// Cluster j's sum of the rows rows[0..cnt) (LDS, in order; NOROW adds
-// nothing) into sums[j] (and acc[j] += it), by the workgroup's 256 threads.
-// With VEC4 a thread adds four columns (16-byte loads, SU4 rows in flight),
-// else one column (SU rows in flight).
-constexpr int SU4 = 32;
+// Cluster j's sum of the rows rows[0..cnt) (in order; NOROW adds nothing)
+// into sums[j] (and acc[j] += it), by the workgroup's 256 threads. rows is
+// the cluster's run of the placement (global memory, read at uniform
+// addresses: scalar loads, no staging). With VEC4 a thread adds four columns
+// (16-byte loads, SU4 rows in flight), else one column (SU rows in flight).
+constexpr int SU4 = 16;
 template <bool VEC4>
 __device__ __forceinline__ void sum_rows(const float* __restrict__ x, size_t d,
                                          const uint32_t* rows, uint32_t cnt, size_t j,
@@ -596,19 +598,18 @@ __global__ __launch_bounds__(BT) void k_sums(const float* __restrict__ x, size_t
                                              uint32_t* __restrict__ small) {
   __shared__ __attribute__((aligned(16))) float vals[2][BC * BRP];
   __shared__ uint32_t idl[2][IDB];
-  static_assert(IDB >= SMALL, "the small path's rows fit one row-id buffer");
   if ((int)blockIdx.x < nbb) {
-    const int bi = blockIdx.x / strips, strip = blockIdx.x % strips;
-    if (bi >= (int)small[SW_NBIG]) return;
-    sum_big(bi, strip, x, d, rid, bigj, sums, acc, vals, idl);
+    // Slot slot of nslots takes listed clusters slot, slot + nslots, ...
+    const int slot = blockIdx.x / strips, strip = blockIdx.x % strips, nslots = nbb / strips;
+    const int nbig = (int)small[SW_NBIG];
+    for (int bi = slot; bi < nbig; bi += nslots)
+      sum_big(bi, strip, x, d, rid, bigj, sums, acc, vals, idl);
     return;
   }
   const size_t j = blockIdx.x - nbb;
   const uint32_t b = start[j], cnt = start[j + 1] - b;
   if (cnt > (uint32_t)SMALL) return;  // a large cluster: done above
-  if (threadIdx.x < cnt) idl[0][threadIdx.x] = rid[b + threadIdx.x];
-  __syncthreads();
-  sum_rows<VEC4>(x, d, idl[0], cnt, j, sums, acc);
+  sum_rows<VEC4>(x, d, rid + b, cnt, j, sums, acc);
 }
 
 }  // namespace
@@ -678,7 +679,10 @@ void launch_scatter_sums(emh_ctx* c, const float* x, size_t nx, size_t d, const 
                        start, ids, nx, c->small, rid);
     EMH_HIP(hipGetLastError());
   }
-  const int nbb = n > (size_t)SMALL ? (int)(maxbig * strips) : 0;
+  // Workgroups for the large clusters: up to BIG_SLOTS slots of `strips`
+  // each (a slot takes every BIG_SLOTS-th listed cluster), so that few
+  // workgroups start only to find no cluster.
+  const int nbb = n > (size_t)SMALL ? (int)(std::min(maxbig, (size_t)BIG_SLOTS) * strips) : 0;
   auto kern = d % 4 == 0 ? k_sums<true> : k_sums<false>;
   hipLaunchKernelGGL(kern, dim3((unsigned)(nbb + k)), dim3(BT), 0, c->stream, x, nx, d, rid, start,
                      k, bigj, strips, nbb, sums, acc, c->small);
