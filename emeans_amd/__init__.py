@@ -379,6 +379,16 @@ def _epoch_rows(n, cfg):
     return [int(r) for r in rows[:ne.value]]
 
 
+def recipe_batch(n, cfg) -> int:
+    """Recipe::resolve's batch size for n rows (emh_host_recipe, no device)."""
+    b, a0, ne, tot = C.c_uint64(), C.c_double(), C.c_uint64(), C.c_uint64()
+    rows = np.zeros(64, np.uint64)
+    ccfg = cfg._c()
+    check(lib().emh_host_recipe(n, C.byref(ccfg), C.byref(b), C.byref(a0), _p(rows), 64,
+                                C.byref(ne), C.byref(tot)))
+    return int(b.value)
+
+
 class Backend:
     """The backend names of this package, as emeans_cluster::Backend gives
     them (backend.rs:41-102): NAMES lists what from_str accepts for help

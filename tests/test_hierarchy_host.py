@@ -1,0 +1,96 @@
+"""The hierarchy's host rules (emeans_amd.hierarchy) against the reference's
+own known-answer tests: leaf_floors (auto.rs:1313-1336,
+floors_flag_stragglers_not_a_fixed_share), the Hungarian matching and stable
+ids (incremental.rs:1079-1130, hungarian_finds_the_optimum,
+matching_keeps_ids_under_permutation); plus quantile against its definition
+(metrics.rs:271-279) and unit means against f64 brute force."""
+
+import itertools
+
+import numpy as np
+
+from emeans_amd import hierarchy as H
+
+
+def test_floors_flag_stragglers_not_a_fixed_share():
+    inc = H.IncrementalConfig()
+    clean = np.array([np.float32(0.88) + np.float32(0.0002) * np.float32(i) for i in range(200)],
+                     np.float32)
+    small = [np.float32(0.90) + np.float32(0.002) * np.float32(i) for i in range(9)]
+    small = np.array(small + [np.float32(0.55)], np.float32)
+    sims = [clean, small, np.zeros(0, np.float32)]
+    f = H.leaf_floors(sims, inc)
+    flagged = lambda v, fl: int(np.sum(v < fl))
+    assert flagged(clean, f[0]) == 0, "a clean leaf flags no row"
+    assert flagged(small, f[1]) == 1, "a small leaf flags its straggler"
+    assert 0.55 < f[1] < 0.90
+    assert np.isfinite(f[2]), "an empty leaf still has a floor"
+    absf = H.IncrementalConfig(outlier_min_sim=0.5)
+    assert [float(v) for v in H.leaf_floors(sims, absf)] == [0.5] * 3
+    same = [np.full(30, np.float32(0.9), np.float32)]
+    assert flagged(same[0], H.leaf_floors(same, inc)[0]) == 0
+
+
+def test_hungarian_finds_the_optimum():
+    c = [[7.0, 3.0, 9.0, 1.0, 4.0],
+         [2.0, 8.0, 6.0, 5.0, 3.0],
+         [4.0, 4.0, 2.0, 7.0, 9.0],
+         [6.0, 1.0, 3.0, 8.0, 2.0],
+         [5.0, 7.0, 4.0, 2.0, 6.0]]
+    a = H.hungarian(c)
+    total = sum(c[i][j] for i, j in enumerate(a))
+    best = min(sum(c[i][p[i]] for i in range(5)) for p in itertools.permutations(range(5)))
+    assert total == best
+    assert sorted(a) == list(range(5))
+
+
+def test_hungarian_rectangular_matches_brute_force():
+    rng = np.random.default_rng(4)
+    for _ in range(20):
+        n, m = 3, 5
+        c = rng.integers(0, 20, size=(n, m)).astype(float).tolist()
+        a = H.hungarian(c)
+        assert len(set(a)) == n
+        total = sum(c[i][j] for i, j in enumerate(a))
+        best = min(sum(c[i][p[i]] for i in range(n)) for p in itertools.permutations(range(m), n))
+        assert total == best
+
+
+def test_matching_keeps_ids_under_permutation():
+    d = 4
+    old = np.array([1, 0, 0, 0, 0, 1, 0, 0, 0, 0, 1, 0], np.float32)
+    new = np.array([0, 0, 1, 0, 1, 0, 0, 0, 0, 0, 0, 1], np.float32)
+    m = H.match_centroids(old, new, d, 0.8)
+    assert m == [2, 0, None]
+    ids, nxt = H.carry_ids(m, [10, 11, 12], 3)
+    assert ids == [12, 10, 3] and nxt == 4
+
+
+def test_quantile_rounds_half_away_and_orders_totally():
+    v = np.array([3.0, -0.0, 0.0, 1.0, -2.0, 5.0], np.float32)
+    # sorted (total order): -2, -0, 0, 1, 3, 5; q (n - 1) = 2.5 rounds to 3
+    assert H.quantile(v, 0.5) == np.float32(1.0)
+    assert H.quantile(v, 0.0) == np.float32(-2.0)
+    assert H.quantile(v, 1.0) == np.float32(5.0)
+    assert np.isnan(H.quantile(np.zeros(0, np.float32), 0.5))
+    z = H.quantile(np.array([0.0, -0.0], np.float32), 0.0)
+    assert z == 0 and np.signbit(z), "-0 sorts before +0"
+
+
+def test_unit_means_against_f64_brute_force():
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((500, 24)).astype(np.float32)
+    rows = [np.arange(0, 500, 3), np.arange(1, 200), np.zeros(0, np.int64)]
+    c = H.unit_means(x, rows)
+    for g, r in enumerate(rows):
+        acc = np.zeros(24, np.float64)
+        for i in r:
+            acc += x[i].astype(np.float64)
+        want = acc.astype(np.float32)
+        mx = np.float32(np.max(np.abs(want))) if len(r) else np.float32(0)
+        want = want / (mx if mx > 0 else np.float32(1))
+        nrm = np.float32(0)
+        for v in want:
+            nrm = np.float32(nrm + np.float32(v * v))
+        want = (want / (np.float32(np.sqrt(nrm)) if nrm > 0 else np.float32(1))).astype(np.float32)
+        assert c[g].tobytes() == want.astype(np.float32).tobytes(), g
