@@ -515,11 +515,14 @@ def autok_workload(args):
     sweep of auto_cluster over the first 900,000 rows (k = 2 .. 40, four
     k-means++ restarts each: 156 spherical e-means fits with their
     assignments, scored by internal_scores, the k chosen by the silhouette;
-    auto.rs:457-542), then the add of the last 100,000 rows at the top level
-    (incremental.rs:306-360: 11% new rows call for the EMA update: assign the
-    new rows, then resume the model from its EMA state for one epoch on all
-    rows). The data stay bound on one context. CPU baseline: the oracle's fit
-    at the median k on the same 900,000 rows."""
+    auto.rs:457-542), a level-2 model of 16 leaves per level-1 group (the
+    generator's sub-groups; auto_cluster's level-2 sweeps are not built), the
+    hierarchy's labels and outlier floors (auto.rs:1135-1215), then
+    Hierarchy::add of the last 100,000 rows (incremental.rs:306-596: 11 % new
+    rows call for the EMA update: every group's leaves resume on its rows,
+    stable ids by matching, level 1 from the groups' means). The data stay
+    bound on one context. CPU baseline: the oracle's fit at the median k on
+    the same 900,000 rows."""
     from emeans_amd import Config, HipDevice, auto, synth
     from oracle import oracle as O
 
@@ -543,21 +546,40 @@ def autok_workload(args):
     pick = auto.select(scores, cfg, False)
     lvl1 = out[pick][1]
     log(f"autok: level-1 sweep {sweep_s:.2f} s ({tm['fits']} fits), k1 = {ks[pick]}")
-    # Hierarchy::add of the last 100,000 rows at the top level.
-    xa = dev.bind(x_all)
-    xn = dev.bind(x_all[n:])
-    cb = dev.upload_f32(lvl1.centroids)
-    lab, sco = dev.zeros_u32(n_all - n), dev.zeros_f32(n_all - n)
-    dev.sync()
+    # The hierarchy: a level-2 model per level-1 group (k2 = 16 k-means++ rows,
+    # the generator's sub-groups per top group), assembled, then Hierarchy::add
+    # of the last 100,000 rows (11 % new rows: the EMA update).
+    from emeans_amd import hierarchy as H
+    lab1 = dev.read_u32(lvl1.labels)
+    k2 = 16
+    cfg2 = lambda k, s: Config(d=d, k=k, spherical=True, nepochs=cfg.nepochs, seed=s,
+                               capture_assignments=False)
     t0 = time.perf_counter()
-    dev.assign_dev(xn, n_all - n, d, cb, lvl1.k, "ip", lab, sco)
+    leaves = []
+    for g in range(lvl1.k):
+        rows = np.flatnonzero(lab1 == g)
+        if len(rows) < 2 * k2:
+            leaves.append(None)
+            continue
+        xg = np.ascontiguousarray(x[rows])
+        xgb = dev.bind(xg)
+        s2 = auto.seed_for(cfg, 1 + g, k2, 0)
+        f2 = auto.fit(dev, xg, xgb, k2, cfg.nepochs, s2, dev.kmeans_pp(xgb, len(rows), d, k2, s2))
+        leaves.append(H.Model(cfg2(k2, s2), f2.centroids.reshape(k2, d), f2.positions, f2.usage))
     dev.sync()
-    t1 = time.perf_counter()
-    c1 = Config(d=d, k=lvl1.k, spherical=True, nepochs=1.0, seed=lvl1.seed,
-                capture_assignments=False)
-    dev.train_dev(xa, n_all, c1, state=(lvl1.positions, lvl1.usage))
-    dev.sync()
-    t2 = time.perf_counter()
+    t_leaves = time.perf_counter() - t0
+    level1 = H.Model(cfg2(lvl1.k, lvl1.seed), lvl1.centroids.reshape(lvl1.k, d), lvl1.positions,
+                     lvl1.usage)
+    t0 = time.perf_counter()
+    h = H.Hierarchy.from_models(x, level1, leaves, H.HipBackend(dev),
+                                H.IncrementalConfig(grow_min_size=0), cfg.nepochs, cfg.seed)
+    t_build = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    rep = h.add(x_all, n)
+    t_add = time.perf_counter() - t0
+    nfit2 = sum(m is not None for m in leaves)
+    log(f"autok: {nfit2} level-2 fits {t_leaves:.2f} s; hierarchy labels {t_build:.2f} s; "
+        f"add of {n_all - n} rows: {rep.action}, {t_add:.2f} s")
     # CPU baseline: the oracle's fit (train_from + assign) at the median k.
     kc = ks[len(ks) // 2]
     init = x[dev.kmeans_pp(xb, n, d, kc, 7)]
@@ -571,7 +593,10 @@ def autok_workload(args):
             "fits": tm["fits"], "ms_per_fit": gpu_fit_s * 1e3,
             "kmeans_pp_s": tm["kmeans_pp_s"], "internal_scores_s": tm["scores_s"],
             "k1": ks[pick], "level1": [vars(s) for s in scores],
-            "add": {"assign_100k_s": t1 - t0, "resume_1M_1epoch_s": t2 - t1},
+            "hierarchy": {"level2_fits": nfit2, "level2_k": k2, "level2_fit_s": t_leaves,
+                          "ms_per_level2_fit": t_leaves / max(nfit2, 1) * 1e3,
+                          "assemble_s": t_build, "add_rows": n_all - n, "add_action": rep.action,
+                          "add_s": t_add, "new_outliers": rep.new_outliers},
             "cpu_baseline": {"value": 1.0 / cpu_fit_s, "unit": "fits/s", "cores": O.get_threads(),
                              "kind": "port", "fit_s": cpu_fit_s,
                              "sample": f"one fit (k = {kc}: train_from k-means++ rows, 5 epochs, "

@@ -246,12 +246,11 @@ def hungarian(cost: List[List[float]]) -> List[int]:
     return ans
 
 
-def _sim64(a: np.ndarray, b: np.ndarray) -> float:
-    """Σ a_t b_t in f64, in order (incremental.rs:244-250)."""
-    s = -0.0
-    for p, q in zip(a.astype(np.float64).tolist(), b.astype(np.float64).tolist()):
-        s += p * q
-    return s
+def _sims64(old: np.ndarray, new: np.ndarray) -> np.ndarray:
+    """sim[a][b] = Σ_t old_a,t new_b,t in f64, added in order (incremental.rs:
+    244-250; the f64 products of f32 values are exact)."""
+    p = old.astype(np.float64)[:, None, :] * new.astype(np.float64)[None, :, :]
+    return np.add.accumulate(p, axis=2)[:, :, -1]
 
 
 def match_centroids(old: np.ndarray, new: np.ndarray, d: int, min_sim: float):
@@ -263,7 +262,7 @@ def match_centroids(old: np.ndarray, new: np.ndarray, d: int, min_sim: float):
     out: List[Optional[int]] = [None] * kn
     if ko == 0 or kn == 0:
         return out
-    sim = [[_sim64(old[a], new[b]) for b in range(kn)] for a in range(ko)]
+    sim = _sims64(old, new).tolist()
     ms = float(np.float32(min_sim))
     if kn <= ko:
         for b, a in enumerate(hungarian([[-sim[a][b] for a in range(ko)] for b in range(kn)])):
@@ -404,17 +403,20 @@ class Hierarchy:
         return out
 
     def leaf_sims(self, labels: Labels):
-        """auto.rs:1191-1205: every leaf's member cosines, group then leaf order."""
+        """auto.rs:1191-1205: every leaf's member cosines (in row order), group
+        then leaf order."""
         at, first = [], []
         for g, grp in enumerate(self.groups):
             first.append(len(at))
             at.extend((g, j) for j in range(len(grp.ids)))
-        sims = [[] for _ in at]
-        for i in range(len(labels.sim)):
-            g, j = int(labels.slot1[i]), int(labels.slot2[i])
-            if j < len(self.groups[g].ids):
-                sims[first[g] + j].append(labels.sim[i])
-        return at, [np.asarray(v, np.float32) for v in sims]
+        nids = np.asarray([len(g.ids) for g in self.groups] + [0], np.int64)
+        s1, s2 = labels.slot1.astype(np.int64), labels.slot2.astype(np.int64)
+        keep = s2 < nids[s1]
+        flat = np.asarray(first + [0], np.int64)[s1[keep]] + s2[keep]
+        order = np.argsort(flat, kind="stable")
+        cuts = np.searchsorted(flat[order], np.arange(len(at) + 1))
+        sv = labels.sim[keep][order].astype(np.float32)
+        return at, [sv[cuts[i]:cuts[i + 1]] for i in range(len(at))]
 
     def set_floors(self, labels: Labels):
         """auto.rs:1207-1215."""
