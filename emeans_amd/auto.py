@@ -9,10 +9,8 @@ the data bound once.
   select     auto.rs:513-542  the chosen k of a sweep
   kmeans_pp  auto.rs:401-455  on the device (HipDevice.kmeans_pp)
 
-Two-level auto_cluster and Hierarchy (auto.rs:1001-1101, incremental.rs) are
-callers of these: a level-1 sweep, then a level-2 sweep inside each group;
-Hierarchy::add assigns new rows and, by its policy, resumes the models from
-their EMA state (Emeans.train_resume).
+Two-level auto_cluster (emeans_amd.autocluster) and the hierarchy
+(emeans_amd.hierarchy) are callers of these.
 """
 
 import time
@@ -35,9 +33,14 @@ class AutoConfig:
     level2_tolerance: float = 0.05
     min_cluster_size: int = 20
     max_cluster_size: int = 200
+    min_split_size: int = 60
+    split_min_silhouette: float = 0.05
     restarts: int = 4
     nepochs: float = 5.0
     init: str = "kmeans_plus_plus"  # or "random_rows"
+    level1_method: str = "bottom_up"  # or "top_down"
+    resplit_passes: int = 2
+    level1_max_share: float = 0.5
     seed: int = 1234
 
 
@@ -112,6 +115,12 @@ def browsable(sizes, cfg: AutoConfig) -> float:
     return float(ok) / float(max(int(sizes.sum()), 1))
 
 
+def score(k: int, i: dict, cfg: AutoConfig, seconds: float) -> KScore:
+    """auto.rs:386-397: a k's KScore from its internal_scores."""
+    return KScore(k, i["k_eff"], i["silhouette"], i["calinski_harabasz"], i["davies_bouldin"],
+                  i["objective"], browsable(i["sizes"], cfg), seconds)
+
+
 def sweep(dev: HipDevice, x: np.ndarray, xb, ks: List[int], cfg: AutoConfig, salt: int,
           verbose: bool = False, timing: Optional[dict] = None):
     """auto.rs:457-510: for every k, the best (lowest objective) of
@@ -141,8 +150,7 @@ def sweep(dev: HipDevice, x: np.ndarray, xb, ks: List[int], cfg: AutoConfig, sal
         tm["fit_s"] += t1 - t
         i = dev.internal_scores(xb, n, d, best.labels, k)
         tm["scores_s"] += time.perf_counter() - t1
-        s = KScore(k, i["k_eff"], i["silhouette"], i["calinski_harabasz"], i["davies_bouldin"],
-                   i["objective"], browsable(i["sizes"], cfg), time.perf_counter() - t)
+        s = score(k, i, cfg, time.perf_counter() - t)
         if verbose:
             print(f"  k={k:3} k_eff={s.k_eff:3} sil={s.silhouette:.4f} "
                   f"ch={s.calinski_harabasz:.1f} db={s.davies_bouldin:.3f} "

@@ -19,11 +19,10 @@ and on the host, as in the reference: the outlier floors (auto.rs:1194-1292),
 the policy, the centroid matching that keeps stable ids (incremental.rs:
 176-290), unit means (auto.rs:750-765) and model_from (auto.rs:955-987).
 
+The full retrain runs auto_cluster (emeans_amd.autocluster) on all rows.
 Not built here: the grow step's leaf formation from pending outliers
-(incremental.rs:376-540; its early exits are kept, and a call that would form
-leaves raises) and the full retrain, which runs auto_cluster's level-2
-sweeps (auto.rs:1001-1101); both raise NotImplementedError rather than
-returning other results.
+(incremental.rs:376-540); its early exits are kept, and a call that would
+form leaves raises NotImplementedError rather than returning other results.
 
 The device work goes through a backend object with two methods, so that the
 same host logic runs over any device:
@@ -305,19 +304,24 @@ def normalize_rows(m: np.ndarray) -> np.ndarray:
     return (m / s[:, None]).astype(np.float32)
 
 
-def unit_means(x: np.ndarray, rows: List[np.ndarray]) -> np.ndarray:
-    """auto.rs:750-765: each group's f64 sum of its rows in order, cast to f32,
-    then normalize_rows."""
+def row_sums_f64(x: np.ndarray, rows: List[np.ndarray]) -> np.ndarray:
+    """Each group's f64 sum of its rows, added row by row in order (from 0)."""
     d = x.shape[1]
-    c = np.zeros((len(rows), d), np.float32)
+    out = np.zeros((len(rows), d), np.float64)
     for g, r in enumerate(rows):
         acc = np.zeros(d, np.float64)
-        for lo in range(0, len(r), 4096):  # sequential f64 adds, row by row
+        for lo in range(0, len(r), 4096):
             blk = x[np.asarray(r[lo:lo + 4096], np.int64)].astype(np.float64)
             blk[0] += acc
             acc = np.add.accumulate(blk, axis=0)[-1]
-        c[g] = acc.astype(np.float32)
-    return normalize_rows(c)
+        out[g] = acc
+    return out
+
+
+def unit_means(x: np.ndarray, rows: List[np.ndarray]) -> np.ndarray:
+    """auto.rs:750-765: each group's f64 sum of its rows in order, cast to f32,
+    then normalize_rows."""
+    return normalize_rows(row_sums_f64(x, rows).astype(np.float32))
 
 
 def model_from(centroids: np.ndarray, counts: List[int], d: int, nepochs: float, seed: int) -> Model:
@@ -345,6 +349,8 @@ class Hierarchy:
         self.state, self.backend = state, backend
         self.inc = inc or IncrementalConfig()
         self.nepochs, self.seed = nepochs, seed
+        self.retrain = None  # full retrain (x_all) -> None, set by auto_cluster
+        self.diagnostics = None
 
     @staticmethod
     def from_models(x: np.ndarray, level1: Model, leaves: List[Optional[Model]], backend,
@@ -362,6 +368,18 @@ class Hierarchy:
 
     def level1_centroids(self) -> np.ndarray:
         return self.level1.centroids
+
+    def leaf_centroids(self, g: int) -> np.ndarray:
+        """auto.rs:1123-1128: group g's leaf centroids; its level-1 centroid
+        when it has no model."""
+        m = self.groups[g].model
+        if m is not None:
+            return m.centroids.reshape(-1, self.d)
+        return self.level1_centroids().reshape(-1, self.d)[g:g + 1]
+
+    def chosen_k(self):
+        """auto.rs:1104-1113: (k1, [k2 of each group])."""
+        return self.level1.k, [g.model.k if g.model is not None else 0 for g in self.groups]
 
     def assign(self, x: np.ndarray) -> Labels:
         """auto.rs:1135-1189: the nearest leaf over all leaves (cosine); level 1
@@ -459,7 +477,9 @@ class Hierarchy:
         if action == "EmaUpdate":
             new_leaves = self.ema_update(x_all)
         elif action == "FullRetrain":
-            raise NotImplementedError("a full retrain runs auto_cluster's sweeps, not built here")
+            if self.retrain is None:
+                raise NotImplementedError("a full retrain needs a hierarchy from auto_cluster")
+            self.retrain(x_all)
         return AddReport(action, self.assign(x_all), new_outliers, len(self.state.pending),
                          outlier_fraction, new_leaves)
 

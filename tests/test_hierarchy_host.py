@@ -94,3 +94,34 @@ def test_unit_means_against_f64_brute_force():
             nrm = np.float32(nrm + np.float32(v * v))
         want = (want / (np.float32(np.sqrt(nrm)) if nrm > 0 else np.float32(1))).astype(np.float32)
         assert c[g].tobytes() == want.astype(np.float32).tobytes(), g
+
+
+def test_average_linkage_merges_the_closest_mean_cosine():
+    """Each merge joins the pair of live clusters with the largest mean
+    pairwise row cosine (brute force over the rows), the lower id kept."""
+    from emeans_amd import autocluster as A
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((60, 8)).astype(np.float32)
+    x /= np.linalg.norm(x, axis=1, keepdims=True)
+    rows = [np.arange(i, 60, 7) for i in range(7)]
+    merges = A.average_linkage(x, rows)
+    assert len(merges) == 6
+    members = {j: list(rows[j]) for j in range(7)}
+    x64 = x.astype(np.float64)
+    for a, b, s in merges:
+        assert a < b and a in members and b in members
+        best = max(((p, q) for p in members for q in members if p < q),
+                   key=lambda pq: np.mean(x64[members[pq[0]]] @ x64[members[pq[1]]].T))
+        want = np.mean(x64[members[a]] @ x64[members[b]].T)
+        assert (a, b) == best
+        assert abs(s - want) < 1e-12
+        members[a] += members.pop(b)
+
+
+def test_cut_numbers_groups_by_lowest_leaf():
+    from emeans_amd import autocluster as A
+    merges = [(2, 4, 0.9), (0, 3, 0.8), (0, 2, 0.7)]
+    assert A.cut(5, merges, 5).tolist() == [0, 1, 2, 3, 4]
+    assert A.cut(5, merges, 4).tolist() == [0, 1, 2, 3, 2]
+    assert A.cut(5, merges, 3).tolist() == [0, 1, 2, 0, 2]
+    assert A.cut(5, merges, 2).tolist() == [0, 1, 0, 0, 0]
