@@ -510,20 +510,19 @@ def assign_workload(args):
 
 
 def autok_workload(args):
-    """C5's GPU work (auto_cluster + Hierarchy::add on 1,000,000 x 768 nested
-    unit rows, 64 Zipf(1.3) top groups of 16 sub-groups, seed 3): the level-1
-    sweep of auto_cluster over the first 900,000 rows (k = 2 .. 40, four
-    k-means++ restarts each: 156 spherical e-means fits with their
-    assignments, scored by internal_scores, the k chosen by the silhouette;
-    auto.rs:457-542), a level-2 model of 16 leaves per level-1 group (the
-    generator's sub-groups; auto_cluster's level-2 sweeps are not built), the
-    hierarchy's labels and outlier floors (auto.rs:1135-1215), then
+    """C5 (two-level auto_cluster plus incremental add on 1,000,000 x 768
+    nested unit rows, 64 Zipf(1.3) top groups of 16 sub-groups, seed 3):
+    auto_cluster of the first 900,000 rows with the reference's defaults
+    (auto.rs:1001-1101: the level-1 sweep k = 2..40 with four k-means++
+    restarts each, a level-2 sweep per group, resplits, refine, average
+    linkage and the cut, the hierarchy's labels and floors), then
     Hierarchy::add of the last 100,000 rows (incremental.rs:306-596: 11 % new
-    rows call for the EMA update: every group's leaves resume on its rows,
-    stable ids by matching, level 1 from the groups' means). The data stay
-    bound on one context. CPU baseline: the oracle's fit at the median k on
-    the same 900,000 rows."""
-    from emeans_amd import Config, HipDevice, auto, synth
+    rows call for the EMA update). The sweeps' trainings, assignments,
+    seedings and internal scores run on the device, the data bound on one
+    context. `value`: spherical e-means fits per second of auto_cluster's
+    wall time. CPU baseline: the oracle's fit at k = 21 on the same rows."""
+    from emeans_amd import HipDevice, auto, autocluster, synth
+    from emeans_amd import hierarchy as H
     from oracle import oracle as O
 
     n_all, n, d = 1_000_000, 900_000, 768
@@ -533,70 +532,42 @@ def autok_workload(args):
     log(f"autok data: {n_all} x {d} generated in {time.time() - t:.1f} s")
     dev = HipDevice()
     xb = dev.bind(x)
-    cfg = auto.AutoConfig(restarts=args.autok_restarts, seed=3)
-    ks = list(range(cfg.k1_range[0], cfg.k1_range[1] + 1))
+    cfg = auto.AutoConfig(restarts=args.autok_restarts, seed=3, verbose=True)
     auto.fit(dev, x, xb, 8, 1.0, 1, None)  # warm the kernels up
     dev.sync()
     tm = {}
     t0 = time.perf_counter()
-    out, _ = auto.sweep(dev, x, xb, ks, cfg, salt=0, timing=tm)
+    h, labels = autocluster.auto_cluster(dev, x, cfg, H.IncrementalConfig(grow_min_size=0),
+                                         timing=tm)
     dev.sync()
-    sweep_s = time.perf_counter() - t0
-    scores = [s for s, _ in out]
-    pick = auto.select(scores, cfg, False)
-    lvl1 = out[pick][1]
-    log(f"autok: level-1 sweep {sweep_s:.2f} s ({tm['fits']} fits), k1 = {ks[pick]}")
-    # The hierarchy: a level-2 model per level-1 group (k2 = 16 k-means++ rows,
-    # the generator's sub-groups per top group), assembled, then Hierarchy::add
-    # of the last 100,000 rows (11 % new rows: the EMA update).
-    from emeans_amd import hierarchy as H
-    lab1 = dev.read_u32(lvl1.labels)
-    k2 = 16
-    cfg2 = lambda k, s: Config(d=d, k=k, spherical=True, nepochs=cfg.nepochs, seed=s,
-                               capture_assignments=False)
-    t0 = time.perf_counter()
-    leaves = []
-    for g in range(lvl1.k):
-        rows = np.flatnonzero(lab1 == g)
-        if len(rows) < 2 * k2:
-            leaves.append(None)
-            continue
-        xg = np.ascontiguousarray(x[rows])
-        xgb = dev.bind(xg)
-        s2 = auto.seed_for(cfg, 1 + g, k2, 0)
-        f2 = auto.fit(dev, xg, xgb, k2, cfg.nepochs, s2, dev.kmeans_pp(xgb, len(rows), d, k2, s2))
-        leaves.append(H.Model(cfg2(k2, s2), f2.centroids.reshape(k2, d), f2.positions, f2.usage))
-    dev.sync()
-    t_leaves = time.perf_counter() - t0
-    level1 = H.Model(cfg2(lvl1.k, lvl1.seed), lvl1.centroids.reshape(lvl1.k, d), lvl1.positions,
-                     lvl1.usage)
-    t0 = time.perf_counter()
-    h = H.Hierarchy.from_models(x, level1, leaves, H.HipBackend(dev),
-                                H.IncrementalConfig(grow_min_size=0), cfg.nepochs, cfg.seed)
-    t_build = time.perf_counter() - t0
+    ac_s = time.perf_counter() - t0
+    k1, k2 = h.chosen_k()
+    dg = h.diagnostics
+    log(f"autok: auto_cluster {ac_s:.1f} s ({tm['fits']} sweep fits), k1 = {k1}, "
+        f"{sum(k2)} leaves, {dg.resplits} resplits; stages "
+        + ", ".join(f"{kk[:-2]} {v:.1f} s" for kk, v in tm.items() if kk.endswith("_s")))
     t0 = time.perf_counter()
     rep = h.add(x_all, n)
-    t_add = time.perf_counter() - t0
-    nfit2 = sum(m is not None for m in leaves)
-    log(f"autok: {nfit2} level-2 fits {t_leaves:.2f} s; hierarchy labels {t_build:.2f} s; "
-        f"add of {n_all - n} rows: {rep.action}, {t_add:.2f} s")
-    # CPU baseline: the oracle's fit (train_from + assign) at the median k.
-    kc = ks[len(ks) // 2]
+    add_s = time.perf_counter() - t0
+    log(f"autok: add of {n_all - n} rows: {rep.action}, {add_s:.2f} s, "
+        f"{rep.new_outliers} new outliers")
+    # CPU baseline: the oracle's fit (train_from k-means++ rows + assign) at k = 21.
+    kc = 21
     init = x[dev.kmeans_pp(xb, n, d, kc, 7)]
     c0 = time.perf_counter()
     o = O.train(x, d, kc, spherical=True, seed=7, init=init)
     O.assign(x, d, o["centroids"], "ip")
     cpu_fit_s = time.perf_counter() - c0
-    gpu_fit_s = tm["fit_s"] / max(tm["fits"], 1)
     dev.close()
-    return {"value": tm["fits"] / sweep_s, "unit": "fits/s", "sweep_s": sweep_s,
-            "fits": tm["fits"], "ms_per_fit": gpu_fit_s * 1e3,
+    return {"value": tm["fits"] / ac_s, "unit": "fits/s", "auto_cluster_s": ac_s,
+            "sweep_fits": tm["fits"], "ms_per_fit": tm["fit_s"] / max(tm["fits"], 1) * 1e3,
             "kmeans_pp_s": tm["kmeans_pp_s"], "internal_scores_s": tm["scores_s"],
-            "k1": ks[pick], "level1": [vars(s) for s in scores],
-            "hierarchy": {"level2_fits": nfit2, "level2_k": k2, "level2_fit_s": t_leaves,
-                          "ms_per_level2_fit": t_leaves / max(nfit2, 1) * 1e3,
-                          "assemble_s": t_build, "add_rows": n_all - n, "add_action": rep.action,
-                          "add_s": t_add, "new_outliers": rep.new_outliers},
+            "stages_s": {kk[:-2]: v for kk, v in tm.items()
+                         if kk.endswith("_s") and kk not in ("fit_s", "kmeans_pp_s", "scores_s")},
+            "k1": k1, "leaves": sum(k2), "k2": k2, "resplits": dg.resplits, "flat": dg.flat,
+            "level1_candidates": [vars(s) for s in dg.level1],
+            "add": {"rows": n_all - n, "action": rep.action, "seconds": add_s,
+                    "new_outliers": rep.new_outliers},
             "cpu_baseline": {"value": 1.0 / cpu_fit_s, "unit": "fits/s", "cores": O.get_threads(),
                              "kind": "port", "fit_s": cpu_fit_s,
                              "sample": f"one fit (k = {kc}: train_from k-means++ rows, 5 epochs, "

@@ -42,6 +42,7 @@ class AutoConfig:
     resplit_passes: int = 2
     level1_max_share: float = 0.5
     seed: int = 1234
+    verbose: bool = False
 
 
 @dataclass

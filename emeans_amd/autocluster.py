@@ -20,6 +20,7 @@ Float sums follow Rust's Sum (a left fold from -0.0: a sum is its first term
 plus the rest in order); f64 row sums are sequential, as unit_means'.
 """
 
+import sys
 import time
 from dataclasses import dataclass, field
 from typing import List, Optional
@@ -71,7 +72,7 @@ def _total_key64(v: float) -> int:
     return b ^ 0x7FFFFFFFFFFFFFFF if b < 0 else b
 
 
-def fit_group(dev: HipDevice, xg: np.ndarray, cfg, salt: int):
+def fit_group(dev: HipDevice, xg: np.ndarray, cfg, salt: int, tm: Optional[dict] = None):
     """auto.rs:544-590: (Fitted or None, decision, sweep scores)."""
     n, d = xg.shape
     if n == 0:
@@ -84,7 +85,7 @@ def fit_group(dev: HipDevice, xg: np.ndarray, cfg, salt: int):
     kmax = min(cfg.k2_max, n // max(cfg.min_cluster_size, 1))
     if n < cfg.min_split_size or kmax < 2:
         return one(), ("TooSmall", None), []
-    runs, _ = auto.sweep(dev, xg, xgb, list(range(2, kmax + 1)), cfg, salt)
+    runs, _ = auto.sweep(dev, xg, xgb, list(range(2, kmax + 1)), cfg, salt, timing=tm)
     scores = [s for s, _ in runs]
     best_sil = _fmax_fold(s.silhouette for s in scores)
     if best_sil < cfg.split_min_silhouette:
@@ -98,12 +99,13 @@ def _split_rows(r: np.ndarray, labels: np.ndarray, k: int) -> List[np.ndarray]:
     return [r[labels == j] for j in range(k)]
 
 
-def stage_a(dev: HipDevice, x: np.ndarray, xb, cfg, diag: Diagnostics) -> Leaves:
+def stage_a(dev: HipDevice, x: np.ndarray, xb, cfg, diag: Diagnostics,
+            tm: Optional[dict] = None) -> Leaves:
     """auto.rs:603-660."""
     n, d = x.shape
     k1_hi = min(cfg.k1_range[1], n)
     k1_lo = min(cfg.k1_range[0], k1_hi)
-    runs, _ = auto.sweep(dev, x, xb, list(range(k1_lo, k1_hi + 1)), cfg, 0)
+    runs, _ = auto.sweep(dev, x, xb, list(range(k1_lo, k1_hi + 1)), cfg, 0, timing=tm)
     scores = [s for s, _ in runs]
     pick = auto.select(scores, cfg, False)
     level1 = runs[pick][1]
@@ -116,7 +118,10 @@ def stage_a(dev: HipDevice, x: np.ndarray, xb, cfg, diag: Diagnostics) -> Leaves
             diag.level2.append([])
             continue
         xg = np.ascontiguousarray(x[r])
-        model, decision, sc = fit_group(dev, xg, cfg, 1 + g)
+        model, decision, sc = fit_group(dev, xg, cfg, 1 + g, tm)
+        if cfg.verbose:
+            print(f"  group {g}: {len(r)} rows, {decision[0]} {decision[1]}", file=sys.stderr,
+                  flush=True)
         best = _fmax_fold(s.silhouette for s in sc)
         diag.level2.append(sc)
         sub = _split_rows(r, dev.read_u32(model.labels), model.k)
@@ -130,7 +135,7 @@ def stage_a(dev: HipDevice, x: np.ndarray, xb, cfg, diag: Diagnostics) -> Leaves
     return leaves
 
 
-def resplit(dev: HipDevice, x: np.ndarray, cfg, leaves: Leaves):
+def resplit(dev: HipDevice, x: np.ndarray, cfg, leaves: Leaves, tm: Optional[dict] = None):
     """auto.rs:666-748: (leaves, number of splits)."""
     cur, splits = leaves, 0
     for pas in range(cfg.resplit_passes):
@@ -149,15 +154,21 @@ def resplit(dev: HipDevice, x: np.ndarray, cfg, leaves: Leaves):
             screen = list(range(2, min(kmax, SCREEN_K) + 1))
             screen_best = -np.inf
             if screen:
-                runs, _ = auto.sweep(dev, xg, dev.bind(xg), screen, cfg, salt)
+                runs, _ = auto.sweep(dev, xg, dev.bind(xg), screen, cfg, salt, timing=tm)
                 screen_best = _fmax_fold(s.silhouette for s, _ in runs)
             if not screen or screen_best < cfg.split_min_silhouette:
+                if cfg.verbose:
+                    print(f"  resplit pass {pas} leaf {li}: {len(r)} rows, screen {screen_best:.3f}",
+                          file=sys.stderr, flush=True)
                 nxt.rows.append(r)
                 nxt.parent.append(p)
                 nxt.sweep.append(screen_best if np.isfinite(screen_best) else None)
                 continue
-            model, decision, sc = fit_group(dev, xg, cfg, salt)
+            model, decision, sc = fit_group(dev, xg, cfg, salt, tm)
             best = _fmax_fold(s.silhouette for s in sc)
+            if cfg.verbose:
+                print(f"  resplit pass {pas} leaf {li}: {len(r)} rows, {decision[0]} {decision[1]}",
+                      file=sys.stderr, flush=True)
             if decision[0] == "Split" and model is not None:
                 for s in _split_rows(r, dev.read_u32(model.labels), decision[1]):
                     if len(s) == 0:
@@ -286,8 +297,12 @@ def group_bottom_up(dev: HipDevice, x: np.ndarray, xb, cfg, leaves: Leaves,
     return cut(l, merges, ks[best])
 
 
-def auto_cluster(dev: HipDevice, x: np.ndarray, cfg, inc: Optional[H.IncrementalConfig] = None):
-    """auto.rs:1001-1101: (Hierarchy, Labels) of the unit rows of x."""
+def auto_cluster(dev: HipDevice, x: np.ndarray, cfg, inc: Optional[H.IncrementalConfig] = None,
+                 timing: Optional[dict] = None):
+    """auto.rs:1001-1101: (Hierarchy, Labels) of the unit rows of x. With
+    timing, the sweeps' counters (auto.sweep) and each stage's seconds
+    accumulate in it."""
+    tm = timing if timing is not None else {}
     x = np.ascontiguousarray(x, np.float32)
     if x.ndim != 2:
         raise ValueError("x must be n x d")
@@ -299,9 +314,22 @@ def auto_cluster(dev: HipDevice, x: np.ndarray, cfg, inc: Optional[H.Incremental
     t = time.perf_counter()
     xb = dev.bind(x)
     diag = Diagnostics()
-    leaves = stage_a(dev, x, xb, cfg, diag)
-    leaves, resplits = resplit(dev, x, cfg, leaves)
+    lap = time.perf_counter()
+
+    def stage(name):  # the reference's verbose laps (auto.rs:1015-1020)
+        nonlocal lap
+        now = time.perf_counter()
+        tm[name + "_s"] = tm.get(name + "_s", 0.0) + now - lap
+        lap = now
+        if cfg.verbose:
+            print(f"[{now - t:.1f}s] {name}", file=sys.stderr, flush=True)
+
+    leaves = stage_a(dev, x, xb, cfg, diag, tm)
+    stage("stage_a")
+    leaves, resplits = resplit(dev, x, cfg, leaves, tm)
+    stage("resplit")
     leaves = refine(dev, x, leaves)
+    stage("refine")
     diag.resplits = resplits
     diag.leaves = len(leaves.rows)
     if cfg.level1_method == "bottom_up":
@@ -312,6 +340,7 @@ def auto_cluster(dev: HipDevice, x: np.ndarray, cfg, inc: Optional[H.Incremental
             ids.setdefault(p, len(ids))
         diag.level1 = list(diag.stage_a_level1)
         group_of_leaf = np.array([ids[p] for p in leaves.parent], np.int64)
+    stage("level1")
     k1 = int(group_of_leaf.max()) + 1 if len(group_of_leaf) else 0
     groups, group_rows = [], []
     for g in range(k1):
@@ -331,6 +360,7 @@ def auto_cluster(dev: HipDevice, x: np.ndarray, cfg, inc: Optional[H.Incremental
     labels = h.assign(x)
     h.set_floors(labels)
     labels = h.assign(x)
+    stage("assemble")
     diag.seconds = time.perf_counter() - t
     return h, labels
 
