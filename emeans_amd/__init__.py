@@ -347,6 +347,14 @@ class HipDevice:
         exact kernels alone. Every mode gives the same bits."""
         check(lib().emh_set_screen(self._ctx, int(mode)))
 
+    EXACT_BELOW = 2048
+
+    def set_exact_below(self, items: int):
+        """Top-1 calls of at most `items` row items (rows x ceil(k / 64)) take
+        the exact kernels alone even when the mode screens (default
+        EXACT_BELOW); 0 screens every call the mode screens. Same bits."""
+        check(lib().emh_set_exact_below(self._ctx, int(items)))
+
 
 def _train_init(k, d, init, state):
     """The emh_train_init of a run (or None) and the arrays it points into."""

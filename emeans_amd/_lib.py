@@ -130,6 +130,7 @@ SIGNATURES = {
     "emh_screen_margin": (_i, [_vp, _vp, _sz, _vp, _sz, _sz, _vp, _vp, _sz, _i, _vp]),
     "emh_screen_margin_topk": (_i, [_vp, _vp, _sz, _vp, _sz, _sz, _i, _vp]),
     "emh_set_screen": (_i, [_vp, _i]),
+    "emh_set_exact_below": (_i, [_vp, _u64]),
     "emh_host_permutation": (None, [_u32, _u64, _vp]),
     "emh_host_random_sample": (_d, [_u32, _u64]),
     "emh_host_recipe": (_i, [_u64, _vp, C.POINTER(_u64), C.POINTER(_d), _vp, _u64,

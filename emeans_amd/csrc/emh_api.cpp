@@ -598,6 +598,13 @@ int emh_set_screen(emh_ctx* c, int on) {
   });
 }
 
+int emh_set_exact_below(emh_ctx* c, uint64_t items) {
+  return guard([&] {
+    EMH_ENSURE(c, "null context");
+    c->exact_below = (size_t)items;
+  });
+}
+
 int emh_profile(emh_ctx* c, int on) {
   return guard([&] {
     EMH_ENSURE(c, "null context");

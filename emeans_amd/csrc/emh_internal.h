@@ -120,6 +120,11 @@ struct Pinned {
 // Top-1 / top-k path (emh_set_screen): the exact kernels alone, or the MFMA
 // screen in bf16 three-pass or f32 arithmetic ahead of the exact check.
 enum ScreenMode : int { SCREEN_OFF = 0, SCREEN_BF3 = 1, SCREEN_F32 = 2 };
+// Top-1 calls of at most this many row items (rows x ceil(k / 64): the exact
+// scan's passes of a wave over 64 centroids) run the exact kernels alone by
+// default: below it the scan takes less time than the screen's three launches
+// (d = 768: ~30 us for up to 1024 rows at k <= 64 against ~52 us).
+constexpr size_t EXACT_BELOW = 2048;
 
 // Words of the context's small device block.
 enum SmallWord : int {
@@ -150,6 +155,7 @@ struct emh_ctx {
   hipStream_t copy_stream = nullptr;  // host<->device staging that overlaps the kernels
   int cus = 256;
   int screen = emh::SCREEN_BF3;
+  size_t exact_below = emh::EXACT_BELOW;  // emh_set_exact_below
   uint32_t* small = nullptr;  // SW_WORDS u32 on the device
   char* scratch = nullptr;    // the device's fixed scratch block (emh_top1_noalloc)
   uint64_t fallback_total = 0;
@@ -358,19 +364,21 @@ struct SplitCents {
 };
 // pre: x's rows already split, pc: the centroids (used when the call takes
 // the split-operand screen; see split_screen).
-// tally: tally the labels (see LabelTally; the call must take the screen with
-// d % 4 == 0, where the check and the queued-row scan write every label).
+// tally: tally the labels (see LabelTally; the call must screen with d % 4 ==
+// 0, where the check and the queued-row scan write every label: a tallied call
+// screens also when its rows are fewer than the context's exact_below).
 void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids, size_t lo, size_t hi,
                  const float* cents, const float* cnorm, size_t k, bool ip, uint32_t* labels,
                  float* scores, bool words_clear = false, Arena* ar = nullptr,
                  const SplitRows* pre = nullptr, const SplitCents* pc = nullptr,
                  const LabelTally* tally = nullptr);
-// Whether top-1 calls with d dimensions and k centroids take the
+// Whether top-1 calls of n rows with d dimensions and k centroids take the
 // split-operand screen (k_screen4), whose rows a caller may split ahead.
-bool split_screen(emh_ctx* c, size_t d, size_t k);
-// Whether top-1 calls with d dimensions and k centroids run a screen (and so
-// the check and the queued-row scan).
-bool top1_screens(emh_ctx* c, size_t d, size_t k);
+bool split_screen(emh_ctx* c, size_t n, size_t d, size_t k);
+// Whether top-1 calls of n rows with d dimensions and k centroids run a
+// screen (and so the check and the queued-row scan). A tallied call always
+// does, whatever its rows.
+bool top1_screens(emh_ctx* c, size_t n, size_t d, size_t k);
 // Split rows of x (n rows, or ids[lo..lo+n)) into bf16 halves in out,
 // slab-major, with their |x|^2 in norm; with part, each of the
 // halves_blocks(n) blocks leaves the largest |x|^2 of its rows and the

@@ -25,42 +25,72 @@ __global__ __launch_bounds__(256) void k_fill_u32(uint32_t* p, size_t n, uint32_
   if (i < n) p[i] = v;
 }
 
-// s + v[0] + v[1] + ... in order (one lane), with 8 LDS reads in flight.
+constexpr int NU = CH / WAVE;  // values per lane in one chunk
+
+__device__ __forceinline__ void ld8(float4* q, const float* v) {
+#pragma unroll
+  for (int u = 0; u < 8; u++) q[u] = *reinterpret_cast<const float4*>(v + 4 * u);
+}
+__device__ __forceinline__ float add8(float s, const float4* q) {
+#pragma unroll
+  for (int u = 0; u < 8; u++) {
+    s = s + q[u].x;
+    s = s + q[u].y;
+    s = s + q[u].z;
+    s = s + q[u].w;
+  }
+  return s;
+}
+
+// s + v[0] + v[1] + ... + v[len - 1] in order (one lane), v a CH-float LDS
+// slice: the next 32 values are read while the current 32 are added (reads
+// clamped into the slice, so none is conditional).
 __device__ __forceinline__ float seq_add(const float* v, int len, float s) {
+  float4 a[8], b[8];
+  ld8(a, v);
   int t = 0;
-  for (; t + 32 <= len; t += 32) {
-    float4 q[8];
-#pragma unroll
-    for (int u = 0; u < 8; u++) q[u] = *reinterpret_cast<const float4*>(v + t + 4 * u);
-#pragma unroll
-    for (int u = 0; u < 8; u++) {
-      s = s + q[u].x;
-      s = s + q[u].y;
-      s = s + q[u].z;
-      s = s + q[u].w;
-    }
+  for (; t + 64 <= len; t += 64) {
+    ld8(b, v + t + 32);
+    s = add8(s, a);
+    ld8(a, v + min(t + 64, CH - 32));
+    s = add8(s, b);
+  }
+  if (t + 32 <= len) {
+    s = add8(s, a);
+    t += 32;
   }
   for (; t < len; t++) s = s + v[t];
   return s;
 }
 
+// One chunk (len <= CH values) of a row into registers, lane-strided: every
+// load issued before any is used (indices clamped into the chunk; the lanes'
+// values past len are not used).
+__device__ __forceinline__ void ld_chunk(float* r, const float* row, int len, int lane) {
+#pragma unroll
+  for (int u = 0; u < NU; u++) r[u] = row[min(lane + WAVE * u, len - 1)];
+}
+
+__device__ __forceinline__ void wave_sync_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Sequential sum of rounded squares of row r (assign.rs:150-155): the lanes of
-// wave w square one chunk into sq[w]; lane 0 adds the chunk in column order.
+// wave w square one chunk into sq; lane 0 adds the chunk in column order.
 __device__ float seq_sq_sum(const float* row, size_t d, float* sq, int lane) {
   float s = 0.0f;
   for (size_t c0 = 0; c0 < d; c0 += CH) {
-    int len = (int)min((size_t)CH, d - c0);
-    for (int t = lane; t < len; t += WAVE) {
-      float v = row[c0 + t];
-      sq[t] = v * v;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int len = (int)min((size_t)CH, d - c0);
+    float v[NU];
+    ld_chunk(v, row + c0, len, lane);
+#pragma unroll
+    for (int u = 0; u < NU; u++)
+      if (lane + WAVE * u < len) sq[lane + WAVE * u] = v[u] * v[u];
+    wave_sync_lds();
     if (lane == 0) s = seq_add(sq, len, s);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    wave_sync_lds();
   }
   return s;  // valid in lane 0
 }
@@ -90,33 +120,55 @@ __global__ __launch_bounds__(256) void k_normalize_rows(const float* __restrict_
   size_t r = (size_t)blockIdx.x * WAVES + w;
   if (r >= rows) return;
   const float* row = src + r * d;
-  float mx = 0.0f;  // fold from 0 with max(|v|): NaN never wins (fmaxf)
+  float* out = dst + r * d;
+  if (d <= (size_t)CH) {  // one chunk: the row stays in registers for all three passes
+    const int len = (int)d;
+    float v[NU];
+    ld_chunk(v, row, len, lane);
+    float mx = 0.0f;  // fold from 0 with max(|v|): NaN never wins (fmaxf)
+#pragma unroll
+    for (int u = 0; u < NU; u++) mx = fmaxf(mx, lane + WAVE * u < len ? fabsf(v[u]) : 0.0f);
+    mx = wave_max(mx);
+    const float s1 = mx > 0.0f ? mx : 1.0f;
+#pragma unroll
+    for (int u = 0; u < NU; u++) {
+      v[u] = v[u] / s1;
+      if (lane + WAVE * u < len) sq[w][lane + WAVE * u] = v[u] * v[u];
+    }
+    wave_sync_lds();
+    float s = 0.0f;
+    if (lane == 0) s = seq_add(sq[w], len, s);
+    s = __shfl(s, 0, WAVE);
+    const float norm = sqrtf(s);
+    const float s2 = norm > 0.0f ? norm : 1.0f;
+#pragma unroll
+    for (int u = 0; u < NU; u++)
+      if (lane + WAVE * u < len) out[lane + WAVE * u] = v[u] / s2;
+    return;
+  }
+  float mx = 0.0f;
   for (size_t t = lane; t < d; t += WAVE) mx = fmaxf(mx, fabsf(row[t]));
   mx = wave_max(mx);
   const float s1 = mx > 0.0f ? mx : 1.0f;
   float s = 0.0f;
   for (size_t c0 = 0; c0 < d; c0 += CH) {
-    int len = (int)min((size_t)CH, d - c0);
-    for (int t = lane; t < len; t += WAVE) {
-      float v = row[c0 + t] / s1;
-      sq[w][t] = v * v;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int len = (int)min((size_t)CH, d - c0);
+    float v[NU];
+    ld_chunk(v, row + c0, len, lane);
+#pragma unroll
+    for (int u = 0; u < NU; u++)
+      if (lane + WAVE * u < len) {
+        const float q = v[u] / s1;
+        sq[w][lane + WAVE * u] = q * q;
+      }
+    wave_sync_lds();
     if (lane == 0) s = seq_add(sq[w], len, s);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    wave_sync_lds();
   }
   s = __shfl(s, 0, WAVE);
-  float norm = sqrtf(s);
+  const float norm = sqrtf(s);
   const float s2 = norm > 0.0f ? norm : 1.0f;
-  float* out = dst + r * d;
-  for (size_t t = lane; t < d; t += WAVE) {
-    float v = row[t] / s1;
-    out[t] = v / s2;
-  }
+  for (size_t t = lane; t < d; t += WAVE) out[t] = (row[t] / s1) / s2;
 }
 
 // EMA step (core/cpu.rs:389-432): all masses decay unless replace; each cluster

@@ -73,12 +73,15 @@ struct Top1Geom {
   bool screen, big, split;
   int row_tiles, ntiles, parts, tpp;
 };
-Top1Geom top1_geom(emh_ctx* c, size_t n, size_t d, size_t k, bool split) {
+Top1Geom top1_geom(emh_ctx* c, size_t n, size_t d, size_t k, bool split, bool small_exact) {
   Top1Geom g{};
   // The screen for any k >= 2 with d >= 32: below that, and for k = 1, the
   // exact scan is as fast. (At small k the exact scan's items leave most
   // lanes idle: 900,000 rows against 40 centroids took 10x the screen's time.)
-  g.screen = c->screen && k >= 2 && d >= 32;
+  // With small_exact, calls of at most c->exact_below row items take the
+  // exact scan too: its one launch beats the screen's three there.
+  g.screen = c->screen && k >= 2 && d >= 32 &&
+             !(small_exact && n * ((k + 63) / 64) <= c->exact_below);
   if (!g.screen) return g;
   const int nt3 = (int)((k + TC3 - 1) / TC3);
   // (k_screen4 addresses a slab's rows with 32-bit offsets: fewer than 2^25 rows.)
@@ -103,11 +106,15 @@ Top1Geom top1_geom(emh_ctx* c, size_t n, size_t d, size_t k, bool split) {
 }
 }  // namespace
 
-bool split_screen(emh_ctx* c, size_t d, size_t k) { return top1_geom(c, 1, d, k, true).split; }
-bool top1_screens(emh_ctx* c, size_t d, size_t k) { return top1_geom(c, 1, d, k, false).screen; }
+bool split_screen(emh_ctx* c, size_t n, size_t d, size_t k) {
+  return top1_geom(c, n, d, k, true, true).split;
+}
+bool top1_screens(emh_ctx* c, size_t n, size_t d, size_t k) {
+  return top1_geom(c, n, d, k, false, true).screen;
+}
 
 size_t top1_scratch_bytes(emh_ctx* c, size_t n, size_t d, size_t k) {
-  const Top1Geom g = top1_geom(c, n, d, k, false);
+  const Top1Geom g = top1_geom(c, n, d, k, false, true);
   if (!g.screen) return exact1_scratch_bytes(n, d, k, false);
   auto r = [](size_t b) { return (b + 255) & ~size_t(255); };
   return r((size_t)g.parts * n * L1 * sizeof(Cand)) + 2 * r(n * 4) +
@@ -128,9 +135,9 @@ struct Top1Screen {
 Top1Screen screen_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
                        size_t lo, size_t n, const float* cents, const float* cnorm, size_t k,
                        bool ip, bool words_clear, Arena* ar, const SplitRows* pre,
-                       const SplitCents* pc) {
+                       const SplitCents* pc, bool small_exact) {
   Top1Screen s;
-  s.g = top1_geom(c, n, d, k, !ar);
+  s.g = top1_geom(c, n, d, k, !ar, small_exact);
   if (!s.g.screen) return s;
   const Top1Geom& g = s.g;
   const size_t cbytes = (size_t)g.parts * n * L1 * sizeof(Cand);
@@ -209,8 +216,8 @@ void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t
   const size_t n = hi - lo;
   EMH_ENSURE(d <= 16384, "top1: d = %zu above the supported 16384", d);
   EMH_ENSURE(n < (1u << 31) && k < (1u << 31), "top1: shape too large");
-  const Top1Screen s =
-      screen_top1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, words_clear, ar, pre, pc);
+  const Top1Screen s = screen_top1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, words_clear, ar,
+                                   pre, pc, !tally);
   EMH_ENSURE(!tally || (s.g.screen && d % 4 == 0),
              "top1: labels are tallied only on the screen with d %% 4 == 0");
   if (!s.g.screen) {
@@ -230,7 +237,8 @@ void screen_margin_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const u
   const size_t n = hi - lo;
   EMH_ENSURE(d <= 16384 && n < (1u << 31) && k < (1u << 31), "top1: shape too large");
   const Top1Screen s =
-      screen_top1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, false, nullptr, nullptr, nullptr);
+      screen_top1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, false, nullptr, nullptr, nullptr,
+                  false);
   if (!s.g.screen) return;  // variant 0: no screen, nothing to measure
   out->variant = s.g.big ? (s.tagged ? EMH_SCREEN_BIG_TAGGED : EMH_SCREEN_BIG_SORTED)
                          : (c->screen == SCREEN_F32 ? EMH_SCREEN_SMALL_F32 : EMH_SCREEN_SMALL_BF16);

@@ -36,6 +36,7 @@ pytestmark = pytest.mark.gpu
 def dev():
     from emeans_amd import HipDevice
     d = HipDevice()
+    d.set_exact_below(0)  # The screens run at every size here
     yield d
     d.close()
 

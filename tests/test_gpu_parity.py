@@ -19,6 +19,7 @@ pytestmark = pytest.mark.gpu
 def dev():
     from emeans_amd import HipDevice
     d = HipDevice()
+    d.set_exact_below(0)  # These tests exercise the screens at small sizes too
     yield d
     d.close()
 
@@ -134,6 +135,27 @@ def test_top1_small_k(dev, screen, k, d, metric):
     mid = (0.5 * (c[0].astype(np.float64) + c[k // 2])).astype(np.float32)
     x[::7] = mid
     _check_top1(dev, x, c, metric, f"small k={k} d={d} {metric}")
+
+
+@pytest.mark.parametrize("metric", ["ip", "l2"])
+def test_small_calls_take_the_exact_scan(dev, metric):
+    """By default, calls of at most 2048 row items (rows x ceil(k / 64)) run the
+    exact kernels alone instead of the screen: a choice of speed only. On both
+    sides of the boundary the bits equal the screened call's and the oracle's."""
+    d = 768
+    for n, k in ((2048, 64), (2049, 64), (1024, 65), (1025, 65), (64, 4), (300, 2)):
+        x = _mix(n, d, 9, 0.4, metric == "ip", n + k)
+        c = (x[(np.arange(k) * 101) % n] * np.float32(0.97)).astype(np.float32)
+        c[k - 1] = c[0]  # the lower id wins
+        dev.set_exact_below(dev.EXACT_BELOW)
+        try:
+            dl, ds = _gpu_top1(dev, x, c, metric)
+        finally:
+            dev.set_exact_below(0)
+        sl, ss = _gpu_top1(dev, x, c, metric)
+        ol, osc = O.top1(x, d, c, metric)
+        assert np.array_equal(dl, ol) and ds.tobytes() == osc.tobytes(), f"n={n} k={k} default"
+        assert np.array_equal(sl, ol) and ss.tobytes() == osc.tobytes(), f"n={n} k={k} screened"
 
 
 def _noise(i):
@@ -383,7 +405,7 @@ def test_scatter_label_out_of_range_fails(dev, k):
     assert dev.read_f32(sums).tobytes() == os_.tobytes()
 
 
-@pytest.mark.parametrize("d", [768, 20, 13, 64, 2500])
+@pytest.mark.parametrize("d", [768, 20, 13, 33, 64, 96, 1000, 1024, 1056, 2500])
 def test_norms_and_normalize(dev, d):
     """contract.rs:500-554: a zero row and a 1e30-scaled row (the max-prescale path)."""
     rows = 300
