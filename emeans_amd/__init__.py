@@ -347,11 +347,11 @@ class HipDevice:
         exact kernels alone. Every mode gives the same bits."""
         check(lib().emh_set_screen(self._ctx, int(mode)))
 
-    EXACT_BELOW = 2048
+    EXACT_BELOW = 4096
 
     def set_exact_below(self, items: int):
-        """Top-1 calls of at most `items` row items (rows x ceil(k / 64)) take
-        the exact kernels alone even when the mode screens (default
+        """Top-1 calls of at most `items` exact items (rows x max(ceil(k / 64),
+        2)) take the exact kernels alone even when the mode screens (default
         EXACT_BELOW); 0 screens every call the mode screens. Same bits."""
         check(lib().emh_set_exact_below(self._ctx, int(items)))
 

@@ -384,7 +384,7 @@ int emh_top1_noalloc(emh_ctx* c, const emh_buf* x, size_t d, const emh_buf* ids,
   return guard([&] {
     const Top1Call t = check_top1(c, x, d, ids, lo, hi, cents, cnorm, k, metric, labels, scores);
     if (hi <= lo) return;
-    const size_t need = emh::top1_scratch_bytes(c, hi - lo, d, k);
+    const size_t need = emh::top1_scratch_bytes(c, hi - lo, d, k, metric == EMH_IP);
     EMH_ENSURE(need <= SCRATCH_BYTES,
                "top1_noalloc: %zu rows x k = %zu x d = %zu need %zu bytes of scratch, above the "
                "fixed %zu",

@@ -551,7 +551,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   // by id instead of splitting them again.
   SplitRows pre_rows{};
   const SplitRows* pre = nullptr;
-  if (split_screen(c, bsz, d, k) && n < (1u << 25)) {
+  if (split_screen(c, bsz, d, k, sph) && n < (1u << 25)) {
     pre_rows = SplitRows{c->xpre.get(halves_bytes(n, d)), (float*)c->xpre_norm.get(n * 4), n,
                          n * 128};
     launch_halves(c, x, n, d, nullptr, 0, n, (void*)pre_rows.xs, (float*)pre_rows.xn, nullptr,
@@ -572,7 +572,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   // the queued-row scan tally the labels they write (counts and the chunk
   // histograms of the counting sort), so scatter_add needs no count launch;
   // the EMA clears both for the next batch.
-  const bool tally = top1_screens(c, bsz, d, k) && d % 4 == 0 && scatter_tallied(bsz, k);
+  const bool tally = top1_screens(c, bsz, d, k, sph) && d % 4 == 0 && scatter_tallied(bsz, k);
   const size_t tstride = tally_stride(bsz);
   uint32_t* tcnt = tally ? (uint32_t*)c->tally_cnt.get(tstride * k * 4) : nullptr;
   if (tally) launch_fill_u32(c, tcnt, tstride * k, 0);

@@ -120,11 +120,20 @@ struct Pinned {
 // Top-1 / top-k path (emh_set_screen): the exact kernels alone, or the MFMA
 // screen in bf16 three-pass or f32 arithmetic ahead of the exact check.
 enum ScreenMode : int { SCREEN_OFF = 0, SCREEN_BF3 = 1, SCREEN_F32 = 2 };
-// Top-1 calls of at most this many row items (rows x ceil(k / 64): the exact
-// scan's passes of a wave over 64 centroids) run the exact kernels alone by
-// default: below it the scan takes less time than the screen's three launches
-// (d = 768: ~30 us for up to 1024 rows at k <= 64 against ~52 us).
-constexpr size_t EXACT_BELOW = 2048;
+// Top-1 calls of at most this many exact items (rows x max(ceil(k / 64), 2))
+// run the exact kernels alone by default: there one launch takes less time
+// than the screen's three (d = 768: the screen ~60 us at any size up to 8,192
+// rows for k <= 16, ~85 us for k = 64 .. 256 up to 4,096 rows).
+constexpr size_t EXACT_BELOW = 4096;
+// Direct selections of at most this many items of the latency-bound scan
+// (k_queued1: 4 rows x 16 centroids each, plus one per 4 rows for L2) take
+// that scan instead of k_exact1 (~13 us against ~32 us at 64 items).
+constexpr size_t QUEUED_DIRECT = 1024;
+// A top-1 call's exact items.
+inline size_t exact_items(size_t n, size_t k) {
+  const size_t g = (k + 63) / 64;
+  return n * (g < 2 ? 2 : g);
+}
 
 // Words of the context's small device block.
 enum SmallWord : int {
@@ -374,11 +383,11 @@ void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t
                  const LabelTally* tally = nullptr);
 // Whether top-1 calls of n rows with d dimensions and k centroids take the
 // split-operand screen (k_screen4), whose rows a caller may split ahead.
-bool split_screen(emh_ctx* c, size_t n, size_t d, size_t k);
+bool split_screen(emh_ctx* c, size_t n, size_t d, size_t k, bool ip);
 // Whether top-1 calls of n rows with d dimensions and k centroids run a
 // screen (and so the check and the queued-row scan). A tallied call always
 // does, whatever its rows.
-bool top1_screens(emh_ctx* c, size_t n, size_t d, size_t k);
+bool top1_screens(emh_ctx* c, size_t n, size_t d, size_t k, bool ip);
 // Split rows of x (n rows, or ids[lo..lo+n)) into bf16 halves in out,
 // slab-major, with their |x|^2 in norm; with part, each of the
 // halves_blocks(n) blocks leaves the largest |x|^2 of its rows and the
@@ -390,7 +399,7 @@ inline size_t halves_bytes(size_t n, size_t d) { return n * ((d + 31) / 32) * 12
 inline size_t halves_blocks(size_t n) { return (n + 7) / 8; }
 // Bytes of fixed-block scratch launch_top1 takes for a call of n rows (an
 // upper bound: each region rounded up to 256 bytes).
-size_t top1_scratch_bytes(emh_ctx* c, size_t n, size_t d, size_t k);
+size_t top1_scratch_bytes(emh_ctx* c, size_t n, size_t d, size_t k, bool ip);
 
 // With rep, the screen runs and its lists are measured (launch_margin) instead
 // of checked: nothing is written to ids or sims.

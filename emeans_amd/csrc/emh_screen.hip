@@ -73,15 +73,18 @@ struct Top1Geom {
   bool screen, big, split;
   int row_tiles, ntiles, parts, tpp;
 };
-Top1Geom top1_geom(emh_ctx* c, size_t n, size_t d, size_t k, bool split, bool small_exact) {
+Top1Geom top1_geom(emh_ctx* c, size_t n, size_t d, size_t k, bool ip, bool split,
+                   bool small_exact) {
   Top1Geom g{};
   // The screen for any k >= 2 with d >= 32: below that, and for k = 1, the
   // exact scan is as fast. (At small k the exact scan's items leave most
   // lanes idle: 900,000 rows against 40 centroids took 10x the screen's time.)
-  // With small_exact, calls of at most c->exact_below row items take the
-  // exact scan too: its one launch beats the screen's three there.
+  // With small_exact, calls of at most c->exact_below exact items, or small
+  // enough for the latency-bound scan, take the exact kernels too: one launch
+  // beats the screen's three there.
   g.screen = c->screen && k >= 2 && d >= 32 &&
-             !(small_exact && n * ((k + 63) / 64) <= c->exact_below);
+             !(small_exact && (exact_items(n, k) <= c->exact_below ||
+                               queued_direct(c, n, d, k, ip)));
   if (!g.screen) return g;
   const int nt3 = (int)((k + TC3 - 1) / TC3);
   // (k_screen4 addresses a slab's rows with 32-bit offsets: fewer than 2^25 rows.)
@@ -106,19 +109,19 @@ Top1Geom top1_geom(emh_ctx* c, size_t n, size_t d, size_t k, bool split, bool sm
 }
 }  // namespace
 
-bool split_screen(emh_ctx* c, size_t n, size_t d, size_t k) {
-  return top1_geom(c, n, d, k, true, true).split;
+bool split_screen(emh_ctx* c, size_t n, size_t d, size_t k, bool ip) {
+  return top1_geom(c, n, d, k, ip, true, true).split;
 }
-bool top1_screens(emh_ctx* c, size_t n, size_t d, size_t k) {
-  return top1_geom(c, n, d, k, false, true).screen;
+bool top1_screens(emh_ctx* c, size_t n, size_t d, size_t k, bool ip) {
+  return top1_geom(c, n, d, k, ip, false, true).screen;
 }
 
-size_t top1_scratch_bytes(emh_ctx* c, size_t n, size_t d, size_t k) {
-  const Top1Geom g = top1_geom(c, n, d, k, false, true);
-  if (!g.screen) return exact1_scratch_bytes(n, d, k, false);
+size_t top1_scratch_bytes(emh_ctx* c, size_t n, size_t d, size_t k, bool ip) {
+  const Top1Geom g = top1_geom(c, n, d, k, ip, false, true);
+  if (!g.screen) return exact1_scratch_bytes(c, n, d, k, ip, false);
   auto r = [](size_t b) { return (b + 255) & ~size_t(255); };
   return r((size_t)g.parts * n * L1 * sizeof(Cand)) + 2 * r(n * 4) +
-         exact1_scratch_bytes(n, d, k, true);
+         exact1_scratch_bytes(c, n, d, k, ip, true);
 }
 
 namespace {
@@ -137,7 +140,7 @@ Top1Screen screen_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const ui
                        bool ip, bool words_clear, Arena* ar, const SplitRows* pre,
                        const SplitCents* pc, bool small_exact) {
   Top1Screen s;
-  s.g = top1_geom(c, n, d, k, !ar, small_exact);
+  s.g = top1_geom(c, n, d, k, ip, !ar, small_exact);
   if (!s.g.screen) return s;
   const Top1Geom& g = s.g;
   const size_t cbytes = (size_t)g.parts * n * L1 * sizeof(Cand);

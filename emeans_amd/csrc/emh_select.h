@@ -169,7 +169,15 @@ void launch_exact1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32
                    const float* cnorm, size_t k, bool ip, uint32_t* labels, float* scores,
                    Arena* ar = nullptr, const LabelTally* tally = nullptr);
 // Fixed-block bytes launch_exact1 takes for n rows (an upper bound).
-size_t exact1_scratch_bytes(size_t n, size_t d, size_t k, bool list);
+size_t exact1_scratch_bytes(emh_ctx* c, size_t n, size_t d, size_t k, bool ip, bool list);
+// The latency-bound scan's (k_queued1's) items for n rows against k centroids.
+size_t queued_items(size_t n, size_t k, bool ip);
+// Whether a direct selection of n rows takes the latency-bound scan instead
+// of k_exact1: d % 4 == 0 and at most QUEUED_DIRECT of its items (and the
+// context's exact_below not 0, which keeps k_exact1 for every selection).
+inline bool queued_direct(emh_ctx* c, size_t n, size_t d, size_t k, bool ip) {
+  return d % 4 == 0 && c->exact_below > 0 && queued_items(n, k, ip) <= QUEUED_DIRECT;
+}
 void launch_exactk(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,
                    size_t kk, bool exclude_self, const uint32_t* fb, uint32_t* ids, float* sims);
 

@@ -332,8 +332,8 @@ __device__ __forceinline__ bool unpack_best(uint64_t w, float& key, uint32_t& id
 }
 
 __global__ __launch_bounds__(64) void k_queued1(
-    const float* __restrict__ x, size_t nx, int d, const uint32_t* __restrict__ ids,
-    const uint32_t* __restrict__ list, uint32_t* __restrict__ small,
+    const float* __restrict__ x, size_t nx, int d, const uint32_t* __restrict__ ids, size_t lo,
+    int n_direct, const uint32_t* __restrict__ list, uint32_t* __restrict__ small,
     const float* __restrict__ cents, const float* __restrict__ cnorm, int k, int ip,
     unsigned long long* __restrict__ best, uint32_t* __restrict__ tickets,
     float* __restrict__ xnq, uint32_t* __restrict__ labels, float* __restrict__ scores,
@@ -342,8 +342,10 @@ __global__ __launch_bounds__(64) void k_queued1(
   __shared__ v4f cs[QU * QJ];
   __shared__ v4f xs[QU * QR];
   __shared__ uint32_t xid_s[QR];
-  const int nrows = (int)small[SW_FALLBACK_COUNT];
-  if (blockIdx.x == 0 && threadIdx.x == 0) small[SW_FALLBACK_TOTAL] += (uint32_t)nrows;
+  // Queued rows (list: positions, count on the device), or a direct
+  // selection of n_direct rows at positions lo, lo + 1, ...
+  const int nrows = list ? (int)small[SW_FALLBACK_COUNT] : n_direct;
+  if (list && blockIdx.x == 0 && threadIdx.x == 0) small[SW_FALLBACK_TOTAL] += (uint32_t)nrows;
   const int nch = (k + QJ - 1) / QJ;
   const int per = nch + (ip ? 0 : 1);  // items per group (the last one: |x|^2)
   const int ngr = (nrows + QR - 1) / QR;
@@ -356,7 +358,8 @@ __global__ __launch_bounds__(64) void k_queued1(
       const int f = g * QR + lane;
       uint32_t xid = NONE;
       if (f < nrows) {
-        const size_t id = ids ? (size_t)ids[list[f]] : (size_t)list[f];
+        const size_t p = list ? (size_t)list[f] : lo + (size_t)f;
+        const size_t id = ids ? (size_t)ids[p] : p;
         if (id < nx)
           xid = (uint32_t)id;
         else
@@ -442,7 +445,7 @@ __global__ __launch_bounds__(64) void k_queued1(
           float bk = INFINITY;
           uint32_t bid = 0;  // nothing wins: label 0 and the initial score
           unpack_best(w, bk, bid);
-          const size_t p = list[f];
+          const size_t p = list ? (size_t)list[f] : lo + (size_t)f;
           labels[p] = bid;
           scores[p] = ip ? -bk : fmaxf(xnq[f] + bk, 0.0f);
           if (tcnt) {  // the tally (few rows: one atomic each)
@@ -581,9 +584,14 @@ __global__ __launch_bounds__(256) void k_exactk(const float* __restrict__ q, int
 
 }  // namespace
 
-size_t exact1_scratch_bytes(size_t n, size_t d, size_t k, bool list) {
+// The latency-bound scan's items for n rows against k centroids.
+size_t queued_items(size_t n, size_t k, bool ip) {
+  return ((n + QR - 1) / QR) * ((k + QJ - 1) / QJ + (ip ? 0 : 1));
+}
+
+size_t exact1_scratch_bytes(emh_ctx* c, size_t n, size_t d, size_t k, bool ip, bool list) {
   auto r = [](size_t b) { return (b + 255) & ~size_t(255); };
-  if (list && d % 4 == 0) {
+  if ((list && d % 4 == 0) || (!list && queued_direct(c, n, d, k, ip))) {
     const size_t ngr = (n + QR - 1) / QR;
     return r(n * 8 + ngr * 4) + r(n * 4);
   }
@@ -599,7 +607,10 @@ void launch_exact1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32
   EMH_ENSURE(!tally || (list && d % 4 == 0), "exact: a tally needs the queued-row scan");
   // Both kernels read row 0 in place of a row whose id is out of range.
   EMH_ENSURE(nx > 0, "top1: a selection of %zu rows over no data rows", n);
-  if (list && d % 4 == 0) {  // queued rows, few: the latency-bound scan
+  // Queued rows (few), or a small direct selection: the latency-bound scan.
+  // (k_exact1's tiles each wait a memory round trip: ~30 us at any size up
+  // to a few thousand rows.)
+  if ((list && d % 4 == 0) || (!list && queued_direct(c, n, d, k, ip))) {
     const size_t ngr = (n + QR - 1) / QR;
     const size_t per = (k + QJ - 1) / QJ + (ip ? 0 : 1);
     // Self-cleaning: the best words, then the tickets, all left at zero (a
@@ -615,8 +626,9 @@ void launch_exact1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32
       xnq = (float*)c->knn_tmp.get(n * 4);
     }
     const unsigned g = (unsigned)std::min<size_t>(ngr * per, (size_t)2 * c->cus);
-    hipLaunchKernelGGL(k_queued1, dim3(g), dim3(64), 0, c->stream, x, nx, (int)d, ids, list,
-                       c->small, cents, cnorm, (int)k, ip ? 1 : 0, (unsigned long long*)z,
+    hipLaunchKernelGGL(k_queued1, dim3(g), dim3(64), 0, c->stream, x, nx, (int)d, ids, lo,
+                       (int)n, list, c->small, cents, cnorm, (int)k, ip ? 1 : 0,
+                       (unsigned long long*)z,
                        (uint32_t*)(z + n * 8), xnq, labels, scores,
                        tally ? tally->cnt : nullptr, tally ? tally->counts : nullptr,
                        tally ? tally->lo : 0, tally ? tally->stride : 0);

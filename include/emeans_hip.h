@@ -365,12 +365,13 @@ uint64_t emh_fallback_rows(emh_ctx* ctx);
  * 0 = exact kernels only (the reference "FP32 kernel alone", emeans-cuda
  * tests/contract.rs:27-37). Results are the same bits in every mode. */
 int emh_set_screen(emh_ctx* ctx, int on);
-/* Top-1 calls of at most `items` row items (rows x ceil(k / 64)) run the exact
- * kernels alone even when the mode screens (default 2048: there one exact
- * launch takes less time than the screen's three); 0 screens every call the
- * mode screens. A training run decides once, by its batch size. Results are
- * the same bits either way. No reference counterpart (a performance knob of
- * this backend, like emh_set_screen). */
+/* Top-1 calls of at most `items` exact items (rows x max(ceil(k / 64), 2))
+ * run the exact kernels alone even when the mode screens (default 4096: there
+ * one exact launch takes less time than the screen's three); 0 screens every
+ * call the mode screens and keeps the exact scan of a call without the screen
+ * on its throughput kernel. A training run decides once, by its batch size.
+ * Results are the same bits either way. No reference counterpart (a
+ * performance knob of this backend, like emh_set_screen). */
 int emh_set_exact_below(emh_ctx* ctx, uint64_t items);
 /* Ops that emh_profile times. */
 #define EMH_PROF_SCREEN 0  /* the MFMA screen kernel of top-1 and top-k; units: 2 rows k d FLOP */

@@ -139,11 +139,14 @@ def test_top1_small_k(dev, screen, k, d, metric):
 
 @pytest.mark.parametrize("metric", ["ip", "l2"])
 def test_small_calls_take_the_exact_scan(dev, metric):
-    """By default, calls of at most 2048 row items (rows x ceil(k / 64)) run the
-    exact kernels alone instead of the screen: a choice of speed only. On both
-    sides of the boundary the bits equal the screened call's and the oracle's."""
+    """By default, calls of at most 4096 exact items (rows x max(ceil(k / 64), 2)),
+    or of at most 1024 items of the latency-bound scan (4 rows x 16 centroids,
+    d % 4 == 0), run the exact kernels alone instead of the screen: a choice of
+    speed only. On both sides of each boundary the bits equal the screened
+    call's and the oracle's."""
     d = 768
-    for n, k in ((2048, 64), (2049, 64), (1024, 65), (1025, 65), (64, 4), (300, 2)):
+    for n, k in ((2048, 64), (2049, 64), (2048, 65), (2049, 65), (64, 4), (300, 2),
+                 (4096, 2), (4097, 2), (1024, 256), (1025, 256)):
         x = _mix(n, d, 9, 0.4, metric == "ip", n + k)
         c = (x[(np.arange(k) * 101) % n] * np.float32(0.97)).astype(np.float32)
         c[k - 1] = c[0]  # the lower id wins
