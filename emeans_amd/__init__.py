@@ -309,6 +309,21 @@ class HipDevice:
                 "calinski_harabasz": r.calinski_harabasz, "davies_bouldin": r.davies_bouldin,
                 "objective": r.objective, "sizes": sizes.astype(np.int64)}
 
+    def dots(self, a: np.ndarray, b: np.ndarray) -> np.ndarray:
+        """gemm_nt (emeans-core/src/assign.rs:813-825) on the device: the
+        (m x nb) dots of the rows of a (m x d) with the rows of b (nb x d),
+        each one fma chain over the columns in order."""
+        a, b = np.ascontiguousarray(a, np.float32), np.ascontiguousarray(b, np.float32)
+        if a.ndim != 2 or b.ndim != 2 or a.shape[1] != b.shape[1]:
+            raise ValueError("a and b must be m x d and nb x d")
+        m, nb, d = a.shape[0], b.shape[0], a.shape[1]
+        if m == 0 or nb == 0:
+            return np.zeros((m, nb), np.float32)
+        ab, bb = self.upload_f32(a), self.upload_f32(b)
+        out = self.zeros_f32(m * nb)
+        check(lib().emh_dots(self._ctx, ab.h, m, bb.h, nb, d, out.h))
+        return self.read_f32(out).reshape(m, nb)
+
     SCREEN_VARIANTS = {0: "none", 1: "big_tagged", 2: "big_sorted", 3: "small_bf16",
                        4: "small_f32"}
 
@@ -643,14 +658,7 @@ class Emeans:
 
     def save(self, path):
         """Write the model file to a temporary file, then rename it over path (io.rs:74-88)."""
-        import os
-        b = self.to_bytes()
-        tmp = os.path.splitext(str(path))[0] + ".tmp"
-        with open(tmp, "wb") as f:
-            f.write(b)
-            f.flush()
-            os.fsync(f.fileno())
-        os.replace(tmp, path)
+        model_file.save_bytes(path, self.to_bytes())
 
     @classmethod
     def from_bytes_with(cls, b, assigner: Optional[HipDevice] = None) -> "Emeans":

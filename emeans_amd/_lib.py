@@ -127,6 +127,7 @@ SIGNATURES = {
     "emh_fallback_rows": (_u64, [_vp]),
     "emh_kmeans_pp": (_i, [_vp, _vp, _sz, _sz, _sz, _u32, _vp, C.POINTER(_sz)]),
     "emh_internal_scores": (_i, [_vp, _vp, _sz, _sz, _vp, _sz, _vp, _vp]),
+    "emh_dots": (_i, [_vp, _vp, _sz, _vp, _sz, _sz, _vp]),
     "emh_screen_margin": (_i, [_vp, _vp, _sz, _vp, _sz, _sz, _vp, _vp, _sz, _i, _vp]),
     "emh_screen_margin_topk": (_i, [_vp, _vp, _sz, _vp, _sz, _sz, _i, _vp]),
     "emh_set_screen": (_i, [_vp, _i]),

@@ -37,7 +37,7 @@ class AutoConfig:
     split_min_silhouette: float = 0.05
     restarts: int = 4
     nepochs: float = 5.0
-    init: str = "kmeans_plus_plus"  # or "random_rows"
+    init: str = "k_means_plus_plus"  # or "random_rows"
     level1_method: str = "bottom_up"  # or "top_down"
     resplit_passes: int = 2
     level1_max_share: float = 0.5
@@ -56,6 +56,22 @@ class KScore:
     objective: float
     browsable: float
     seconds: float
+
+
+@dataclass
+class Diagnostics:
+    """Sweep results (auto.rs:209-238): the level-1 candidates, each group's
+    level-2 sweep, seconds, the stage-A level-1 sweep, resplits, leaves, the
+    gap cut, flatness and the rejected cuts."""
+    level1: list = field(default_factory=list)
+    level2: list = field(default_factory=list)
+    seconds: float = 0.0
+    stage_a_level1: list = field(default_factory=list)
+    resplits: int = 0
+    leaves: int = 0
+    gap_k: int = 0
+    flat: bool = False
+    level1_rejected: list = field(default_factory=list)
 
 
 @dataclass
@@ -136,7 +152,7 @@ def sweep(dev: HipDevice, x: np.ndarray, xb, ks: List[int], cfg: AutoConfig, sal
     kmax = max(ks) if ks else 1
     t0 = time.perf_counter()
     inits = [dev.kmeans_pp(xb, n, d, kmax, seed_for(cfg, salt, 0, r))
-             if cfg.init == "kmeans_plus_plus" else None for r in range(max(cfg.restarts, 1))]
+             if cfg.init == "k_means_plus_plus" else None for r in range(max(cfg.restarts, 1))]
     tm["kmeans_pp_s"] += time.perf_counter() - t0
     out = []
     for k in ks:

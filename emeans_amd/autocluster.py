@@ -22,7 +22,7 @@ plus the rest in order); f64 row sums are sequential, as unit_means'.
 
 import sys
 import time
-from dataclasses import dataclass, field
+from dataclasses import dataclass
 from typing import List, Optional
 
 import numpy as np
@@ -30,6 +30,7 @@ import numpy as np
 from . import HipDevice
 from . import auto
 from . import hierarchy as H
+from .auto import Diagnostics
 
 SCREEN_K = 4  # auto.rs:663
 
@@ -41,20 +42,6 @@ class Leaves:
     rows: List[np.ndarray]
     parent: List[int]
     sweep: List[Optional[float]]
-
-
-@dataclass
-class Diagnostics:
-    """auto.rs:209-238."""
-    level1: list = field(default_factory=list)
-    level2: list = field(default_factory=list)
-    seconds: float = 0.0
-    stage_a_level1: list = field(default_factory=list)
-    resplits: int = 0
-    leaves: int = 0
-    gap_k: int = 0
-    flat: bool = False
-    level1_rejected: list = field(default_factory=list)
 
 
 def _fmax_fold(vals) -> float:
@@ -297,6 +284,20 @@ def group_bottom_up(dev: HipDevice, x: np.ndarray, xb, cfg, leaves: Leaves,
     return cut(l, merges, ks[best])
 
 
+def _decision(members: List[int], leaves: Leaves, size: int, cfg):
+    """auto.rs:1058-1072: why a group has its level-2 k."""
+    if len(members) >= 2:
+        return H.decision_split(len(members))
+    b = leaves.sweep[members[0]]
+    if b is not None and b < cfg.split_min_silhouette:
+        return H.decision_no_structure(b)
+    if size < cfg.min_split_size or size <= cfg.max_cluster_size:
+        return H.DECISION_TOO_SMALL
+    if b is not None:
+        return H.decision_no_structure(b)
+    return H.DECISION_TOO_SMALL
+
+
 def auto_cluster(dev: HipDevice, x: np.ndarray, cfg, inc: Optional[H.IncrementalConfig] = None,
                  timing: Optional[dict] = None):
     """auto.rs:1001-1101: (Hierarchy, Labels) of the unit rows of x. With
@@ -350,12 +351,12 @@ def auto_cluster(dev: HipDevice, x: np.ndarray, cfg, inc: Optional[H.Incremental
         model = H.model_from(H.unit_means(x, rows), counts, d, cfg.nepochs, cfg.seed)
         group_rows.append(np.concatenate(rows) if rows else np.zeros(0, np.int64))
         k2 = len(members)
-        groups.append(H.Group(model, list(range(k2)), np.full(k2, np.nan, np.float32), k2))
+        groups.append(H.Group(model, list(range(k2)), np.full(k2, np.nan, np.float32), k2,
+                              _decision(members, leaves, sum(counts), cfg)))
     counts1 = [len(r) for r in group_rows]
     level1 = H.model_from(H.unit_means(x, group_rows), counts1, d, cfg.nepochs, cfg.seed)
     h = H.Hierarchy(d, level1, groups, list(range(k1)), H.State.new(n, k1),
-                    H.HipBackend(dev), inc or H.IncrementalConfig(), cfg.nepochs, cfg.seed)
-    h.retrain = lambda xa, hh=h: full_retrain(dev, hh, xa, cfg)
+                    H.HipBackend(dev), inc or H.IncrementalConfig(), config=cfg)
     h.diagnostics = diag
     labels = h.assign(x)
     h.set_floors(labels)

@@ -1446,6 +1446,22 @@ int emh_internal_scores(emh_ctx* c, const emh_buf* x, size_t n, size_t d, const 
   });
 }
 
+int emh_dots(emh_ctx* c, const emh_buf* a, size_t m, const emh_buf* b, size_t nb, size_t d,
+             emh_buf* out) {
+  return guard2([&] {
+    EMH_ENSURE(c && a && b && out, "null argument");
+    EMH_ENSURE(a->kind == 0 && b->kind == 0 && out->kind == 0, "a, b and out must be f32 buffers");
+    EMH_ENSURE(d > 0 && d < (1ull << 31), "d must be positive");
+    EMH_ENSURE(nb < (1ull << 31), "dots: too many b rows");
+    EMH_ENSURE(a->len >= m * d && b->len >= nb * d, "a must be m x d and b nb x d");
+    EMH_ENSURE(out->len >= m * nb, "out must hold m x nb");
+    if (m == 0 || nb == 0) return;
+    EMH_HIP(hipSetDevice(c->device));
+    emh::launch_row_dots(c, (const float*)a->ptr, m, d, (const float*)b->ptr, nb, (float*)out->ptr,
+                    nullptr);
+  });
+}
+
 // Host-side pieces of the loop, exported for checks that need no device.
 void emh_host_permutation(uint32_t seed, uint64_t n, uint32_t* out) {
   RandomState::permutation_into(seed, n, out);

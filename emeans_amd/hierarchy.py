@@ -10,25 +10,31 @@ model per group (its leaves). What runs on the device:
   Hierarchy.add      incremental.rs:306-360   label new rows, then by the
                                         policy: nothing, the EMA update, or a
                                         full retrain
+  grow               incremental.rs:376-458   new leaves from coherent pending
+                                        outliers: the candidates' pairwise dots
+                                        and their dots with each trial mean on
+                                        the device (fma chains)
   ema_update         incremental.rs:546-596   each group's leaves resume from
                                         their EMA state on the group's rows
                                         (the training loop on the device); the
                                         level 1 follows its groups' means
 
-and on the host, as in the reference: the outlier floors (auto.rs:1194-1292),
+and on the host, as in the reference: the outlier floors (auto.rs:1194-1300),
 the policy, the centroid matching that keeps stable ids (incremental.rs:
-176-290), unit means (auto.rs:750-765) and model_from (auto.rs:955-987).
+176-290), unit means (auto.rs:750-765), model_from (auto.rs:955-987), the
+new leaf's placement (incremental.rs:460-538) and the hierarchy files
+(incremental.rs:862-1073: a directory or one blob, each model in the model
+file layout).
 
 The full retrain runs auto_cluster (emeans_amd.autocluster) on all rows.
-Not built here: the grow step's leaf formation from pending outliers
-(incremental.rs:376-540); its early exits are kept, and a call that would
-form leaves raises NotImplementedError rather than returning other results.
 
-The device work goes through a backend object with two methods, so that the
-same host logic runs over any device:
+The device work goes through a backend object, so that the same host logic
+runs over any device:
   leaf_top1(x, cents) -> (labels u32, sims f32)   top-1 by inner product
-  resume(config, x, positions, usage) -> (centroids, positions, usage)
-HipBackend is the gfx950 one.
+  resume(config, x, positions, usage) -> (centroids, positions, usage[, run])
+  dots(a, b) -> a b^T                             f32 dots (grow)
+HipBackend is the gfx950 one; it also returns each resumed run's record
+(recipe, splits, epoch statistics) for the model files.
 """
 
 import math
@@ -37,7 +43,8 @@ from typing import List, Optional
 
 import numpy as np
 
-from . import Config, HipDevice, recipe_batch
+from . import Config, HipDevice, _epoch_rows, model_file, recipe_batch
+from .auto import AutoConfig, Diagnostics, KScore
 
 MAD_SIGMA = np.float32(1.4826)  # auto.rs:1220
 OWN_SPREAD_MIN = 20             # auto.rs:1217
@@ -76,24 +83,64 @@ class State:
 
 @dataclass
 class Model:
-    """An e-means model's state: its config, centroids and EMA state (k x d)."""
+    """An e-means model's state: its config, centroids and EMA state (k x d),
+    and what its last run recorded (recipe, splits, per-epoch statistics as
+    (obj, time, imbalance_factor, nsplit)); a model made by model_from has
+    run nothing (io.rs Snapshot with recipe None)."""
     config: Config
     centroids: np.ndarray
     positions: np.ndarray
     usage: np.ndarray
+    recipe: Optional[dict] = None
+    n_splits: int = 0
+    stats: list = field(default_factory=list)
 
     @property
     def k(self) -> int:
         return self.config.k
 
+    def to_bytes(self) -> bytes:
+        """The model file's bytes (io.rs:92-121)."""
+        return model_file.to_bytes(self.config, self.recipe, self.n_splits, self.stats,
+                                   self.centroids, self.positions,
+                                   self.usage if self.usage is not None else [])
+
+    @staticmethod
+    def from_bytes(b) -> "Model":
+        """A model from a model file's bytes (io.rs:137-186)."""
+        header, cent, pos, usage = model_file.from_bytes(b)
+        cfg = Config(**header["config"])
+        if cent is None:
+            raise ValueError("model has no centroids")
+        stats = [(s["obj"], s["time"], s["imbalance_factor"], int(s["nsplit"]))
+                 for s in header["iteration_stats"]]
+        return Model(cfg, cent.reshape(cfg.k, cfg.d), pos, usage, header["recipe"],
+                     int(header["n_splits"]), stats)
+
+
+def decision_split(k: int):
+    """GroupDecision::Split (auto.rs:195-206) as serde writes it."""
+    return {"split": {"k": int(k)}}
+
+
+def decision_no_structure(best: float):
+    """GroupDecision::NoStructure (auto.rs:195-206) as serde writes it."""
+    return {"no_structure": {"best_silhouette": float(best)}}
+
+
+DECISION_EMPTY, DECISION_TOO_SMALL = "empty", "too_small"
+
 
 @dataclass
 class Group:
-    """A level-1 slot (auto.rs Group): its leaves' model, their stable ids and outlier floors."""
+    """A level-1 slot (auto.rs Group): its leaves' model, their stable ids,
+    outlier floors, the next unused id and why it has the level-2 k it has
+    (GroupDecision, held as its serde value)."""
     model: Optional[Model]
     ids: List[int]
     floors: np.ndarray
     next_id: int
+    decision: object = DECISION_TOO_SMALL
 
 
 @dataclass
@@ -129,9 +176,17 @@ class HipBackend:
         return self.dev.assign(x, x.shape[1], cents, "ip", 1 << 16)
 
     def resume(self, config: Config, x: np.ndarray, positions, usage):
+        """train_resume on x: (centroids, positions, usage, the run's record)."""
         n, d = x.shape
         cent, info = self.dev.train_dev(self.dev.bind(x), n, config, state=(positions, usage))
-        return cent, info["positions"], info["usage"]
+        run = {"recipe": model_file.recipe_dict(config, n, info["batch_size"], info["alpha0"],
+                                                _epoch_rows(n, config), self.dev.name()),
+               "n_splits": info["n_splits"],
+               "stats": [(s.obj, s.time, s.imbalance_factor, s.nsplit) for s in info["stats"]]}
+        return cent, info["positions"], info["usage"], run
+
+    def dots(self, a: np.ndarray, b: np.ndarray) -> np.ndarray:
+        return self.dev.dots(a, b)
 
 
 # ---------------------------------------------------------------- host rules
@@ -192,6 +247,22 @@ def leaf_floors(sims: List[np.ndarray], inc: IncrementalConfig) -> List[np.float
         else:
             out.append(np.float32(np.fmin.reduce(v, initial=np.inf)))  # fold(inf, f32::min)
     return out
+
+
+def pooled_floor(median, sp: Spread, inc: IncrementalConfig) -> np.float32:
+    """auto.rs:1294-1300: the floor of a leaf whose median member cosine is
+    median, with the pooled spread (f32, left to right)."""
+    if inc.outlier_min_sim is not None:
+        return np.float32(inc.outlier_min_sim)
+    return np.float32(np.float32(median) - np.float32(inc.outlier_mad_k) * MAD_SIGMA *
+                      sp.pooled_mad)
+
+
+def _dot_sum(a: np.ndarray, b: np.ndarray) -> np.float32:
+    """The f32 sum, in order, of the rounded products a_t b_t
+    (incremental.rs:462, iterator sum)."""
+    p = (np.asarray(a, np.float32) * np.asarray(b, np.float32)).astype(np.float32)
+    return np.float32(np.add.accumulate(p, dtype=np.float32)[-1]) if p.size else np.float32(0)
 
 
 def hungarian(cost: List[List[float]]) -> List[int]:
@@ -344,13 +415,16 @@ class Hierarchy:
 
     def __init__(self, d: int, level1: Model, groups: List[Group], ids1: List[int],
                  state: State, backend, inc: Optional[IncrementalConfig] = None,
-                 nepochs: float = 5.0, seed: int = 1234):
+                 nepochs: float = 5.0, seed: int = 1234, config: Optional[AutoConfig] = None,
+                 dedup=None):
         self.d, self.level1, self.groups, self.ids1 = d, level1, groups, ids1
         self.state, self.backend = state, backend
         self.inc = inc or IncrementalConfig()
-        self.nepochs, self.seed = nepochs, seed
-        self.retrain = None  # full retrain (x_all) -> None, set by auto_cluster
-        self.diagnostics = None
+        # The AutoConfig the hierarchy was built with (its policy is self.inc).
+        self.config = config if config is not None else AutoConfig(nepochs=nepochs, seed=seed)
+        self.nepochs, self.seed = self.config.nepochs, self.config.seed
+        self.dedup = dedup  # DedupConfig used upstream, or None
+        self.diagnostics = Diagnostics()
 
     @staticmethod
     def from_models(x: np.ndarray, level1: Model, leaves: List[Optional[Model]], backend,
@@ -365,6 +439,25 @@ class Hierarchy:
                       State.new(x.shape[0], level1.k), backend, inc, nepochs, seed)
         h.set_floors(h.assign(x))
         return h
+
+    # -- files (incremental.rs:862-1047); the functions are below the class
+    def to_bytes(self) -> bytes:
+        """The hierarchy as one blob (incremental.rs:898-915)."""
+        return _hierarchy_to_bytes(self)
+
+    @staticmethod
+    def from_bytes(b, backend) -> "Hierarchy":
+        """A hierarchy from the bytes of to_bytes (incremental.rs:917-946)."""
+        return _hierarchy_from_bytes(b, backend)
+
+    def save(self, path):
+        """Write the hierarchy to directory path, replaced as a whole (incremental.rs:864-894)."""
+        _hierarchy_save(self, path)
+
+    @staticmethod
+    def load(path, backend) -> "Hierarchy":
+        """A hierarchy written by save (incremental.rs:978-988)."""
+        return _hierarchy_load(path, backend)
 
     def level1_centroids(self) -> np.ndarray:
         return self.level1.centroids
@@ -477,29 +570,145 @@ class Hierarchy:
         if action == "EmaUpdate":
             new_leaves = self.ema_update(x_all)
         elif action == "FullRetrain":
-            if self.retrain is None:
-                raise NotImplementedError("a full retrain needs a hierarchy from auto_cluster")
-            self.retrain(x_all)
+            self.full_retrain(x_all)
         return AddReport(action, self.assign(x_all), new_outliers, len(self.state.pending),
                          outlier_fraction, new_leaves)
 
-    def _grow(self, x_all: np.ndarray):
-        """incremental.rs:376-395: the grow step's early exits; forming leaves
-        from coherent pending outliers is not built here."""
-        min_size = self.inc.grow_min_size
+    def full_retrain(self, x_all: np.ndarray):
+        """incremental.rs:598-633: auto_cluster on all rows on the device,
+        old ids carried over (emeans_amd.autocluster.full_retrain)."""
+        dev = getattr(self.backend, "dev", None)
+        if dev is None:
+            raise NotImplementedError("a full retrain runs auto_cluster on a device backend")
+        from . import autocluster
+        autocluster.full_retrain(dev, self, x_all, self.config)
+
+    def grow(self, x_all: np.ndarray):
+        """incremental.rs:376-458: new leaves from the pending rows that are
+        still outliers and form coherent groups. The row with the most
+        candidates within `pair` seeds a group; four rounds of mean and
+        members (within the pooled floor of the leaves' 10 % median cosine,
+        and nearer than their current leaf); a group of grow_min_size rows
+        whose median cosine to its mean reaches that cohesion becomes a leaf
+        (add_leaf); three failed seeds end the search. The dots (gemm_nt in
+        the reference) run on the backend: the device's fma chains."""
+        d, inc = self.d, self.inc
+        min_size = inc.grow_min_size
+        made = []
         if min_size == 0 or len(self.state.pending) < min_size:
-            return []
+            return made
         labels = self.assign(x_all)
-        pend = [i for i in self.state.pending if labels.outlier[i]]
-        if len(pend) < min_size:
-            return []
-        raise NotImplementedError("forming leaves from pending outliers (grow) is not built here")
+        pend = np.asarray([i for i in self.state.pending if labels.outlier[i]], np.int64)
+        p = len(pend)
+        if p < min_size:
+            return made
+        _, sims = self.leaf_sims(labels)
+        sp = spread(sims)
+        medians = [m for m in sp.median if np.isfinite(m)]
+        cohesion = quantile(np.asarray(medians, np.float32), 0.10)
+        floor = pooled_floor(cohesion, sp, inc)
+        if not np.isfinite(floor):
+            raise ValueError("no leaf statistics to grow from")
+        f0 = np.float32(max(floor, np.float32(0.0)))
+        pair = np.float32(f0 * f0)
+        xp = np.ascontiguousarray(x_all[pend], np.float32)
+        cur = labels.sim[pend].astype(np.float32)
+        degree = np.zeros(p, np.int64)
+        for b0 in range(0, p, 1024):
+            out = self.backend.dots(xp[b0:b0 + 1024], xp)
+            degree[b0:b0 + len(out)] = ((out >= pair).sum(axis=1) - 1) & 0xFFFFFFFF
+
+        def to(c):
+            return self.backend.dots(xp, np.asarray(c, np.float32).reshape(1, d))[:, 0]
+
+        def mean_of(mem):
+            return unit_means(xp, [np.asarray(mem, np.int64)])[0]
+
+        free = np.ones(p, bool)
+        tried = np.zeros(p, bool)
+        fails = 0
+        while fails < 3 and int(free.sum()) >= min_size:
+            cand = np.flatnonzero(free & ~tried)
+            if len(cand) == 0:
+                break
+            # max_by_key((degree, Reverse(t))): the highest degree, then the lowest t
+            seed = int(cand[np.lexsort((cand, -degree[cand]))[0]])
+            tried[seed] = True
+            s0 = to(xp[seed])
+            mem = np.flatnonzero(free & (s0 >= pair))
+            for _ in range(4):
+                if len(mem) < min_size:
+                    break
+                s = to(mean_of(mem))
+                mem = np.flatnonzero(free & (s >= floor) & (s > cur))
+            if len(mem) < min_size:
+                fails += 1
+                continue
+            center = mean_of(mem)
+            s = to(center)
+            if quantile(s[mem], 0.5) < cohesion:
+                fails += 1
+                continue
+            free[mem] = False
+            made.append(self.add_leaf(center, len(mem), labels))
+        return made
+
+    def add_leaf(self, center: np.ndarray, rows: int, labels: Labels):
+        """incremental.rs:460-538: the new leaf joins the level-1 group (of two
+        or more leaves) whose centroid it is as close to as that group's own
+        leaves are, the closest such group; otherwise it becomes a new level-1
+        group. Slots are appended; models are rebuilt by model_from with the
+        current labels' counts. Returns the leaf's stable (level-1, leaf) ids."""
+        d = self.d
+        center = np.asarray(center, np.float32).reshape(d)
+        c1 = self.level1_centroids().reshape(-1, d)
+        home = None
+        for g, grp in enumerate(self.groups):
+            m = grp.model
+            if m is None or m.k < 2:
+                continue
+            cg = c1[g]
+            reach = np.float32(np.inf)
+            for leaf in m.centroids.reshape(-1, d):
+                v = _dot_sum(leaf, cg)
+                if not np.isnan(v):
+                    reach = min(reach, v)  # fold(inf, f32::min)
+            s = _dot_sum(center, cg)
+            if s >= reach and (home is None or s > home[0]):
+                home = (s, g)
+        ng = len(self.groups)
+        count1 = np.bincount(labels.slot1.astype(np.int64), minlength=ng)[:ng]
+        if home is not None:
+            g = home[1]
+            grp = self.groups[g]
+            k = grp.model.k
+            cents = np.concatenate([grp.model.centroids.reshape(k, d), center[None, :]])
+            sel = labels.slot1 == g
+            counts = np.bincount(labels.slot2[sel].astype(np.int64), minlength=k)[:k]
+            counts = [max(int(c), 1) for c in counts] + [rows]
+            grp.model = model_from(cents, counts, d, self.nepochs, self.seed)
+            nid = grp.next_id
+            grp.next_id += 1
+            grp.ids.append(nid)
+            grp.floors = np.append(grp.floors.astype(np.float32), np.float32(np.nan))
+            grp.decision = decision_split(k + 1)
+            return (self.ids1[g], nid)
+        model = model_from(center[None, :], [rows], d, self.nepochs, self.seed)
+        self.groups.append(Group(model, [0], np.full(1, np.nan, np.float32), 1,
+                                 DECISION_TOO_SMALL))
+        id1 = self.state.next_id1
+        self.state.next_id1 += 1
+        self.ids1.append(id1)
+        cents1 = np.concatenate([c1, center[None, :]])
+        counts1 = [max(int(c), 1) for c in count1] + [rows]
+        self.level1 = model_from(cents1, counts1, d, self.nepochs, self.seed)
+        return (id1, 0)
 
     def ema_update(self, x_all: np.ndarray):
         """incremental.rs:546-596: leaves resume on their groups' rows for
         update_epochs, keeping stable ids by matching; level 1 follows."""
         d, n = self.d, x_all.shape[0]
-        new_leaves = self._grow(x_all)
+        new_leaves = self.grow(x_all)
         labels = self.assign(x_all)
         rows = [np.flatnonzero(labels.slot1 == g) for g in range(len(self.groups))]
         for g, grp in enumerate(self.groups):
@@ -508,9 +717,13 @@ class Hierarchy:
                 continue
             old2 = mdl.centroids.copy()
             c = Config(**{**mdl.config.__dict__, "nepochs": self.inc.update_epochs})
-            cent, pos, usage = self.backend.resume(c, x_all[rows[g]], mdl.positions, mdl.usage)
+            r = self.backend.resume(c, x_all[rows[g]], mdl.positions, mdl.usage)
+            cent, pos, usage = r[:3]
             mdl.centroids = np.asarray(cent, np.float32).reshape(mdl.k, d)
             mdl.positions, mdl.usage = pos, usage
+            if len(r) > 3:  # the run's record, kept for the model file
+                mdl.recipe, mdl.n_splits, mdl.stats = r[3]["recipe"], r[3]["n_splits"], \
+                    r[3]["stats"]
             m2 = match_centroids(old2, mdl.centroids, d, self.inc.match_min_sim)
             grp.ids, grp.next_id = carry_ids(m2, grp.ids, grp.next_id)
         labels = self.assign(x_all)
@@ -529,3 +742,310 @@ class Hierarchy:
         st.added_since_update = 0
         st.n_update = n
         return new_leaves
+
+
+# ---------------------------------------------------------------- hierarchy files
+# incremental.rs:862-1070. A directory holds hierarchy.json (the manifest,
+# serde_json's pretty form), level1.emeans and group-<g>.emeans for every
+# group with a model. The blob is EMHIER\0\x01, u64 manifest length, the
+# manifest (compact), then each model as u64 length + model file bytes (level
+# 1, then the groups with a model, in group order); little-endian.
+MANIFEST_VERSION = 1
+BLOB_MAGIC = b"EMHIER\x00\x01"
+
+
+def _opt_f32(v):
+    return None if v is None else model_file.F32(float(np.float32(v)))
+
+
+def _kscore_dict(s: KScore):
+    """KScore (auto.rs:178-192), fields in declaration order."""
+    return {"k": int(s.k), "k_eff": int(s.k_eff), "silhouette": float(s.silhouette),
+            "calinski_harabasz": float(s.calinski_harabasz),
+            "davies_bouldin": float(s.davies_bouldin), "objective": float(s.objective),
+            "browsable": float(s.browsable), "seconds": float(s.seconds)}
+
+
+def _f64(v, what):
+    """An f64 field: serde reads null (a non-finite value it wrote) as an error."""
+    if isinstance(v, bool) or not isinstance(v, (int, float)):
+        raise ValueError(f"invalid type for {what}: expected f64, found {json_type(v)}")
+    return float(v)
+
+
+def json_type(v):
+    return "null" if v is None else type(v).__name__
+
+
+def _kscore(d) -> KScore:
+    return KScore(int(d["k"]), int(d["k_eff"]),
+                  *[_f64(d[f], f) for f in ("silhouette", "calinski_harabasz", "davies_bouldin",
+                                             "objective", "browsable", "seconds")])
+
+
+def _auto_config_dict(c: AutoConfig, inc: IncrementalConfig):
+    """AutoConfig (auto.rs:99-147) without the backend (serde skip), with
+    IncrementalConfig (incremental.rs:52-83) in its place before verbose."""
+    return {"k1_range": [int(c.k1_range[0]), int(c.k1_range[1])], "k2_max": int(c.k2_max),
+            "criterion1": c.criterion1, "criterion2": c.criterion2,
+            "level1_tolerance": float(c.level1_tolerance),
+            "level2_tolerance": float(c.level2_tolerance),
+            "min_cluster_size": int(c.min_cluster_size),
+            "max_cluster_size": int(c.max_cluster_size), "min_split_size": int(c.min_split_size),
+            "split_min_silhouette": float(c.split_min_silhouette), "restarts": int(c.restarts),
+            "nepochs": float(c.nepochs), "init": c.init, "level1_method": c.level1_method,
+            "resplit_passes": int(c.resplit_passes),
+            "level1_max_share": float(c.level1_max_share), "seed": int(c.seed) & 0xFFFFFFFF,
+            "incremental": {
+                "outlier_mad_k": float(inc.outlier_mad_k),
+                "outlier_min_sim": _opt_f32(inc.outlier_min_sim),
+                "grow_min_size": int(inc.grow_min_size),
+                "update_min_outliers": int(inc.update_min_outliers),
+                "update_added_fraction": float(inc.update_added_fraction),
+                "update_epochs": float(inc.update_epochs),
+                "retrain_added_fraction": float(inc.retrain_added_fraction),
+                "retrain_outlier_fraction": float(inc.retrain_outlier_fraction),
+                "match_min_sim": _opt_f32(inc.match_min_sim)},
+            "verbose": bool(c.verbose)}
+
+
+def _auto_config(d):
+    """AutoConfig and IncrementalConfig from the manifest, serde's defaults
+    for the fields marked #[serde(default)]."""
+    i = d["incremental"]
+    inc = IncrementalConfig(
+        outlier_mad_k=_f64(i.get("outlier_mad_k", 3.0), "outlier_mad_k"),
+        outlier_min_sim=None if i["outlier_min_sim"] is None else float(np.float32(
+            i["outlier_min_sim"])),
+        grow_min_size=int(i.get("grow_min_size", 20)),
+        update_min_outliers=int(i["update_min_outliers"]),
+        update_added_fraction=_f64(i["update_added_fraction"], "update_added_fraction"),
+        update_epochs=_f64(i["update_epochs"], "update_epochs"),
+        retrain_added_fraction=_f64(i["retrain_added_fraction"], "retrain_added_fraction"),
+        retrain_outlier_fraction=_f64(i["retrain_outlier_fraction"], "retrain_outlier_fraction"),
+        match_min_sim=float(np.float32(_f64(i["match_min_sim"], "match_min_sim"))))
+    for key, allowed in (("criterion1", CRITERIA), ("criterion2", CRITERIA),
+                         ("init", ("k_means_plus_plus", "random_rows")),
+                         ("level1_method", ("bottom_up", "top_down"))):
+        if d.get(key, "bottom_up") not in allowed:
+            raise ValueError(f"unknown variant {d.get(key)!r} for {key}")
+    c = AutoConfig(
+        k1_range=(int(d["k1_range"][0]), int(d["k1_range"][1])), k2_max=int(d["k2_max"]),
+        criterion1=d["criterion1"], criterion2=d["criterion2"],
+        level1_tolerance=_f64(d["level1_tolerance"], "level1_tolerance"),
+        level2_tolerance=_f64(d["level2_tolerance"], "level2_tolerance"),
+        min_cluster_size=int(d["min_cluster_size"]), max_cluster_size=int(d["max_cluster_size"]),
+        min_split_size=int(d["min_split_size"]),
+        split_min_silhouette=_f64(d["split_min_silhouette"], "split_min_silhouette"),
+        restarts=int(d["restarts"]), nepochs=_f64(d["nepochs"], "nepochs"), init=d["init"],
+        level1_method=d.get("level1_method", "bottom_up"),
+        resplit_passes=int(d.get("resplit_passes", 2)),
+        level1_max_share=_f64(d.get("level1_max_share", 0.5), "level1_max_share"),
+        seed=int(d["seed"]), verbose=bool(d["verbose"]))
+    return c, inc
+
+
+CRITERIA = ("silhouette", "calinski_harabasz", "davies_bouldin")
+
+
+def _dedup_dict(c):
+    """DedupConfig (dedup.rs:39-51)."""
+    if c is None:
+        return None
+    return {"k": int(c.k), "sim_threshold": model_file.F32(float(np.float32(c.sim_threshold))),
+            "rep_threshold": _opt_f32(c.rep_threshold),
+            "max_gap_secs": None if c.max_gap_secs is None else float(c.max_gap_secs)}
+
+
+def _dedup(d):
+    if d is None:
+        return None
+    from . import DedupConfig
+    return DedupConfig(int(d["k"]), float(np.float32(_f64(d["sim_threshold"], "sim_threshold"))),
+                       None if d["rep_threshold"] is None else float(np.float32(
+                           d["rep_threshold"])),
+                       None if d["max_gap_secs"] is None else float(d["max_gap_secs"]))
+
+
+def _decision(v):
+    """GroupDecision from its serde value (externally tagged, snake_case)."""
+    if v in (DECISION_EMPTY, DECISION_TOO_SMALL):
+        return v
+    if isinstance(v, dict) and len(v) == 1:
+        if "split" in v:
+            return decision_split(int(v["split"]["k"]))
+        if "no_structure" in v:
+            return decision_no_structure(_f64(v["no_structure"]["best_silhouette"],
+                                              "best_silhouette"))
+    raise ValueError(f"unknown group decision {v!r}")
+
+
+def _diag_dict(g: Diagnostics):
+    """Diagnostics (auto.rs:209-238), fields in declaration order."""
+    return {"level1": [_kscore_dict(s) for s in g.level1],
+            "level2": [[_kscore_dict(s) for s in sw] for sw in g.level2],
+            "seconds": float(g.seconds),
+            "stage_a_level1": [_kscore_dict(s) for s in g.stage_a_level1],
+            "resplits": int(g.resplits), "leaves": int(g.leaves), "gap_k": int(g.gap_k),
+            "flat": bool(g.flat), "level1_rejected": [int(k) for k in g.level1_rejected]}
+
+
+def _diag(d) -> Diagnostics:
+    return Diagnostics(level1=[_kscore(s) for s in d["level1"]],
+                       level2=[[_kscore(s) for s in sw] for sw in d["level2"]],
+                       seconds=_f64(d["seconds"], "seconds"),
+                       stage_a_level1=[_kscore(s) for s in d.get("stage_a_level1", [])],
+                       resplits=int(d.get("resplits", 0)), leaves=int(d.get("leaves", 0)),
+                       gap_k=int(d.get("gap_k", 0)), flat=bool(d.get("flat", False)),
+                       level1_rejected=[int(k) for k in d.get("level1_rejected", [])])
+
+
+def _state_dict(st: State):
+    """State (incremental.rs:105-122)."""
+    return {"n_seen": int(st.n_seen), "n_full": int(st.n_full), "n_update": int(st.n_update),
+            "added_since_full": int(st.added_since_full),
+            "outliers_since_full": int(st.outliers_since_full),
+            "added_since_update": int(st.added_since_update),
+            "pending": [int(i) for i in st.pending], "next_id1": int(st.next_id1)}
+
+
+def manifest(h: "Hierarchy"):
+    """Manifest (incremental.rs:1052-1073, built at 949-975): floors that are
+    not finite are written as null."""
+    return {"version": MANIFEST_VERSION, "d": int(h.d),
+            "config": _auto_config_dict(h.config, h.inc), "dedup": _dedup_dict(h.dedup),
+            "ids1": [int(i) for i in h.ids1],
+            "groups": [{"has_model": g.model is not None, "ids": [int(i) for i in g.ids],
+                        "floors": [model_file.F32(float(f)) if np.isfinite(f) else None
+                                   for f in np.asarray(g.floors, np.float32)],
+                        "decision": g.decision, "next_id": int(g.next_id)}
+                       for g in h.groups],
+            "diagnostics": _diag_dict(h.diagnostics), "state": _state_dict(h.state)}
+
+
+def _assemble(mf, backend, model) -> "Hierarchy":
+    """incremental.rs:990-1047: the hierarchy of a manifest; model(None)
+    reads the level-1 model, model(g) group g's, in that order."""
+    if mf["version"] != MANIFEST_VERSION:
+        raise ValueError(f"unsupported hierarchy version {mf['version']}")
+    d = int(mf["d"])
+    cfg, inc = _auto_config(mf["config"])
+    level1 = model(None)
+    if level1.config.d != d:
+        raise ValueError("level-1 model d differs from the manifest")
+    ids1 = [int(i) for i in mf["ids1"]]
+    if level1.k != len(ids1) or len(mf["groups"]) != len(ids1):
+        raise ValueError("level-1 k, ids and groups disagree")
+    groups = []
+    for g, gf in enumerate(mf["groups"]):
+        m = None
+        ids = [int(i) for i in gf["ids"]]
+        if gf["has_model"]:
+            m = model(g)
+            if m.k != len(ids) or m.config.d != d:
+                raise ValueError(f"group {g}: model and ids disagree")
+        floors = np.array([np.nan if f is None else f for f in gf["floors"]], np.float32)
+        groups.append(Group(m, ids, floors, int(gf["next_id"]), _decision(gf["decision"])))
+    st = mf["state"]
+    state = State(int(st["n_seen"]), int(st["n_full"]), int(st["n_update"]),
+                  int(st["added_since_full"]), int(st["outliers_since_full"]),
+                  int(st["added_since_update"]), [int(i) for i in st["pending"]],
+                  int(st["next_id1"]))
+    h = Hierarchy(d, level1, groups, ids1, state, backend, inc, config=cfg,
+                  dedup=_dedup(mf["dedup"]))
+    h.diagnostics = _diag(mf["diagnostics"])
+    return h
+
+
+def _hierarchy_to_bytes(h: "Hierarchy") -> bytes:
+    """Hierarchy::to_bytes (incremental.rs:898-915)."""
+    import struct
+    js = model_file.to_json(manifest(h)).encode()
+    parts = [BLOB_MAGIC, struct.pack("<Q", len(js)), js]
+    for m in [h.level1] + [g.model for g in h.groups if g.model is not None]:
+        b = m.to_bytes()
+        parts += [struct.pack("<Q", len(b)), b]
+    return b"".join(parts)
+
+
+def _hierarchy_from_bytes(b, backend) -> "Hierarchy":
+    """Hierarchy::from_bytes (incremental.rs:917-946): the same checks and errors."""
+    import json
+    import struct
+    b = bytes(b)
+    if len(b) < 8 or b[:8] != BLOB_MAGIC:
+        raise ValueError("not an emeans hierarchy")
+    off = 8
+
+    def take(what):
+        nonlocal off
+        if len(b) - off < 8:
+            raise ValueError(f"truncated {what}")
+        n = struct.unpack("<Q", b[off:off + 8])[0]
+        if n > len(b) - off - 8:
+            raise ValueError(f"truncated {what}")
+        part = b[off + 8:off + 8 + n]
+        off += 8 + n
+        return part
+
+    mf = json.loads(take("manifest"))
+
+    def model(g):
+        what = "level-1 model" if g is None else f"group {g} model"
+        part = take(what)
+        try:
+            return Model.from_bytes(part)
+        except ValueError as e:
+            raise ValueError(f"{what}: {e}") from e
+
+    h = _assemble(mf, backend, model)
+    if off != len(b):
+        raise ValueError(f"{len(b) - off} bytes after the last model")
+    return h
+
+
+def _hierarchy_save(h: "Hierarchy", path):
+    """Hierarchy::save (incremental.rs:864-894): the directory is written as
+    <dir>.tmp, then renamed over <dir> (the old one moved to <dir>.old and
+    removed)."""
+    import os
+    import shutil
+    path = os.fspath(path).rstrip("/") or "/"
+    base = os.path.splitext(path)[0]
+    tmp, old = base + ".tmp", base + ".old"
+    if os.path.exists(tmp):
+        shutil.rmtree(tmp)
+    os.makedirs(tmp)
+    model_file.save_bytes(os.path.join(tmp, "level1.emeans"), h.level1.to_bytes())
+    for g, grp in enumerate(h.groups):
+        if grp.model is not None:
+            model_file.save_bytes(os.path.join(tmp, f"group-{g}.emeans"), grp.model.to_bytes())
+    with open(os.path.join(tmp, "hierarchy.json"), "wb") as f:
+        f.write(model_file.to_json_pretty(manifest(h)).encode())
+    if os.path.exists(old):
+        shutil.rmtree(old)
+    if os.path.exists(path):
+        os.rename(path, old)
+    os.rename(tmp, path)
+    if os.path.exists(old):
+        shutil.rmtree(old)
+
+
+def _hierarchy_load(path, backend) -> "Hierarchy":
+    """Hierarchy::load (incremental.rs:978-988)."""
+    import json
+    import os
+    path = os.fspath(path)
+    try:
+        with open(os.path.join(path, "hierarchy.json"), "rb") as f:
+            mf = json.loads(f.read())
+    except OSError as e:
+        raise ValueError(f"read {path}/hierarchy.json: {e}") from e
+
+    def model(g):
+        name = "level1.emeans" if g is None else f"group-{g}.emeans"
+        with open(os.path.join(path, name), "rb") as f:
+            return Model.from_bytes(f.read())
+
+    return _assemble(mf, backend, model)
+

@@ -101,6 +101,35 @@ def to_json(v):
     raise TypeError(f"cannot serialize {type(v).__name__}")
 
 
+def to_json_pretty(v, indent=""):
+    """serde_json's pretty form (to_vec_pretty): two-space indents, one
+    element or key per line, "key": value, and [] / {} when empty."""
+    inner = indent + "  "
+    if isinstance(v, dict):
+        if not v:
+            return "{}"
+        items = (inner + json.dumps(k) + ": " + to_json_pretty(x, inner) for k, x in v.items())
+        return "{\n" + ",\n".join(items) + "\n" + indent + "}"
+    if isinstance(v, (list, tuple)):
+        if not v:
+            return "[]"
+        return "[\n" + ",\n".join(inner + to_json_pretty(x, inner) for x in v) + "\n" + \
+            indent + "]"
+    return to_json(v)
+
+
+def save_bytes(path, b):
+    """Write b to path's .tmp sibling, flush it to disk, then rename it over
+    path (io.rs:74-88)."""
+    import os
+    tmp = os.path.splitext(str(path))[0] + ".tmp"
+    with open(tmp, "wb") as f:
+        f.write(b)
+        f.flush()
+        os.fsync(f.fileno())
+    os.replace(tmp, path)
+
+
 def config_dict(c):
     """model.rs:24-52, field order kept."""
     return {"d": int(c.d), "k": int(c.k), "nepochs": float(c.nepochs),

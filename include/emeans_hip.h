@@ -307,6 +307,15 @@ typedef struct emh_internal {
 int emh_internal_scores(emh_ctx* ctx, const emh_buf* x, size_t n, size_t d, const emh_buf* labels,
                         size_t k, emh_internal* out, uint64_t* sizes);
 
+/* gemm_nt (emeans-core/src/assign.rs:813-825) as Hierarchy::grow calls it
+ * (emeans-cluster/src/incremental.rs:423-440): out[i * nb + j] = a_i . b_j for
+ * a (m x d f32 buffer) and b (nb x d f32 buffer) into out (f32 buffer of at
+ * least m * nb entries). Each dot is one fma chain over the columns in order;
+ * the reference's gemm-crate order is not reproduced (its callers compare
+ * dots with thresholds). Queued; read out to wait. */
+int emh_dots(emh_ctx* ctx, const emh_buf* a, size_t m, const emh_buf* b, size_t nb, size_t d,
+             emh_buf* out);
+
 /* ------------------------------------------------- host replay (no device) */
 /* The seeded host-side pieces of the device loop, exported so that callers and
  * tests can check them without a GPU. They never touch the device. */

@@ -1020,6 +1020,19 @@ uint64_t orc_kmeans_pp(const float* x, uint64_t n, uint64_t d, uint64_t kmax, ui
   return pk.size();
 }
 
+// --- gemm_nt (crates/emeans-core/src/assign.rs:813-825) as Hierarchy::grow
+// calls it (crates/emeans-cluster/src/incremental.rs:423-440): out[i * nb + j]
+// = a_i . b_j. The reference takes these from the `gemm` crate; here each is
+// one fma chain over t in order from +0, the order of the top-1 dots.
+void orc_dots(const float* a, uint64_t m, const float* b, uint64_t nb, uint64_t d, float* out) {
+  for (size_t i = 0; i < m; i++)
+    for (size_t j = 0; j < nb; j++) {
+      float acc = 0.0f;
+      for (size_t t = 0; t < d; t++) acc = std::fma(a[i * d + t], b[j * d + t], acc);
+      out[i * nb + j] = acc;
+    }
+}
+
 // --- internal_scores (crates/emeans-cluster/src/metrics.rs:113-268): cosine
 // silhouette, Calinski-Harabasz, Davies-Bouldin and the spherical objective of
 // `labels` (< k) on unit rows. The row-by-cluster-sum dots come from the

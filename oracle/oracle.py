@@ -55,6 +55,7 @@ def _load():
         "orc_train": (i32, [_f32p, u64, vp, vp]),
         "orc_train_from": (i32, [_f32p, u64, vp, vp, vp, vp, vp]),
         "orc_kmeans_pp": (u64, [_f32p, u64, u64, u64, u32, _u32p]),
+        "orc_dots": (None, [_f32p, u64, _f32p, u64, u64, _f32p]),
         "orc_internal_scores": (i32, [_f32p, u64, u64, _u32p, u64, _f64p,
                                       np.ctypeslib.ndpointer(np.uint64), C.POINTER(u64)]),
         "orc_dedup": (u64, [_f32p, u64, u64, _u32p, _f32p, u64, C.c_float, C.c_float, i32, f64,
@@ -325,6 +326,16 @@ def kmeans_pp(x, d, kmax, seed):
     picks = np.zeros(max(min(kmax, n), 1), np.uint32)
     m = lib.orc_kmeans_pp(x, n, d, kmax, seed & 0xFFFFFFFF, picks)
     return picks[:m]
+
+
+def dots(a, b):
+    """gemm_nt (emeans-core/src/assign.rs:813-825) as fma chains: (m x nb)."""
+    a, b = np.ascontiguousarray(a, np.float32), np.ascontiguousarray(b, np.float32)
+    m, nb, d = a.shape[0], b.shape[0], a.shape[1]
+    out = np.zeros((m, nb), np.float32)
+    if m and nb:
+        lib.orc_dots(a, m, b, nb, d, out)
+    return out
 
 
 def internal_scores(x, d, labels, k):

@@ -156,3 +156,22 @@ def with_bursts(x, d, n_bursts, size_range, eps, seed):
             truth.append(b)
             created.append(created[b] + 1.0 + float(t))
     return np.stack(out).astype(np.float32), np.array(truth, np.uint32), np.array(created)
+
+
+def new_group(d, rows, seed):
+    """tests/hierarchy.rs:489-503: rows of one tight group around a random
+    direction (center + 0.5 z, renormalised)."""
+    rng = Normal(seed)
+    center = normalize_rows(rng.direction(d).reshape(1, d).copy(), d)[0]
+    out = []
+    for _ in range(rows):
+        v = (center + np.float32(0.5) * rng.direction(d)).astype(np.float32)
+        out.append(normalize_rows(v.reshape(1, d), d)[0])
+    return np.stack(out).astype(np.float32)
+
+
+def scattered_rows(d, rows, seed):
+    """tests/hierarchy.rs:587-592: unrelated random unit rows."""
+    rng = Normal(seed)
+    return np.stack([normalize_rows(rng.direction(d).reshape(1, d).copy(), d)[0]
+                     for _ in range(rows)]).astype(np.float32)

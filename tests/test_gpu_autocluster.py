@@ -1,18 +1,31 @@
-"""auto_cluster on the gfx950 backend (emeans_amd.autocluster) against the
-reference's own tests of it (emeans-cluster/tests/hierarchy.rs:48-67
-auto_cluster_finds_both_levels, 276-295 flat_data_stays_flat) on the same
-data: the reference's nested generator (synth.rs, restated in
-tests/ref_synth.py) with the tests' specs and AutoConfig (k1 in 2..10,
-k2 <= 8). The assertions are the reference's: chosen k, sweep lengths, ARI
-of both levels against the generating groups, leaf count, and labels that
-the hierarchy reproduces. Then a full retrain through Hierarchy::add
-(incremental.rs:598-650) on the same rows keeps the level-1 ids."""
+"""auto_cluster and Hierarchy::add on the gfx950 backend
+(emeans_amd.autocluster, emeans_amd.hierarchy) against the reference's own
+tests of them (emeans-cluster/tests/hierarchy.rs) on the same data: the
+reference's nested generator (synth.rs, restated in tests/ref_synth.py) with
+the tests' specs and AutoConfig (k1 in 2..10, k2 <= 8). The assertions are
+the reference's:
+
+  auto_cluster_finds_both_levels (48-67)     chosen k, sweep lengths, ARI of
+                                             both levels, leaf count, labels
+                                             the hierarchy reproduces
+  incremental_adds_keep_ids_and_survive_save_load (69-119)
+                                             directory and blob round trips,
+                                             append-only rows, adds in four
+                                             chunks: an EMA update, no
+                                             retrain, stable leaf ids
+  full_retrain_carries_ids (121-140)         a retrain keeps level-1 ids
+  flat_data_stays_flat (276-295)
+  outlier_flag_carries_information (505-536)
+  update_grows_a_leaf_for_a_new_group (538-600)
+                                             one new leaf for a new group,
+                                             kept by the files; none for
+                                             scattered rows"""
 
 import numpy as np
 import pytest
 from sklearn.metrics import adjusted_rand_score as ari
 
-from .ref_synth import nested
+from .ref_synth import nested, new_group, scattered_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -73,3 +86,115 @@ def test_flat_data_stays_flat(dev):
     assert k1 == 6
     assert all(k == 1 for k in k2), k2
     assert ari(broad, l.l1) > 0.98
+
+
+def _data():
+    d = 96
+    x, broad, sub = nested(n=3000, d=d, n_broad=4, sub_range=(2, 4), min_sub=60,
+                           noise_frac=0.0, seed=31)
+    return np.asarray(x, np.float32).reshape(-1, d), np.asarray(broad), np.asarray(sub)
+
+
+def _same(a, b):
+    for f in ("l1", "l2", "sim1", "sim", "outlier", "slot1", "slot2"):
+        assert np.asarray(getattr(a, f)).tobytes() == np.asarray(getattr(b, f)).tobytes(), f
+
+
+def _stability(a, b):
+    """label_stability (auto.rs:1303-1307): rows whose stable leaf id is the same."""
+    n = min(len(a.l1), len(b.l1))
+    same = (a.l1[:n] == b.l1[:n]) & (a.l2[:n] == b.l2[:n])
+    return float(same.sum()) / max(n, 1)
+
+
+def test_incremental_adds_keep_ids_and_survive_save_load(dev, tmp_path):
+    from emeans_amd import autocluster as A, hierarchy as H
+    x, broad, sub = _data()
+    d, n = x.shape[1], x.shape[0]
+    n0 = n * 8 // 10
+    h, l0 = A.auto_cluster(dev, x[:n0], _cfg())
+    path = tmp_path / "hier"
+    h.save(path)
+    h2 = H.Hierarchy.load(path, H.HipBackend(dev))
+    _same(h2.assign(x[:n0]), l0)
+    assert h2.chosen_k() == h.chosen_k()
+    blob = h.to_bytes()
+    h3 = H.Hierarchy.from_bytes(blob, H.HipBackend(dev))
+    _same(h3.assign(x[:n0]), l0)
+    assert h3.chosen_k() == h.chosen_k()
+    assert h3.to_bytes() == blob
+    with pytest.raises(ValueError):
+        H.Hierarchy.from_bytes(blob[:-1], H.HipBackend(dev))
+    with pytest.raises(ValueError):
+        H.Hierarchy.from_bytes(blob + b"\x00", H.HipBackend(dev))
+    with pytest.raises(ValueError):
+        h.add(x, n0 + 1)  # rows are append-only
+    chunk = (n - n0) // 4
+    seen, actions, last = n0, [], None
+    while seen < n:
+        end = min(seen + chunk, n)
+        r = h.add(x[:end], seen)
+        assert len(r.labels.l1) == end
+        actions.append(r.action)
+        seen, last = end, r.labels
+    assert h.state.n_seen == n
+    assert "EmaUpdate" in actions and "FullRetrain" not in actions, actions
+    assert _stability(l0, last) > 0.97
+    assert ari(sub, _leaf_codes(last)) > 0.85
+    # The updated hierarchy (resumed leaves with their run records) survives the blob.
+    h4 = H.Hierarchy.from_bytes(h.to_bytes(), H.HipBackend(dev))
+    assert h4.to_bytes() == h.to_bytes()
+    _same(h4.assign(x), h.assign(x))
+
+
+def test_full_retrain_carries_ids(dev):
+    from emeans_amd import autocluster as A, hierarchy as H
+    x, broad, sub = _data()
+    n = x.shape[0]
+    n0 = n // 2
+    h, l0 = A.auto_cluster(dev, x[:n0], _cfg(), H.IncrementalConfig(retrain_added_fraction=0.5))
+    r = h.add(x, n0)
+    assert r.action == "FullRetrain"
+    stable1 = float(np.mean(l0.l1 == r.labels.l1[:n0]))
+    assert stable1 > 0.98, f"level-1 id stability {stable1}"
+    assert _stability(l0, r.labels) > 0.9
+
+
+def test_outlier_flag_carries_information(dev):
+    from emeans_amd import autocluster as A
+    x, broad, sub = _data()
+    d, n = x.shape[1], x.shape[0]
+    n0 = n * 8 // 10
+    h, l0 = A.auto_cluster(dev, x[:n0], _cfg())
+    assert l0.outlier.mean() < 0.01, "clean training rows flagged"
+    assert h.assign(x[n0:]).outlier.mean() < 0.02, "held-out rows of the same groups flagged"
+    assert h.assign(new_group(d, 50, 77)).outlier.all(), "rows of an unseen group must be flagged"
+
+
+def test_update_grows_a_leaf_for_a_new_group(dev, tmp_path):
+    from emeans_amd import autocluster as A, hierarchy as H
+    x, broad, sub = _data()
+    d, n = x.shape[1], x.shape[0]
+    n0 = n * 8 // 10
+    inc = H.IncrementalConfig(update_min_outliers=20, retrain_outlier_fraction=0.9)
+    h, l0 = A.auto_cluster(dev, x[:n0], _cfg(), inc)
+    old_ids = set(zip(l0.l1.tolist(), l0.l2.tolist()))
+    leaves0 = sum(h.chosen_k()[1])
+    xa = np.concatenate([x[:n0 + 340], new_group(d, 60, 99)])
+    first_new = n0 + 340
+    r = h.add(xa, n0)
+    assert r.action == "EmaUpdate", "precondition"
+    assert len(r.new_leaves) == 1, r.new_leaves
+    leaf = r.new_leaves[0]
+    assert leaf not in old_ids, "the new leaf reuses an old id"
+    in_leaf = (r.labels.l1 == leaf[0]) & (r.labels.l2 == leaf[1])
+    assert in_leaf[first_new:].sum() >= 60 * 95 // 100
+    assert in_leaf[:first_new].sum() <= 3
+    assert sum(h.chosen_k()[1]) == leaves0 + 1
+    assert _stability(l0, r.labels) > 0.97
+    path = tmp_path / "grown"
+    h.save(path)
+    _same(H.Hierarchy.load(path, H.HipBackend(dev)).assign(xa), r.labels)
+    r2 = h.add(np.concatenate([xa, scattered_rows(d, 30, 5)]), xa.shape[0])
+    assert r2.action == "EmaUpdate", "precondition"
+    assert r2.new_leaves == []

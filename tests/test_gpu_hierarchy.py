@@ -30,13 +30,43 @@ def dev():
 
 
 class OracleBackend:
+    """The hierarchy's device work by the oracle; resumed runs carry the
+    record a model file keeps (recipe under the device's backend name, epoch
+    times zero: wall-clock time is not part of the trajectory)."""
+
+    def __init__(self, name="hip"):
+        self.name = name
+
     def leaf_top1(self, x, cents):
         return O.assign(x, x.shape[1], cents, "ip")
 
     def resume(self, config, x, positions, usage):
+        from emeans_amd import _epoch_rows, model_file as MF
         o = O.train(x, config.d, config.k, nepochs=config.nepochs, seed=config.seed,
-                    spherical=config.spherical, positions=positions, usage=usage)
-        return o["centroids"], o["positions"], o["usage"]
+                    spherical=config.spherical, unused_threshold=config.unused_threshold,
+                    positions=positions, usage=usage)
+        n = x.shape[0]
+        run = {"recipe": MF.recipe_dict(config, n, o["batch_size"], o["alpha0"],
+                                        _epoch_rows(n, config), self.name),
+               "n_splits": o["n_splits"],
+               "stats": [(ob, 0.0, im, int(ns)) for ob, im, ns in zip(o["obj"], o["imbalance"],
+                                                                     o["nsplit"])]}
+        return o["centroids"], o["positions"], o["usage"], run
+
+    def dots(self, a, b):
+        return O.dots(a, b)
+
+
+def _same_files(hg, ho):
+    """The two hierarchies' blobs are equal once the oracle side takes the
+    device runs' epoch times."""
+    for a, b in zip([hg.level1] + [g.model for g in hg.groups],
+                    [ho.level1] + [g.model for g in ho.groups]):
+        if a is not None and b is not None:
+            assert len(a.stats) == len(b.stats)
+            b.stats = [(s[0], t[1], s[2], s[3]) for s, t in zip(b.stats, a.stats)]
+    ho.diagnostics = hg.diagnostics
+    assert hg.to_bytes() == ho.to_bytes(), "hierarchy files differ"
 
 
 def _same_labels(a, b):
@@ -86,7 +116,7 @@ def test_hierarchy_assign_and_ema_update_reduced_c5(dev):
     inc = H.IncrementalConfig(grow_min_size=0)
     build = lambda be: H.Hierarchy.from_models(x, copy.deepcopy(level1), copy.deepcopy(leaves),
                                                be, inc)
-    hg, ho = build(H.HipBackend(dev)), build(OracleBackend())
+    hg, ho = build(H.HipBackend(dev)), build(OracleBackend(dev.name()))
     _same_hierarchy(hg, ho)
     lg, lo = hg.assign(x), ho.assign(x)
     _same_labels(lg, lo)
@@ -100,3 +130,32 @@ def test_hierarchy_assign_and_ema_update_reduced_c5(dev):
     moved = sum(not np.array_equal(a.model.centroids, m.centroids)
                 for a, m in zip(hg.groups, leaves) if m is not None)
     assert moved >= 1, "the update resumed no group"
+    _same_files(hg, ho)
+
+
+def test_grow_on_the_device_equals_the_oracle(dev):
+    """Hierarchy::add with the grow step (incremental.rs:376-538) on the
+    reference's update_grows_a_leaf_for_a_new_group data (tests/hierarchy.rs:
+    538-575): a hierarchy from auto_cluster on the device, then the same
+    hierarchy read from its blob over the oracle; both add 340 known rows and
+    60 rows of a new group. Labels, the new leaf, every model and the files
+    must be equal bit for bit."""
+    from emeans_amd import autocluster as A, auto, hierarchy as H
+    from .ref_synth import nested, new_group
+    d = 96
+    x, _, _ = nested(n=3000, d=d, n_broad=4, sub_range=(2, 4), min_sub=60, noise_frac=0.0,
+                     seed=31)
+    x = np.asarray(x, np.float32).reshape(-1, d)
+    n0 = 2400
+    inc = H.IncrementalConfig(update_min_outliers=20, retrain_outlier_fraction=0.9)
+    hg, _ = A.auto_cluster(dev, x[:n0], auto.AutoConfig(k1_range=(2, 10), k2_max=8), inc)
+    ho = H.Hierarchy.from_bytes(hg.to_bytes(), OracleBackend(dev.name()))
+    xa = np.concatenate([x[:n0 + 340], new_group(d, 60, 99)])
+    rg, ro = hg.add(xa, n0), ho.add(xa, n0)
+    assert rg.action == ro.action == "EmaUpdate"
+    assert rg.new_leaves == ro.new_leaves and len(rg.new_leaves) == 1, (rg.new_leaves,
+                                                                       ro.new_leaves)
+    _same_labels(rg.labels, ro.labels)
+    _same_hierarchy(hg, ho)
+    assert hg.state == ho.state
+    _same_files(hg, ho)
