@@ -210,8 +210,9 @@ def headline(args):
             "the bound of each lane's best)", SCREEN_TRAFFIC_BYTES),
         "update_rooflines": {
             "scatter_add": hbm_roofline(*main["update"]["scatter_add"],
-                                        "k_hist_total + k_place_sum + k_sums (chunked "
-                                        "counting sort, ordered per-cluster sums)"),
+                                        "k_place_scan + k_sums (labels tallied by the "
+                                        "check and the queued-row scan, chunked counting-sort "
+                                        "placement, ordered per-cluster sums)"),
             "ema_update": hbm_roofline(*main["update"]["ema_update"], "k_ema"),
         },
     }

@@ -88,7 +88,13 @@ Top1Geom top1_geom(emh_ctx* c, size_t n, size_t d, size_t k, bool ip, bool split
   if (!g.screen) return g;
   const int nt3 = (int)((k + TC3 - 1) / TC3);
   // (k_screen4 addresses a slab's rows with 32-bit offsets: fewer than 2^25 rows.)
-  if (split && c->screen != SCREEN_F32 && k >= 64 && nt3 <= MAX_PARTS && n < (1u << 25)) {
+  // A selection that gives the large tiles fewer blocks than half the CUs (an
+  // epoch's tail batch: 3,392 rows x 1,024 centroids in 56 blocks took 55 us)
+  // takes the 128 x 128 screen, whose 216 blocks there take 45 us.
+  const size_t blocks3 = (n + TR3 - 1) / TR3 * (size_t)nt3;
+  const bool few = 2 * blocks3 < (size_t)c->cus;
+  if (split && !few && c->screen != SCREEN_F32 && k >= 64 && nt3 <= MAX_PARTS &&
+      n < (1u << 25)) {
     g.big = g.split = true;
     g.row_tiles = (int)((n + TR3 - 1) / TR3);
     g.ntiles = g.parts = nt3;
@@ -98,7 +104,7 @@ Top1Geom top1_geom(emh_ctx* c, size_t n, size_t d, size_t k, bool ip, bool split
   // The large-tile bf16 screen (one 512-thread block per CU, 256-centroid
   // tiles) when d % 4 == 0 and k >= 64; smaller k fill a 128-centroid tile
   // better.
-  g.big = c->screen != SCREEN_F32 && d % 4 == 0 && k >= 64;
+  g.big = c->screen != SCREEN_F32 && d % 4 == 0 && k >= 64 && !(split && few);
   const int TR = g.big ? TR3 : 128;
   g.row_tiles = (int)((n + TR - 1) / TR);
   g.ntiles = (int)((k + (g.big ? TC3 : TC) - 1) / (g.big ? TC3 : TC));

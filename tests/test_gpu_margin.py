@@ -110,7 +110,7 @@ def _crowds(k, d, seed):
 @pytest.mark.parametrize("metric", ["ip", "l2"])
 @pytest.mark.parametrize("d", [36, 99, 768, 2500])
 def test_margin_near_tie_crowds(dev, mode, metric, d):
-    n, k = 4096, 512
+    n, k = 16384, 512  # 64 row tiles x 2 parts: enough blocks for the split-operand screen
     c, groups = _crowds(k, d, 21)
     rows = _mix(n, d, groups, 0.05, True, 21)
     scale = np.array([1.0, 1e3, 1e-3, 1e-15], np.float32)[np.arange(n) % 4]
@@ -206,6 +206,8 @@ def test_margin_headline_batch(dev):
     c = x[(np.arange(1024) * 37) % x.shape[0]].copy()
     ids = ((np.arange(16384, dtype=np.uint64) * 7919 + 11) % x.shape[0]).astype(np.uint32)
     _margin(dev, x, c, "l2", "headline batch", "big_tagged", ids=ids)
+    # An epoch's tail batch (3,392 rows: 56 large-tile blocks) takes the 128 x 128 screen.
+    _margin(dev, x, c, "l2", "headline tail batch", "small_bf16", ids=ids[:3392].copy())
 
 
 @pytest.mark.parametrize("mode", [1, 2], ids=["bf16x3", "f32"])
