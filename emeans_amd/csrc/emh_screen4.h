@@ -24,6 +24,7 @@
 
 #include <type_traits>
 
+#include "emh_dma.h"
 #include "emh_halves.h"
 #include "emh_screen_kern.h"
 
@@ -32,47 +33,6 @@ namespace {
 
 constexpr int S4_HALF = TR3 * SLAB_BYTES;  // one operand's slab in LDS: 32 KB
 constexpr int S4_STAGE = 2 * S4_HALF;      // rows and centroids: 64 KB
-
-// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding:
-// vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-// LDS DMA: each lane moves 16 (or 4) bytes from its global address to
-// lds + 16 lane (4 lane); lds is wave-uniform (M0 holds its LDS address).
-// Issued as inline assembly, which the compiler's wait counting does not
-// see: the kernel orders these DMAs against its LDS reads itself (vmcnt
-// waits and barriers), where the compiler, unable to tell the ring's stages
-// apart across loop iterations, would wait for every DMA in flight before
-// each read. (Other loads the compiler waits for stay correct: DMAs it does
-// not count only make its vmcnt waits stricter.) M0 is saved and restored
-// around the DMA, so no value the compiler keeps there is disturbed.
-__device__ __forceinline__ uint32_t lds_addr(const void* lds) {
-  return __builtin_amdgcn_readfirstlane(
-      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds);
-}
-// From a wave-uniform base plus a 32-bit per-lane byte offset.
-__device__ __forceinline__ void dma16o(const void* base, uint32_t off, void* lds) {
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "v"(off), "s"(base), "s"(lds_addr(lds))
-      : "memory");
-}
-__device__ __forceinline__ void dma4(const void* g, void* lds) {
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\t"
-      "global_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "v"(g), "s"(lds_addr(lds))
-      : "memory");
-}
 
 // Chunks of a slab row: 4 kk + (0, 1) the hi halves of dimensions 16 kk +
 // (0-7, 8-15), 4 kk + (2, 3) their lo halves, for MFMA step kk = 0, 1. In LDS

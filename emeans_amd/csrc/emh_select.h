@@ -8,8 +8,8 @@
 namespace emh {
 
 constexpr uint32_t NONE = 0xffffffffu;
-constexpr int L1 = 5;    // top-1: the smallest screen keys each part keeps
-constexpr int C1 = 8;    // top-1: most candidates a row sends to the exact chains
+constexpr int L1 = 6;    // top-1: the smallest screen keys each part keeps
+constexpr int C1 = 16;   // top-1: most candidates a row sends to the exact chains
 constexpr int LK = 24;   // top-k list: kk <= 16 plus 7 spare + the bound
 constexpr int KMAX = 16;  // largest kk (emeans-core/src/knn.rs:16)
 constexpr int MAX_PARTS = 8;  // centroid parts per row tile: lists per row the verify merges
