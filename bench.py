@@ -53,10 +53,11 @@ METRIC = "train s & assign Mrows/s at 200k×768 k=1024 FP32; % of FP32 MFMA peak
 # HBM bytes per screen launch over this workload's launch mix (calibrated
 # FETCH_SIZE + WRITE_SIZE from two rocprofv3 --pmc passes of this script, with
 # a plain copy kernel of known size as the scale;
-# profiles/k_screen_train_assign_200kx768_k1024_hbm_traffic.md): 88.7 MB per
+# profiles/k_screen_train_assign_200kx768_k1024_hbm_traffic.md): 89.2 MB per
 # 16,384-row batch launch (50.3 MB of split rows, the centroids once per XCD),
-# 332 MB per 65,536-row assignment chunk, 45 MB per epoch-tail batch.
-SCREEN_TRAFFIC_BYTES = 95.4e6
+# 332 MB per 65,536-row assignment chunk, 40 MB per epoch-tail batch (the
+# 128 x 128 screen).
+SCREEN_TRAFFIC_BYTES = 95.6e6
 # The screen's roofline times every PROFILE_EVERY-th launch of the timed steps
 # with HIP events (an event pair between two kernels costs the stream a few
 # microseconds; on every launch that was ~5 % of the headline step).
@@ -207,7 +208,8 @@ def headline(args):
             ms, launches, flop,
             "k_screen4 (bf16 MFMA, three passes xh.ch + xh.cl + xl.ch on operands split "
             "ahead of time, f32 accumulation, LDS-DMA ring; per-row candidate lists within "
-            "the bound of each lane's best)", SCREEN_TRAFFIC_BYTES),
+            "the bound of each lane's best); the epoch tails' 3,392-row batches on the "
+            "128 x 128 k_screen", SCREEN_TRAFFIC_BYTES),
         "update_rooflines": {
             "scatter_add": hbm_roofline(*main["update"]["scatter_add"],
                                         "k_place_scan + k_sums (labels tallied by the "
