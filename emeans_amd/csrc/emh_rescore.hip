@@ -366,6 +366,7 @@ __device__ __forceinline__ void unroll_steps(F&& f) {
   }
 }
 
+template <int L>
 __global__ __launch_bounds__(256) void k_check1(
     const float* __restrict__ x, size_t nx, int d, const uint32_t* __restrict__ ids, size_t lo,
     int nrows, const float* __restrict__ cents, const float* __restrict__ cnorm, int ip,
@@ -385,10 +386,10 @@ __global__ __launch_bounds__(256) void k_check1(
   {
     const int r = tid >> 3, j = tid & 7;
     const bool live = r < rows;
-    float key[L1];
-    uint32_t idv[L1];
+    float key[L];
+    uint32_t idv[L];
 #pragma unroll
-    for (int e = 0; e < L1; e++) {
+    for (int e = 0; e < L; e++) {
       key[e] = INFINITY;
       idv[e] = NONE;
     }
@@ -402,9 +403,9 @@ __global__ __launch_bounds__(256) void k_check1(
       xid = badid ? NONE : (uint32_t)xi;
       xn = xnorm[r0 + r];
       if (j < parts) {
-        const Cand* c = cand + ((size_t)(r0 + r) * parts + j) * L1;
+        const Cand* c = cand + ((size_t)(r0 + r) * parts + j) * L;
 #pragma unroll
-        for (int e = 0; e < L1; e++) {
+        for (int e = 0; e < L; e++) {
           const Cand v = c[e];
           key[e] = v.key;
           idv[e] = v.id;
@@ -428,14 +429,14 @@ __global__ __launch_bounds__(256) void k_check1(
                                    __uint_as_float(small[SW_CNMAX]), d, l2, bf3 != 0, bf3 == 2);
       const float thr = best + 2.0f * E;
 #pragma unroll
-      for (int e = 0; e < L1; e++)
+      for (int e = 0; e < L; e++)
         if (idv[e] != NONE && (key[e] <= thr || thr != thr)) {
           inc |= 1u << e;
           cj++;
         }
       // This part's list holds all of its centroids within thr: not full, or
       // its last key above thr (never with a NaN thr).
-      cert = idv[L1 - 1] == NONE || key[L1 - 1] > thr;
+      cert = idv[L - 1] == NONE || key[L - 1] > thr;
     }
     int tot = cj, incl = cj;
 #pragma unroll
@@ -471,7 +472,7 @@ __global__ __launch_bounds__(256) void k_check1(
     if (settled) {
       int o = roff[r] + incl - cj;
 #pragma unroll
-      for (int e = 0; e < L1; e++)
+      for (int e = 0; e < L; e++)
         if ((inc >> e) & 1u) {
           prow[o] = (uint32_t)r;
           pcid[o] = idv[e];
@@ -733,15 +734,17 @@ void launch_margin(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32
 void launch_verify1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
                     size_t lo, size_t n, const float* cents, const float* cnorm, size_t k, bool ip,
                     const Cand* cand, int parts, const float* xnorm, uint32_t* labels,
-                    float* scores, uint32_t* fb, bool tagged, const LabelTally* tally) {
+                    float* scores, uint32_t* fb, bool tagged, const LabelTally* tally, int L) {
   const dim3 g((unsigned)((n + R1 - 1) / R1));
   // The bound follows the screen's arithmetic: 0 f32, 1 bf16, 2 bf16 with tagged keys.
   const int bf3 = c->screen == SCREEN_F32 ? 0 : tagged ? 2 : 1;
   static_assert(TALLY_CP % CR == 0, "a check block's rows lie in one tally chunk");
   EMH_ENSURE(!tally || (d % 4 == 0 && lo >= tally->lo && (lo - tally->lo) % TALLY_CP == 0),
              "check: a tally needs d %% 4 == 0 and chunk-aligned positions");
+  EMH_ENSURE(L == L1 || (L == L1S && d % 4 == 0), "check: lists of %d entries", L);
   if (d % 4 == 0)
-    hipLaunchKernelGGL(k_check1, dim3((unsigned)((n + CR - 1) / CR)), dim3(256), 0, c->stream, x,
+    hipLaunchKernelGGL(L == L1S ? k_check1<L1S> : k_check1<L1>,
+                       dim3((unsigned)((n + CR - 1) / CR)), dim3(256), 0, c->stream, x,
                        nx, (int)d, ids, lo, (int)n, cents, cnorm, ip ? 1 : 0, cand, parts, xnorm,
                        labels, scores, fb, c->small, bf3, tally ? tally->cnt : nullptr,
                        tally ? tally->counts : nullptr, tally ? tally->lo : 0,

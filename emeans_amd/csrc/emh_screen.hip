@@ -139,6 +139,7 @@ struct Top1Screen {
   uint32_t* fb = nullptr;
   float* xnorm = nullptr;
   bool tagged = false;
+  int L = L1;  // entries per part list: L1S for the sorted insert's lists
 };
 
 Top1Screen screen_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
@@ -157,6 +158,7 @@ Top1Screen screen_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const ui
     launch_fill_u32(c, c->small, 3, 0);
   const unsigned blocks = (unsigned)(g.row_tiles * g.parts);
   s.tagged = g.big && g.tpp == 1;
+  s.L = g.big && !s.tagged ? L1S : L1;
   if (g.split) {
     // The centroids' halves and the bound's centroid maxima (the caller's,
     // split ahead, or split here), then the rows' halves (the caller's, or
@@ -234,7 +236,7 @@ void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t
     return;
   }
   launch_verify1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, s.cand, s.g.parts, s.xnorm, labels,
-                 scores, s.fb, s.tagged, tally);
+                 scores, s.fb, s.tagged, tally, s.L);
   launch_exact1(c, x, nx, d, ids, lo, n, s.fb, cents, cnorm, k, ip, labels, scores, ar, tally);
 }
 
@@ -253,7 +255,7 @@ void screen_margin_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const u
                          : (c->screen == SCREEN_F32 ? EMH_SCREEN_SMALL_F32 : EMH_SCREEN_SMALL_BF16);
   out->parts = s.g.parts;
   out->tiles_per_part = s.g.tpp;
-  launch_margin(c, x, nx, d, ids, lo, n, cents, cnorm, ip, s.cand, s.g.parts, L1, s.xnorm,
+  launch_margin(c, x, nx, d, ids, lo, n, cents, cnorm, ip, s.cand, s.g.parts, s.L, s.xnorm,
                 bound_kind(c, s.tagged), out);
 }
 

@@ -9,6 +9,7 @@ namespace emh {
 
 constexpr uint32_t NONE = 0xffffffffu;
 constexpr int L1 = 6;    // top-1: the smallest screen keys each part keeps
+constexpr int L1S = 5;   // ... with the sorted insert (parts of several 256-centroid tiles)
 constexpr int C1 = 16;   // top-1: most candidates a row sends to the exact chains
 constexpr int LK = 24;   // top-k list: kk <= 16 plus 7 spare + the bound
 constexpr int KMAX = 16;  // largest kk (emeans-core/src/knn.rs:16)
@@ -148,7 +149,7 @@ void launch_verify1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint3
                     size_t lo, size_t n, const float* cents, const float* cnorm, size_t k, bool ip,
                     const Cand* cand, int parts, const float* xnorm, uint32_t* labels,
                     float* scores, uint32_t* fb, bool tagged = false,
-                    const LabelTally* tally = nullptr);
+                    const LabelTally* tally = nullptr, int L = L1);
 void launch_verifyk(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,
                     size_t kk, const Cand* cand, int parts, const float* xnorm, uint32_t* ids,
                     float* sims, uint32_t* fb);
