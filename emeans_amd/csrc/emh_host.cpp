@@ -568,11 +568,12 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
                           : nullptr;
   uint32_t* tpart_e = keep_csplit ? tpart_h + 2 * halves_blocks(k) : nullptr;
   SplitCents pcents{tsplit, tpart_h, (int)halves_blocks(k)};
-  // When the batches' top-1 runs the screen with d % 4 == 0, the check and
-  // the queued-row scan tally the labels they write (counts and the chunk
-  // histograms of the counting sort), so scatter_add needs no count launch;
-  // the EMA clears both for the next batch.
-  const bool tally = top1_screens(c, bsz, d, k, sph) && d % 4 == 0 && scatter_tallied(bsz, k);
+  // When the batches' top-1 runs the screen with d % 4 == 0 (the check and
+  // the queued-row scan), or the latency-bound exact scan alone (small k),
+  // it tallies the labels it writes (counts and the chunk histograms of the
+  // counting sort), so scatter_add needs no count launch; the EMA clears
+  // both for the next batch.
+  const bool tally = top1_tallies(c, bsz, d, k, sph) && scatter_tallied(bsz, k);
   const size_t tstride = tally_stride(bsz);
   uint32_t* tcnt = tally ? (uint32_t*)c->tally_cnt.get(tstride * k * 4) : nullptr;
   if (tally) launch_fill_u32(c, tcnt, tstride * k, 0);
@@ -602,8 +603,28 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
                            hipMemcpyHostToDevice, c->copy_stream));
     ev_order[buf].record(c->copy_stream);
   };
+  // The revival stream (RandomState(seed)) serves only revivals, k uniforms
+  // per revival that splits: the next k Gumbel terms are drawn ahead.
+  RandomState split_rng(cfg.seed);
+  // Helper tasks (the next epoch's order, Gumbel terms, epoch statistics)
+  // reference this frame, and their futures do not wait when destroyed: on
+  // any exit, an error included, Join waits for those still running before
+  // anything they use goes.
+  std::future<void> next;
+  std::future<std::vector<double>> gnext;
+  std::future<emh_epoch_stats> pending;
+  struct Join {
+    std::future<void>& a;
+    std::future<std::vector<double>>& b;
+    std::future<emh_epoch_stats>& p;
+    ~Join() {
+      if (a.valid()) a.wait();
+      if (b.valid()) b.wait();
+      if (p.valid()) p.wait();
+    }
+  } join{next, gnext, pending};
   // The first epoch's order is drawn while the initial centroids are (model.rs:783-784).
-  std::future<void> next = beside([&] { fill_order(0); });
+  next = beside([&] { fill_order(0); });
 
   // The start (model.rs:772-797): saved EMA state as it is (begin_with_state);
   // else initial centroids, given (begin) or the rows permutation(n)[..k],
@@ -647,19 +668,18 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
     fprintf(stderr, "Clustering %zu points in %zuD to %zu clusters, %g epochs (batch %zu, alpha0 %.3f%s)\n",
             n, d, k, cfg.nepochs, bsz, R.alpha0, sph ? ", spherical" : "");
 
-  // The revival stream (RandomState(seed)) serves only revivals, k uniforms
-  // per revival that splits: the next k Gumbel terms are drawn ahead.
-  RandomState split_rng(cfg.seed);
-  std::future<std::vector<double>> gnext =
-      beside([&] { return gumbel_terms(split_rng, k); });
+  gnext = beside([&] { return gumbel_terms(split_rng, k); });
   // After a revival used them, the next block is drawn on a helper once the
   // next batch's kernels are queued, off the GPU's path.
   auto take_gumbel = [&] { return gnext.get(); };
   bool refill = false;
   size_t n_splits = 0, step = 0;
   bool norms_stale = true;  // L2 readout: the EMA keeps the norms of the rows it moves
+  // Spherical readout: the EMA writes the normalized rows it moves, so a full
+  // normalize_rows runs only at the start and after a revival's splits.
+  const bool ema_readout = sph && d <= EMA_READOUT_MAX_D;
+  bool readout_stale = true;
   std::vector<emh_epoch_stats> stats;
-  std::future<emh_epoch_stats> pending;
   for (size_t epoch = 0; epoch < n_epochs; epoch++) {
     const size_t rows = R.epoch_rows[epoch];
     const bool last = epoch + 1 == n_epochs;
@@ -676,7 +696,8 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
     for (size_t b = 0; b < rows; b += bsz) {
       const size_t e = std::min(b + bsz, rows);
       if (sph) {
-        launch_normalize_rows(c, pos.f(), k, d, readout.f());
+        if (!ema_readout || readout_stale) launch_normalize_rows(c, pos.f(), k, d, readout.f());
+        readout_stale = false;
       } else if (norms_stale) {
         launch_row_norms(c, pos.f(), k, d, readout.f());
         norms_stale = false;
@@ -724,7 +745,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
         ProfScope p(c, EMH_PROF_EMA, ema_bytes(k, d), prof_take(c, EMH_PROF_EMA));
         launch_ema(c, pos.f(), mass.f(), sums.f(), counts.u(), k, d, af, df, replace,
                    sph ? nullptr : readout.f(), true, d_tally[buf], true, tsplit, tpart_e, tcnt,
-                   tally ? tstride * k : 0);
+                   tally ? tstride * k : 0, ema_readout ? readout.f() : nullptr);
         if (keep_csplit) {
           pcents.part = tpart_e;
           pcents.nparts = (int)ema_blocks(k);
@@ -741,6 +762,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
           launch_split(c, pos.f(), mass.f(), d_plan, np, d, true);  // donors and dead are disjoint
           n_splits += np;
           norms_stale = true;
+          readout_stale = true;
         }
         refill = !gnext.valid();  // scheduled after the next batch's launches
       }

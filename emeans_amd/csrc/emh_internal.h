@@ -267,12 +267,15 @@ void launch_normalize_rows(emh_ctx* c, const float* src, size_t rows, size_t d, 
 // rewrites the bf16 halves (launch_halves' layout, k rows) of the rows it
 // moves and leaves the bound's centroid maxima of its ema_blocks(k) blocks in
 // cpart, as launch_halves' part does. With zero_words, also clears
-// zero_words[0..nzero) (a tally's chunk histograms).
+// zero_words[0..nzero) (a tally's chunk histograms). With readout (spherical
+// runs, no norms, d <= EMA_READOUT_MAX_D), each moved row's normalize_rows
+// readout is written there too (rows that did not move keep theirs).
+constexpr size_t EMA_READOUT_MAX_D = 1024;
 void launch_ema(emh_ctx* c, float* pos, float* usage, const float* sums, const uint32_t* counts,
                 size_t k, size_t d, float alpha, float decay, int replace, float* norms = nullptr,
                 bool clear_screen_words = false, uint32_t* tally = nullptr,
                 bool zero_counts = false, void* csplit = nullptr, uint32_t* cpart = nullptr,
-                uint32_t* zero_words = nullptr, size_t nzero = 0);
+                uint32_t* zero_words = nullptr, size_t nzero = 0, float* readout = nullptr);
 size_t ema_blocks(size_t k);
 // The masses launch_ema will leave, into out (usage untouched); with
 // small_out, also a copy of the small block's words; with seq_out, then seq
@@ -388,6 +391,9 @@ bool split_screen(emh_ctx* c, size_t n, size_t d, size_t k, bool ip);
 // screen (and so the check and the queued-row scan). A tallied call always
 // does, whatever its rows.
 bool top1_screens(emh_ctx* c, size_t n, size_t d, size_t k, bool ip);
+// Whether a top-1 call of n rows (and of any fewer) can tally the labels it
+// writes: the screen with d % 4 == 0, or the latency-bound exact scan.
+bool top1_tallies(emh_ctx* c, size_t n, size_t d, size_t k, bool ip);
 // Split rows of x (n rows, or ids[lo..lo+n)) into bf16 halves in out,
 // slab-major, with their |x|^2 in norm; with part, each of the
 // halves_blocks(n) blocks leaves the largest |x|^2 of its rows and the

@@ -171,6 +171,35 @@ __global__ __launch_bounds__(256) void k_normalize_rows(const float* __restrict_
   for (size_t t = lane; t < d; t += WAVE) out[t] = (row[t] / s1) / s2;
 }
 
+// v[0] + v[1] + ... + v[len - 1] in order from +0 (one lane; v 16-byte
+// aligned LDS): the next 16 values' reads are in flight while 16 are added.
+__device__ __forceinline__ float ordered_sum(const float* v, int len) {
+  float s = 0.0f;
+  const int len16 = len & ~15;
+  int t = 0;
+  if (len16 > 0) {
+    float4 cur[4], nxt[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) cur[u] = *reinterpret_cast<const float4*>(v + 4 * u);
+    for (; t < len16; t += 16) {
+      const int tn = min(t + 16, len16 - 16);  // the last step reloads its own group
+#pragma unroll
+      for (int u = 0; u < 4; u++) nxt[u] = *reinterpret_cast<const float4*>(v + tn + 4 * u);
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        s = s + cur[u].x;
+        s = s + cur[u].y;
+        s = s + cur[u].z;
+        s = s + cur[u].w;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; u++) cur[u] = nxt[u];
+    }
+  }
+  for (; t < len; t++) s = s + v[t];
+  return s;
+}
+
 // EMA step (core/cpu.rs:389-432): all masses decay unless replace; each cluster
 // with rows gets mass = retained + alpha n, w = alpha n / mass and
 // c = (w == 1) ? s / n : c + w (s / n - c), two roundings, no FMA.
@@ -205,8 +234,12 @@ __device__ __forceinline__ float ema_mass(float u, uint32_t cnt, float alpha, fl
 // different banks with aligned 16-byte reads); the chains of EC clusters run
 // side by side.
 constexpr int EC = 4;
+// LDS floats per cluster row of k_ema: seg values rounded up to a multiple of
+// four, plus four (rows stay 16-byte aligned).
+__host__ __device__ constexpr int ema_row(int seg) { return ((seg + 3) & ~3) + 4; }
 constexpr int TPC = 256 / EC;  // threads per cluster in the update
 constexpr int ECH = 1024;  // dimensions per LDS pass
+static_assert(ECH == (int)EMA_READOUT_MAX_D, "the fused readout takes one pass");
 constexpr int EU = 16;    // elements per thread whose loads are in flight together
 __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __restrict__ usage,
                                              const float* __restrict__ sums,
@@ -218,9 +251,10 @@ __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __r
                                              uint32_t* zero_counts,  // counts itself, or null
                                              char* __restrict__ csplit,
                                              uint32_t* __restrict__ cpart,
-                                             uint32_t* __restrict__ zero_words, size_t nzero) {
-  // EC rows of min(d, ECH) + 4 floats (norms only): the rounded squares;
-  // with csplit, then as many for the values.
+                                             uint32_t* __restrict__ zero_words, size_t nzero,
+                                             float* __restrict__ readout) {
+  // EC rows of min(d, ECH) + 4 floats (norms, or readout): the rounded
+  // squares; with csplit or readout, then as many for the values.
   extern __shared__ __attribute__((aligned(16))) float sq[];
   __shared__ float wgt[EC], cntf[EC];
   const int tid = threadIdx.x;
@@ -239,7 +273,7 @@ __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __r
     cntf[tid] = (float)cnt;
   }
   __syncthreads();
-  const int seg = (int)min(d, (size_t)ECH), row = seg + 4;  // rows stay 16-byte aligned
+  const int seg = (int)min(d, (size_t)ECH), row = ema_row(seg);
   float* vs = sq + EC * row;
   // Thread layout of the update: TPC threads per cluster, thread q of cluster
   // c takes dimensions q, q + TPC, ...
@@ -247,6 +281,7 @@ __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __r
   const float weight = c < nc ? wgt[c] : -1.0f;
   const float count = c < nc ? cntf[c] : 1.0f;
   float nrm = 0.0f;  // lane c < nc of wave 0: cluster c's chain
+  float tmx = 0.0f;  // readout: max |v| of this thread's values (fold from 0, fmaxf)
   for (size_t c0 = 0; c0 < d; c0 += ECH) {
     const int len = (int)min((size_t)ECH, d - c0);
     if (weight >= 0.0f) {
@@ -275,7 +310,8 @@ __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __r
           }
           p[t] = v;
           if (norms) sq[c * row + t] = v * v;
-          if (csplit) vs[c * row + t] = v;
+          if (csplit || readout) vs[c * row + t] = v;
+          if (readout) tmx = fmaxf(tmx, fabsf(v));
         }
       }
     }
@@ -329,6 +365,30 @@ __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __r
       for (; t < len; t++) nrm = nrm + r[t];
     }
     __syncthreads();
+  }
+  if (readout) {
+    // The spherical readout (faiss normalize_into, as k_normalize_rows: v /
+    // max|v|, then / sqrt of the in-order sum of the squares) of each moved
+    // row; d <= ECH, and a cluster is one wave (TPC == WAVE). Rows that did
+    // not move keep their readout.
+    __shared__ float rnorm[EC];
+    const float mx = wave_max(tmx);
+    const float s1 = mx > 0.0f ? mx : 1.0f;
+    const int len = (int)d;
+    if (weight >= 0.0f)
+      for (int t = q; t < len; t += TPC) {
+        const float qv = vs[c * row + t] / s1;
+        vs[c * row + t] = qv;
+        sq[c * row + t] = qv * qv;
+      }
+    __syncthreads();
+    if (tid < nc && wgt[tid] >= 0.0f) rnorm[tid] = sqrtf(ordered_sum(sq + tid * row, len));
+    __syncthreads();
+    if (weight >= 0.0f) {
+      const float nv = rnorm[c];
+      const float s2 = nv > 0.0f ? nv : 1.0f;
+      for (int t = q; t < len; t += TPC) readout[(j0 + c) * d + t] = vs[c * row + t] / s2;
+    }
   }
   if (norms && tid < nc && wgt[tid] >= 0.0f) norms[j0 + tid] = nrm;
   if (cpart && tid < WAVE) {
@@ -519,16 +579,18 @@ void launch_normalize_rows(emh_ctx* c, const float* src, size_t rows, size_t d, 
 void launch_ema(emh_ctx* c, float* pos, float* usage, const float* sums, const uint32_t* counts,
                 size_t k, size_t d, float alpha, float decay, int replace, float* norms,
                 bool clear_screen_words, uint32_t* tally, bool zero_counts, void* csplit,
-                uint32_t* cpart, uint32_t* zero_words, size_t nzero) {
+                uint32_t* cpart, uint32_t* zero_words, size_t nzero, float* readout) {
   if (k == 0) return;
   EMH_ENSURE(!csplit || (norms && cpart), "ema: the centroid halves need the norms and maxima");
-  const size_t lds = norms ? (size_t)EC * (std::min(d, (size_t)ECH) + 4) * sizeof(float) *
-                                 (csplit ? 2 : 1)
-                           : 0;
+  EMH_ENSURE(!readout || (!norms && !csplit && d <= (size_t)ECH),
+             "ema: the fused readout is for spherical runs with d <= %d", ECH);
+  const size_t lds = norms || readout ? (size_t)EC * ema_row((int)std::min(d, (size_t)ECH)) *
+                                            sizeof(float) * (csplit || readout ? 2 : 1)
+                                      : 0;
   hipLaunchKernelGGL(k_ema, grid1(k, EC), dim3(256), lds, c->stream, pos, usage, sums, counts, k,
                      d, alpha, decay, replace, norms, clear_screen_words ? c->small : nullptr,
                      tally, zero_counts ? const_cast<uint32_t*>(counts) : nullptr,
-                     (char*)csplit, cpart, zero_words, zero_words ? nzero : 0);
+                     (char*)csplit, cpart, zero_words, zero_words ? nzero : 0, readout);
   EMH_HIP(hipGetLastError());
 }
 

@@ -121,6 +121,10 @@ bool split_screen(emh_ctx* c, size_t n, size_t d, size_t k, bool ip) {
 bool top1_screens(emh_ctx* c, size_t n, size_t d, size_t k, bool ip) {
   return top1_geom(c, n, d, k, ip, false, true).screen;
 }
+bool top1_tallies(emh_ctx* c, size_t n, size_t d, size_t k, bool ip) {
+  // queued_direct holds for every smaller selection too (its items grow with n).
+  return d % 4 == 0 && (top1_screens(c, n, d, k, ip) || queued_direct(c, n, d, k, ip));
+}
 
 size_t top1_scratch_bytes(emh_ctx* c, size_t n, size_t d, size_t k, bool ip) {
   const Top1Geom g = top1_geom(c, n, d, k, ip, false, true);
@@ -227,12 +231,16 @@ void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t
   const size_t n = hi - lo;
   EMH_ENSURE(d <= 16384, "top1: d = %zu above the supported 16384", d);
   EMH_ENSURE(n < (1u << 31) && k < (1u << 31), "top1: shape too large");
+  // A tallying call takes the screen, or the latency-bound exact scan, which
+  // tallies too; never k_exact1.
+  const bool small_exact = !tally || queued_direct(c, n, d, k, ip);
   const Top1Screen s = screen_top1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, words_clear, ar,
-                                   pre, pc, !tally);
-  EMH_ENSURE(!tally || (s.g.screen && d % 4 == 0),
-             "top1: labels are tallied only on the screen with d %% 4 == 0");
+                                   pre, pc, small_exact);
+  EMH_ENSURE(!tally || (d % 4 == 0 && (s.g.screen || queued_direct(c, n, d, k, ip))),
+             "top1: labels are tallied only by the screen or the queued-row scan, d %% 4 == 0");
   if (!s.g.screen) {
-    launch_exact1(c, x, nx, d, ids, lo, n, nullptr, cents, cnorm, k, ip, labels, scores, ar);
+    launch_exact1(c, x, nx, d, ids, lo, n, nullptr, cents, cnorm, k, ip, labels, scores, ar,
+                  tally);
     return;
   }
   launch_verify1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, s.cand, s.g.parts, s.xnorm, labels,

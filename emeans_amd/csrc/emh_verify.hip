@@ -604,7 +604,8 @@ void launch_exact1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32
                    const float* cnorm, size_t k, bool ip, uint32_t* labels, float* scores,
                    Arena* ar, const LabelTally* tally) {
   if (n == 0) return;
-  EMH_ENSURE(!tally || (list && d % 4 == 0), "exact: a tally needs the queued-row scan");
+  EMH_ENSURE(!tally || (d % 4 == 0 && (list || queued_direct(c, n, d, k, ip))),
+             "exact: a tally needs the queued-row scan");
   // Both kernels read row 0 in place of a row whose id is out of range.
   EMH_ENSURE(nx > 0, "top1: a selection of %zu rows over no data rows", n);
   // Queued rows (few), or a small direct selection: the latency-bound scan.
