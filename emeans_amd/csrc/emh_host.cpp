@@ -873,6 +873,12 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
     if (out->positions) std::memcpy(out->positions, h_out + k * d, k * d * 4);
     if (out->usage) std::memcpy(out->usage, h_out + 2 * k * d, k * 4);
   });
+  struct JoinSide {  // an error below must not leave the task using this frame
+    std::future<void>& f;
+    ~JoinSide() {
+      if (f.valid()) f.wait();
+    }
+  } join_side{side};
   EMH_HIP(hipStreamSynchronize(c->stream));
   stats.push_back(pending.get());
   raise_flags(c, h_small);
