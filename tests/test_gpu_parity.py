@@ -109,7 +109,9 @@ def test_top1_parts_of_several_tiles(dev, screen, n, k, metric):
     (tagged keys); 4,096 centroids (16 tiles, more than eight parts): the
     large-tile screen that splits its own slabs, on 256 CUs eight parts of two
     tiles each, so its lists take the sorted insert across tiles. Bit-equal to
-    the oracle."""
+    the oracle; with the bf16 screen, the variant that ran is the intended one
+    (the parts follow the device's CU count)."""
+    from emeans_amd import Mat, Select
     d = 256
     x = _mix(n, d, 64, 0.6, metric == "ip", 7 * n + k)
     c = (x[(np.arange(k) * 37) % n] * np.float32(0.95)).astype(np.float32)
@@ -117,6 +119,16 @@ def test_top1_parts_of_several_tiles(dev, screen, n, k, metric):
     ol, osc = O.top1(x, d, c, metric)
     assert np.array_equal(gl, ol)
     assert gs.tobytes() == osc.tobytes()
+    if screen == 1:
+        cb = dev.upload_f32(c)
+        cn = None
+        if metric == "l2":
+            cn = dev.zeros_f32(k)
+            dev.row_norms(cb, k, d, cn)
+        r = dev.screen_margin(Mat(dev.bind(x), d), Select(None, (0, n)), cb, cn, k, metric)
+        want = "big_tagged" if k <= 2048 else "big_sorted"
+        assert r["variant"] == want, r
+        assert (r["tiles_per_part"] == 1) == (want == "big_tagged"), r
 
 
 @pytest.mark.parametrize("k", [2, 3, 21, 40, 63])
