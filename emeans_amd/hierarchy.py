@@ -10,6 +10,10 @@ model per group (its leaves). What runs on the device:
   Hierarchy.add      incremental.rs:306-360   label new rows, then by the
                                         policy: nothing, the EMA update, or a
                                         full retrain
+  add_photos         incremental.rs:615-860   new photos against the dedup
+                                        groups of the old ones (neighbours and
+                                        the new groups' dedup on the device),
+                                        then add of the representatives
   grow               incremental.rs:376-458   new leaves from coherent pending
                                         outliers: the candidates' pairwise dots
                                         and their dots with each trial mean on
@@ -458,6 +462,11 @@ class Hierarchy:
     def load(path, backend) -> "Hierarchy":
         """A hierarchy written by save (incremental.rs:978-988)."""
         return _hierarchy_load(path, backend)
+
+    def add_photos(self, photos, n_old: int, dd, input=None, dev=None) -> "PhotoAddReport":
+        """New photos when the hierarchy clusters dedup representatives
+        (incremental.rs:615-860); the function below the class."""
+        return add_photos(self, photos, n_old, dd, input, dev)
 
     def level1_centroids(self) -> np.ndarray:
         return self.level1.centroids
@@ -1049,3 +1058,171 @@ def _hierarchy_load(path, backend) -> "Hierarchy":
 
     return _assemble(mf, backend, model)
 
+
+
+# ---------------------------------------------------------------- photos
+@dataclass
+class PhotoAddReport:
+    """incremental.rs PhotoAddReport: new photos that joined existing dedup
+    groups, new groups formed, every photo's stable leaf and outlier flag (via
+    its group's representative), and the representatives' AddReport."""
+    joined_existing: int
+    new_groups: int
+    leaf: list
+    outlier: np.ndarray
+    reps: AddReport
+
+
+def add_photos(h: "Hierarchy", photos, n_old: int, dd, input=None, dev=None) -> PhotoAddReport:
+    """Hierarchy::add_photos (incremental.rs:615-860) when the hierarchy
+    clusters dedup representatives. Each new photo joins an existing group when
+    it shares a burst id with one of the group's photos, or when one of its k
+    neighbours among all photos is an old photo with cos >= sim_threshold (and
+    the time rule) and the photo is within rep_threshold of that group's anchor
+    (and the time rule to it); the closest such anchor wins, and a new burst
+    joins only when every one of its photos fits. The rest are grouped among
+    themselves by dedup, each new group appending one representative, which
+    then go through Hierarchy.add. dd (a DedupResult of the old photos) is
+    updated in place. The neighbours and the new groups' dedup run on the
+    device; the star rule's dots are f32 sums in order, as the reference's."""
+    from . import NONE, DedupConfig, DedupInput, dedup, knn
+    d = h.d
+    photos = np.ascontiguousarray(photos, np.float32)
+    if photos.size % d:
+        raise ValueError("photos must be n x d")
+    photos = photos.reshape(-1, d)
+    n = photos.shape[0]
+    if n < n_old:
+        raise ValueError("photos has fewer rows than n_old")
+    if len(dd.group_of) != n_old:
+        raise ValueError(f"dedup result covers {len(dd.group_of)} photos but n_old is {n_old}")
+    n_reps_old = len(dd.representatives)
+    if n_reps_old != h.state.n_seen:
+        raise ValueError(f"the hierarchy has seen {h.state.n_seen} rows but the dedup result "
+                         f"has {n_reps_old} groups")
+    inp = input or DedupInput()
+    t_all = None if inp.created_unix is None else np.asarray(inp.created_unix, np.float64)
+    if t_all is not None and len(t_all) != n:
+        raise ValueError("one timestamp per photo")
+    if inp.burst is not None and len(inp.burst) != n:
+        raise ValueError("one burst id per photo")
+    if inp.priority is not None and len(inp.priority) != n:
+        raise ValueError("one priority per photo")
+    if dev is None:
+        dev = getattr(h.backend, "dev", None)
+        if dev is None:
+            raise ValueError("add_photos needs a device for its neighbours and dedup")
+    cfg = h.dedup if h.dedup is not None else DedupConfig()
+    sim_t = np.float32(cfg.sim_threshold)
+    rep_t = np.float32(cfg.rep_threshold if cfg.rep_threshold is not None else cfg.sim_threshold)
+
+    def time_ok(i, j):
+        if cfg.max_gap_secs is None or t_all is None:
+            return True
+        a, b = t_all[i], t_all[j]
+        if not (np.isfinite(a) and np.isfinite(b)):
+            return True
+        return abs(a - b) <= cfg.max_gap_secs
+
+    m = n - n_old
+    # Neighbours of the new photos among all photos (self excluded below).
+    k = max(min(cfg.k, max(n - 1, 0)), 1)
+    nb = knn(photos[n_old:], photos, d, k + 1, dev) if m > 0 and n > 1 else None
+    # Results written before anchors were stored tested against the representative.
+    if len(dd.anchors) != n_reps_old:
+        dd.anchors = np.asarray(dd.representatives, np.uint32).copy()
+    burst = inp.burst
+    burst_group = {}
+    if burst is not None:
+        for i in range(n_old):
+            if burst[i] is not None and burst[i] not in burst_group:
+                burst_group[burst[i]] = int(dd.group_of[i])
+    # Units of new photos: a burst is one unit and always stays together.
+    units, unit_of_burst = [], {}
+    for t in range(m):
+        bid = burst[n_old + t] if burst is not None else None
+        if bid is None:
+            units.append([t])
+        else:
+            if bid not in unit_of_burst:
+                unit_of_burst[bid] = len(units)
+                units.append([])
+            units[unit_of_burst[bid]].append(t)
+
+    def fits(i, g):
+        """The star rule of dedup: within the threshold of the group's anchor."""
+        a = dd.anchor(g)
+        s = _dot_sum(photos[i], photos[a])
+        return s if (s >= rep_t and time_ok(i, a)) else None
+
+    joined = [None] * m
+    nn_new = np.full(m, -np.inf, np.float32)
+    for unit in units:
+        linked, forced = set(), None
+        for t in unit:
+            i = n_old + t
+            if forced is None and burst is not None and burst[i] is not None:
+                forced = burst_group.get(burst[i])
+            if nb is None:
+                continue
+            ids, sims = nb.row(t)
+            for j, s in zip(ids.tolist(), sims):
+                if j == NONE or j == i:
+                    continue
+                if s > nn_new[t]:
+                    nn_new[t] = s
+                if j < n_old and s >= sim_t and time_ok(i, j):
+                    linked.add(int(dd.group_of[j]))
+        # Every row of the unit must fit the anchor; the closest anchor wins.
+        best = None
+        for g in sorted(linked):
+            worst = np.float32(np.inf)
+            for t in unit:
+                s = fits(n_old + t, g)
+                if s is None:
+                    worst = None
+                    break
+                worst = min(worst, s)
+            if worst is not None and (best is None or worst > best[0]):
+                best = (worst, g)
+        group = forced if forced is not None else (best[1] if best is not None else None)
+        for t in unit:
+            joined[t] = group
+
+    # Group the remaining new photos among themselves.
+    rest = [t for t in range(m) if joined[t] is None]
+    group_of_new = np.array([0xFFFFFFFF if g is None else g for g in joined], np.uint32)
+    new_groups = sub_split = sub_pairs = 0
+    reps, anchors, sizes = list(dd.representatives), list(dd.anchors), list(dd.sizes)
+    if rest:
+        idx = np.array([n_old + t for t in rest], np.int64)
+        sub_in = DedupInput(
+            None if t_all is None else t_all[idx],
+            None if burst is None else [burst[i] for i in idx],
+            None if inp.priority is None else np.asarray(inp.priority, np.float32)[idx])
+        r = dedup(photos[idx], d, sub_in, cfg, dev)
+        base = len(reps)
+        for t, g in zip(rest, r.group_of.tolist()):
+            group_of_new[t] = base + g
+        for g, (rep, size) in enumerate(zip(r.representatives.tolist(), r.sizes.tolist())):
+            reps.append(int(idx[rep]))
+            anchors.append(int(idx[r.anchor(g)]))
+            sizes.append(size)
+        new_groups = r.n_groups()
+        sub_split, sub_pairs = r.split_components, r.linked_pairs
+    for g in group_of_new.tolist():
+        if g < n_reps_old:
+            sizes[g] += 1
+    dd.representatives = np.array(reps, np.uint32)
+    dd.anchors = np.array(anchors, np.uint32)
+    dd.sizes = np.array(sizes, np.uint32)
+    dd.group_of = np.concatenate([np.asarray(dd.group_of, np.uint32), group_of_new])
+    dd.nn_sim = np.concatenate([np.asarray(dd.nn_sim, np.float32), nn_new])
+    dd.split_components += sub_split
+    dd.linked_pairs += sub_pairs
+
+    report = h.add(photos[dd.representatives.astype(np.int64)], n_reps_old)
+    g_of = dd.group_of.astype(np.int64)
+    leaf = list(zip(report.labels.l1[g_of].tolist(), report.labels.l2[g_of].tolist()))
+    return PhotoAddReport(sum(g is not None for g in joined), new_groups, leaf,
+                          report.labels.outlier[g_of], report)

@@ -19,7 +19,11 @@ the reference's:
   update_grows_a_leaf_for_a_new_group (538-600)
                                              one new leaf for a new group,
                                              kept by the files; none for
-                                             scattered rows"""
+                                             scattered rows
+  add_photos_joins_near_duplicate_groups (164-245), add_photos_follows_burst_ids
+  (247-274), add_photos_agrees_with_a_fresh_dedup (392-477)
+                                             Hierarchy::add_photos over
+                                             dedup representatives"""
 
 import numpy as np
 import pytest
@@ -198,3 +202,130 @@ def test_update_grows_a_leaf_for_a_new_group(dev, tmp_path):
     r2 = h.add(np.concatenate([xa, scattered_rows(d, 30, 5)]), xa.shape[0])
     assert r2.action == "EmaUpdate", "precondition"
     assert r2.new_leaves == []
+
+
+# ---------------------------------------------------------------- add_photos
+def _reps(x, dd):
+    return np.ascontiguousarray(x[np.asarray(dd.representatives, np.int64)])
+
+
+def _crafted(d, parts):
+    """tests/hierarchy.rs:382-390: a unit row with the given (axis, weight) parts."""
+    from .ref_synth import normalize_rows
+    v = np.zeros((1, d), np.float32)
+    for a, w in parts:
+        v[0, a] = np.float32(w)
+    return normalize_rows(v, d)[0]
+
+
+def test_add_photos_joins_near_duplicate_groups(dev):
+    """tests/hierarchy.rs:164-245: near copies of old photos join their
+    groups, new pairs and fresh photos form new groups, sizes add up, and a
+    wrong offset fails."""
+    from emeans_amd import DedupConfig, DedupInput, autocluster as A, dedup
+    from .ref_synth import Normal, normalize_rows, with_bursts
+    x, _, _ = _data()
+    d = x.shape[1]
+    old, _, _ = with_bursts(x[:1500], d, 60, (1, 4), 0.1, 3)
+    n_old = old.shape[0]
+    dd = dedup(old, d, DedupInput(), DedupConfig(), dev)
+    h, _ = A.auto_cluster(dev, _reps(old, dd), _cfg())
+    h.dedup = DedupConfig()
+    n_reps_old = dd.n_groups()
+    rng = Normal(11)
+
+    def near(src):
+        v = (src + np.float32(0.05) * rng.direction(d)).astype(np.float32)
+        return normalize_rows(v.reshape(1, d).copy(), d)[0]
+
+    rows = [old, np.stack([near(old[i]) for i in range(20)])]
+    pairs = []
+    for i in range(10):
+        pairs += [x[2000 + i], near(x[2000 + i])]
+    rows += [np.stack(pairs), x[2010:2040]]
+    photos = np.concatenate(rows).astype(np.float32)
+    n = photos.shape[0]
+    r = h.add_photos(photos, n_old, dd, DedupInput(), dev)
+    assert r.joined_existing == 20 and r.new_groups == 40
+    assert len(r.leaf) == n and len(dd.group_of) == n
+    assert dd.n_groups() == n_reps_old + 40 and h.state.n_seen == dd.n_groups()
+    for i in range(20):
+        assert dd.group_of[n_old + i] == dd.group_of[i], f"copy {i} did not join its source"
+        assert r.leaf[n_old + i] == r.leaf[i]
+    for p in range(10):
+        a, b = n_old + 20 + 2 * p, n_old + 21 + 2 * p
+        assert dd.group_of[a] == dd.group_of[b] and dd.group_of[a] >= n_reps_old
+        assert r.leaf[a] == r.leaf[b]
+    fresh = {int(dd.group_of[i]) for i in range(n_old + 40, n)}
+    assert len(fresh) == 30 and all(g >= n_reps_old for g in fresh)
+    assert int(np.sum(dd.sizes, dtype=np.int64)) == n
+    with pytest.raises(ValueError):
+        h.add_photos(photos, n_old, dd, DedupInput(), dev)
+
+
+def test_add_photos_follows_burst_ids(dev):
+    """tests/hierarchy.rs:247-274: a new photo sharing an old photo's burst id
+    joins that photo's group; an unrelated one does not."""
+    from emeans_amd import DedupConfig, DedupInput, autocluster as A, dedup
+    x, _, _ = _data()
+    d, n_old = x.shape[1], 800
+    old = x[:n_old]
+    burst = [None] * (n_old + 2)
+    burst[5] = 9
+    dd = dedup(old, d, DedupInput(burst=burst[:n_old]), DedupConfig(), dev)
+    h, _ = A.auto_cluster(dev, _reps(old, dd), _cfg())
+    burst[n_old] = 9
+    r = h.add_photos(x[:n_old + 2], n_old, dd, DedupInput(burst=burst), dev)
+    assert r.joined_existing == 1
+    assert dd.group_of[n_old] == dd.group_of[5] and dd.group_of[n_old + 1] != dd.group_of[5]
+    assert r.leaf[n_old] == r.leaf[5]
+
+
+def test_add_photos_agrees_with_a_fresh_dedup(dev):
+    """tests/hierarchy.rs:392-477: add_photos and a fresh dedup of the same
+    photos apply one rule (within the threshold of the group's anchor, the star
+    center, whatever the representative), and give the same partition,
+    sizes, anchors and representatives."""
+    from emeans_amd import DedupConfig, DedupInput, auto, autocluster as A, dedup
+    from .ref_synth import normalize_rows
+    x, _, _ = _data()
+    d, n_bg = x.shape[1], 800
+    old = []
+    for i in range(n_bg):
+        r = x[i].copy()
+        r[80:] = 0.0
+        old.append(normalize_rows(r.reshape(1, d), d)[0])
+    old.append(_crafted(d, [(80, 1.0)]))
+    for a in range(81, 87):
+        old.append(_crafted(d, [(80, 0.96), (a, 0.28)]))
+    old = np.stack(old).astype(np.float32)
+    n_old = old.shape[0]
+    a_row, r1 = n_bg, n_bg + 1
+    n2 = (np.float32(0.96) * old[r1]).astype(np.float32)
+    n2[88] = np.float32(0.28)
+    photos = np.concatenate([old, np.stack([_crafted(d, [(80, 0.96), (87, 0.28)]), n2,
+                                            _crafted(d, [(80, 0.96), (89, 0.28)]),
+                                            _crafted(d, [(90, 1.0)])])]).astype(np.float32)
+    n = photos.shape[0]
+    n1, n2i, n3, n4 = n_old, n_old + 1, n_old + 2, n_old + 3
+    priority = np.zeros(n, np.float32)
+    priority[r1] = 1.0
+    burst = [None] * n
+    burst[n3] = burst[n4] = 4
+    cfg = DedupConfig()
+    dd = dedup(old, d, DedupInput(priority=priority[:n_old], burst=burst[:n_old]), cfg, dev)
+    ga = int(dd.group_of[a_row])
+    assert dd.sizes[ga] == 7, "precondition: A and its rim are one group"
+    assert dd.representatives[ga] == r1 and dd.anchors[ga] == a_row, "precondition"
+    h, _ = A.auto_cluster(dev, _reps(old, dd), auto.AutoConfig(k1_range=(2, 6), k2_max=4,
+                                                              restarts=1))
+    h.dedup = cfg
+    inp = DedupInput(priority=priority, burst=burst)
+    h.add_photos(photos, n_old, dd, inp, dev)
+    fresh = dedup(photos, d, inp, cfg, dev)
+    assert dd.group_of[n1] == dd.group_of[a_row], "N1 is within the threshold of the anchor"
+    assert dd.group_of[n2i] != dd.group_of[a_row], "N2 is outside the threshold of the anchor"
+    assert dd.group_of[n3] == dd.group_of[n4], "a new burst stays together"
+    assert dd.group_of[n4] != dd.group_of[a_row]
+    for f in ("group_of", "sizes", "anchors", "representatives"):
+        assert np.array_equal(np.asarray(getattr(dd, f)), np.asarray(getattr(fresh, f))), f
