@@ -552,13 +552,22 @@ __global__ __launch_bounds__(256) void k_check1(
           if (dl) {
             const v4f* cp = &stage[c & 1][cs * CDP4];
             if (n4 == CDC4) {
+              // The chunk's operands are read into registers before the
+              // chain starts, so the chain waits for LDS once per chunk
+              // rather than once per four fmas.
+              v4f xa[CDC4], wa[CDC4];
 #pragma unroll
               for (int f = 0; f < CDC4; f++) {
-                const v4f a = xp[f], w = cp[f];
-                acc = fmaf(a.x, w.x, acc);
-                acc = fmaf(a.y, w.y, acc);
-                acc = fmaf(a.z, w.z, acc);
-                acc = fmaf(a.w, w.w, acc);
+                xa[f] = xp[f];
+                wa[f] = cp[f];
+              }
+              __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+              for (int f = 0; f < CDC4; f++) {
+                acc = fmaf(xa[f].x, wa[f].x, acc);
+                acc = fmaf(xa[f].y, wa[f].y, acc);
+                acc = fmaf(xa[f].z, wa[f].z, acc);
+                acc = fmaf(xa[f].w, wa[f].w, acc);
               }
             } else {
               for (int f = 0; f < n4; f++) {
@@ -571,9 +580,13 @@ __global__ __launch_bounds__(256) void k_check1(
             }
           } else if (nl) {
             if (n4 == CDC4) {
+              v4f xa[CDC4];
+#pragma unroll
+              for (int f = 0; f < CDC4; f++) xa[f] = xp[f];
+              __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
               for (int f = 0; f < CDC4; f++) {
-                const v4f a = xp[f];
+                const v4f a = xa[f];
                 const float p0 = a.x * a.x, p1 = a.y * a.y, p2 = a.z * a.z, p3 = a.w * a.w;
                 nrm = nrm + p0;
                 nrm = nrm + p1;
