@@ -36,12 +36,16 @@ constexpr int S4_STAGE = 2 * S4_HALF;      // rows and centroids: 64 KB
 
 // Chunks of a slab row: 4 kk + (0, 1) the hi halves of dimensions 16 kk +
 // (0-7, 8-15), 4 kk + (2, 3) their lo halves, for MFMA step kk = 0, 1. In LDS
-// the chunks of row r are XOR-swizzled by (r >> 1) & 7, so that the sixteen
-// lanes of a b128 read served together (sixteen consecutive rows, one
-// chunk) hit sixteen different 16-byte bank groups.
-__device__ __forceinline__ int slot8(int r, int q) {
-  return r * SLAB_BYTES + ((q ^ ((r >> 1) & 7)) << 4);
-}
+// the chunks of row r are XOR-swizzled by swz(r). A b128 read of an operand
+// has lane l read row 32 y + (l % 32) at chunk c + l / 32 (c even); the 64
+// banks serve sixteen 16-byte groups at a time, and row r's group is
+// 8 (r % 2) + slot. With swz, the sixteen lanes l .. l + 15 (l % 16 == 0)
+// and the eight-lane pairs l .. l + 7, l + 32 .. l + 39 (l % 8 == 0) each hit
+// sixteen different groups: within a parity the rows' swz values differ in
+// bits 1-2 over rows 2 j + p (j < 4) and in bit 0 between the two halves of
+// sixteen rows, and c + l / 32 only flips bit 0. ((r >> 1) & 7 alone was
+// conflict-free only for the first grouping.)
+__device__ __forceinline__ int swz(int r) { return (((r >> 1) & 3) << 1) | ((r >> 3) & 1); }
 
 template <bool VEC4>
 __device__ __forceinline__ void load32(const float* p, int col, int d, float (&v)[32]) {
@@ -200,10 +204,11 @@ __global__ __launch_bounds__(NW * 64, 1) void k_screen4(
 
   // Loader: DMA j (0 .. ND - 1) of wave w fills LDS rows 8 NW j + 8 w + lane / 8
   // of an operand; lane's 16 bytes land in slot lane % 8 of its row, which
-  // holds chunk (lane % 8) ^ ((row >> 1) & 7) (slot8). Rows past the
-  // selection (or with a bad id) read data row 0; their lists are never written.
-  const int lq = ((lane & 7) ^ ((w * 4 + (lane >> 4)) & 7)) << 4;
+  // holds chunk (lane % 8) ^ swz(row) (8 NW j is a multiple of 32). Rows past
+  // the selection (or with a bad id) read data row 0; their lists are never
+  // written.
   const int lrow = w * 8 + (lane >> 3);
+  const int lq = ((lane & 7) ^ swz(lrow)) << 4;
   uint32_t xo[ND];  // byte offsets of the lanes' rows in a slab (nx < 2^25)
 #pragma unroll
   for (int j = 0; j < ND; j++) {
@@ -246,7 +251,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_screen4(
   // Operand reads of MFMA step kk (0, 1) of a slab from its stage X: lane
   // half h takes dimensions 16 kk + 8 h .. + 7 (chunk 4 kk + h of the hi
   // half, 4 kk + 2 + h of the lo half).
-  const int sw = (li >> 1) & 7;  // rows wr * RW + y * 32 + li: (row >> 1) & 7 = sw
+  const int sw = swz(li);  // rows wr * RW + y * 32 + li: swz(row) = sw
   struct Rows {
     v8bf bh[WN], bl[WN];
   };
@@ -471,10 +476,14 @@ __global__ __launch_bounds__(NW * 64, 1) void k_screen4(
     }
   }
   // Merge the four partial lists of each row (two lane halves x two centroid
-  // waves): keys [TR3][4][L] in stage 0, ids in stage 1.
+  // waves): keys in stage 0, ids in stage 1, entry e of contribution c for
+  // row r at c CS + r RS + e. RS is odd, so the merge's reads (one row per
+  // lane) touch 64 different banks; CS is 32 banks past a multiple of 64, so
+  // the two lane halves' stores (rows li, contributions 2 wc + h) do too.
+  constexpr int RS = L | 1, CS = (TR3 * RS + 63) / 64 * 64 + 32;
   float* MK = reinterpret_cast<float*>(s0);
   uint32_t* MI = reinterpret_cast<uint32_t*>(s1);
-  static_assert(TR3 * 4 * L * 4 <= S4_STAGE, "merge space");
+  static_assert(4 * CS * 4 <= S4_STAGE, "merge space");
   __syncthreads();
 #pragma unroll
   for (int y = 0; y < WN; y++) {
@@ -482,8 +491,8 @@ __global__ __launch_bounds__(NW * 64, 1) void k_screen4(
     const int contrib = wc * 2 + h;
 #pragma unroll
     for (int e = 0; e < L; e++) {
-      MK[(row * 4 + contrib) * L + e] = lkey[y][e];
-      MI[(row * 4 + contrib) * L + e] = lid[y][e];
+      MK[contrib * CS + row * RS + e] = lkey[y][e];
+      MI[contrib * CS + row * RS + e] = lid[y][e];
     }
   }
   __syncthreads();
@@ -496,9 +505,12 @@ __global__ __launch_bounds__(NW * 64, 1) void k_screen4(
       mk[e] = INFINITY;
       mi[e] = NONE;
     }
-    for (int q = 0; q < 4 * L; q++) {
-      const uint32_t id = MI[row * 4 * L + q];
-      if (id != NONE) insert<L>(mk, mi, MK[row * 4 * L + q], id);
+    for (int c = 0; c < 4; c++) {
+#pragma unroll
+      for (int e = 0; e < L; e++) {
+        const uint32_t id = MI[c * CS + row * RS + e];
+        if (id != NONE) insert<L>(mk, mi, MK[c * CS + row * RS + e], id);
+      }
     }
     Cand* out = cand + ((size_t)(row0 + row) * parts + part) * L;  // [row][part][L]
 #pragma unroll
