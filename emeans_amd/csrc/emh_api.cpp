@@ -21,9 +21,15 @@ static __device__ __align__(256) char scratch[SCRATCH_BYTES];
 constexpr int SCRATCH_DEVICES = 64;
 std::mutex g_scratch_mu;
 char* g_scratch[SCRATCH_DEVICES] = {};
+// Per device: an event recorded on the stream of the last call that used the
+// block (g_scratch_used once one has), which the next call's stream waits
+// for, so that calls from different streams or contexts run one after another.
+hipEvent_t g_scratch_done[SCRATCH_DEVICES] = {};
+bool g_scratch_used[SCRATCH_DEVICES] = {};
 
 // The device address of `scratch` on `device`, looked up once per device with
-// that device current (emh_create calls this after hipSetDevice).
+// that device current (emh_create calls this after hipSetDevice), and the
+// device's ordering event.
 char* scratch_setup(int device) {
   EMH_ENSURE(device >= 0 && device < SCRATCH_DEVICES, "device %d: at most %d devices", device,
              SCRATCH_DEVICES);
@@ -37,6 +43,7 @@ char* scratch_setup(int device) {
                hipGetErrorString(e));
       throw emh::Failure(m);
     }
+    EMH_HIP(hipEventCreateWithFlags(&g_scratch_done[device], hipEventDisableTiming));
     g_scratch[device] = (char*)p;
   }
   return g_scratch[device];
@@ -390,6 +397,27 @@ int emh_top1_noalloc(emh_ctx* c, const emh_buf* x, size_t d, const emh_buf* ids,
                "fixed %zu",
                hi - lo, k, d, need, SCRATCH_BYTES);
     use_device(c);
+    // The block is the GPU's, not the context's: hold the lock while queueing,
+    // make this stream wait for the previous call's work on the block, and
+    // mark this call's end for the next one (also when queueing fails midway).
+    // A stream under graph capture takes no part (an event from outside the
+    // capture cannot order it): the caller orders its graph's launches.
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    const int dv = c->device;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    EMH_HIP(hipStreamIsCapturing(c->stream, &cap));
+    const bool order = cap == hipStreamCaptureStatusNone;
+    if (order && g_scratch_used[dv])
+      EMH_HIP(hipStreamWaitEvent(c->stream, g_scratch_done[dv], 0));
+    struct Mark {
+      emh_ctx* c;
+      int dv;
+      bool on;
+      ~Mark() {
+        if (on && hipEventRecord(g_scratch_done[dv], c->stream) == hipSuccess)
+          g_scratch_used[dv] = true;
+      }
+    } mark{c, dv, order};
     emh::Arena ar{c->scratch, SCRATCH_BYTES, 0};
     emh::launch_top1(c, t.x, t.nx, d, t.ids, lo, hi, t.cents, t.cn, k, metric == EMH_IP, t.lab,
                      t.sco, false, &ar);

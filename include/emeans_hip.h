@@ -106,9 +106,13 @@ int emh_top1(emh_ctx* ctx, const emh_buf* x, size_t d, const emh_buf* ids, size_
  * d % 4 == 0; with d % 4 != 0, or without the screen, 8 ceil(k / 64) bytes
  * per row more. A call whose scratch would exceed the block fails with
  * EMH_INVALID before anything is queued.
- * Every call on a GPU shares that GPU's block: calls that overlap on one GPU
- * (two streams or contexts at once) race, so serialize them. The call is not
- * timed by emh_profile. */
+ * Every call on a GPU shares that GPU's block, which keeps the last call's
+ * contents. Calls from different streams or contexts on one GPU run one
+ * after another: each call's stream waits for the previous call's work
+ * (an event per GPU, recorded at the end of each call). A stream under HIP
+ * graph capture takes no part in that ordering: calls captured into graphs
+ * that run at once on one GPU race, so the caller orders such graphs. The
+ * call is not timed by emh_profile. */
 int emh_top1_noalloc(emh_ctx* ctx, const emh_buf* x, size_t d, const emh_buf* ids, size_t lo,
                      size_t hi, const emh_buf* centroids, const emh_buf* cnorm, size_t k,
                      int metric, emh_buf* labels, emh_buf* scores);

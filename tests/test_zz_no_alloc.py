@@ -88,3 +88,42 @@ def test_noalloc_refuses_a_call_beyond_its_block(dev):
     assert rc == _lib.EMH_INVALID
     assert b"scratch" in lib.emh_last_error()
     assert np.all(dev.read_u32(lab, (0, 16)) == 0), "nothing ran"
+
+
+def test_noalloc_two_contexts_back_to_back(dev):
+    """Two contexts (two streams) call emh_top1_noalloc one right after the
+    other with no wait between them: the block is the GPU's, so the second
+    call's stream must wait for the first call's work. Both results equal
+    emh_top1's."""
+    from emeans_amd import HipDevice
+    lib = _lib.lib()
+    d, k, metric = 768, 1024, "l2"
+    n1, n2 = 30_000, 7_000
+    x = O.contract_mixture(n1, d, 60, 0.3, False, 31).reshape(n1, d)
+    c = x[(np.arange(k) * 11) % n1].copy()
+    c[k // 2:k // 2 + 16] = c[:16]
+    other = HipDevice()
+    other.set_exact_below(0)
+    try:
+        calls = []
+        for dv, n in ((dev, n1), (other, n2)):
+            cb = dv.upload_f32(c)
+            cn = dv.zeros_f32(k)
+            dv.row_norms(cb, k, d, cn)
+            xb = dv.bind(x[:n])
+            lab = dv.upload_u32(np.full(n, 0xFFFFFFFF, np.uint32))
+            sco = dv.upload_f32(np.full(n, np.nan, np.float32))
+            dv.sync()
+            calls.append((dv, n, xb, cb, cn, lab, sco))
+        for dv, n, xb, cb, cn, lab, sco in calls:  # queued back to back, no wait between
+            _lib.check(lib.emh_top1_noalloc(dv._ctx, xb.h, d, None, 0, n, cb.h, cn.h, k,
+                                            _lib.EMH_L2, lab.h, sco.h))
+        for dv, n, xb, cb, cn, lab, sco in calls:
+            got_l, got_s = dv.read_u32(lab), dv.read_f32(sco)
+            wl, ws = dv.zeros_u32(n), dv.zeros_f32(n)
+            _lib.check(lib.emh_top1(dv._ctx, xb.h, d, None, 0, n, cb.h, cn.h, k, _lib.EMH_L2,
+                                    wl.h, ws.h))
+            assert np.array_equal(got_l, dv.read_u32(wl)), f"n = {n}: labels differ"
+            assert got_s.tobytes() == dv.read_f32(ws).tobytes(), f"n = {n}: scores differ"
+    finally:
+        other.close()
