@@ -32,11 +32,12 @@ __all__ = [
     "Assignment", "EpochStats", "Neighbors", "DedupConfig", "DedupInput", "DedupResult",
     "knn_self", "knn", "dedup", "dedup_with_neighbors", "make_assigner", "available_backends",
     "Backend", "BACKEND_NAME", "EmeansHipError", "EmeansHipInvalid",
-    "GPU_KMAX", "NONE",
+    "GPU_KMAX", "KLONG", "NONE",
 ]
 
 BACKEND_NAME = "hip"
-GPU_KMAX = 16          # emeans-core/src/knn.rs:16
+GPU_KMAX = 16          # emeans-core/src/knn.rs:16: the screened top-k's largest k
+KLONG = 4096           # the exact top-k's largest k beyond GPU_KMAX (no CPU fallback)
 NONE = 0xFFFFFFFF      # emeans-core/src/knn.rs:19
 
 
@@ -701,8 +702,10 @@ def _search(queries, data, d, k, exclude_self, dev):
         raise ValueError("queries and data must be n x d")
     if k <= 0:
         raise ValueError("k must be positive")
-    if k > GPU_KMAX:
-        raise ValueError(f"the gfx950 top-k keeps at most {GPU_KMAX} neighbours")
+    if k > KLONG:
+        raise ValueError(f"the gfx950 top-k keeps at most {KLONG} neighbours")
+    # k <= GPU_KMAX: the MFMA screen; above it (the reference's CPU search,
+    # knn.rs:42) the exact top-k on the GPU, with the same results.
     dev = dev or make_assigner()
     ids, sims = dev.topk(q, q if exclude_self else x, d, k, exclude_self)
     return Neighbors(k, ids, sims)

@@ -189,7 +189,8 @@ int emh_destroy(emh_ctx* c) {
     for (emh::Scratch* s : {&c->cand, &c->fblist, &c->order, &c->start, &c->misc, &c->knn_tmp,
                             &c->xnorm, &c->bigj, &c->chunkcnt, &c->tickets,
                             &c->preview_ticket, &c->xsplit, &c->csplit, &c->csplit_norm, &c->csplit_part,
-                            &c->xpre, &c->xpre_norm, &c->tsplit, &c->tsplit_part, &c->tally_cnt})
+                            &c->xpre, &c->xpre_norm, &c->tsplit, &c->tsplit_part, &c->tally_cnt,
+                            &c->klong})
       s->release();
     for (emh::Pinned* s : {&c->pin_usage, &c->pin_plan, &c->pin_small, &c->pin_order[0],
                            &c->pin_order[1], &c->pin_lab[0], &c->pin_lab[1], &c->pin_sco[0],
@@ -462,7 +463,8 @@ int emh_topk_dev(emh_ctx* c, const emh_buf* q, size_t m, const emh_buf* data, si
     EMH_ENSURE(c, "null context");
     EMH_ENSURE(d > 0, "d must be positive");
     EMH_ENSURE(kk > 0, "k must be positive");
-    EMH_ENSURE(kk <= 16, "topk keeps at most 16 neighbours (knn.rs:16), got %zu", kk);
+    EMH_ENSURE(kk <= (size_t)emh::KLONG, "topk keeps at most %d neighbours, got %zu", emh::KLONG,
+               kk);
     EMH_ENSURE(!exclude_self || m == n, "exclude_self needs queries == data");
     const float* qp = F(q, "queries");
     const float* dp = F(data, "data");
@@ -479,7 +481,8 @@ int emh_topk(emh_ctx* c, const float* queries, size_t m, const float* data, size
              size_t kk, int exclude_self, uint32_t* ids, float* sims) {
   return guard([&] {
     EMH_ENSURE(c && (m == 0 || (queries && ids && sims)) && (n == 0 || data), "null argument");
-    EMH_ENSURE(d > 0 && kk > 0 && kk <= 16, "need d > 0 and 1 <= k <= 16");
+    EMH_ENSURE(d > 0 && kk > 0 && kk <= (size_t)emh::KLONG, "need d > 0 and 1 <= k <= %d",
+               emh::KLONG);
     EMH_ENSURE(!exclude_self || m == n, "exclude_self needs queries == data");
     if (m == 0) return;
     use_device(c);

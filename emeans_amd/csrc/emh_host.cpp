@@ -1437,7 +1437,8 @@ int emh_dedup(emh_ctx* c, const float* x, size_t n, size_t d, const emh_dedup_in
     std::vector<uint32_t> ids(n * k, 0xffffffffu);
     std::vector<float> sims(n * k, -INFINITY);
     if (n > 1) {
-      EMH_ENSURE(k <= 16, "dedup on the GPU searches at most 16 neighbours");
+      EMH_ENSURE(k <= (size_t)emh::KLONG, "dedup on the GPU searches at most %d neighbours",
+                 emh::KLONG);
       if (emh_topk(c, x, n, x, n, d, k, 1, ids.data(), sims.data()) != EMH_OK)
         throw emh::Failure(emh_last_error());
     }

@@ -173,6 +173,7 @@ struct emh_ctx {
   emh::Scratch xpre, xpre_norm;              // a training run's rows, split once
   emh::Scratch tsplit, tsplit_part;          // a training run's centroids, kept split by the EMA
   emh::Scratch tally_cnt;                    // a training run's label tally (chunk histograms)
+  emh::Scratch klong;                        // top-k beyond 16: a query block's scores
   emh::Scratch preview_ticket;  // k_mass_preview's last-block ticket (left at zero)
   // Host staging of the device loop: masses, plan, flags, epoch orders and
   // epoch labels/scores (double-buffered), results.
@@ -412,6 +413,10 @@ size_t top1_scratch_bytes(emh_ctx* c, size_t n, size_t d, size_t k, bool ip);
 void launch_topk(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,
                  size_t kk, bool exclude_self, uint32_t* ids, float* sims,
                  emh_screen_report* rep = nullptr);
+// Exact top-k for 16 < kk <= KLONG (emh_topk_long.hip): no screen.
+constexpr int KLONG = 4096;
+void launch_topk_long(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,
+                      size_t kk, bool exclude_self, uint32_t* ids, float* sims);
 // The screen stage of a top-1 call, its lists measured instead of checked.
 void screen_margin_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
                         size_t lo, size_t hi, const float* cents, const float* cnorm, size_t k,

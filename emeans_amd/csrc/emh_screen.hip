@@ -270,6 +270,10 @@ void screen_margin_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const u
 void launch_topk(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,
                  size_t kk, bool exclude_self, uint32_t* ids, float* sims, emh_screen_report* rep) {
   if (m == 0) return;
+  if (kk > (size_t)KMAX && !rep) {  // beyond the screen's lists: the exact top-k
+    launch_topk_long(c, q, m, data, n, d, kk, exclude_self, ids, sims);
+    return;
+  }
   EMH_ENSURE(kk >= 1 && kk <= (size_t)KMAX, "topk: kk = %zu must be in 1..16", kk);
   EMH_ENSURE(d <= 16384, "topk: d = %zu above the supported 16384", d);
   EMH_ENSURE(m < (1u << 31) && n < (1u << 31), "topk: shape too large");

@@ -12,7 +12,7 @@ constexpr int L1 = 6;    // top-1: the smallest screen keys each part keeps
 constexpr int L1S = 5;   // ... with the sorted insert (parts of several 256-centroid tiles)
 constexpr int C1 = 16;   // top-1: most candidates a row sends to the exact chains
 constexpr int LK = 24;   // top-k list: kk <= 16 plus 7 spare + the bound
-constexpr int KMAX = 16;  // largest kk (emeans-core/src/knn.rs:16)
+constexpr int KMAX = 16;  // largest kk of the screened top-k (emeans-core/src/knn.rs:16)
 constexpr int MAX_PARTS = 8;  // centroid parts per row tile: lists per row the verify merges
 
 // A screen candidate: key (smaller is better: -dot for IP, |c|^2 - 2 dot for L2) and id.

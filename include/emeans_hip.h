@@ -117,9 +117,13 @@ int emh_top1_noalloc(emh_ctx* ctx, const emh_buf* x, size_t d, const emh_buf* id
                      size_t hi, const emh_buf* centroids, const emh_buf* cnorm, size_t k,
                      int metric, emh_buf* labels, emh_buf* scores);
 
-/* Device::topk (core/mod.rs:114-124): best kk (<= 16) data rows per query by
- * inner product, best first (larger score, then lower id); with exclude_self
- * query i is data row i and is skipped; missing: id 0xFFFFFFFF, score -inf.
+/* Device::topk (core/mod.rs:114-124): best kk data rows per query by inner
+ * product, best first (larger score, then lower id); with exclude_self query
+ * i is data row i and is skipped; missing: id 0xFFFFFFFF, score -inf.
+ * kk <= 16 (GPU_KMAX, emeans-core/src/knn.rs:16) runs the MFMA screen; for
+ * 16 < kk <= 4096, where the reference's knn (emeans-cluster/src/knn.rs:42)
+ * turns to its CPU search (core/src/knn.rs:53-107), an exact search on the
+ * GPU with the same results; larger kk fails with EMH_INVALID.
  * Host pointers in and out (the reference signature). */
 int emh_topk(emh_ctx* ctx, const float* queries, size_t m, const float* data, size_t n, size_t d,
              size_t kk, int exclude_self, uint32_t* ids, float* sims);
