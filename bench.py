@@ -28,7 +28,10 @@ reports train seconds, assignment Mrows/s, the rooflines and the CPU baseline:
                    bit-exact parity check;
   other_workloads  assign-only 2M x 1024 vs k = 16,384 (IP) and knn_self k = 10
                    on 500k x 384, data resident, with the oracle on a sample
-                   of queries.
+                   of queries; C5, auto_cluster of 900,000 x 768 nested rows
+                   then the add of 100,000 (stage times, fits per second, the
+                   oracle's fit rate, and a reduced C5 sequence compared with
+                   the oracle whole).
 
 `f32_screen` repeats the step with the screen on v_mfma_f32_32x32x2_f32
 (same bits, checked).
@@ -401,6 +404,8 @@ def other_workloads(args):
         "duplicates_found_as_a_neighbour": recall}
     log(f"knn 500k: {step_s * 1e3:.1f} ms per run")
     dev.close()
+    if not args.no_autok:
+        res["auto_cluster_900k_add_100k"] = autok_run(args)
     return res
 
 
@@ -513,6 +518,11 @@ def assign_workload(args):
 
 
 def autok_workload(args):
+    """C5 alone (`--workload autok`): the autok leg of the headline run."""
+    return autok_run(args)
+
+
+def autok_run(args):
     """C5 (two-level auto_cluster plus incremental add on 1,000,000 x 768
     nested unit rows, 64 Zipf(1.3) top groups of 16 sub-groups, seed 3):
     auto_cluster of the first 900,000 rows with the reference's defaults
@@ -522,13 +532,17 @@ def autok_workload(args):
     Hierarchy::add of the last 100,000 rows (incremental.rs:306-596: 11 % new
     rows call for the EMA update). The sweeps' trainings, assignments,
     seedings and internal scores run on the device, the data bound on one
-    context. `value`: spherical e-means fits per second of auto_cluster's
-    wall time. CPU baseline: the oracle's fit at k = 21 on the same rows."""
+    context (each sweep's restarts at once on four). `value`: spherical
+    e-means fits per second of auto_cluster's wall time. CPU baseline: the
+    oracle's fit at k = 21 on the same rows. Parity: the same sequence on a
+    reduced C5 set (8,000 rows of the same generator with 8 x 4 groups;
+    k1 in 2..4, k2 <= 4, leaves above 100 rows split again, so that every
+    stage runs) over the device and over the oracle, compared whole."""
     from emeans_amd import HipDevice, auto, autocluster, synth
     from emeans_amd import hierarchy as H
     from oracle import oracle as O
 
-    n_all, n, d = 1_000_000, 900_000, 768
+    n_all, n, d = args.autok_n, args.autok_n * 9 // 10, 768
     t = time.time()
     x_all, _ = synth.nested(n=n_all, d=d, seed=3)
     x = x_all[:n]
@@ -561,20 +575,62 @@ def autok_workload(args):
     o = O.train(x, d, kc, spherical=True, seed=7, init=init)
     O.assign(x, d, o["centroids"], "ip")
     cpu_fit_s = time.perf_counter() - c0
+    rep_action, rep_outliers = rep.action, rep.new_outliers
+    best1 = max(dg.level1, key=lambda s: s.silhouette) if dg.level1 else None
+    del h, labels, rep, xb, x, x_all
+    parity = autok_parity(dev)
     dev.close()
-    return {"value": tm["fits"] / ac_s, "unit": "fits/s", "auto_cluster_s": ac_s,
+    return {"value": tm["fits"] / ac_s, "unit": "fits/s", "rows": n, "added_rows": n_all - n,
+            "auto_cluster_s": ac_s,
             "sweep_fits": tm["fits"], "ms_per_fit": tm["fit_s"] / max(tm["fits"], 1) * 1e3,
             "kmeans_pp_s": tm["kmeans_pp_s"], "internal_scores_s": tm["scores_s"],
             "stages_s": {kk[:-2]: v for kk, v in tm.items()
                          if kk.endswith("_s") and kk not in ("fit_s", "kmeans_pp_s", "scores_s")},
-            "k1": k1, "leaves": sum(k2), "k2": k2, "resplits": dg.resplits, "flat": dg.flat,
-            "level1_candidates": [vars(s) for s in dg.level1],
-            "add": {"rows": n_all - n, "action": rep.action, "seconds": add_s,
-                    "new_outliers": rep.new_outliers},
+            "k1": k1, "leaves": sum(k2), "resplits": dg.resplits, "flat": dg.flat,
+            "level1_cuts_scored": len(dg.level1),
+            "level1_best_silhouette": None if best1 is None else
+            {"k": best1.k, "silhouette": best1.silhouette},
+            "add": {"rows": n_all - n, "action": rep_action, "seconds": add_s,
+                    "new_outliers": rep_outliers},
             "cpu_baseline": {"value": 1.0 / cpu_fit_s, "unit": "fits/s", "cores": O.get_threads(),
                              "kind": "port", "fit_s": cpu_fit_s,
                              "sample": f"one fit (k = {kc}: train_from k-means++ rows, 5 epochs, "
-                                       f"then assign) on the same {n} rows"}}
+                                       f"then assign) on the same {n} rows"},
+            "parity": parity}
+
+
+def autok_parity(dev):
+    """auto_cluster then Hierarchy::add on a reduced C5 set, on the device and
+    over the oracle (tests/oracle_device.py): sweeps, resplits, leaves, the
+    cut, labels, the hierarchy and its file, the add's labels."""
+    from emeans_amd import auto, autocluster, synth
+    from tests.oracle_device import OracleDevice
+
+    x, _ = synth.nested(n=8000, d=768, top=8, sub=4, seed=3)
+    cfg = auto.AutoConfig(k1_range=(2, 4), k2_max=4, max_cluster_size=100, restarts=2)
+    out = {}
+    hs = []
+    for name, dv in (("device", dev), ("oracle", OracleDevice(dev.name()))):
+        t = time.perf_counter()
+        h, lab = autocluster.auto_cluster(dv, x[:7200], cfg)
+        rep = h.add(x, 7200)
+        out[f"{name}_s"] = time.perf_counter() - t
+        hs.append((h, lab, rep))
+    (hg, lg, rg), (ho, lo, ro) = hs
+    same = lambda a, b: all(np.asarray(getattr(a, f)).tobytes() == np.asarray(getattr(b, f)).tobytes()
+                            for f in ("l1", "l2", "sim1", "sim", "outlier", "slot1", "slot2"))
+    ho.diagnostics = hg.diagnostics  # wall-clock seconds aside, compared below
+    for a, b in zip([hg.level1] + [g.model for g in hg.groups],
+                    [ho.level1] + [g.model for g in ho.groups]):
+        if a is not None and b is not None:
+            b.stats = [(s[0], t[1], s[2], s[3]) for s, t in zip(b.stats, a.stats)]
+    out.update({"rows": 7200, "added": 800, "resplits": hg.diagnostics.resplits,
+                "leaves": sum(hg.chosen_k()[1]), "chosen_k_equal": hg.chosen_k() == ho.chosen_k(),
+                "add_action_equal": rg.action == ro.action,
+                "labels_equal": same(rg.labels, ro.labels),
+                "hierarchy_file_equal": hg.to_bytes() == ho.to_bytes()})
+    log(f"autok parity (reduced C5, device vs oracle): {out}")
+    return out
 
 
 def copy_probe(mib):
@@ -614,6 +670,10 @@ def main():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run a plain device copy of MIB MiB (HBM counter calibration)")
     ap.add_argument("--autok-restarts", type=int, default=4)
+    ap.add_argument("--autok-n", type=int, default=1_000_000,
+                    help="C5 rows (auto_cluster on 90 %%, then the add of the rest)")
+    ap.add_argument("--no-autok", action="store_true",
+                    help="skip the C5 leg of the headline run's other workloads")
     ap.add_argument("--workload", choices=["headline", "knn", "assign", "autok"],
                     default="headline",
                     help="headline: train + assign 200k x 768 (the metric); knn: knn_self "

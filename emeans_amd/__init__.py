@@ -115,8 +115,23 @@ class HipDevice:
         h = C.c_void_p()
         check(lib().emh_create(device, C.byref(h)))
         self._ctx = h
+        self._device = device
+        self._more: List["HipDevice"] = []
+
+    def contexts(self, n: int) -> List["HipDevice"]:
+        """This context and n - 1 more on the same GPU (made once, closed with
+        this one): independent work, one thread per context, runs at once on
+        their streams. Buffers of any of them serve the others, but each
+        context orders only its own stream: a buffer another context writes is
+        ready once that context's read (or sync) has returned."""
+        while len(self._more) < n - 1:
+            self._more.append(HipDevice(self._device))
+        return [self] + self._more[:max(n - 1, 0)]
 
     def close(self):
+        for m in getattr(self, "_more", []):
+            m.close()
+        self._more = []
         if self._ctx:
             lib().emh_destroy(self._ctx)
             self._ctx = None

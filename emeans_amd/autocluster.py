@@ -82,8 +82,12 @@ def fit_group(dev: HipDevice, xg: np.ndarray, cfg, salt: int, tm: Optional[dict]
 
 
 def _split_rows(r: np.ndarray, labels: np.ndarray, k: int) -> List[np.ndarray]:
-    """The rows r grouped by their labels 0..k, each group in row order."""
-    return [r[labels == j] for j in range(k)]
+    """The rows r grouped by their labels 0..k, each group in row order (a
+    stable sort by label keeps the order within a label)."""
+    labels = np.asarray(labels, np.int64)
+    order = np.argsort(labels, kind="stable")
+    counts = np.bincount(labels, minlength=k)[:k]
+    return np.split(np.asarray(r)[order[:int(counts.sum())]], np.cumsum(counts)[:-1])
 
 
 def stage_a(dev: HipDevice, x: np.ndarray, xb, cfg, diag: Diagnostics,
@@ -208,18 +212,35 @@ def average_linkage(x: np.ndarray, rows: List[np.ndarray]):
         dots[a, a:] = v
         dots[a:, a] = v
     alive = np.ones(l, bool)
-    upper = np.triu(np.ones((l, l), bool), 1)
+    neg = -np.inf
+    # The pair merged next is the first (a < b, both alive) in row-major order
+    # of the largest s = dots[a, b] / (size[a] size[b]) above -inf (NaN never
+    # wins), as a scan with a strict > finds it. Each row keeps its own first
+    # best column (bv, bb); a merge changes row a, column a and kills b, so
+    # only rows whose best was a or b are scanned again, and the others
+    # compare their new column a with their best.
+    bv = np.full(l, neg)
+    bb = np.full(l, -1, np.int64)
+
+    def scan(a):
+        if a >= l - 1 or not alive[a]:
+            bv[a], bb[a] = neg, -1
+            return
+        s = dots[a, a + 1:] / (size[a] * size[a + 1:])
+        v = np.where(alive[a + 1:] & (s > neg), s, neg)
+        j = int(np.argmax(v))
+        bv[a], bb[a] = (float(v[j]), a + 1 + j) if v[j] > neg else (neg, -1)
+
+    for a in range(l):
+        scan(a)
     merges = []
     for _ in range(1, l):
-        ok = upper & alive[:, None] & alive[None, :]
-        s = dots / (size[:, None] * size[None, :])
-        valid = ok & (s > -np.inf)
-        if valid.any():
-            flat = int(np.argmax(np.where(valid, s, -np.inf)))
-            a, b = divmod(flat, l)
-            best = float(s[a, b])
+        cand = np.where(alive & (bb >= 0), bv, neg)
+        a = int(np.argmax(cand))
+        if cand[a] > neg:
+            b, best = int(bb[a]), float(bv[a])
         else:
-            best, a, b = -np.inf, 0, 0
+            best, a, b = neg, 0, 0
         alive[b] = False
         size[a] += size[b]
         sums[a] = sums[a] + sums[b]
@@ -228,6 +249,18 @@ def average_linkage(x: np.ndarray, rows: List[np.ndarray]):
         dots[a] = merged
         dots[a, a] = float(np.add.accumulate(sums[a] * sums[a])[-1])
         merges.append((a, b, best))
+        scan(b)
+        scan(a)
+        rows = np.flatnonzero(alive[:a])
+        if len(rows):
+            v = dots[rows, a] / (size[rows] * size[a])
+            redo = (bb[rows] == a) | (bb[rows] == b)
+            up = ~redo & (v > neg) & ((v > bv[rows]) | ((v == bv[rows]) & (a < bb[rows])))
+            bv[rows[up]], bb[rows[up]] = v[up], a
+            for r in rows[redo]:
+                scan(int(r))
+        for r in np.flatnonzero(alive[a + 1:b] & (bb[a + 1:b] == b)) + a + 1:
+            scan(int(r))
     return merges
 
 

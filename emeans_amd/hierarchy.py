@@ -380,7 +380,11 @@ def normalize_rows(m: np.ndarray) -> np.ndarray:
 
 
 def row_sums_f64(x: np.ndarray, rows: List[np.ndarray]) -> np.ndarray:
-    """Each group's f64 sum of its rows, added row by row in order (from 0)."""
+    """Each group's f64 sum of its rows, added row by row in order (from 0).
+    numpy reduces axis 0 of a C-contiguous block one row after another into
+    the accumulator (the pairwise scheme is for the contiguous axis), so the
+    reduce is that chain; tests/test_hierarchy_host.py holds it bit-equal to
+    the running sums of np.add.accumulate."""
     d = x.shape[1]
     out = np.zeros((len(rows), d), np.float64)
     for g, r in enumerate(rows):
@@ -388,7 +392,7 @@ def row_sums_f64(x: np.ndarray, rows: List[np.ndarray]) -> np.ndarray:
         for lo in range(0, len(r), 4096):
             blk = x[np.asarray(r[lo:lo + 4096], np.int64)].astype(np.float64)
             blk[0] += acc
-            acc = np.add.accumulate(blk, axis=0)[-1]
+            acc = np.add.reduce(blk, axis=0)
         out[g] = acc
     return out
 
@@ -503,17 +507,20 @@ class Hierarchy:
         slot1, slot2 = sl[:, 0].astype(np.uint32), sl[:, 1].astype(np.uint32)
         ids1 = np.asarray(self.ids1, np.uint32)
         c1 = self.level1_centroids().reshape(-1, d)
-        l2 = np.zeros(x.shape[0], np.uint32)
-        floor = np.full(x.shape[0], np.nan, np.float32)
+        # Per leaf of the concatenation: its stable id (0 past the group's
+        # ids) and its floor (NaN past the group's floors).
+        l2_of, floor_of = [], []
         for g, grp in enumerate(self.groups):
-            sel = slot1 == g
-            if not sel.any():
+            if grp.model is None:
                 continue
-            j = slot2[sel].astype(np.int64)
+            j = np.arange(grp.model.k)
             ids = np.asarray(grp.ids + [0], np.uint32)
-            l2[sel] = ids[np.minimum(j, len(grp.ids))]
             fl = np.concatenate([grp.floors.astype(np.float32), [np.float32(np.nan)]])
-            floor[sel] = fl[np.minimum(j, len(grp.floors))]
+            l2_of.append(ids[np.minimum(j, len(grp.ids))])
+            floor_of.append(fl[np.minimum(j, len(grp.floors))])
+        li = leaf.astype(np.int64)
+        l2 = np.concatenate(l2_of)[li]
+        floor = np.concatenate(floor_of).astype(np.float32)[li]
         sim1 = np.empty(x.shape[0], np.float32)
         for lo in range(0, x.shape[0], 16384):
             p = (x[lo:lo + 16384] * c1[slot1[lo:lo + 16384]]).astype(np.float32)

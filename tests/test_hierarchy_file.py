@@ -280,3 +280,36 @@ def test_grow_forms_a_leaf_for_a_new_group_over_the_oracle():
     r2 = h.add(np.concatenate([xa, scattered]), xa.shape[0])
     assert r2.action == "EmaUpdate", "precondition"
     assert r2.new_leaves == []
+
+
+def test_assign_lookup_equals_the_per_group_loop():
+    """Hierarchy.assign's leaf tables (stable id, floor) give what a loop over
+    the groups gives (auto.rs:1135-1189): groups without a model, NaN floors,
+    and a group with fewer ids and floors than leaves (0 and NaN past them)."""
+    h = _small_hierarchy()
+    h.groups[0].ids = [7]
+    h.groups[0].floors = np.array([0.25], np.float32)
+    d = h.d
+    x = normalize_rows(np.random.RandomState(8).standard_normal((500, d)).astype(np.float32), d)
+    got = h.assign(x)
+    cents, slot = [], []
+    for g, grp in enumerate(h.groups):
+        if grp.model is not None:
+            cents.append(grp.model.centroids.reshape(-1, d))
+            slot.extend((g, j) for j in range(grp.model.k))
+    leaf, sims = OracleBackend().leaf_top1(x, np.concatenate(cents))
+    sl = np.asarray(slot, np.int64)[leaf.astype(np.int64)]
+    l2 = np.zeros(len(x), np.uint32)
+    floor = np.full(len(x), np.nan, np.float32)
+    for g, grp in enumerate(h.groups):
+        sel = sl[:, 0] == g
+        if not sel.any():
+            continue
+        j = sl[sel, 1]
+        ids = np.asarray(grp.ids + [0], np.uint32)
+        l2[sel] = ids[np.minimum(j, len(grp.ids))]
+        fl = np.concatenate([grp.floors.astype(np.float32), [np.float32(np.nan)]])
+        floor[sel] = fl[np.minimum(j, len(grp.floors))]
+    assert np.array_equal(got.l2, l2)
+    assert np.array_equal(got.outlier, np.isfinite(floor) & (sims.astype(np.float32) < floor))
+    assert set(got.l2[got.slot1 == 0].tolist()) <= {7, 0} and 0 in got.l2[got.slot1 == 0]

@@ -125,3 +125,86 @@ def test_cut_numbers_groups_by_lowest_leaf():
     assert A.cut(5, merges, 4).tolist() == [0, 1, 2, 3, 2]
     assert A.cut(5, merges, 3).tolist() == [0, 1, 2, 0, 2]
     assert A.cut(5, merges, 2).tolist() == [0, 1, 0, 0, 0]
+
+
+def _linkage_full_scan(x, rows):
+    """auto.rs:799-858 as a full scan per merge: the first pair (row-major,
+    a < b, both alive) of the largest s = dots / (|A| |B|) above -inf."""
+    from emeans_amd import autocluster as A
+    from emeans_amd import hierarchy as H
+    l = len(rows)
+    sums = H.row_sums_f64(x, rows)
+    size = np.array([float(len(r)) for r in rows], np.float64)
+    dots = np.zeros((l, l), np.float64)
+    for a in range(l):
+        v = A._seq_dot64(sums[a:], sums[a])
+        dots[a, a:] = v
+        dots[a:, a] = v
+    alive = np.ones(l, bool)
+    merges = []
+    for _ in range(1, l):
+        best, a, b = -np.inf, 0, 0
+        for p in range(l):
+            for q in range(p + 1, l):
+                if alive[p] and alive[q]:
+                    s = dots[p, q] / (size[p] * size[q])
+                    if s > best:
+                        best, a, b = float(s), p, q
+        alive[b] = False
+        size[a] += size[b]
+        sums[a] = sums[a] + sums[b]
+        merged = dots[a] + dots[b]
+        dots[:, a] = merged
+        dots[a] = merged
+        dots[a, a] = float(np.add.accumulate(sums[a] * sums[a])[-1])
+        merges.append((a, b, best))
+    return merges
+
+
+def test_average_linkage_equals_a_full_scan_per_merge():
+    """The incremental search (each row's best partner, rescanned only when a
+    merge touches it) makes the merges a strict-> full scan makes: exact ties
+    (rows of -1/0/1, all-equal rows), NaN sums, random data."""
+    from emeans_amd import autocluster as A
+    g = np.random.default_rng(5)
+    for trial in range(24):
+        n, d, l = int(g.integers(30, 800)), int(g.integers(2, 12)), int(g.integers(2, 40))
+        kind = trial % 4
+        if kind == 0:
+            x = g.standard_normal((n, d)).astype(np.float32)
+        elif kind == 1:
+            x = g.integers(-1, 2, (n, d)).astype(np.float32)
+        elif kind == 2:
+            x = g.standard_normal((n, d)).astype(np.float32)
+            x[g.integers(0, n, 2)] = np.nan
+        else:
+            x = np.zeros((n, d), np.float32)
+            x[:, 0] = 1.0
+        lab = g.integers(0, l, n)
+        rows = [np.flatnonzero(lab == j) for j in range(l)]
+        rows = [r if len(r) else np.array([0]) for r in rows]
+        want, got = _linkage_full_scan(x, rows), A.average_linkage(x, rows)
+        assert [(a, b) for a, b, _ in got] == [(a, b) for a, b, _ in want], trial
+        assert np.array([s for _, _, s in got]).tobytes() == \
+            np.array([s for _, _, s in want]).tobytes(), trial
+
+
+def test_row_sums_are_the_running_sum_and_splits_keep_row_order():
+    """row_sums_f64 equals np.add.accumulate's last running sum bit for bit
+    (values over 16 orders of magnitude, groups above the 4,096-row block),
+    and _split_rows groups rows by label in row order."""
+    from emeans_amd import autocluster as A
+    from emeans_amd import hierarchy as H
+    g = np.random.default_rng(9)
+    n, d, l = 20_000, 24, 5
+    x = (g.standard_normal((n, d)) * 10.0 ** g.integers(-8, 8, (n, 1))).astype(np.float32)
+    lab = g.integers(0, l, n)
+    rows = [np.flatnonzero(lab == j) for j in range(l)]
+    got = H.row_sums_f64(x, rows)
+    for j, r in enumerate(rows):
+        want = np.add.accumulate(x[r].astype(np.float64), axis=0)[-1]
+        assert got[j].tobytes() == want.tobytes(), j
+    r = g.permutation(n)[:9000]
+    lr = g.integers(0, 7, 9000)
+    for j, part in enumerate(A._split_rows(r, lr, 7)):
+        assert np.array_equal(part, r[lr == j]), j
