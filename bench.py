@@ -395,7 +395,8 @@ def other_workloads(args):
     res["knn_self_500kx384_k10"] = {
         "value": 2.0 * n * n * d / step_s / 1e12, "unit": "TFLOP/s", "ms_per_run": step_s * 1e3,
         "steps": args.other_steps,
-        "roofline": screen_roofline(ms, launches, flop, "k_screen (kNN, 24-entry lists)"),
+        "roofline": screen_roofline(ms, launches, flop,
+                                    "k_screen4kn (kNN over rows split once, 24-entry lists)"),
         "cpu_baseline": {"value": 2.0 * len(sample) * n * d / cpu_s / 1e12, "unit": "TFLOP/s",
                          "cores": O.get_threads(), "kind": "port",
                          "sample": f"{len(sample)} queries against all {n} rows"},
@@ -439,7 +440,9 @@ def knn_workload(args):
            "ms_per_step": step_s * 1e3, "higher_is_better": True, "scaling": "weak",
            "vs_baseline": None, "dtype": "f32", "data": "synthetic",
            "config": {"workload": f"knn_self k=10 {n}x{d} unit rows, 5% near-duplicates, seed 2"},
-           "roofline": screen_roofline(ms, launches, flop, "k_screen (kNN, bf16 three-pass MFMA, 24-entry lists)")}
+           "roofline": screen_roofline(ms, launches, flop,
+                                       "k_screen4kn (kNN over rows split once, bf16 three-pass "
+                                       "MFMA, 24-entry lists)")}
     if not args.no_cpu:
         from oracle import oracle as O
         g = np.random.default_rng(0)

@@ -341,7 +341,7 @@ class HipDevice:
         return self.read_f32(out).reshape(m, nb)
 
     SCREEN_VARIANTS = {0: "none", 1: "big_tagged", 2: "big_sorted", 3: "small_bf16",
-                       4: "small_f32"}
+                       4: "small_f32", 5: "big_knn"}
 
     def screen_margin(self, x: Mat, sel: Select, centroids: DevBuf, cnorm: Optional[DevBuf],
                       k: int, metric) -> dict:

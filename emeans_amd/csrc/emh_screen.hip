@@ -277,6 +277,25 @@ void launch_topk(emh_ctx* c, const float* q, size_t m, const float* data, size_t
   EMH_ENSURE(kk >= 1 && kk <= (size_t)KMAX, "topk: kk = %zu must be in 1..16", kk);
   EMH_ENSURE(d <= 16384, "topk: d = %zu above the supported 16384", d);
   EMH_ENSURE(m < (1u << 31) && n < (1u << 31), "topk: shape too large");
+  if (n > 0 && screen4kn_fits(c, m, n, d)) {
+    // The operands split once, the 128 x 256 DMA-fed screen, then the same check.
+    Cand* cand = nullptr;
+    float* xnorm = nullptr;
+    const int parts = screen4kn(c, q, m, data, n, d, kk, exclude_self, &cand, &xnorm);
+    if (rep) {
+      *rep = emh_screen_report{};
+      rep->variant = EMH_SCREEN_BIG_KNN;
+      rep->parts = parts;
+      rep->tiles_per_part = 0;
+      launch_margin(c, q, m, d, nullptr, 0, m, data, nullptr, true, cand, parts, LK, xnorm, 1,
+                    rep);
+      return;
+    }
+    uint32_t* fb = (uint32_t*)c->fblist.get(m * 4);
+    launch_verifyk(c, q, m, data, n, d, kk, cand, parts, xnorm, ids, sims, fb);
+    launch_exactk(c, q, m, data, n, d, kk, exclude_self, fb, ids, sims);
+    return;
+  }
   const int TR = 64;
   const int row_tiles = (int)((m + TR - 1) / TR);
   const int ntiles = (int)((n + TC - 1) / TC);

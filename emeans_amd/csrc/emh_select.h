@@ -150,6 +150,12 @@ void launch_verify1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint3
                     const Cand* cand, int parts, const float* xnorm, uint32_t* labels,
                     float* scores, uint32_t* fb, bool tagged = false,
                     const LabelTally* tally = nullptr, int L = L1);
+// The kNN screen over split operands (emh_screen4kn.hip): whether it takes a
+// call, and the call's screen (candidate lists [m][parts][LK] and the queries'
+// |q|^2, in the context's scratch); returns the parts.
+bool screen4kn_fits(emh_ctx* c, size_t m, size_t n, size_t d);
+int screen4kn(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,
+              size_t kk, bool exclude_self, Cand** cand, float** xnorm);
 void launch_verifyk(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,
                     size_t kk, const Cand* cand, int parts, const float* xnorm, uint32_t* ids,
                     float* sims, uint32_t* fb);

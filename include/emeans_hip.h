@@ -351,8 +351,9 @@ float emh_host_numpy_sum_f32(const float* a, uint64_t n);
 #define EMH_SCREEN_NONE 0        /* no screen: k < 2, d < 32 or emh_set_screen(ctx, 0) */
 #define EMH_SCREEN_BIG_TAGGED 1  /* large-tile bf16 screen, one tile per part, tagged keys */
 #define EMH_SCREEN_BIG_SORTED 2  /* large-tile bf16 screen, several tiles per part */
-#define EMH_SCREEN_SMALL_BF16 3  /* 128 x 128 bf16 screen (d % 4 != 0, and kNN) */
+#define EMH_SCREEN_SMALL_BF16 3  /* 128 x 128 bf16 screen (d % 4 != 0, and small kNN calls) */
 #define EMH_SCREEN_SMALL_F32 4   /* 128 x 128 f32 screen (emh_set_screen(ctx, 2)) */
+#define EMH_SCREEN_BIG_KNN 5     /* kNN: 128 x 256 bf16 screen over operands split once */
 typedef struct emh_screen_report {
   int variant;          /* EMH_SCREEN_* */
   int parts;            /* centroid (or data row) parts per row tile */

@@ -223,5 +223,16 @@ def test_margin_knn_lists(dev, mode):
     finally:
         dev.set_screen(1)
     _record(f"knn 20000x384 screen={mode}", r)
-    assert r["variant"] == ("small_f32" if mode == 2 else "small_bf16")
+    assert r["variant"] == ("small_f32" if mode == 2 else "big_knn")
+    assert r["pairs"] > 0 and r["over"] == 0 and r["max_dot_ratio"] <= 0.5, r
+
+
+def test_margin_knn_lists_small_screen(dev):
+    """The 128 x 128 kNN screen, which calls of fewer than 256 queries take."""
+    from emeans_amd import synth
+    n, d = 8_000, 384
+    x, _, _ = synth.knn_near_duplicates(n=n, d=d, seed=4)
+    r = dev.screen_margin_topk(dev.bind(x[:200]), 200, dev.bind(x), n, d, False)
+    _record("knn 200x8000x384 small screen", r)
+    assert r["variant"] == "small_bf16"
     assert r["pairs"] > 0 and r["over"] == 0 and r["max_dot_ratio"] <= 0.5, r

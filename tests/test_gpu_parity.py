@@ -478,6 +478,29 @@ def test_topk_production_duplicates(dev, screen):
     assert np.array_equal(gi, oi) and gs.tobytes() == osims.tobytes()
 
 
+@pytest.mark.parametrize("m,n,d,kk,self_", [
+    (256, 20_000, 384, 10, False),   # two query tiles: eight parts of ten data tiles
+    (1000, 3000, 100, 16, False),    # a partial last slab (100 = 3 x 32 + 4)
+    (777, 5000, 99, 7, False),       # d % 4 != 0 (the split's scalar loads)
+    (3000, 3000, 64, 16, True),      # exclude_self
+    (2048, 2048, 768, 1, True),      # k = 1
+])
+def test_topk_split_screen(dev, screen, m, n, d, kk, self_):
+    """Calls of at least 256 queries against at least 512 rows take the kNN
+    screen over operands split once (k_screen4kn): ids and sims bit-equal to
+    the oracle, with exact duplicates among the data rows."""
+    data = _mix(n, d, 12, 0.25, True, m + n + d)
+    data[n // 2:n // 2 + 64] = data[:64]  # exact duplicates: equal scores, lower id first
+    q = data[:m].copy() if self_ else _mix(m, d, 12, 0.25, True, 3 * m + d)
+    if not self_:
+        q[:32] = data[n // 2:n // 2 + 32]
+    gi, gs = dev.topk(q if not self_ else data, data, d, kk, self_)
+    oi, osims = O.knn(q if not self_ else data, data, d, kk, self_)
+    bad = np.nonzero(gi != oi)[0]
+    assert bad.size == 0, f"{bad.size} ids differ, first {bad[:4]}"
+    assert gs.tobytes() == osims.tobytes()
+
+
 def test_backend_is_available_by_name():
     """available_backends lists "hip" on a gfx950 machine; make_assigner builds
     it from either name (backend.rs:84-114)."""
