@@ -243,6 +243,7 @@ def headline(args):
     if not args.no_others:
         del xb, labels, scores, cb
         dev.close()
+        out["ops_bench"] = ops_bench()
         out["other_workloads"] = other_workloads(args)
     return out
 
@@ -520,6 +521,71 @@ def assign_workload(args):
     return out
 
 
+def ops_bench(reps=5, n=200_000, d=768, k=1024, b=16_384):
+    """Each Device op on one training batch, the reference's ops_bench pattern
+    (bench/src/bin/ops_bench.rs:23-167): unit rows from 500 blobs (sigma 0.5,
+    seed 5), one warm-up, then the median of `reps` calls, each followed by a
+    one-element read that waits for the device (so a time includes one round
+    trip, which "sync" alone measures). Milliseconds per call."""
+    from emeans_amd import EmaStep, HipDevice, Mat, Select, synth
+
+    x, _ = synth.blobs_spherical(n=n, d=d, k=500, sigma=0.5, seed=5)
+    dev = HipDevice()
+    xb = dev.bind(x)
+    perm = ((np.arange(n, dtype=np.uint64) * 7919 + 1) % n).astype(np.uint32)
+    ids = dev.upload_u32(perm)
+    c = dev.upload_f32(x[:k])
+    unit, cn = dev.zeros_f32(k * d), dev.zeros_f32(k)
+    lab, sco = dev.zeros_u32(n), dev.zeros_f32(n)
+    sums, counts, pas = dev.zeros_f32(k * d), dev.zeros_u32(k), dev.zeros_f32(k * d)
+    pos, usage = dev.upload_f32(x[:k]), dev.upload_f32(np.ones(k, np.float32))
+    probe = dev.zeros_u32(1)
+    kq, kk = 2048, 10
+    knn_ids, knn_sims = dev.zeros_u32(kq * kk), dev.zeros_f32(kq * kk)
+    plan = [(j, k - 1 - j) for j in range(16)]
+    out = {}
+
+    def time_op(name, f):
+        f()
+        dev.read_u32(probe, (0, 1))
+        t = []
+        for _ in range(reps):
+            s = time.perf_counter()
+            f()
+            dev.read_u32(probe, (0, 1))
+            t.append((time.perf_counter() - s) * 1e3)
+        out[name] = float(np.median(t))
+
+    time_op("sync", lambda: None)
+    time_op("normalize_rows", lambda: dev.normalize_rows(c, k, d, unit))
+    time_op("row_norms", lambda: dev.row_norms(c, k, d, cn))
+    time_op("top1", lambda: dev.top1(Mat(xb, d), Select(ids, (0, b)), unit, None, k, "ip", lab,
+                                     sco))
+    time_op("top1_dense", lambda: dev.top1(Mat(xb, d), Select(None, (0, b)), unit, None, k, "ip",
+                                           lab, sco))
+    time_op("top1_l2", lambda: dev.top1(Mat(xb, d), Select(ids, (0, b)), c, cn, k, "l2", lab,
+                                        sco))
+    time_op("scatter_add", lambda: dev.scatter_add(Mat(xb, d), Select(ids, (0, b)), lab, k, sums,
+                                                   counts, pas))
+    time_op("ema_update", lambda: dev.ema_update(pos, usage, sums, counts, k, d,
+                                                 EmaStep.new(0.3)))
+    time_op("split", lambda: dev.split(pos, usage, plan, d))
+    time_op(f"topk_{kq}x{n}_k{kk}", lambda: dev.topk_dev(xb, kq, xb, n, d, kk, False, knn_ids,
+                                                         knn_sims))
+    time_op("read_usage", lambda: dev.read_f32(usage, (0, k)))
+    time_op("read_pos", lambda: dev.read_f32(pos, (0, k * d)))
+    dev.close()
+    log("ops_bench (ms, median of %d, synced): " % reps
+        + ", ".join(f"{kk_} {v:.3f}" for kk_, v in out.items()))
+    return {"unit": "ms per call (median, one device round trip included)", "reps": reps,
+            "n": n, "d": d, "k": k, "batch": b, "ops": out}
+
+
+def ops_workload(args):
+    """The per-op table alone (`--workload ops`)."""
+    return ops_bench(reps=max(args.steps, 5))
+
+
 def autok_workload(args):
     """C5 alone (`--workload autok`): the autok leg of the headline run."""
     return autok_run(args)
@@ -677,7 +743,7 @@ def main():
                     help="C5 rows (auto_cluster on 90 %%, then the add of the rest)")
     ap.add_argument("--no-autok", action="store_true",
                     help="skip the C5 leg of the headline run's other workloads")
-    ap.add_argument("--workload", choices=["headline", "knn", "assign", "autok"],
+    ap.add_argument("--workload", choices=["headline", "knn", "assign", "autok", "ops"],
                     default="headline",
                     help="headline: train + assign 200k x 768 (the metric); knn: knn_self "
                          "500k x 384; assign: 2M x 1024 vs k = 16384")
@@ -695,7 +761,7 @@ def main():
     if args.copy_probe:
         copy_probe(args.copy_probe)
     out = {"headline": headline, "knn": knn_workload, "assign": assign_workload,
-           "autok": autok_workload}[args.workload](args)
+           "autok": autok_workload, "ops": ops_workload}[args.workload](args)
     print(json.dumps(out), flush=True)
 
 

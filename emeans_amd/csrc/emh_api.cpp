@@ -2,6 +2,7 @@
 // Device ops, each validated like the reference CPU backend
 // (crates/emeans-core/src/core/cpu.rs) before anything is queued.
 
+#include <atomic>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -68,10 +69,13 @@ int guard(F&& f) {
 
 void use_device(emh_ctx* c) { EMH_HIP(hipSetDevice(c->device)); }
 
+std::atomic<uint64_t> g_serial{0};
+
 emh_buf* new_buf(emh_ctx* c, size_t len, int kind) {
   auto* b = new emh_buf;
   b->len = len;
   b->kind = kind;
+  b->serial = ++g_serial;
   if (len > 0) {
     hipError_t e = hipMalloc(&b->ptr, len * 4);
     if (e != hipSuccess) {
@@ -91,6 +95,7 @@ const float* F(const emh_buf* b, const char* what) {
 }
 float* Fm(emh_buf* b, const char* what) {
   EMH_ENSURE(b && b->kind == 0, "%s must be an f32 buffer", what);
+  ++b->gen;  // an output: its contents change
   return (float*)b->ptr;
 }
 const uint32_t* U(const emh_buf* b, const char* what) {
@@ -273,6 +278,7 @@ static int write(emh_ctx* c, emh_buf* b, size_t off, const void* v, size_t len, 
     EMH_ENSURE(off + len <= b->len, "write past the buffer");
     if (len == 0) return;
     use_device(c);
+    ++b->gen;
     EMH_HIP(hipMemcpyAsync((char*)b->ptr + off * 4, v, len * 4, hipMemcpyHostToDevice,
                            c->stream));
     EMH_HIP(hipStreamSynchronize(c->stream));
@@ -325,11 +331,16 @@ int emh_wrap(emh_ctx* c, void* p, size_t len, int kind, emh_buf** out) {
     b->len = len;
     b->kind = kind;
     b->owned = false;
+    b->serial = ++g_serial;
+    b->exposed = true;  // foreign memory: written from outside
     *out = b;
   });
 }
 
-void* emh_buf_ptr(const emh_buf* b) { return b ? b->ptr : nullptr; }
+void* emh_buf_ptr(const emh_buf* b) {
+  if (b) b->exposed = true;  // the caller may write it from now on
+  return b ? b->ptr : nullptr;
+}
 size_t emh_buf_len(const emh_buf* b) { return b ? b->len : 0; }
 
 // ---------------------------------------------------------------------- ops

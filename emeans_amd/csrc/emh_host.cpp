@@ -551,12 +551,16 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   // by id instead of splitting them again.
   SplitRows pre_rows{};
   const SplitRows* pre = nullptr;
+  c->xpre_of = emh_ctx::SplitOf{};  // xpre is rewritten (or left stale) below
   if (split_screen(c, bsz, d, k, sph) && n < (1u << 25)) {
     pre_rows = SplitRows{c->xpre.get(halves_bytes(n, d)), (float*)c->xpre_norm.get(n * 4), n,
                          n * 128};
     launch_halves(c, x, n, d, nullptr, 0, n, (void*)pre_rows.xs, (float*)pre_rows.xn, nullptr,
                   nullptr);
     pre = &pre_rows;
+    c->xpre_of.ptr = x;  // which buffer: emh_train_dev names it once the run has ended
+    c->xpre_of.n = n;
+    c->xpre_of.d = d;
   }
   // L2 batches on the split-operand screen keep the centroids split for the
   // run: a full split after each row-norms readout (the first batch, and
@@ -1310,7 +1314,16 @@ int emh_train_dev(emh_ctx* c, const emh_buf* x, size_t n, const emh_config* cfg,
     check_init(cfg, init);
     EMH_ENSURE(x->len == n * cfg->d, "x must be n x d");
     EMH_HIP(hipSetDevice(c->device));
+    if (out->centroids_dev) ++out->centroids_dev->gen;
     train_dev(c, (const float*)x->ptr, n, *cfg, init, out);
+    // The run split x's rows: an assignment of the same rows may take them,
+    // while the buffer keeps these contents (Assigner::bind_data keeps the
+    // bound copy only while bound, assign.rs:75-83).
+    if (c->xpre_of.ptr == x->ptr && c->xpre_of.n == n && x->owned && !x->exposed) {
+      c->xpre_of.serial = x->serial;
+      c->xpre_of.gen = x->gen;
+      c->xpre_of.valid = true;
+    }
   });
 }
 
@@ -1391,14 +1404,22 @@ int emh_assign_dev(emh_ctx* c, const emh_buf* x, size_t n, size_t d, const emh_b
     EMH_ENSURE(labels->len >= n && scores->len >= n, "outputs too short");
     if (n == 0) return;
     EMH_HIP(hipSetDevice(c->device));
+    ++scores->gen;
     chunk = chunk ? chunk : 65536;
     Buf cn(c, metric == EMH_L2 ? k * 4 : 0);
     if (metric == EMH_L2) emh::launch_row_norms(c, (const float*)cents->ptr, k, d, cn.f());
+    // The rows' bf16 halves, when the context's last training run split these
+    // very rows and nothing has written them since.
+    const emh_ctx::SplitOf& so = c->xpre_of;
+    const bool reuse = so.valid && so.ptr == x->ptr && so.serial == x->serial &&
+                       so.gen == x->gen && !x->exposed && so.d == d && n <= so.n;
+    const emh::SplitRows pre{c->xpre.ptr, (const float*)c->xpre_norm.ptr, so.n, so.n * 128};
     for (size_t b = 0; b < n; b += chunk) {
       const size_t e = std::min(b + chunk, n);
       emh::launch_top1(c, (const float*)x->ptr, n, d, nullptr, b, e, (const float*)cents->ptr,
                        metric == EMH_L2 ? cn.f() : nullptr, k, metric == EMH_IP,
-                       (uint32_t*)labels->ptr, (float*)scores->ptr);
+                       (uint32_t*)labels->ptr, (float*)scores->ptr, false, nullptr,
+                       reuse ? &pre : nullptr);
     }
     EMH_HIP(hipStreamSynchronize(c->stream));  // cn is freed on return
   });
@@ -1486,6 +1507,7 @@ int emh_dots(emh_ctx* c, const emh_buf* a, size_t m, const emh_buf* b, size_t nb
     EMH_ENSURE(out->len >= m * nb, "out must hold m x nb");
     if (m == 0 || nb == 0) return;
     EMH_HIP(hipSetDevice(c->device));
+    ++out->gen;
     emh::launch_row_dots(c, (const float*)a->ptr, m, d, (const float*)b->ptr, nb, (float*)out->ptr,
                     nullptr);
   });

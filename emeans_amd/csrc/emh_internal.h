@@ -156,6 +156,13 @@ struct emh_buf {
   size_t len = 0;   // elements
   int kind = 0;     // 0 f32, 1 u32
   bool owned = true;
+  // Which buffer and which contents, for the split rows a context keeps: a
+  // serial number unique over the process, a generation every entry point
+  // that writes the buffer advances, and whether its address was handed out
+  // (emh_buf_ptr), after which writes can come from outside.
+  uint64_t serial = 0;
+  uint64_t gen = 0;
+  mutable bool exposed = false;
 };
 
 struct emh_ctx {
@@ -171,6 +178,14 @@ struct emh_ctx {
   emh::Scratch cand, fblist, order, start, misc, knn_tmp, xnorm, bigj, chunkcnt, tickets;
   emh::Scratch xsplit, csplit, csplit_norm, csplit_part;  // split-operand screen: a call's rows, centroids
   emh::Scratch xpre, xpre_norm;              // a training run's rows, split once
+  // What xpre holds: the rows [0, n) of buffer `serial` at generation `gen`
+  // (d dimensions, at address ptr); valid only for a buffer the library owns.
+  struct SplitOf {
+    bool valid = false;
+    const void* ptr = nullptr;
+    uint64_t serial = 0, gen = 0;
+    size_t n = 0, d = 0;
+  } xpre_of;
   emh::Scratch tsplit, tsplit_part;          // a training run's centroids, kept split by the EMA
   emh::Scratch tally_cnt;                    // a training run's label tally (chunk histograms)
   emh::Scratch klong;                        // top-k beyond 16: a query block's scores

@@ -137,6 +137,38 @@ def test_headline_config_bit_exact(dev):
     assert a.mean_objective(False) == O.mean_objective(osc, False)
 
 
+def test_assign_after_training_reuses_split_rows_only_while_unchanged(dev):
+    """A training run on bound rows leaves them split in bf16 halves, and an
+    assignment of the same buffer takes those halves instead of splitting
+    again. The results must be those of the rows as they are: right after the
+    run, after a write into the bound rows (the halves are stale then), and
+    after the buffer's address was handed out (writes may come from outside)."""
+    from emeans_amd import Config, synth
+    n, d, k = 40_000, 256, 512
+    x, _ = synth.gmm_zipf(n=n, d=d, comps=k, s=1.1, seed=7)
+    xb = dev.bind(x)
+    cfg = Config(d=d, k=k, seed=3)
+    cb = dev.zeros_f32(k * d)
+    cent, _ = dev.train_dev(xb, n, cfg, centroids_out=cb)
+    lab, sco = dev.zeros_u32(n), dev.zeros_f32(n)
+
+    def check(rows, tag):
+        dev.assign_dev(xb, n, d, cb, k, "l2", lab, sco)
+        ol, osc = O.assign(rows, d, cent, "l2")
+        assert np.array_equal(dev.read_u32(lab), ol), tag
+        assert dev.read_f32(sco).tobytes() == osc.tobytes(), tag
+
+    check(x, "right after training")
+    y = x.copy()
+    y[1000:1500] = x[30_000:30_500] * np.float32(1.5)  # moved rows: other labels and scores
+    dev.write_f32(xb, 1000 * d, y[1000:1500].reshape(-1))
+    check(y, "after a write into the bound rows")
+    dev.train_dev(xb, n, cfg, centroids_out=cb)  # split again, at the new contents
+    cent = dev.read_f32(cb).reshape(k, d)
+    _ = xb.ptr  # the address is out: no reuse from here on
+    check(y, "after the address was handed out")
+
+
 def test_knn_self_and_dedup(dev):
     """knn_self k = 10 and dedup at 0.97 on unit rows with injected near-duplicates."""
     from emeans_amd import DedupConfig, dedup, knn_self, synth
