@@ -59,8 +59,12 @@ METRIC = "train s & assign Mrows/s at 200k×768 k=1024 FP32; % of FP32 MFMA peak
 # profiles/k_screen_train_assign_200kx768_k1024_hbm_traffic.md): 89.2 MB per
 # 16,384-row batch launch (50.3 MB of split rows, the centroids once per XCD),
 # 332 MB per 65,536-row assignment chunk, 40 MB per epoch-tail batch (the
-# 128 x 128 screen).
+# 128 x 128 screen). Measured at commit 43a9093; the run does not count it
+# again (counters need a profiler pass of their own), so the line names where
+# the figure comes from.
 SCREEN_TRAFFIC_BYTES = 95.6e6
+SCREEN_TRAFFIC_SOURCE = ("profiles/k_screen_train_assign_200kx768_k1024_hbm_traffic.md, "
+                         "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE at commit 43a9093")
 # The screen's roofline times every PROFILE_EVERY-th launch of the timed steps
 # with HIP events (an event pair between two kernels costs the stream a few
 # microseconds; on every launch that was ~5 % of the headline step).
@@ -71,7 +75,7 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def screen_roofline(ms, launches, flop, kernel, traffic=None):
+def screen_roofline(ms, launches, flop, kernel, traffic=None, traffic_source=None):
     """The screen's roofline: algorithmic FLOP (2 rows k d per launch) over its
     HIP-event time against the dense bf16 MFMA peak of the unit it runs on.
     Beside it: the bf16 MFMA work it issues (three products per multiply-add)
@@ -80,6 +84,7 @@ def screen_roofline(ms, launches, flop, kernel, traffic=None):
     alg = flop / (ms * 1e-3) / 1e12 if ms > 0 else 0.0
     return {"bound": "mfma", "kernel": kernel, "achieved": alg, "peak": BF16_MFMA_PEAK,
             "unit": "TFLOP/s", "frac": alg / BF16_MFMA_PEAK, "traffic": traffic,
+            "traffic_source": traffic_source,
             "launches": launches, "avg_launch_ms": ms / max(launches, 1),
             "flop_per_launch": flop / max(launches, 1),
             "issued_bf16": {"achieved": 3.0 * alg, "frac": 3.0 * alg / BF16_MFMA_PEAK},
@@ -212,7 +217,7 @@ def headline(args):
             "k_screen4 (bf16 MFMA, three passes xh.ch + xh.cl + xl.ch on operands split "
             "ahead of time, f32 accumulation, LDS-DMA ring; per-row candidate lists within "
             "the bound of each lane's best); the epoch tails' 3,392-row batches on the "
-            "128 x 128 k_screen", SCREEN_TRAFFIC_BYTES),
+            "128 x 128 k_screen", SCREEN_TRAFFIC_BYTES, SCREEN_TRAFFIC_SOURCE),
         "update_rooflines": {
             "scatter_add": hbm_roofline(*main["update"]["scatter_add"],
                                         "k_place_scan + k_sums (labels tallied by the "
