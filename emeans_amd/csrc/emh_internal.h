@@ -419,6 +419,11 @@ void launch_halves(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32
                    size_t n, void* out, float* norm, const float* cnorm, uint32_t* part);
 inline size_t halves_bytes(size_t n, size_t d) { return n * ((d + 31) / 32) * 128; }
 inline size_t halves_blocks(size_t n) { return (n + 7) / 8; }
+// out[0], out[1] = the largest part[2 i], part[2 i + 1] over i < nparts (f32
+// bits as u32), for a screen whose blocks would otherwise each read more than
+// PART_MAX_ONCE partials.
+constexpr size_t PART_MAX_ONCE = 1024;
+void launch_part_max(emh_ctx* c, const uint32_t* part, size_t nparts, uint32_t* out);
 // Bytes of fixed-block scratch launch_top1 takes for a call of n rows (an
 // upper bound: each region rounded up to 256 bytes).
 size_t top1_scratch_bytes(emh_ctx* c, size_t n, size_t d, size_t k, bool ip);

@@ -172,31 +172,50 @@ __global__ __launch_bounds__(256) void k_normalize_rows(const float* __restrict_
 }
 
 // v[0] + v[1] + ... + v[len - 1] in order from +0 (one lane; v 16-byte
-// aligned LDS): the next 16 values' reads are in flight while 16 are added.
+// aligned LDS): two groups of 16 values alternate, one group's reads in
+// flight while the other's are added. The base address goes through a VGPR:
+// when the compiler proves it uniform it addresses the LDS from scalar
+// registers with one 4-byte read per value, issued after the previous
+// group's adds, and the chain waits on every group's reads.
 __device__ __forceinline__ float ordered_sum(const float* v, int len) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  typedef const float __attribute__((address_space(3)))* lf;
+  typedef const f4 __attribute__((address_space(3)))* lf4;
+  uint32_t base = (uint32_t)(uintptr_t)v;
+  asm volatile("" : "+v"(base));
+  const lf lv = (lf)(uintptr_t)base;
+  auto load = [&](f4 (&g)[4], int t) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < 4; u++) g[u] = *(lf4)(lv + t + 4 * u);
+  };
+  auto add = [](float s, const f4 (&g)[4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      s = s + g[u].x;
+      s = s + g[u].y;
+      s = s + g[u].z;
+      s = s + g[u].w;
+    }
+    return s;
+  };
   float s = 0.0f;
   const int len16 = len & ~15;
   int t = 0;
   if (len16 > 0) {
-    float4 cur[4], nxt[4];
-#pragma unroll
-    for (int u = 0; u < 4; u++) cur[u] = *reinterpret_cast<const float4*>(v + 4 * u);
-    for (; t < len16; t += 16) {
-      const int tn = min(t + 16, len16 - 16);  // the last step reloads its own group
-#pragma unroll
-      for (int u = 0; u < 4; u++) nxt[u] = *reinterpret_cast<const float4*>(v + tn + 4 * u);
-#pragma unroll
-      for (int u = 0; u < 4; u++) {
-        s = s + cur[u].x;
-        s = s + cur[u].y;
-        s = s + cur[u].z;
-        s = s + cur[u].w;
-      }
-#pragma unroll
-      for (int u = 0; u < 4; u++) cur[u] = nxt[u];
+    f4 a[4], b[4];
+    load(a, 0);
+    for (; t + 32 <= len16; t += 32) {
+      load(b, t + 16);
+      s = add(s, a);
+      load(a, min(t + 32, len16 - 16));  // the last step reloads a group it has
+      s = add(s, b);
+    }
+    if (t < len16) {
+      s = add(s, a);
+      t += 16;
     }
   }
-  for (; t < len; t++) s = s + v[t];
+  for (; t < len; t++) s = s + lv[t];
   return s;
 }
 

@@ -47,6 +47,35 @@ constexpr int S4_STAGE = 2 * S4_HALF;      // rows and centroids: 64 KB
 // conflict-free only for the first grouping.)
 __device__ __forceinline__ int swz(int r) { return (((r >> 1) & 3) << 1) | ((r >> 3) & 1); }
 
+// The largest of part[2 i] and of part[2 i + 1] over i < nparts (f32 bits
+// compared as u32: a NaN or negative value wins), in every lane of the wave.
+// Each lane's loads of a batch of PMB partials are issued together: a loop
+// of load-then-max would wait once per 64 partials.
+constexpr int PMB = 16;
+__device__ __forceinline__ void part_max(const uint32_t* __restrict__ part, int nparts,
+                                         uint32_t& ma, uint32_t& mb) {
+  const int lane = threadIdx.x & 63;
+  ma = 0;
+  mb = 0;
+  for (int i0 = 0; i0 < nparts; i0 += 64 * PMB) {
+    uint2 v[PMB];
+#pragma unroll
+    for (int u = 0; u < PMB; u++) {
+      const int i = i0 + 64 * u + lane;
+      v[u] = i < nparts ? reinterpret_cast<const uint2*>(part)[i] : make_uint2(0u, 0u);
+    }
+#pragma unroll
+    for (int u = 0; u < PMB; u++) {
+      ma = max(ma, v[u].x);
+      mb = max(mb, v[u].y);
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    ma = max(ma, (uint32_t)__shfl_xor((int)ma, o, 64));
+    mb = max(mb, (uint32_t)__shfl_xor((int)mb, o, 64));
+  }
+}
+
 template <bool VEC4>
 __device__ __forceinline__ void load32(const float* p, int col, int d, float (&v)[32]) {
   if (VEC4 && col + 32 <= d) {
@@ -298,15 +327,8 @@ __global__ __launch_bounds__(NW * 64, 1) void k_screen4(
     // The bound's centroid maxima from the centroid split's per-block
     // partials (max of the f32 bits: a NaN or negative value wins); block 0
     // leaves them in the small block for the check.
-    uint32_t ma = 0, mb = 0;
-    for (int i = lane; i < nparts; i += 64) {
-      ma = max(ma, cmax_part[2 * i]);
-      mb = max(mb, cmax_part[2 * i + 1]);
-    }
-    for (int o = 32; o > 0; o >>= 1) {
-      ma = max(ma, (uint32_t)__shfl_xor((int)ma, o, 64));
-      mb = max(mb, (uint32_t)__shfl_xor((int)mb, o, 64));
-    }
+    uint32_t ma, mb;
+    part_max(cmax_part, nparts, ma, mb);
     if (blockIdx.x == 0 && tid == 0) {
       small[SW_CMAX2] = ma;
       small[SW_CNMAX] = L2 ? mb : 0u;

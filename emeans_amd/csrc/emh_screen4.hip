@@ -19,6 +19,47 @@ void launch_screen4(emh_ctx* c, const Screen4Args& a, bool ip) {
   EMH_HIP(hipGetLastError());
 }
 
+namespace {
+// out[0], out[1] = the largest part[2 i], part[2 i + 1] over i < nparts.
+__global__ __launch_bounds__(256) void k_part_max(const uint32_t* __restrict__ part, size_t nparts,
+                                                  uint32_t* __restrict__ out) {
+  __shared__ uint32_t w[2][4];
+  const int tid = threadIdx.x;
+  uint32_t ma = 0, mb = 0;
+  for (size_t i0 = 0; i0 < nparts; i0 += 256 * PMB) {
+    uint2 v[PMB];
+#pragma unroll
+    for (int u = 0; u < PMB; u++) {
+      const size_t i = i0 + 256 * (size_t)u + tid;
+      v[u] = i < nparts ? reinterpret_cast<const uint2*>(part)[i] : make_uint2(0u, 0u);
+    }
+#pragma unroll
+    for (int u = 0; u < PMB; u++) {
+      ma = max(ma, v[u].x);
+      mb = max(mb, v[u].y);
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    ma = max(ma, (uint32_t)__shfl_xor((int)ma, o, 64));
+    mb = max(mb, (uint32_t)__shfl_xor((int)mb, o, 64));
+  }
+  if ((tid & 63) == 0) {
+    w[0][tid >> 6] = ma;
+    w[1][tid >> 6] = mb;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    out[0] = max(max(w[0][0], w[0][1]), max(w[0][2], w[0][3]));
+    out[1] = max(max(w[1][0], w[1][1]), max(w[1][2], w[1][3]));
+  }
+}
+}  // namespace
+
+void launch_part_max(emh_ctx* c, const uint32_t* part, size_t nparts, uint32_t* out) {
+  hipLaunchKernelGGL(k_part_max, dim3(1), dim3(256), 0, c->stream, part, nparts, out);
+  EMH_HIP(hipGetLastError());
+}
+
 void launch_halves(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids, size_t lo,
                    size_t n, void* out, float* norm, const float* cnorm, uint32_t* part) {
   if (n == 0) return;

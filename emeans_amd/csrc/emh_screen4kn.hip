@@ -119,9 +119,8 @@ __global__ __launch_bounds__(512, 1) void k_screen4kn(
   // check), with a margin for its own rounding.
   float thr_e;
   {
-    uint32_t ma = 0;
-    for (int i = lane; i < nparts; i += 64) ma = max(ma, cmax_part[2 * i]);
-    for (int o = 32; o > 0; o >>= 1) ma = max(ma, (uint32_t)__shfl_xor((int)ma, o, 64));
+    uint32_t ma, mb;
+    part_max(cmax_part, nparts, ma, mb);
     if (blockIdx.x == 0 && tid == 0) small[SW_CMAX2] = ma;
     const float cm2 = __uint_as_float(ma);
     const float xv = qown < (uint32_t)m ? qn[qown] : 0.f;
@@ -136,12 +135,16 @@ __global__ __launch_bounds__(512, 1) void k_screen4kn(
     lkey[e] = INFINITY;
     lid[e] = NONE;
   }
-  // After an insert: the new limit. The kk-th key is read with an unrolled
-  // select (kk is a runtime value; an indexed register array would go to memory).
+  // After an insert: the new limit. The list is sorted ascending (never NaN),
+  // so the kk-th key is the largest of the first kk: a max over a masked
+  // unrolled chain. (kk is a runtime value. A chain of selects of list
+  // elements was folded by the compiler into one indexed read, which put the
+  // list in LDS: 48 KB more per block and bank-conflicting stores of the
+  // whole list on every insert.)
   auto relimit = [&]() __attribute__((always_inline)) {
     float kth = lkey[0];
 #pragma unroll
-    for (int e = 1; e < L; e++) kth = e == kk - 1 ? lkey[e] : kth;
+    for (int e = 1; e < L; e++) kth = fmaxf(kth, e < kk ? lkey[e] : -INFINITY);
     const float t = kth + thr_e + fabsf(kth) * 9.5367431640625e-07f + 1e-42f;  // + 2^-20 |kth|
     lim = fminf(lkey[L - 1], t);  // a NaN bound leaves the L-th key
   };
@@ -337,8 +340,17 @@ int screen4kn(emh_ctx* c, const float* q, size_t m, const float* data, size_t n,
   const bool same = q == data && m == n;
   void* xs = c->csplit.get(halves_bytes(n, d));
   float* xn = (float*)c->csplit_norm.get(n * 4);
-  uint32_t* part = (uint32_t*)c->csplit_part.get(halves_blocks(n) * 8);
+  // Past PART_MAX_ONCE partials, one workgroup reduces them ahead of the
+  // screen, whose every block would otherwise read them all.
+  const size_t hb = halves_blocks(n);
+  uint32_t* part = (uint32_t*)c->csplit_part.get((hb + 1) * 8);
   launch_halves(c, data, n, d, nullptr, 0, n, xs, xn, nullptr, part);
+  int nparts = (int)hb;
+  if (hb > PART_MAX_ONCE) {
+    launch_part_max(c, part, hb, part + 2 * hb);
+    part += 2 * hb;
+    nparts = 1;
+  }
   const void* qs = xs;
   const float* qn = xn;
   if (!same) {
@@ -367,7 +379,7 @@ int screen4kn(emh_ctx* c, const float* q, size_t m, const float* data, size_t n,
   hipLaunchKernelGGL(kern, dim3((unsigned)(row_tiles * parts)), dim3(512), 0, c->stream,
                      (const char*)qs, m * (size_t)SLAB_BYTES, qn, (int)m, (const char*)xs,
                      n * (size_t)SLAB_BYTES, (int)n, (int)d, (int)kk, tpp, parts, ntiles, cand,
-                     xnorm, part, (int)halves_blocks(n), c->small);
+                     xnorm, part, nparts, c->small);
   EMH_HIP(hipGetLastError());
   *cand_out = cand;
   *xnorm_out = xnorm;
