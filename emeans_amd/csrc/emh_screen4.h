@@ -353,11 +353,15 @@ __global__ __launch_bounds__(NW * 64, 1) void k_screen4(
   // in its low 6 mantissa bits (the bound covers the change), so that an
   // insert of bare floats keeps the lane's L smallest per row; the tags then
   // give the ids. (A tagged +inf or NaN is a NaN, which no compare takes.)
+  // The lane's smallest tagged key is always within its threshold: it opens
+  // the list, and the insert pass (a wave-wide branch, taken when any lane
+  // has a key to insert) is left with the near-ties, which are rare; keys
+  // carry distinct tags, so the list is the one inserting every key gives.
   auto fold_tagged = [&](int tile) __attribute__((always_inline)) {
     const float* ns = Ns[tile & 3];
-    float m[WN];
+    float m[WN], tm[WN];  // the lane's smallest key, and smallest tagged key
 #pragma unroll
-    for (int y = 0; y < WN; y++) m[y] = INFINITY;
+    for (int y = 0; y < WN; y++) m[y] = tm[y] = INFINITY;
 #pragma unroll
     for (int a = 0; a < WA; a++) {
 #pragma unroll
@@ -374,7 +378,10 @@ __global__ __launch_bounds__(NW * 64, 1) void k_screen4(
             const float v = acc[a][y][r];
             const float key = L2 ? fmaf(-2.0f, v, nn) : nn - v;  // one rounding: within E
             m[y] = fminf(m[y], key);
-            acc[a][y][r] = __uint_as_float((__float_as_uint(key) & ~63u) | (uint32_t)(16 * a + r));
+            const float tagged =
+                __uint_as_float((__float_as_uint(key) & ~63u) | (uint32_t)(16 * a + r));
+            tm[y] = fminf(tm[y], tagged);  // a tagged +-inf is a NaN: never the minimum
+            acc[a][y][r] = tagged;
           }
         }
       }
@@ -384,8 +391,9 @@ __global__ __launch_bounds__(NW * 64, 1) void k_screen4(
 #pragma unroll
     for (int y = 0; y < WN; y++) {
       thr[y] = threshold(m[y], y);
+      tk[y][0] = tm[y] <= thr[y] ? tm[y] : INFINITY;  // not when the bound is NaN
 #pragma unroll
-      for (int e = 0; e < L; e++) tk[y][e] = INFINITY;
+      for (int e = 1; e < L; e++) tk[y][e] = INFINITY;
     }
 #pragma unroll
     for (int a = 0; a < WA; a++) {
@@ -394,8 +402,8 @@ __global__ __launch_bounds__(NW * 64, 1) void k_screen4(
 #pragma unroll
         for (int y = 0; y < WN; y++) {
           const float tagged = acc[a][y][r];
-          if (__ballot(tagged <= thr[y]) != 0ull)
-            insert_key<L>(tk[y], tagged <= thr[y] ? tagged : INFINITY);
+          const bool in = tagged <= thr[y] && tagged != tm[y];
+          if (__ballot(in) != 0ull) insert_key<L>(tk[y], in ? tagged : INFINITY);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
