@@ -170,8 +170,9 @@ __global__ __launch_bounds__(512, 1) void k_screen4kn(
   // accumulator layout: element r of lane l is (data row 8 (r / 4) +
   // 4 (l / 32) + r % 4 of the block, query l % 32 of query block y); block y's
   // queries are kept by the lanes of half y. First every element is compared
-  // with its query's limit (dot >= -lim is key <= lim, exactly), and the wave
-  // notes the (a, r) positions of block y where some lane's element passes;
+  // with its query's limit (dot >= -lim is key <= lim, exactly; a block's
+  // maximum first), and the wave notes the (a, r) positions of block y where
+  // some lane's element passes;
   // then, for those positions only, the element and its partner half's (one
   // swap) go to the query's list. Most positions pass nowhere once the lists
   // hold good keys, and the insert is written once per block y.
@@ -182,10 +183,19 @@ __global__ __launch_bounds__(512, 1) void k_screen4kn(
 #pragma unroll
     for (int y = 0; y < WN; y++)
 #pragma unroll
-      for (int a = 0; a < WA; a++)
+      for (int a = 0; a < WA; a++) {
+        // The block's largest element first (fmaxf passes over NaN, which
+        // never passes): once the lists hold good keys most blocks have no
+        // passing element in any lane, and one ballot skips their sixteen.
+        float mx = acc[a][y][0];
 #pragma unroll
-        for (int r = 0; r < 16; r++)
-          pos[y] |= __ballot(acc[a][y][r] >= nl[y]) != 0ull ? 1u << (16 * a + r) : 0u;
+        for (int r = 1; r < 16; r++) mx = fmaxf(mx, acc[a][y][r]);
+        if (__ballot(mx >= nl[y]) != 0ull) {
+#pragma unroll
+          for (int r = 0; r < 16; r++)
+            pos[y] |= __ballot(acc[a][y][r] >= nl[y]) != 0ull ? 1u << (16 * a + r) : 0u;
+        }
+      }
 #pragma unroll
     for (int y = 0; y < WN; y++) {
       for (uint32_t mk = pos[y]; mk != 0u; mk &= mk - 1u) {
