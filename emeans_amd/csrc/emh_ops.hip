@@ -171,13 +171,13 @@ __global__ __launch_bounds__(256) void k_normalize_rows(const float* __restrict_
   for (size_t t = lane; t < d; t += WAVE) out[t] = (row[t] / s1) / s2;
 }
 
-// v[0] + v[1] + ... + v[len - 1] in order from +0 (one lane; v 16-byte
-// aligned LDS): two groups of 16 values alternate, one group's reads in
+// s0 + v[0] + v[1] + ... + v[len - 1] in order (one lane; v 16-byte aligned
+// LDS): two groups of 16 values alternate, one group's reads in
 // flight while the other's are added. The base address goes through a VGPR:
 // when the compiler proves it uniform it addresses the LDS from scalar
 // registers with one 4-byte read per value, issued after the previous
 // group's adds, and the chain waits on every group's reads.
-__device__ __forceinline__ float ordered_sum(const float* v, int len) {
+__device__ __forceinline__ float ordered_sum(const float* v, int len, float s0 = 0.0f) {
   typedef float f4 __attribute__((ext_vector_type(4)));
   typedef const float __attribute__((address_space(3)))* lf;
   typedef const f4 __attribute__((address_space(3)))* lf4;
@@ -198,7 +198,7 @@ __device__ __forceinline__ float ordered_sum(const float* v, int len) {
     }
     return s;
   };
-  float s = 0.0f;
+  float s = s0;
   const int len16 = len & ~15;
   int t = 0;
   if (len16 > 0) {
@@ -356,33 +356,7 @@ __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __r
         *reinterpret_cast<uint2*>(o + 32) = lw;
       }
     }
-    if (tid < nc && wgt[tid] >= 0.0f) {
-      // Adds in order; the next 16 squares' LDS reads are in flight while the
-      // current 16 are added.
-      const float* r = sq + tid * row;
-      const int len16 = len & ~15;
-      int t = 0;
-      if (len16 > 0) {
-        float4 cur[4], nxt[4];
-#pragma unroll
-        for (int u = 0; u < 4; u++) cur[u] = *reinterpret_cast<const float4*>(r + 4 * u);
-        for (; t < len16; t += 16) {
-          const int tn = min(t + 16, len16 - 16);  // the last step reloads its own group
-#pragma unroll
-          for (int u = 0; u < 4; u++) nxt[u] = *reinterpret_cast<const float4*>(r + tn + 4 * u);
-#pragma unroll
-          for (int u = 0; u < 4; u++) {
-            nrm = nrm + cur[u].x;
-            nrm = nrm + cur[u].y;
-            nrm = nrm + cur[u].z;
-            nrm = nrm + cur[u].w;
-          }
-#pragma unroll
-          for (int u = 0; u < 4; u++) cur[u] = nxt[u];
-        }
-      }
-      for (; t < len; t++) nrm = nrm + r[t];
-    }
+    if (tid < nc && wgt[tid] >= 0.0f) nrm = ordered_sum(sq + tid * row, len, nrm);  // in order
     __syncthreads();
   }
   if (readout) {

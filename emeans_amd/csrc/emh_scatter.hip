@@ -103,6 +103,7 @@ __global__ __launch_bounds__(256) void k_count(const uint32_t* __restrict__ labe
 // ---- chunked count and placement (k <= KCH): positions in chunks of CP.
 constexpr int CP = TALLY_CP;
 constexpr int KCH = 8192;  // LDS histogram of one chunk
+static_assert(CP == 256, "a chunk is one position per thread of a 256-thread block");
 
 // Chunk c's label histogram (LDS atomics) goes to cnt[c][0..k) and is added
 // to the totals counts[0..k) (zero on entry);
@@ -261,19 +262,31 @@ __global__ __launch_bounds__(256) void k_place_scan(const uint32_t* __restrict__
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const size_t c = blockIdx.x;
   const size_t p = lo + c * CP + tid;
+  // Thread t scans the run [t per, (t + 1) per) of the counts: its loads go
+  // out first, beside the label's, ahead of the label's run.
+  constexpr int PERMAX = KCH / 256;
+  const size_t per = (k + 255) / 256;
+  const size_t a = min(k, (size_t)tid * per), b = min(k, a + per);
+  uint32_t tv[PERMAX];
+#pragma unroll
+  for (int u = 0; u < PERMAX; u++) tv[u] = a + u < b ? counts[a + u] : 0u;
   const uint32_t l = p < hi ? labels[p] : 0xffffffffu;
-  const uint32_t row = l < k ? row_of(ids, nx, (uint32_t)p, small) : NOROW;
+  // The position's row id, loaded beside the label; checked where it is used,
+  // so that no wait on it comes before the run's loads.
+  const uint32_t raw = p < hi ? (ids ? ids[p] : (uint32_t)p) : 0u;
   lab[tid] = l;
   // Rows of label l in earlier chunks: 16-byte loads of the label's run
-  // (stride is a multiple of 4), in flight with the scan's.
+  // (stride is a multiple of 4).
+  // The loads are unconditional, clamped into the label's row (a load per
+  // branch would wait before the next is issued), and masked after.
   uint32_t pre = 0;
-  if (l < k) {
-    const uint4* run4 = reinterpret_cast<const uint4*>(cnt + (size_t)l * stride);
-    const int n4 = (int)((c + 3) >> 2);
+  {
+    const uint4* run4 = reinterpret_cast<const uint4*>(cnt + (size_t)(l < k ? l : 0u) * stride);
+    const int n4 = l < k ? (int)((c + 3) >> 2) : 0, s4 = (int)(stride >> 2);
     for (int q0 = 0; q0 < n4; q0 += 16) {
       uint4 v[16];
 #pragma unroll
-      for (int u = 0; u < 16; u++) v[u] = q0 + u < n4 ? run4[q0 + u] : make_uint4(0, 0, 0, 0);
+      for (int u = 0; u < 16; u++) v[u] = run4[min(q0 + u, s4 - 1)];
 #pragma unroll
       for (int u = 0; u < 16; u++) {
         const size_t e = 4 * (size_t)(q0 + u);
@@ -282,13 +295,6 @@ __global__ __launch_bounds__(256) void k_place_scan(const uint32_t* __restrict__
       }
     }
   }
-  // Thread t scans the run [t per, (t + 1) per) of the counts.
-  constexpr int PERMAX = KCH / 256;
-  const size_t per = (k + 255) / 256;
-  const size_t a = min(k, (size_t)tid * per), b = min(k, a + per);
-  uint32_t tv[PERMAX];
-#pragma unroll
-  for (int u = 0; u < PERMAX; u++) tv[u] = a + u < b ? counts[a + u] : 0u;
   uint32_t sacc = 0;
 #pragma unroll
   for (int u = 0; u < PERMAX; u++) sacc += tv[u];
@@ -326,14 +332,30 @@ __global__ __launch_bounds__(256) void k_place_scan(const uint32_t* __restrict__
     small[SW_NBIG] = nbig;
   }
   if (l >= k) return;
+  // Rows of label l earlier in the chunk: every position of the earlier
+  // waves, then the lanes below this one in its own wave.
   uint32_t rank = 0;
   const uint4* l4 = reinterpret_cast<const uint4*>(lab);
-#pragma unroll 8
-  for (int i4 = 0; i4 < CP / 4; i4++) {
+  for (int i4 = 0; i4 < 16 * w; i4 += 8) {
+    uint4 q[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) q[u] = l4[i4 + u];
+#pragma unroll
+    for (int u = 0; u < 8; u++)
+      rank += (uint32_t)(q[u].x == l) + (uint32_t)(q[u].y == l) + (uint32_t)(q[u].z == l) +
+              (uint32_t)(q[u].w == l);
+  }
+#pragma unroll 4
+  for (int i4 = 16 * w; i4 < 16 * w + 16; i4++) {
     const uint4 q = l4[i4];
     const int i = 4 * i4;
     rank += (uint32_t)(i < tid && q.x == l) + (uint32_t)(i + 1 < tid && q.y == l) +
             (uint32_t)(i + 2 < tid && q.z == l) + (uint32_t)(i + 3 < tid && q.w == l);
+  }
+  uint32_t row = raw;
+  if ((size_t)raw >= nx) {  // a bad id adds nothing; reported at the next read (as row_of)
+    small[SW_BAD_ID] = 1;
+    row = NOROW;
   }
   rid[st[l] + pre + rank] = row;
 }
