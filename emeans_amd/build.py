@@ -22,7 +22,7 @@ SOURCES = ["emh_api.cpp", "emh_host.cpp", "emh_ops.hip", "emh_scatter.hip", "emh
            "emh_screen_kn_bf3_self.hip", "emh_screen_kn_bf3_any.hip",
            "emh_screen_kn_f32_self.hip", "emh_screen_kn_f32_any.hip", "emh_rescore.hip",
            "emh_verify.hip", "emh_autok.hip", "emh_topk_long.hip", "emh_screen4kn.hip",
-           "emh_perm.cpp"]
+           "emh_update.hip", "emh_perm.cpp"]
 # Plain host C++ (no HIP), built by the system compiler.
 HOST_ONLY = {"emh_perm.cpp"}
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

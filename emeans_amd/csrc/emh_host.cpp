@@ -567,9 +567,11 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   // after a revival moved rows), then the EMA rewrites the rows it moves.
   const bool keep_csplit = pre && !sph;
   void* tsplit = keep_csplit ? c->tsplit.get(halves_bytes(k, d)) : nullptr;
-  uint32_t* tpart_h = keep_csplit
-                          ? (uint32_t*)c->tsplit_part.get((halves_blocks(k) + ema_blocks(k)) * 8)
-                          : nullptr;
+  // The bound's centroid maxima: halves_blocks(k) pairs after a full split,
+  // then one pair per EMA block, or per cluster after a small batch's update.
+  uint32_t* tpart_h = keep_csplit ? (uint32_t*)c->tsplit_part.get(
+                                        (halves_blocks(k) + std::max(ema_blocks(k), k)) * 8)
+                                  : nullptr;
   uint32_t* tpart_e = keep_csplit ? tpart_h + 2 * halves_blocks(k) : nullptr;
   SplitCents pcents{tsplit, tpart_h, (int)halves_blocks(k)};
   // When the batches' top-1 runs the screen with d % 4 == 0 (the check and
@@ -740,12 +742,26 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
       if (check)
         launch_mass_preview(c, mass.f(), counts.u(), k, af, df, replace, d_usage_h, d_small_h,
                             d_small_h + 2 * SW_WORDS, ++seq_no);
-      {
-        ProfScope p(c, EMH_PROF_SCATTER, scatter_bytes(e - b, k, d, true, last), tsc);
-        launch_scatter_sums(c, x, n, d, order, b, e, lab, k, sums.f(), last ? pass.f() : nullptr,
-                            tally ? counts.u() : nullptr, tcnt, tstride);
-      }
-      {
+      if (tally && update_small(e - b, d, sph)) {
+        // A small batch (the automatic-k sweeps' fits): placement, sums and
+        // the EMA step in one launch, the same bits.
+        ProfScope p(c, EMH_PROF_SCATTER,
+                    scatter_bytes(e - b, k, d, true, last) + ema_bytes(k, d), tsc);
+        launch_update_small(c, x, n, d, order, b, e, lab, k, counts.u(), tcnt, tstride * k,
+                            last ? pass.f() : nullptr, pos.f(), mass.f(), af, df, replace,
+                            sph ? nullptr : readout.f(), tsplit, tpart_e,
+                            sph ? readout.f() : nullptr, d_tally[buf]);
+        if (keep_csplit) {
+          pcents.part = tpart_e;
+          pcents.nparts = (int)k;
+        }
+      } else {
+        {
+          ProfScope p(c, EMH_PROF_SCATTER, scatter_bytes(e - b, k, d, true, last), tsc);
+          launch_scatter_sums(c, x, n, d, order, b, e, lab, k, sums.f(),
+                              last ? pass.f() : nullptr, tally ? counts.u() : nullptr, tcnt,
+                              tstride);
+        }
         ProfScope p(c, EMH_PROF_EMA, ema_bytes(k, d), prof_take(c, EMH_PROF_EMA));
         launch_ema(c, pos.f(), mass.f(), sums.f(), counts.u(), k, d, af, df, replace,
                    sph ? nullptr : readout.f(), true, d_tally[buf], true, tsplit, tpart_e, tcnt,

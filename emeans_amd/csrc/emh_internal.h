@@ -336,6 +336,25 @@ void launch_scatter_sums(emh_ctx* c, const float* x, size_t nx, size_t d, const 
                          float* acc, const uint32_t* counts_tallied = nullptr,
                          const uint32_t* tally_cnt = nullptr, size_t tally_stride = 0);
 
+// ---- emh_update.hip: a small training batch's scatter_add and EMA step in one
+// launch (the same bits as launch_scatter_sums then launch_ema).
+constexpr size_t UPDATE_SMALL_BATCH = 256;  // most positions per batch
+constexpr size_t UPDATE_SMALL_MAX_D = 1024;
+// Whether a batch of n positions with d dimensions takes it.
+bool update_small(size_t n, size_t d, bool spherical);
+// Labels lo .. hi tallied into counts (and tcnt, ntcnt words) by the batch's
+// top-1 call. As launch_scatter_sums (tallied) then launch_ema with
+// clear_screen_words and zero_counts: moves the centroids that got rows
+// (pos, usage; norms and, with csplit, the bf16 halves for L2 runs; readout
+// for spherical ones), adds the sums into acc (when given) and counts into
+// tally, and leaves counts and tcnt at zero. With csplit, cpart[2 j] =
+// cpart[2 j + 1] = norms[j] bits for every cluster j (k pairs).
+void launch_update_small(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
+                         size_t lo, size_t hi, const uint32_t* labels, size_t k, uint32_t* counts,
+                         uint32_t* tcnt, size_t ntcnt, float* acc, float* pos, float* usage,
+                         float alpha, float decay, int replace, float* norms, void* csplit,
+                         uint32_t* cpart, float* readout, uint32_t* tally);
+
 // ---- emh_autok.hip (kmeans_pp and internal_scores of the automatic-k callers)
 // best[i] = max(best[i], dot(x[i], x[last])), the dot in sequence without fma.
 void launch_pp_best(emh_ctx* c, const float* x, size_t n, size_t d, size_t last, float* best);
