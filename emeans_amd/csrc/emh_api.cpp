@@ -2,10 +2,14 @@
 // Device ops, each validated like the reference CPU backend
 // (crates/emeans-core/src/core/cpu.rs) before anything is queued.
 
+#include <algorithm>
 #include <atomic>
 #include <cstring>
+#include <deque>
+#include <map>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "emh_internal.h"
 
@@ -71,12 +75,137 @@ void use_device(emh_ctx* c) { EMH_HIP(hipSetDevice(c->device)); }
 
 std::atomic<uint64_t> g_serial{0};
 
+// Blocks of freed buffers, kept per device for the next buffer of the same
+// size. hipFree waits for every stream on the device, so a loop of small runs
+// on several contexts at once (the automatic-k sweeps) would run one context
+// at a time. emh_free drains the freeing context's stream; for the work the
+// other live contexts on the device had queued by then, it records an event
+// on each of their streams, and whichever context takes the block again
+// makes its streams wait for those events before its first write.
+constexpr size_t KEEP_BLOCK_MAX = size_t(64) << 20;   // larger blocks are freed
+constexpr size_t KEEP_DEVICE_MAX = size_t(1) << 30;   // kept bytes per device
+struct KeptBlock {
+  int device;
+  size_t bytes;
+  void* ptr;
+  std::vector<hipEvent_t> after;
+};
+std::mutex g_blocks_mu;
+std::vector<emh_ctx*> g_live;                 // contexts not yet destroyed
+std::deque<KeptBlock> g_kept;                 // oldest first
+std::map<int, size_t> g_kept_bytes;           // per device
+std::map<int, std::vector<hipEvent_t>> g_spare_events;  // per device, no timing
+
+hipEvent_t spare_event(int device) {  // with g_blocks_mu held, device current
+  std::vector<hipEvent_t>& v = g_spare_events[device];
+  if (!v.empty()) {
+    hipEvent_t e = v.back();
+    v.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  EMH_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+  return e;
+}
+
+// A kept block of exactly `bytes` on c's device, with c's streams ordered
+// after the work that may still use it; nullptr if none is kept.
+void* take_kept(emh_ctx* c, size_t bytes) {
+  std::lock_guard<std::mutex> g(g_blocks_mu);
+  for (auto it = g_kept.begin(); it != g_kept.end(); ++it) {
+    if (it->device != c->device || it->bytes != bytes) continue;
+    KeptBlock kb = std::move(*it);
+    g_kept.erase(it);
+    g_kept_bytes[c->device] -= bytes;
+    for (hipEvent_t e : kb.after) {
+      EMH_HIP(hipStreamWaitEvent(c->stream, e, 0));
+      EMH_HIP(hipStreamWaitEvent(c->copy_stream, e, 0));
+      g_spare_events[c->device].push_back(e);
+    }
+    return kb.ptr;
+  }
+  return nullptr;
+}
+
+// Keeps the block of a buffer freed on c (whose stream has been drained), or
+// frees it when it is too large. Past the device's limit the oldest kept
+// blocks are freed.
+void keep_block(emh_ctx* c, void* p, size_t bytes) {
+  if (bytes > KEEP_BLOCK_MAX) {
+    EMH_HIP(hipFree(p));
+    return;
+  }
+  std::vector<void*> drop;
+  {
+    std::lock_guard<std::mutex> g(g_blocks_mu);
+    KeptBlock kb{c->device, bytes, p, {}};
+    for (emh_ctx* o : g_live) {
+      if (o == c || o->device != c->device) continue;
+      for (hipStream_t st : {o->stream, o->copy_stream}) {
+        hipEvent_t e = spare_event(c->device);
+        kb.after.push_back(e);
+        EMH_HIP(hipEventRecord(e, st));
+      }
+    }
+    g_kept.push_back(std::move(kb));
+    size_t& total = g_kept_bytes[c->device];
+    total += bytes;
+    for (auto it = g_kept.begin(); total > KEEP_DEVICE_MAX && it != g_kept.end();) {
+      if (it->device != c->device) {
+        ++it;
+        continue;
+      }
+      total -= it->bytes;
+      drop.push_back(it->ptr);
+      for (hipEvent_t e : it->after) g_spare_events[c->device].push_back(e);
+      it = g_kept.erase(it);
+    }
+  }
+  for (void* q : drop) EMH_HIP(hipFree(q));
+}
+
+// Frees the blocks kept on `device` and its spare events (the last context
+// on the device is going).
+void release_kept(int device) {
+  std::vector<void*> drop;
+  std::vector<hipEvent_t> evs;
+  {
+    std::lock_guard<std::mutex> g(g_blocks_mu);
+    for (emh_ctx* o : g_live)
+      if (o->device == device) return;
+    for (auto it = g_kept.begin(); it != g_kept.end();) {
+      if (it->device != device) {
+        ++it;
+        continue;
+      }
+      drop.push_back(it->ptr);
+      evs.insert(evs.end(), it->after.begin(), it->after.end());
+      it = g_kept.erase(it);
+    }
+    g_kept_bytes[device] = 0;
+    std::vector<hipEvent_t>& v = g_spare_events[device];
+    evs.insert(evs.end(), v.begin(), v.end());
+    v.clear();
+  }
+  for (void* q : drop) (void)hipFree(q);
+  for (hipEvent_t e : evs) (void)hipEventDestroy(e);
+}
+
 emh_buf* new_buf(emh_ctx* c, size_t len, int kind) {
   auto* b = new emh_buf;
   b->len = len;
   b->kind = kind;
   b->serial = ++g_serial;
-  if (len > 0) {
+  b->device = c->device;
+  if (len > 0 && len * 4 <= KEEP_BLOCK_MAX) {
+    try {
+      b->ptr = take_kept(c, len * 4);
+    } catch (...) {
+      delete b;
+      throw;
+    }
+  }
+  if (len > 0 && !b->ptr) {
     hipError_t e = hipMalloc(&b->ptr, len * 4);
     if (e != hipSuccess) {
       delete b;
@@ -85,7 +214,6 @@ emh_buf* new_buf(emh_ctx* c, size_t len, int kind) {
       throw emh::Failure(m);
     }
   }
-  (void)c;
   return b;
 }
 
@@ -181,6 +309,10 @@ int emh_create(int device, emh_ctx** out) {
       delete c;
       throw;
     }
+    {
+      std::lock_guard<std::mutex> g(g_blocks_mu);
+      g_live.push_back(c);
+    }
     *out = c;
   });
 }
@@ -195,7 +327,7 @@ int emh_destroy(emh_ctx* c) {
                             &c->xnorm, &c->bigj, &c->chunkcnt, &c->tickets,
                             &c->preview_ticket, &c->xsplit, &c->csplit, &c->csplit_norm, &c->csplit_part,
                             &c->xpre, &c->xpre_norm, &c->tsplit, &c->tsplit_part, &c->tally_cnt,
-                            &c->klong})
+                            &c->klong, &c->trun, &c->kpp, &c->iscore, &c->cnorm})
       s->release();
     for (emh::Pinned* s : {&c->pin_usage, &c->pin_plan, &c->pin_small, &c->pin_order[0],
                            &c->pin_order[1], &c->pin_lab[0], &c->pin_lab[1], &c->pin_sco[0],
@@ -205,6 +337,11 @@ int emh_destroy(emh_ctx* c) {
     if (c->small) (void)hipFree(c->small);
     for (hipEvent_t e : c->ev_pool) (void)hipEventDestroy(e);
     for (hipEvent_t e : c->ev_stage) (void)hipEventDestroy(e);
+    {
+      std::lock_guard<std::mutex> g(g_blocks_mu);
+      g_live.erase(std::remove(g_live.begin(), g_live.end(), c), g_live.end());
+    }
+    release_kept(c->device);  // when c was the device's last context
     (void)hipStreamDestroy(c->stream);
     (void)hipStreamDestroy(c->copy_stream);
     delete c;
@@ -316,7 +453,14 @@ int emh_free(emh_ctx* c, emh_buf* b) {
       use_device(c);
       EMH_HIP(hipStreamSynchronize(c->stream));
     }
-    if (b->owned && b->ptr) EMH_HIP(hipFree(b->ptr));
+    if (b->owned && b->ptr) {
+      // A buffer whose address went out may be in use on streams of the
+      // caller's own: hipFree waits for them.
+      if (c && !b->exposed && b->device == c->device)
+        keep_block(c, b->ptr, b->len * 4);
+      else
+        EMH_HIP(hipFree(b->ptr));
+    }
     delete b;
   });
 }

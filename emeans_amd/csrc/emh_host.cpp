@@ -19,6 +19,7 @@
 #include <cstring>
 #include <deque>
 #include <functional>
+#include <initializer_list>
 #include <future>
 #include <map>
 #include <memory>
@@ -288,21 +289,40 @@ void normalize_row(float* r, size_t d) {  // model.rs:954-967
 }
 
 // ------------------------------------------------------------ device buffers
+// A call's device buffer: its own allocation, or a piece of an Arena laid
+// over one of the context's kept blocks (arena_for), which it does not free.
 struct Buf {
-  emh_ctx* c = nullptr;
   void* p = nullptr;
+  bool own = false;
   Buf() = default;
-  Buf(emh_ctx* ctx, size_t bytes) : c(ctx) {
+  Buf(emh_ctx*, size_t bytes) : own(true) {
     if (bytes) EMH_HIP(hipMalloc(&p, bytes));
   }
+  Buf(Arena& a, size_t bytes) {
+    if (bytes) p = a.take(bytes);
+  }
   ~Buf() {
-    if (p) (void)hipFree(p);
+    if (own && p) (void)hipFree(p);
   }
   Buf(const Buf&) = delete;
   Buf& operator=(const Buf&) = delete;
   float* f() const { return (float*)p; }
   uint32_t* u() const { return (uint32_t*)p; }
 };
+
+// An Arena over the context's kept block s, large enough for Bufs of the
+// given byte sizes taken in that order. The block only grows, so after the
+// first call of a size the call allocates and frees nothing; the work that
+// used the block last is on the same context's streams, which every user
+// drains before it returns.
+Arena arena_for(Scratch& s, std::initializer_list<size_t> sizes) {
+  size_t total = 0;
+  for (size_t b : sizes) total += (b + 255) & ~size_t(255);
+  Arena a;
+  a.base = (char*)s.get(std::max<size_t>(total, 256));
+  a.cap = total;
+  return a;
+}
 
 void h2d(emh_ctx* c, void* dst, const void* src, size_t bytes) {
   if (!bytes) return;
@@ -542,10 +562,11 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
 
   // Epochs alternate between two sets of order/labels/scores buffers, so the
   // copies of one epoch's run on the copy stream beside the next epoch's kernels.
-  Buf order0(c, n * 4), order1(c, n * 4), lab0(c, n * 4), lab1(c, n * 4), sco0(c, n * 4),
-      sco1(c, n * 4), pos(c, k * d * 4), mass(c, k * 4),
-      readout(c, (sph ? k * d : k) * 4), sums(c, k * d * 4), counts(c, k * 4),
-      pass(c, k * d * 4), tally0(c, k * 4), tally1(c, k * 4), init_ids(c, k * 4);
+  const size_t rb = n * 4, kb = k * 4, cb = k * d * 4, ob = (sph ? k * d : k) * 4;
+  Arena ar = arena_for(c->trun, {rb, rb, rb, rb, rb, rb, cb, kb, ob, cb, kb, cb, kb, kb, kb});
+  Buf order0(ar, rb), order1(ar, rb), lab0(ar, rb), lab1(ar, rb), sco0(ar, rb), sco1(ar, rb),
+      pos(ar, cb), mass(ar, kb), readout(ar, ob), sums(ar, cb), counts(ar, kb), pass(ar, cb),
+      tally0(ar, kb), tally1(ar, kb), init_ids(ar, kb);
   // When the batches take the split-operand screen, every row's bf16 halves
   // once (slab-major, with |x|^2): each batch then gathers its rows' halves
   // by id instead of splitting them again.
@@ -1110,7 +1131,8 @@ std::vector<uint32_t> kmeans_pp_dev(emh_ctx* c, const float* x, size_t n, size_t
   RandomState rng(seed);
   size_t last = (size_t)rng.interval(n - 1);
   picks.push_back((uint32_t)last);
-  Buf best(c, n * 4);
+  Arena ar = arena_for(c->kpp, {n * 4});
+  Buf best(ar, n * 4);
   launch_fill_u32(c, best.u(), n, 0xff800000u);  // -inf
   float* hb = (float*)c->pin_aux.get(n * 4);
   std::vector<double> w(n);
@@ -1186,9 +1208,11 @@ void internal_scores_dev(emh_ctx* c, const float* x, size_t n, size_t d, const u
       rid[at[own[i]]++] = (uint32_t)i;
     }
   }
-  Buf rid_d(c, n * 4), start_d(c, (ke + 1) * 4), own_d(c, n * 4), sums_d(c, ke * d * 8),
-      s32_d(c, ke * d * 4), size_d(c, ke * 8), sq_d(c, ke * 8), g_d(c, n * ke * 4),
-      xx_d(c, n * 8), sil_d(c, n * 8), obj_d(c, n * 8), dist_d(c, n * 8);
+  Arena ar = arena_for(c->iscore, {n * 4, (ke + 1) * 4, n * 4, ke * d * 8, ke * d * 4, ke * 8,
+                                    ke * 8, n * ke * 4, n * 8, n * 8, n * 8, n * 8});
+  Buf rid_d(ar, n * 4), start_d(ar, (ke + 1) * 4), own_d(ar, n * 4), sums_d(ar, ke * d * 8),
+      s32_d(ar, ke * d * 4), size_d(ar, ke * 8), sq_d(ar, ke * 8), g_d(ar, n * ke * 4),
+      xx_d(ar, n * 8), sil_d(ar, n * 8), obj_d(ar, n * 8), dist_d(ar, n * 8);
   h2d(c, rid_d.p, rid.data(), n * 4);
   h2d(c, start_d.p, start.data(), (ke + 1) * 4);
   h2d(c, own_d.p, own.data(), n * 4);
@@ -1422,7 +1446,8 @@ int emh_assign_dev(emh_ctx* c, const emh_buf* x, size_t n, size_t d, const emh_b
     EMH_HIP(hipSetDevice(c->device));
     ++scores->gen;
     chunk = chunk ? chunk : 65536;
-    Buf cn(c, metric == EMH_L2 ? k * 4 : 0);
+    emh::Arena ar = arena_for(c->cnorm, {metric == EMH_L2 ? k * 4 : 0});
+    Buf cn(ar, metric == EMH_L2 ? k * 4 : 0);
     if (metric == EMH_L2) emh::launch_row_norms(c, (const float*)cents->ptr, k, d, cn.f());
     // The rows' bf16 halves, when the context's last training run split these
     // very rows and nothing has written them since.
@@ -1437,7 +1462,7 @@ int emh_assign_dev(emh_ctx* c, const emh_buf* x, size_t n, size_t d, const emh_b
                        (uint32_t*)labels->ptr, (float*)scores->ptr, false, nullptr,
                        reuse ? &pre : nullptr);
     }
-    EMH_HIP(hipStreamSynchronize(c->stream));  // cn is freed on return
+    EMH_HIP(hipStreamSynchronize(c->stream));  // cn's block is reused by the next call
   });
 }
 

@@ -156,6 +156,7 @@ struct emh_buf {
   size_t len = 0;   // elements
   int kind = 0;     // 0 f32, 1 u32
   bool owned = true;
+  int device = -1;  // where the library allocated it
   // Which buffer and which contents, for the split rows a context keeps: a
   // serial number unique over the process, a generation every entry point
   // that writes the buffer advances, and whether its address was handed out
@@ -189,6 +190,11 @@ struct emh_ctx {
   emh::Scratch tsplit, tsplit_part;          // a training run's centroids, kept split by the EMA
   emh::Scratch tally_cnt;                    // a training run's label tally (chunk histograms)
   emh::Scratch klong;                        // top-k beyond 16: a query block's scores
+  // Per-call buffers of the entry points that run many times in a row (a
+  // training run's, k-means++'s, internal_scores', the assignment's norms):
+  // carved from a block kept between calls, since hipFree waits for the
+  // whole device, the other contexts' streams included.
+  emh::Scratch trun, kpp, iscore, cnorm;
   emh::Scratch preview_ticket;  // k_mass_preview's last-block ticket (left at zero)
   // Host staging of the device loop: masses, plan, flags, epoch orders and
   // epoch labels/scores (double-buffered), results.
