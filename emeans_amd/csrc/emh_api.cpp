@@ -118,8 +118,13 @@ void* take_kept(emh_ctx* c, size_t bytes) {
     g_kept.erase(it);
     g_kept_bytes[c->device] -= bytes;
     for (hipEvent_t e : kb.after) {
-      EMH_HIP(hipStreamWaitEvent(c->stream, e, 0));
-      EMH_HIP(hipStreamWaitEvent(c->copy_stream, e, 0));
+      // Most have completed by now: a wait between hardware queues is
+      // queued only for those that have not.
+      if (hipEventQuery(e) != hipSuccess) {
+        (void)hipGetLastError();  // not-ready is no error of the next launch
+        EMH_HIP(hipStreamWaitEvent(c->stream, e, 0));
+        EMH_HIP(hipStreamWaitEvent(c->copy_stream, e, 0));
+      }
       g_spare_events[c->device].push_back(e);
     }
     return kb.ptr;

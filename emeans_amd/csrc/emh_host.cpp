@@ -559,6 +559,15 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   // stream); ev_done[b]: the epoch that used order/labels/scores b has run
   // (main stream); ev_epoch[b]: its scores and label counts are on the host.
   Event ev_init, ev_order[2], ev_done[2], ev_epoch[2], ev_last, ev_posout;
+  // The copies' stream: the copy stream, beside the kernels; for a small run
+  // the context stream itself, where the copies are a few KB and a wait
+  // across streams (a barrier packet between hardware queues) would cost more
+  // than the overlap saves. cross_wait orders stream s after event e, which
+  // was recorded on the other stream; with one stream, order is implicit.
+  hipStream_t cps = n <= ONE_STREAM_ROWS ? c->stream : c->copy_stream;
+  auto cross_wait = [&](hipStream_t s, hipEvent_t e) {
+    if (cps != c->stream) EMH_HIP(hipStreamWaitEvent(s, e, 0));
+  };
 
   // Epochs alternate between two sets of order/labels/scores buffers, so the
   // copies of one epoch's run on the copy stream beside the next epoch's kernels.
@@ -625,10 +634,10 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
     const int buf = (int)(epoch & 1);
     ev_order[buf].wait();
     RandomState::permutation_into(epoch_seed(cfg.seed, epoch), n, h_order[buf]);
-    EMH_HIP(hipStreamWaitEvent(c->copy_stream, ev_done[buf].e, 0));
+    cross_wait(cps, ev_done[buf].e);
     EMH_HIP(hipMemcpyAsync(d_order[buf], h_order[buf], R.epoch_rows[epoch] * 4,
-                           hipMemcpyHostToDevice, c->copy_stream));
-    ev_order[buf].record(c->copy_stream);
+                           hipMemcpyHostToDevice, cps));
+    ev_order[buf].record(cps);
   };
   // The revival stream (RandomState(seed)) serves only revivals, k uniforms
   // per revival that splits: the next k Gumbel terms are drawn ahead.
@@ -712,8 +721,8 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
     const bool last = epoch + 1 == n_epochs;
     const int buf = (int)(epoch & 1);
     next.get();
-    EMH_HIP(hipStreamWaitEvent(c->stream, ev_order[buf].e, 0));  // this epoch's order is in
-    EMH_HIP(hipStreamWaitEvent(c->stream, ev_epoch[buf].e, 0));  // labels of epoch - 2 are out
+    cross_wait(c->stream, ev_order[buf].e);  // this epoch's order is in
+    cross_wait(c->stream, ev_epoch[buf].e);  // labels of epoch - 2 are out
     if (!last) next = beside([&, e1 = epoch + 1] { fill_order(e1); });
     launch_fill_u32(c, d_tally[buf], k, 0);
     uint32_t* order = d_order[buf];
@@ -812,10 +821,10 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
     // Epoch end: labels and scores go out; the statistics (train.rs:224-279)
     // wait for them on a helper thread.
     ev_done[buf].record(c->stream);
-    EMH_HIP(hipStreamWaitEvent(c->copy_stream, ev_done[buf].e, 0));
-    EMH_HIP(hipMemcpyAsync(h_lab[buf], d_tally[buf], k * 4, hipMemcpyDeviceToHost, c->copy_stream));
-    EMH_HIP(hipMemcpyAsync(h_sco[buf], sco, rows * 4, hipMemcpyDeviceToHost, c->copy_stream));
-    ev_epoch[buf].record(c->copy_stream);
+    cross_wait(cps, ev_done[buf].e);
+    EMH_HIP(hipMemcpyAsync(h_lab[buf], d_tally[buf], k * 4, hipMemcpyDeviceToHost, cps));
+    EMH_HIP(hipMemcpyAsync(h_sco[buf], sco, rows * 4, hipMemcpyDeviceToHost, cps));
+    ev_epoch[buf].record(cps);
     if (pending.valid()) stats.push_back(pending.get());  // frees the other buffer pair
     const size_t nsplit = n_splits - splits_before;
     pending = beside([&, rows, buf, nsplit, epoch, st = step]() {
@@ -889,10 +898,10 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   const size_t rows_last = R.epoch_rows.back();
   const int lb = (int)((n_epochs - 1) & 1);
   ev_last.record(c->stream);
-  EMH_HIP(hipStreamWaitEvent(c->copy_stream, ev_last.e, 0));
-  EMH_HIP(hipMemcpyAsync(h_out + k * d, pos.p, k * d * 4, hipMemcpyDeviceToHost, c->copy_stream));
-  EMH_HIP(hipMemcpyAsync(h_out + 2 * k * d, mass.p, k * 4, hipMemcpyDeviceToHost, c->copy_stream));
-  ev_posout.record(c->copy_stream);
+  cross_wait(cps, ev_last.e);
+  EMH_HIP(hipMemcpyAsync(h_out + k * d, pos.p, k * d * 4, hipMemcpyDeviceToHost, cps));
+  EMH_HIP(hipMemcpyAsync(h_out + 2 * k * d, mass.p, k * 4, hipMemcpyDeviceToHost, cps));
+  ev_posout.record(cps);
   launch_closing(c, pos.f(), pass.f(), d_tally[lb], k, d, sums.f());
   const float* C = sums.f();
   if (sph) {

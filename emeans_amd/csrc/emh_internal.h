@@ -342,6 +342,10 @@ void launch_scatter_sums(emh_ctx* c, const float* x, size_t nx, size_t d, const 
                          float* acc, const uint32_t* counts_tallied = nullptr,
                          const uint32_t* tally_cnt = nullptr, size_t tally_stride = 0);
 
+// Training runs of at most this many rows queue their host<->device copies
+// on the context stream instead of the copy stream.
+constexpr size_t ONE_STREAM_ROWS = 65536;
+
 // ---- emh_update.hip: a small training batch's scatter_add and EMA step in one
 // launch (the same bits as launch_scatter_sums then launch_ema).
 constexpr size_t UPDATE_SMALL_BATCH = 256;  // most positions per batch
