@@ -599,9 +599,10 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   void* tsplit = keep_csplit ? c->tsplit.get(halves_bytes(k, d)) : nullptr;
   // The bound's centroid maxima: halves_blocks(k) pairs after a full split,
   // then one pair per EMA block, or per cluster after a small batch's update.
-  uint32_t* tpart_h = keep_csplit ? (uint32_t*)c->tsplit_part.get(
-                                        (halves_blocks(k) + std::max(ema_blocks(k), k)) * 8)
-                                  : nullptr;
+  // A revival's split appends one pair per split (at most k / 2) to those.
+  const size_t tpart_pairs = halves_blocks(k) + std::max(ema_blocks(k), k) + k;
+  uint32_t* tpart_h = keep_csplit ? (uint32_t*)c->tsplit_part.get(tpart_pairs * 8) : nullptr;
+  const uint32_t* tpart_end = keep_csplit ? tpart_h + 2 * tpart_pairs : nullptr;
   uint32_t* tpart_e = keep_csplit ? tpart_h + 2 * halves_blocks(k) : nullptr;
   SplitCents pcents{tsplit, tpart_h, (int)halves_blocks(k)};
   // When the batches' top-1 runs the screen with d % 4 == 0 (the check and
@@ -809,9 +810,22 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
         if (!plan.empty()) {
           const size_t np = plan.size() / 2;
           std::memcpy(h_plan, plan.data(), plan.size() * 4);
-          launch_split(c, pos.f(), mass.f(), d_plan, np, d, true);  // donors and dead are disjoint
+          if (!sph && d <= SPLIT_FUSED_MAX_D) {
+            // Donors and dead are disjoint. The split also leaves the moved
+            // rows' norms and (split screen) halves, and appends a bound
+            // partial per pair: no full row_norms and halves pass follows.
+            uint32_t* app = keep_csplit ? const_cast<uint32_t*>(pcents.part) +  // tpart_h's
+                                              2 * (size_t)pcents.nparts
+                                        : nullptr;
+            EMH_ENSURE(!keep_csplit || app + 2 * np <= tpart_end, "bound partials overflow");
+            launch_split_fused(c, pos.f(), mass.f(), d_plan, np, d, k, readout.f(),
+                               keep_csplit ? tsplit : nullptr, app);
+            if (keep_csplit) pcents.nparts += (int)np;
+          } else {
+            launch_split(c, pos.f(), mass.f(), d_plan, np, d, true);
+            norms_stale = true;
+          }
           n_splits += np;
-          norms_stale = true;
           readout_stale = true;
         }
         refill = !gnext.valid();  // scheduled after the next batch's launches

@@ -319,6 +319,14 @@ void launch_labels_by_row(emh_ctx* c, const uint32_t* order, const uint32_t* lab
 void launch_check_finite(emh_ctx* c, const float* v, size_t n, uint32_t* flag);
 void launch_split(emh_ctx* c, float* pos, float* usage, const uint32_t* pairs_dev, size_t npairs,
                   size_t d, bool independent);
+// launch_split of independent pairs that also writes the two moved rows'
+// norms (L2 readout) and, when given, their bf16 halves (csplit, k rows) and
+// one bound partial pair per pair (cpart[2 q], cpart[2 q + 1]); d at most
+// SPLIT_FUSED_MAX_D.
+constexpr size_t SPLIT_FUSED_MAX_D = 1024;
+void launch_split_fused(emh_ctx* c, float* pos, float* usage, const uint32_t* pairs_dev,
+                        size_t npairs, size_t d, size_t k, float* norms, void* csplit,
+                        uint32_t* cpart);
 void launch_gather_rows(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
                         size_t m, float* out);
 

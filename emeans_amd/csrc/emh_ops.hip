@@ -529,6 +529,101 @@ __global__ __launch_bounds__(256) void k_split(float* __restrict__ pos, float* _
   }
 }
 
+// k_split over independent pairs (no row is both a donor and a dead
+// cluster), d <= SPLIT_FUSED_MAX_D, leaving also what the next batch reads of
+// the two rows it moves, as a full row_norms and halves pass would: norms[s]
+// and norms[t] (k_row_norms' in-order chain of the rounded squares); with
+// csplit their bf16 halves in the split layout of k rows; with cpart the pair
+// cpart[2 q] = cpart[2 q + 1] = the larger of the two norms (f32 bits), which
+// the caller appends to the bound's centroid partials. The partials of the
+// blocks the two rows were in stay upper bounds: no other row changed.
+// Workgroup q = pair q. LDS: the two rows' values, then their squares, each
+// row ema_row(d) floats.
+__global__ __launch_bounds__(256) void k_split_fused(float* __restrict__ pos,
+                                                     float* __restrict__ usage,
+                                                     const uint32_t* __restrict__ pairs, size_t d,
+                                                     size_t k, float* __restrict__ norms,
+                                                     char* __restrict__ csplit,
+                                                     uint32_t* __restrict__ cpart) {
+  extern __shared__ __attribute__((aligned(16))) float sl[];
+  __shared__ int diff;
+  __shared__ float nv[2];
+  const int tid = threadIdx.x, q = blockIdx.x, len = (int)d, row = ema_row(len);
+  float* vs = sl;
+  float* sq = sl + 2 * row;
+  const uint32_t s = pairs[2 * q], t = pairs[2 * q + 1];
+  if (tid == 0) diff = 0;
+  __syncthreads();
+  float* cs = pos + (size_t)s * d;
+  float* ct = pos + (size_t)t * d;
+  const float eps = 1e-4f;
+  bool mine = false;
+  for (int i = tid; i < len; i += 256) {
+    const float off = eps * ((i % 2 == 0) ? 1.0f : -1.0f);
+    const float c = cs[i];
+    const float lo = 1.0f - off, hi = 1.0f + off;
+    mine = mine || !(c * lo == c * hi);
+  }
+  if (mine) atomicOr(&diff, 1);
+  __syncthreads();
+  const bool same = diff == 0;
+  const float half = usage[s] / 2.0f;
+  __syncthreads();  // every thread has read usage[s]
+  for (int i = tid; i < len; i += 256) {
+    const float off = eps * ((i % 2 == 0) ? 1.0f : -1.0f);
+    const float c = cs[i];
+    const float lo = 1.0f - off, hi = 1.0f + off;
+    const float dn = c * lo;
+    float ch = c * hi;
+    if (i == 0 && same) {
+      const float up = next_up(ch);
+      ch = isfinite(up) ? up : next_down(ch);
+    }
+    cs[i] = dn;
+    ct[i] = ch;
+    vs[i] = dn;
+    vs[row + i] = ch;
+    sq[i] = dn * dn;
+    sq[row + i] = ch * ch;
+  }
+  if (tid == 0) {
+    usage[s] = half;
+    usage[t] = half;
+  }
+  __syncthreads();
+  if (csplit) {
+    // Quads of the two rows (the last slab's dimensions past d are zero),
+    // beside the chains of lanes 0 and 1.
+    const int nq = ((len + 31) & ~31) >> 2;
+    for (int e = tid; e < 2 * nq; e += 256) {
+      const int r = e / nq, c4 = 4 * (e % nq);
+      const float* vr = vs + r * row;
+      const float4 v4 = make_float4(c4 < len ? vr[c4] : 0.0f, c4 + 1 < len ? vr[c4 + 1] : 0.0f,
+                                    c4 + 2 < len ? vr[c4 + 2] : 0.0f,
+                                    c4 + 3 < len ? vr[c4 + 3] : 0.0f);
+      uint2 hv, lv;
+      split_quad(v4, hv, lv);
+      char* o = csplit + ((size_t)(c4 >> 5) * k + (r ? t : s)) * SLAB_BYTES +
+                quad_hi_offset((c4 & 31) >> 2);
+      *reinterpret_cast<uint2*>(o) = hv;
+      *reinterpret_cast<uint2*>(o + 32) = lv;
+    }
+  }
+  if (tid < 2) {
+    const float nrm = ordered_sum(sq + tid * row, len);
+    norms[tid ? t : s] = nrm;
+    nv[tid] = nrm;
+  }
+  if (cpart) {
+    __syncthreads();
+    if (tid == 0) {
+      const uint32_t m = max(__float_as_uint(nv[0]), __float_as_uint(nv[1]));
+      cpart[2 * q] = m;
+      cpart[2 * q + 1] = m;
+    }
+  }
+}
+
 // out[i] = x[ids[i]] (m rows of d); an id >= nx gives a zero row.
 __global__ __launch_bounds__(256) void k_gather_rows(const float* __restrict__ x, size_t nx,
                                                      size_t d, const uint32_t* __restrict__ ids,
@@ -627,6 +722,17 @@ void launch_labels_by_row(emh_ctx* c, const uint32_t* order, const uint32_t* lab
 void launch_check_finite(emh_ctx* c, const float* v, size_t n, uint32_t* flag) {
   if (n == 0) return;
   hipLaunchKernelGGL(k_check_finite, grid1(n, 256), dim3(256), 0, c->stream, v, n, flag);
+  EMH_HIP(hipGetLastError());
+}
+
+void launch_split_fused(emh_ctx* c, float* pos, float* usage, const uint32_t* pairs_dev,
+                        size_t npairs, size_t d, size_t k, float* norms, void* csplit,
+                        uint32_t* cpart) {
+  if (npairs == 0) return;
+  EMH_ENSURE(d >= 1 && d <= SPLIT_FUSED_MAX_D && norms, "split_fused: shape out of range");
+  const size_t lds = 4 * (size_t)ema_row((int)d) * sizeof(float);
+  hipLaunchKernelGGL(k_split_fused, dim3((unsigned)npairs), dim3(256), lds, c->stream, pos, usage,
+                     pairs_dev, d, k, norms, (char*)csplit, cpart);
   EMH_HIP(hipGetLastError());
 }
 
