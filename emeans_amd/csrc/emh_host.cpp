@@ -576,6 +576,57 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   Buf order0(ar, rb), order1(ar, rb), lab0(ar, rb), lab1(ar, rb), sco0(ar, rb), sco1(ar, rb),
       pos(ar, cb), mass(ar, kb), readout(ar, ob), sums(ar, cb), counts(ar, kb), pass(ar, cb),
       tally0(ar, kb), tally1(ar, kb), init_ids(ar, kb);
+  uint32_t* d_order[2] = {order0.u(), order1.u()};
+  struct Drain {  // nothing queued may outlive the buffers, also on an error
+    emh_ctx* c;
+    ~Drain() {
+      (void)hipStreamSynchronize(c->copy_stream);
+      (void)hipStreamSynchronize(c->stream);
+    }
+  } drain{c};
+  // Epoch e's order: drawn into h_order[e % 2] once the last copy out of it is
+  // done, then copied (copy stream) into d_order[e % 2] once the epoch that
+  // last used that buffer has run. Runs on a helper thread.
+  auto fill_order = [&](size_t epoch) {
+    const int buf = (int)(epoch & 1);
+    ev_order[buf].wait();
+    RandomState::permutation_into(epoch_seed(cfg.seed, epoch), n, h_order[buf]);
+    cross_wait(cps, ev_done[buf].e);
+    EMH_HIP(hipMemcpyAsync(d_order[buf], h_order[buf], R.epoch_rows[epoch] * 4,
+                           hipMemcpyHostToDevice, cps));
+    ev_order[buf].record(cps);
+  };
+  // The revival stream (RandomState(seed)) serves only revivals, k uniforms
+  // per revival that splits: the next k Gumbel terms are drawn ahead.
+  RandomState split_rng(cfg.seed);
+  // Helper tasks (the next epoch's order, Gumbel terms, epoch statistics)
+  // reference this frame, and their futures do not wait when destroyed: on
+  // any exit, an error included, Join waits for those still running before
+  // anything they use goes.
+  std::future<void> next;
+  std::future<std::vector<double>> gnext;
+  std::future<emh_epoch_stats> pending;
+  std::future<void> init_perm;
+  struct Join {
+    std::future<void>& a;
+    std::future<std::vector<double>>& b;
+    std::future<emh_epoch_stats>& p;
+    std::future<void>& q;
+    ~Join() {
+      if (a.valid()) a.wait();
+      if (b.valid()) b.wait();
+      if (p.valid()) p.wait();
+      if (q.valid()) q.wait();
+    }
+  } join{next, gnext, pending, init_perm};
+  // The first epoch's order and the initial centroids' rows (permutation(n)
+  // [..k], model.rs:783-790) are drawn on helpers from the start, while this
+  // thread queues the split of the rows.
+  const bool resume = init && init->positions;
+  const bool draw_init = !resume && !(init && (init->centroids || init->centroids_dev)) && n != k;
+  next = beside([&] { fill_order(0); });
+  if (draw_init)  // into h_order[1], unused until epoch 1
+    init_perm = beside([&] { RandomState::permutation_into(cfg.seed, n, h_order[1]); });
   // When the batches take the split-operand screen, every row's bf16 halves
   // once (slab-major, with |x|^2): each batch then gathers its rows' halves
   // by id instead of splitting them again.
@@ -614,60 +665,15 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   const size_t tstride = tally_stride(bsz);
   uint32_t* tcnt = tally ? (uint32_t*)c->tally_cnt.get(tstride * k * 4) : nullptr;
   if (tally) launch_fill_u32(c, tcnt, tstride * k, 0);
-  uint32_t* d_order[2] = {order0.u(), order1.u()};
   uint32_t* d_lab[2] = {lab0.u(), lab1.u()};
   // The epoch's label counts, tallied batch by batch by the EMA launches: the
   // statistics' histogram, and for the last pass the closing means' counts.
   uint32_t* d_tally[2] = {tally0.u(), tally1.u()};
   float* d_sco[2] = {sco0.f(), sco1.f()};
-  struct Drain {  // nothing queued may outlive the buffers, also on an error
-    emh_ctx* c;
-    ~Drain() {
-      (void)hipStreamSynchronize(c->copy_stream);
-      (void)hipStreamSynchronize(c->stream);
-    }
-  } drain{c};
-
-  // Epoch e's order: drawn into h_order[e % 2] once the last copy out of it is
-  // done, then copied (copy stream) into d_order[e % 2] once the epoch that
-  // last used that buffer has run. Runs on a helper thread.
-  auto fill_order = [&](size_t epoch) {
-    const int buf = (int)(epoch & 1);
-    ev_order[buf].wait();
-    RandomState::permutation_into(epoch_seed(cfg.seed, epoch), n, h_order[buf]);
-    cross_wait(cps, ev_done[buf].e);
-    EMH_HIP(hipMemcpyAsync(d_order[buf], h_order[buf], R.epoch_rows[epoch] * 4,
-                           hipMemcpyHostToDevice, cps));
-    ev_order[buf].record(cps);
-  };
-  // The revival stream (RandomState(seed)) serves only revivals, k uniforms
-  // per revival that splits: the next k Gumbel terms are drawn ahead.
-  RandomState split_rng(cfg.seed);
-  // Helper tasks (the next epoch's order, Gumbel terms, epoch statistics)
-  // reference this frame, and their futures do not wait when destroyed: on
-  // any exit, an error included, Join waits for those still running before
-  // anything they use goes.
-  std::future<void> next;
-  std::future<std::vector<double>> gnext;
-  std::future<emh_epoch_stats> pending;
-  struct Join {
-    std::future<void>& a;
-    std::future<std::vector<double>>& b;
-    std::future<emh_epoch_stats>& p;
-    ~Join() {
-      if (a.valid()) a.wait();
-      if (b.valid()) b.wait();
-      if (p.valid()) p.wait();
-    }
-  } join{next, gnext, pending};
-  // The first epoch's order is drawn while the initial centroids are (model.rs:783-784).
-  next = beside([&] { fill_order(0); });
-
   // The start (model.rs:772-797): saved EMA state as it is (begin_with_state);
   // else initial centroids, given (begin) or the rows permutation(n)[..k],
   // normalized when spherical (model.rs:306-316), masses INIT_USAGE
   // (recipe.rs:14).
-  const bool resume = init && init->positions;
   if (resume) {
     h2d(c, pos.p, init->positions, k * d * 4);
     h2d(c, mass.p, init->usage, k * 4);
@@ -680,7 +686,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
     } else if (n == k) {
       EMH_HIP(hipMemcpyAsync(pos.p, x, k * d * 4, hipMemcpyDeviceToDevice, c->stream));
     } else {
-      RandomState::permutation_into(cfg.seed, n, h_order[1]);  // unused until epoch 1
+      init_perm.get();
       copy_async(c, init_ids.p, h_order[1], k * 4, hipMemcpyHostToDevice);
       launch_gather_rows(c, x, n, d, init_ids.u(), k, pos.f());
     }
@@ -699,8 +705,9 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   copy_async(c, h_small0, c->small, SW_WORDS * 4, hipMemcpyDeviceToHost);
   ev_order[1].record(c->stream);  // the initial ids are out of h_order[1]
   ev_init.record(c->stream);
-  ev_init.wait();
-  raise_flags(c, h_small0);
+  // The check of the initial centroids (finite) is read once the first
+  // batch's top-1 is queued, so the device is not idle meanwhile.
+  bool init_checked = false;
   if (cfg.verbose)
     fprintf(stderr, "Clustering %zu points in %zuD to %zu clusters, %g epochs (batch %zu, alpha0 %.3f%s)\n",
             n, d, k, cfg.nepochs, bsz, R.alpha0, sph ? ", spherical" : "");
@@ -754,6 +761,11 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
         launch_top1(c, x, n, d, order, c0, c1, cents, cn, k, sph, lab, sco,
                     step > 0 && c0 == b, nullptr, pre, keep_csplit ? &pcents : nullptr,
                     tally ? &tl : nullptr);
+      }
+      if (!init_checked) {
+        ev_init.wait();
+        raise_flags(c, h_small0);
+        init_checked = true;
       }
       if (refill) {  // the next check's Gumbel terms, drawn while the GPU works
         gnext = beside([&] { return gumbel_terms(split_rng, k); });
