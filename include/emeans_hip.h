@@ -75,7 +75,12 @@ int emh_write_u32(emh_ctx* ctx, emh_buf* b, size_t offset, const uint32_t* v, si
 /* Device::read_f32 / read_u32 (core/mod.rs:89-91): wait, then copy b[lo..hi). */
 int emh_read_f32(emh_ctx* ctx, const emh_buf* b, size_t lo, size_t hi, float* dst);
 int emh_read_u32(emh_ctx* ctx, const emh_buf* b, size_t lo, size_t hi, uint32_t* dst);
-/* Drop of the backend's buffer type. Waits for queued work first. */
+/* Drop of the backend's buffer type. Waits for ctx's queued work first. A
+ * block of at most 64 MB is kept for the next buffer of the same size on the
+ * device (at most 1 GB a device, released with the device's last context), and
+ * the context that takes it waits on the device for the work the other
+ * contexts had queued when it was freed; a buffer whose address went out
+ * (emh_buf_ptr) is freed at once. */
 int emh_free(emh_ctx* ctx, emh_buf* b);
 /* A non-owning view of caller device memory (for example a torch tensor) as a
  * buffer; freeing the view does not free the memory. kind: 0 f32, 1 u32. */
