@@ -958,12 +958,34 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   EMH_HIP(hipStreamSynchronize(c->stream));
   stats.push_back(pending.get());
   raise_flags(c, h_small);
-  std::memcpy(out->centroids, h_out, k * d * 4);
-  if (out->labels) {
-    if (capture)
-      std::memcpy(out->labels, h_rowlab, n * 4);
-    else
-      std::fill(out->labels, out->labels + n, -1);
+  // The outputs: the centroids in four pieces (three on helpers), the labels
+  // beside them.
+  {
+    constexpr int T = 4;
+    const size_t cb = k * d * 4, part = (cb / T + 63) & ~size_t(63);
+    std::future<void> f[T];
+    struct JoinAll {  // no piece may outlive this frame, also on an error
+      std::future<void>* f;
+      ~JoinAll() {
+        for (int t = 0; t < T; t++)
+          if (f[t].valid()) f[t].wait();
+      }
+    } join_all{f};
+    for (int t = 1; t < T; t++) {
+      const size_t a = std::min(cb, t * part), b = std::min(cb, a + part);
+      if (a < b)
+        f[t] = beside([=] { std::memcpy((char*)out->centroids + a, (const char*)h_out + a, b - a); });
+    }
+    if (out->labels)
+      f[0] = beside([&] {
+        if (capture)
+          std::memcpy(out->labels, h_rowlab, n * 4);
+        else
+          std::fill(out->labels, out->labels + n, -1);
+      });
+    std::memcpy(out->centroids, h_out, std::min(cb, part));
+    for (auto& x : f)
+      if (x.valid()) x.get();
   }
   side.get();
   out->n_epochs = n_epochs;
