@@ -261,11 +261,12 @@ std::vector<uint32_t> plan_revival(const std::vector<float>& usage, double tau, 
     keys.push_back({b, (uint32_t)j});
   }
   // Larger key first, equal keys: higher index first. The order is total, so
-  // the first nsplit of a partial sort are those of a full sort.
-  std::partial_sort(keys.begin(), keys.begin() + nsplit, keys.end(),
-                    [](const Key& a, const Key& b) {
-                      return a.ord != b.ord ? a.ord > b.ord : a.j > b.j;
-                    });
+  // the nsplit first of a selection, sorted, are those of a full sort.
+  const auto before = [](const Key& a, const Key& b) {
+    return a.ord != b.ord ? a.ord > b.ord : a.j > b.j;
+  };
+  if (nsplit < keys.size()) std::nth_element(keys.begin(), keys.begin() + nsplit, keys.end(), before);
+  std::sort(keys.begin(), keys.begin() + nsplit, before);
   for (size_t q = 0; q < nsplit; q++) {
     pairs.push_back(keys[q].j);
     pairs.push_back(dead[q]);

@@ -137,6 +137,35 @@ def test_host_revival_plan_and_pairwise_sum_match_the_oracle(lib):
         assert np.float32(s) == np.sum(usage, dtype=np.float32), k
 
 
+def test_host_revival_plan_over_many_masses_matches_the_oracle(lib):
+    """The plan computes exact keys only for donors an approximate key cannot
+    rule out: the pairs equal the oracle's over mass distributions with few
+    and many dead clusters, ties, subnormal and huge masses, and k = 1024."""
+    g = np.random.default_rng(21)
+    cases = 0
+    for k in (16, 257, 1024):
+        for it in range(12):
+            kind = it % 4
+            if kind == 0:
+                usage = g.gamma(0.3, 1.0, k)
+            elif kind == 1:
+                usage = g.pareto(1.1, k) * 1e-3
+            elif kind == 2:
+                usage = np.repeat(g.random(k // 8 + 1), 8)[:k]  # many ties
+            else:
+                usage = np.exp(g.uniform(-100, 80, k))  # subnormal to huge
+            usage = usage.astype(np.float32)
+            usage[g.choice(k, int(k * g.uniform(0.02, 0.5)), replace=False)] = 0.0
+            tau = float(g.choice([0.05, 0.1, 0.5, 2.0]))
+            seed = int(g.integers(0, 2**32))
+            pairs = np.empty(2 * k, np.uint32)
+            npairs = lib.emh_host_plan_revival(usage.ctypes.data, k, tau, seed, pairs.ctypes.data)
+            want = O.plan_revival(usage, tau, O.RandomState(seed))
+            assert pairs[: 2 * npairs].tolist() == np.asarray(want).reshape(-1).tolist(), (k, it)
+            cases += npairs > 0
+    assert cases > 20
+
+
 def test_dedup_neighbors_matches_the_oracle(lib):
     """The host grouping with every side input: priorities, creation times
     (some unknown) under a time gap, and burst ids, against the oracle."""
