@@ -622,8 +622,9 @@ def autok_run(args):
     x = x_all[:n]
     log(f"autok data: {n_all} x {d} generated in {time.time() - t:.1f} s")
     dev = HipDevice()
-    xb = dev.bind(x)
     cfg = auto.AutoConfig(restarts=args.autok_restarts, seed=3, verbose=True)
+    dev.contexts(min(cfg.restarts, auto.MAX_CONTEXTS))  # before the warm-up fit's copy stream
+    xb = dev.bind(x)
     auto.fit(dev, x, xb, 8, 1.0, 1, None)  # warm the kernels up
     dev.sync()
     tm = {}

@@ -123,7 +123,7 @@ void* take_kept(emh_ctx* c, size_t bytes) {
       if (hipEventQuery(e) != hipSuccess) {
         (void)hipGetLastError();  // not-ready is no error of the next launch
         EMH_HIP(hipStreamWaitEvent(c->stream, e, 0));
-        EMH_HIP(hipStreamWaitEvent(c->copy_stream, e, 0));
+        EMH_HIP(hipStreamWaitEvent(c->copies(), e, 0));
       }
       g_spare_events[c->device].push_back(e);
     }
@@ -147,6 +147,7 @@ void keep_block(emh_ctx* c, void* p, size_t bytes) {
     for (emh_ctx* o : g_live) {
       if (o == c || o->device != c->device) continue;
       for (hipStream_t st : {o->stream, o->copy_stream}) {
+        if (!st) continue;  // no copy stream yet: nothing queued there
         hipEvent_t e = spare_event(c->device);
         kb.after.push_back(e);
         EMH_HIP(hipEventRecord(e, st));
@@ -300,7 +301,6 @@ int emh_create(int device, emh_ctx** out) {
     }
     try {
       EMH_HIP(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
-      EMH_HIP(hipStreamCreateWithFlags(&c->copy_stream, hipStreamNonBlocking));
       for (hipEvent_t& e : c->ev_stage) EMH_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
       EMH_HIP(hipMalloc(&c->small, emh::SW_WORDS * 4));
       EMH_HIP(hipMemsetAsync(c->small, 0, emh::SW_WORDS * 4, c->stream));
@@ -327,7 +327,8 @@ int emh_destroy(emh_ctx* c) {
     if (!c) return;
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
-    (void)hipStreamSynchronize(c->copy_stream);  // copies may still read pinned staging
+    if (c->copy_stream)
+      (void)hipStreamSynchronize(c->copy_stream);  // copies may still read pinned staging
     for (emh::Scratch* s : {&c->cand, &c->fblist, &c->order, &c->start, &c->misc, &c->knn_tmp,
                             &c->xnorm, &c->bigj, &c->chunkcnt, &c->tickets,
                             &c->preview_ticket, &c->xsplit, &c->csplit, &c->csplit_norm, &c->csplit_part,
@@ -348,7 +349,7 @@ int emh_destroy(emh_ctx* c) {
     }
     release_kept(c->device);  // when c was the device's last context
     (void)hipStreamDestroy(c->stream);
-    (void)hipStreamDestroy(c->copy_stream);
+    if (c->copy_stream) (void)hipStreamDestroy(c->copy_stream);
     delete c;
   });
 }

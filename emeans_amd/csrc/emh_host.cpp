@@ -443,7 +443,8 @@ auto beside(F&& f) {
 constexpr size_t STAGE = size_t(32) << 20;
 void upload(emh_ctx* c, void* dst, const void* src, size_t bytes, hipEvent_t after = nullptr) {
   if (!bytes) return;
-  if (after) EMH_HIP(hipStreamWaitEvent(c->copy_stream, after, 0));
+  hipStream_t cs = c->copies();
+  if (after) EMH_HIP(hipStreamWaitEvent(cs, after, 0));
   char* half[2] = {(char*)c->pin_stage[0].get(STAGE), (char*)c->pin_stage[1].get(STAGE)};
   const char* s = (const char*)src;
   for (size_t off = 0, pc = 0; off < bytes; off += STAGE, pc++) {
@@ -460,10 +461,10 @@ void upload(emh_ctx* c, void* dst, const void* src, size_t bytes, hipEvent_t aft
     std::memcpy(half[h], s + off, std::min(len, part));
     for (auto& x : f) x.get();
     EMH_HIP(hipMemcpyAsync((char*)dst + off, half[h], len, hipMemcpyHostToDevice,
-                           c->copy_stream));
-    EMH_HIP(hipEventRecord(c->ev_stage[h], c->copy_stream));
+                           cs));
+    EMH_HIP(hipEventRecord(c->ev_stage[h], cs));
   }
-  EMH_HIP(hipEventRecord(c->ev_stage[2], c->copy_stream));
+  EMH_HIP(hipEventRecord(c->ev_stage[2], cs));
   EMH_HIP(hipStreamWaitEvent(c->stream, c->ev_stage[2], 0));
 }
 
@@ -565,7 +566,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   // across streams (a barrier packet between hardware queues) would cost more
   // than the overlap saves. cross_wait orders stream s after event e, which
   // was recorded on the other stream; with one stream, order is implicit.
-  hipStream_t cps = n <= ONE_STREAM_ROWS ? c->stream : c->copy_stream;
+  hipStream_t cps = n <= ONE_STREAM_ROWS ? c->stream : c->copies();
   auto cross_wait = [&](hipStream_t s, hipEvent_t e) {
     if (cps != c->stream) EMH_HIP(hipStreamWaitEvent(s, e, 0));
   };
@@ -581,7 +582,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   struct Drain {  // nothing queued may outlive the buffers, also on an error
     emh_ctx* c;
     ~Drain() {
-      (void)hipStreamSynchronize(c->copy_stream);
+      if (c->copy_stream) (void)hipStreamSynchronize(c->copy_stream);
       (void)hipStreamSynchronize(c->stream);
     }
   } drain{c};
@@ -1486,7 +1487,7 @@ int emh_assign(emh_ctx* c, const float* x, size_t n, size_t d, const float* cent
     }
     deliver(pend);
     check_flags(c);
-    EMH_HIP(hipStreamSynchronize(c->copy_stream));  // staging is free again
+    EMH_HIP(hipStreamSynchronize(c->copies()));  // staging is free again
   });
 }
 

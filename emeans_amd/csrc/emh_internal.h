@@ -169,7 +169,16 @@ struct emh_buf {
 struct emh_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
-  hipStream_t copy_stream = nullptr;  // host<->device staging that overlaps the kernels
+  // Host<->device staging that overlaps the kernels, made on first use
+  // (copies()): the runtime gives each new stream the least-used hardware
+  // queue, so contexts made together (the automatic-k sweeps' four) get
+  // their kernel streams on different queues when no copy stream comes
+  // between them.
+  hipStream_t copy_stream = nullptr;
+  hipStream_t copies() {
+    if (!copy_stream) EMH_HIP(hipStreamCreateWithFlags(&copy_stream, hipStreamNonBlocking));
+    return copy_stream;
+  }
   int cus = 256;
   int screen = emh::SCREEN_BF3;
   size_t exact_below = emh::EXACT_BELOW;  // emh_set_exact_below
