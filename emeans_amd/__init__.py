@@ -341,7 +341,7 @@ class HipDevice:
         return self.read_f32(out).reshape(m, nb)
 
     SCREEN_VARIANTS = {0: "none", 1: "big_tagged", 2: "big_sorted", 3: "small_bf16",
-                       4: "small_f32", 5: "big_knn"}
+                       4: "small_f32", 5: "big_knn", 6: "big_f16"}
 
     def screen_margin(self, x: Mat, sel: Select, centroids: DevBuf, cnorm: Optional[DevBuf],
                       k: int, metric) -> dict:
@@ -374,8 +374,9 @@ class HipDevice:
 
     def set_screen(self, mode):
         """Top-1 / top-k path: 1 or True = bf16 three-pass MFMA screen + exact
-        check (default), 2 = f32 MFMA screen + exact check, 0 or False = the
-        exact kernels alone. Every mode gives the same bits."""
+        check (default), 3 = the same with the split-operand top-1 screen in
+        fp16 two-pass arithmetic, 2 = f32 MFMA screen + exact check, 0 or
+        False = the exact kernels alone. Every mode gives the same bits."""
         check(lib().emh_set_screen(self._ctx, int(mode)))
 
     EXACT_BELOW = 4096

@@ -6,7 +6,9 @@
 #include <atomic>
 #include <cstring>
 #include <deque>
+#include <exception>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -114,20 +116,21 @@ void* take_kept(emh_ctx* c, size_t bytes) {
   std::lock_guard<std::mutex> g(g_blocks_mu);
   for (auto it = g_kept.begin(); it != g_kept.end(); ++it) {
     if (it->device != c->device || it->bytes != bytes) continue;
-    KeptBlock kb = std::move(*it);
-    g_kept.erase(it);
-    g_kept_bytes[c->device] -= bytes;
-    for (hipEvent_t e : kb.after) {
-      // Most have completed by now: a wait between hardware queues is
-      // queued only for those that have not.
+    // Most have completed by now: a wait between hardware queues is queued
+    // only for those that have not. A failed wait leaves the block kept.
+    for (hipEvent_t e : it->after) {
       if (hipEventQuery(e) != hipSuccess) {
         (void)hipGetLastError();  // not-ready is no error of the next launch
         EMH_HIP(hipStreamWaitEvent(c->stream, e, 0));
         EMH_HIP(hipStreamWaitEvent(c->copies(), e, 0));
       }
-      g_spare_events[c->device].push_back(e);
     }
-    return kb.ptr;
+    std::vector<hipEvent_t>& spare = g_spare_events[c->device];
+    spare.insert(spare.end(), it->after.begin(), it->after.end());
+    void* p = it->ptr;
+    g_kept_bytes[c->device] -= bytes;
+    g_kept.erase(it);
+    return p;
   }
   return nullptr;
 }
@@ -141,21 +144,31 @@ void keep_block(emh_ctx* c, void* p, size_t bytes) {
     return;
   }
   std::vector<void*> drop;
+  std::exception_ptr failed;
   {
     std::lock_guard<std::mutex> g(g_blocks_mu);
     KeptBlock kb{c->device, bytes, p, {}};
-    for (emh_ctx* o : g_live) {
-      if (o == c || o->device != c->device) continue;
-      for (hipStream_t st : {o->stream, o->copy_stream}) {
-        if (!st) continue;  // no copy stream yet: nothing queued there
-        hipEvent_t e = spare_event(c->device);
-        kb.after.push_back(e);
-        EMH_HIP(hipEventRecord(e, st));
+    try {
+      for (emh_ctx* o : g_live) {
+        if (o == c || o->device != c->device) continue;
+        for (hipStream_t st : {o->stream, o->copy_stream}) {
+          if (!st) continue;  // no copy stream yet: nothing queued there
+          hipEvent_t e = spare_event(c->device);
+          kb.after.push_back(e);
+          EMH_HIP(hipEventRecord(e, st));
+        }
       }
+    } catch (...) {
+      // The block is freed instead (hipFree waits for every stream).
+      std::vector<hipEvent_t>& spare = g_spare_events[c->device];
+      spare.insert(spare.end(), kb.after.begin(), kb.after.end());
+      failed = std::current_exception();
     }
-    g_kept.push_back(std::move(kb));
     size_t& total = g_kept_bytes[c->device];
-    total += bytes;
+    if (!failed) {
+      g_kept.push_back(std::move(kb));
+      total += bytes;
+    }
     for (auto it = g_kept.begin(); total > KEEP_DEVICE_MAX && it != g_kept.end();) {
       if (it->device != c->device) {
         ++it;
@@ -167,7 +180,14 @@ void keep_block(emh_ctx* c, void* p, size_t bytes) {
       it = g_kept.erase(it);
     }
   }
-  for (void* q : drop) EMH_HIP(hipFree(q));
+  if (failed) drop.push_back(p);
+  hipError_t first = hipSuccess;
+  for (void* q : drop) {
+    const hipError_t e = hipFree(q);
+    if (first == hipSuccess) first = e;
+  }
+  if (failed) std::rethrow_exception(failed);
+  EMH_HIP(first);
 }
 
 // Frees the blocks kept on `device` and its spare events (the last context
@@ -297,7 +317,7 @@ int emh_create(int device, emh_ctx** out) {
     c->cus = p.multiProcessorCount;
     if (const char* s = getenv("EMEANS_HIP_SCREEN")) {
       const int m = atoi(s);
-      c->screen = m == emh::SCREEN_F32 ? emh::SCREEN_F32 : m ? emh::SCREEN_BF3 : emh::SCREEN_OFF;
+      c->screen = m >= emh::SCREEN_OFF && m <= emh::SCREEN_F16 ? m : emh::SCREEN_BF3;
     }
     try {
       EMH_HIP(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
@@ -455,19 +475,23 @@ int emh_read_u32(emh_ctx* c, const emh_buf* b, size_t lo, size_t hi, uint32_t* d
 int emh_free(emh_ctx* c, emh_buf* b) {
   return guard([&] {
     if (!b) return;
+    std::unique_ptr<emh_buf> hold(b);  // the handle goes, also when the call fails
+    void* p = b->owned ? b->ptr : nullptr;
+    const bool keep = p && c && !b->exposed && b->device == c->device;
     if (c) {
       use_device(c);
-      EMH_HIP(hipStreamSynchronize(c->stream));
+      const hipError_t e = hipStreamSynchronize(c->stream);
+      if (e != hipSuccess) {
+        if (p) (void)hipFree(p);  // waits for every stream on the device
+        EMH_HIP(e);
+      }
     }
-    if (b->owned && b->ptr) {
-      // A buffer whose address went out may be in use on streams of the
-      // caller's own: hipFree waits for them.
-      if (c && !b->exposed && b->device == c->device)
-        keep_block(c, b->ptr, b->len * 4);
-      else
-        EMH_HIP(hipFree(b->ptr));
-    }
-    delete b;
+    // A buffer whose address went out may be in use on streams of the
+    // caller's own: hipFree waits for them.
+    if (keep)
+      keep_block(c, p, b->len * 4);
+    else if (p)
+      EMH_HIP(hipFree(p));
   });
 }
 
@@ -785,7 +809,8 @@ uint64_t emh_fallback_rows(emh_ctx* c) {
 int emh_set_screen(emh_ctx* c, int on) {
   return guard([&] {
     EMH_ENSURE(c, "null context");
-    EMH_ENSURE(on >= 0 && on <= 2, "screen mode %d: 0 (off), 1 (bf16) or 2 (f32)", on);
+    EMH_ENSURE(on >= 0 && on <= 3, "screen mode %d: 0 (off), 1 (bf16), 2 (f32) or 3 (fp16)",
+               on);
     c->screen = on;
   });
 }

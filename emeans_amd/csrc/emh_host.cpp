@@ -629,21 +629,25 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   next = beside([&] { fill_order(0); });
   if (draw_init)  // into h_order[1], unused until epoch 1
     init_perm = beside([&] { RandomState::permutation_into(cfg.seed, n, h_order[1]); });
-  // When the batches take the split-operand screen, every row's bf16 halves
-  // once (slab-major, with |x|^2): each batch then gathers its rows' halves
-  // by id instead of splitting them again.
+  // When the batches take the split-operand screen, every row's halves once
+  // (slab-major, with |x|^2; fp16 for the two-pass screen of SCREEN_F16,
+  // else bf16): each batch then gathers its rows' halves by id instead of
+  // splitting them again.
   SplitRows pre_rows{};
   const SplitRows* pre = nullptr;
   c->xpre_of = emh_ctx::SplitOf{};  // xpre is rewritten (or left stale) below
+  bool run_f16 = false;
   if (split_screen(c, bsz, d, k, sph) && n < (1u << 25)) {
+    run_f16 = c->screen == SCREEN_F16;
     pre_rows = SplitRows{c->xpre.get(halves_bytes(n, d)), (float*)c->xpre_norm.get(n * 4), n,
-                         n * 128};
+                         n * 128, run_f16};
     launch_halves(c, x, n, d, nullptr, 0, n, (void*)pre_rows.xs, (float*)pre_rows.xn, nullptr,
-                  nullptr);
+                  nullptr, run_f16);
     pre = &pre_rows;
     c->xpre_of.ptr = x;  // which buffer: emh_train_dev names it once the run has ended
     c->xpre_of.n = n;
     c->xpre_of.d = d;
+    c->xpre_of.f16 = run_f16;
   }
   // L2 batches on the split-operand screen keep the centroids split for the
   // run: a full split after each row-norms readout (the first batch, and
@@ -657,7 +661,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
   uint32_t* tpart_h = keep_csplit ? (uint32_t*)c->tsplit_part.get(tpart_pairs * 8) : nullptr;
   const uint32_t* tpart_end = keep_csplit ? tpart_h + 2 * tpart_pairs : nullptr;
   uint32_t* tpart_e = keep_csplit ? tpart_h + 2 * halves_blocks(k) : nullptr;
-  SplitCents pcents{tsplit, tpart_h, (int)halves_blocks(k)};
+  SplitCents pcents{tsplit, tpart_h, (int)halves_blocks(k), run_f16};
   // When the batches' top-1 runs the screen with d % 4 == 0 (the check and
   // the queued-row scan), or the latency-bound exact scan alone (small k),
   // it tallies the labels it writes (counts and the chunk histograms of the
@@ -749,7 +753,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
         norms_stale = false;
         if (keep_csplit) {
           launch_halves(c, pos.f(), k, d, nullptr, 0, k, tsplit, (float*)c->csplit_norm.get(k * 4),
-                        readout.f(), tpart_h);
+                        readout.f(), tpart_h, run_f16);
           pcents.part = tpart_h;
           pcents.nparts = (int)halves_blocks(k);
         }
@@ -795,7 +799,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
         launch_update_small(c, x, n, d, order, b, e, lab, k, counts.u(), tcnt, tstride * k,
                             last ? pass.f() : nullptr, pos.f(), mass.f(), af, df, replace,
                             sph ? nullptr : readout.f(), tsplit, tpart_e,
-                            sph ? readout.f() : nullptr, d_tally[buf]);
+                            sph ? readout.f() : nullptr, d_tally[buf], run_f16);
         if (keep_csplit) {
           pcents.part = tpart_e;
           pcents.nparts = (int)k;
@@ -810,7 +814,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
         ProfScope p(c, EMH_PROF_EMA, ema_bytes(k, d), prof_take(c, EMH_PROF_EMA));
         launch_ema(c, pos.f(), mass.f(), sums.f(), counts.u(), k, d, af, df, replace,
                    sph ? nullptr : readout.f(), true, d_tally[buf], true, tsplit, tpart_e, tcnt,
-                   tally ? tstride * k : 0, ema_readout ? readout.f() : nullptr);
+                   tally ? tstride * k : 0, ema_readout ? readout.f() : nullptr, run_f16);
         if (keep_csplit) {
           pcents.part = tpart_e;
           pcents.nparts = (int)ema_blocks(k);
@@ -833,7 +837,7 @@ void train_dev(emh_ctx* c, const float* x, size_t n, const emh_config& cfg,
                                         : nullptr;
             EMH_ENSURE(!keep_csplit || app + 2 * np <= tpart_end, "bound partials overflow");
             launch_split_fused(c, pos.f(), mass.f(), d_plan, np, d, k, readout.f(),
-                               keep_csplit ? tsplit : nullptr, app);
+                               keep_csplit ? tsplit : nullptr, app, run_f16);
             if (keep_csplit) pcents.nparts += (int)np;
           } else {
             launch_split(c, pos.f(), mass.f(), d_plan, np, d, true);
@@ -1508,12 +1512,15 @@ int emh_assign_dev(emh_ctx* c, const emh_buf* x, size_t n, size_t d, const emh_b
     emh::Arena ar = arena_for(c->cnorm, {metric == EMH_L2 ? k * 4 : 0});
     Buf cn(ar, metric == EMH_L2 ? k * 4 : 0);
     if (metric == EMH_L2) emh::launch_row_norms(c, (const float*)cents->ptr, k, d, cn.f());
-    // The rows' bf16 halves, when the context's last training run split these
-    // very rows and nothing has written them since.
+    // The rows' halves, when the context's last training run split these very
+    // rows, in the format the screen mode takes, and nothing has written them
+    // since.
     const emh_ctx::SplitOf& so = c->xpre_of;
     const bool reuse = so.valid && so.ptr == x->ptr && so.serial == x->serial &&
-                       so.gen == x->gen && !x->exposed && so.d == d && n <= so.n;
-    const emh::SplitRows pre{c->xpre.ptr, (const float*)c->xpre_norm.ptr, so.n, so.n * 128};
+                       so.gen == x->gen && !x->exposed && so.d == d && n <= so.n &&
+                       so.f16 == (c->screen == emh::SCREEN_F16);
+    const emh::SplitRows pre{c->xpre.ptr, (const float*)c->xpre_norm.ptr, so.n, so.n * 128,
+                             so.f16};
     for (size_t b = 0; b < n; b += chunk) {
       const size_t e = std::min(b + chunk, n);
       emh::launch_top1(c, (const float*)x->ptr, n, d, nullptr, b, e, (const float*)cents->ptr,

@@ -118,8 +118,11 @@ struct Pinned {
 };
 
 // Top-1 / top-k path (emh_set_screen): the exact kernels alone, or the MFMA
-// screen in bf16 three-pass or f32 arithmetic ahead of the exact check.
-enum ScreenMode : int { SCREEN_OFF = 0, SCREEN_BF3 = 1, SCREEN_F32 = 2 };
+// screen ahead of the exact check: bf16 three-pass (SCREEN_BF3), f32, or
+// (SCREEN_F16) fp16 two-pass on the split-operand top-1 screen with every
+// other screen in bf16 three-pass. Rows or centroids beyond |x| = 32768 make
+// the fp16 bound NaN: those rows take the exact scan.
+enum ScreenMode : int { SCREEN_OFF = 0, SCREEN_BF3 = 1, SCREEN_F32 = 2, SCREEN_F16 = 3 };
 // Top-1 calls of at most this many exact items (rows x max(ceil(k / 64), 2))
 // run the exact kernels alone by default: there one launch takes less time
 // than the screen's three (d = 768: the screen ~60 us at any size up to 8,192
@@ -195,6 +198,7 @@ struct emh_ctx {
     const void* ptr = nullptr;
     uint64_t serial = 0, gen = 0;
     size_t n = 0, d = 0;
+    bool f16 = false;  // the halves' format (emh_halves.h)
   } xpre_of;
   emh::Scratch tsplit, tsplit_part;          // a training run's centroids, kept split by the EMA
   emh::Scratch tally_cnt;                    // a training run's label tally (chunk histograms)
@@ -295,7 +299,8 @@ void launch_normalize_rows(emh_ctx* c, const float* src, size_t rows, size_t d, 
 // next top-1 may skip that fill. With tally, also adds counts into it. With
 // zero_counts, leaves counts at zero once read (the next batch's
 // launch_scatter_count adds into them). With csplit (norms needed), also
-// rewrites the bf16 halves (launch_halves' layout, k rows) of the rows it
+// rewrites the halves (launch_halves' layout, k rows; fp16 with f16, else
+// bf16) of the rows it
 // moves and leaves the bound's centroid maxima of its ema_blocks(k) blocks in
 // cpart, as launch_halves' part does. With zero_words, also clears
 // zero_words[0..nzero) (a tally's chunk histograms). With readout (spherical
@@ -306,7 +311,8 @@ void launch_ema(emh_ctx* c, float* pos, float* usage, const float* sums, const u
                 size_t k, size_t d, float alpha, float decay, int replace, float* norms = nullptr,
                 bool clear_screen_words = false, uint32_t* tally = nullptr,
                 bool zero_counts = false, void* csplit = nullptr, uint32_t* cpart = nullptr,
-                uint32_t* zero_words = nullptr, size_t nzero = 0, float* readout = nullptr);
+                uint32_t* zero_words = nullptr, size_t nzero = 0, float* readout = nullptr,
+                bool f16 = false);
 size_t ema_blocks(size_t k);
 // The masses launch_ema will leave, into out (usage untouched); with
 // small_out, also a copy of the small block's words; with seq_out, then seq
@@ -329,13 +335,14 @@ void launch_check_finite(emh_ctx* c, const float* v, size_t n, uint32_t* flag);
 void launch_split(emh_ctx* c, float* pos, float* usage, const uint32_t* pairs_dev, size_t npairs,
                   size_t d, bool independent);
 // launch_split of independent pairs that also writes the two moved rows'
-// norms (L2 readout) and, when given, their bf16 halves (csplit, k rows) and
+// norms (L2 readout) and, when given, their halves (csplit, k rows; fp16 with
+// f16, else bf16) and
 // one bound partial pair per pair (cpart[2 q], cpart[2 q + 1]); d at most
 // SPLIT_FUSED_MAX_D.
 constexpr size_t SPLIT_FUSED_MAX_D = 1024;
 void launch_split_fused(emh_ctx* c, float* pos, float* usage, const uint32_t* pairs_dev,
                         size_t npairs, size_t d, size_t k, float* norms, void* csplit,
-                        uint32_t* cpart);
+                        uint32_t* cpart, bool f16);
 void launch_gather_rows(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
                         size_t m, float* out);
 
@@ -372,7 +379,8 @@ bool update_small(size_t n, size_t d, bool spherical);
 // Labels lo .. hi tallied into counts (and tcnt, ntcnt words) by the batch's
 // top-1 call. As launch_scatter_sums (tallied) then launch_ema with
 // clear_screen_words and zero_counts: moves the centroids that got rows
-// (pos, usage; norms and, with csplit, the bf16 halves for L2 runs; readout
+// (pos, usage; norms and, with csplit, the halves for L2 runs, fp16 with f16;
+// readout
 // for spherical ones), adds the sums into acc (when given) and counts into
 // tally, and leaves counts and tcnt at zero. With csplit, cpart[2 j] =
 // cpart[2 j + 1] = norms[j] bits for every cluster j (k pairs).
@@ -380,7 +388,7 @@ void launch_update_small(emh_ctx* c, const float* x, size_t nx, size_t d, const 
                          size_t lo, size_t hi, const uint32_t* labels, size_t k, uint32_t* counts,
                          uint32_t* tcnt, size_t ntcnt, float* acc, float* pos, float* usage,
                          float alpha, float decay, int replace, float* norms, void* csplit,
-                         uint32_t* cpart, float* readout, uint32_t* tally);
+                         uint32_t* cpart, float* readout, uint32_t* tally, bool f16);
 
 // ---- emh_autok.hip (kmeans_pp and internal_scores of the automatic-k callers)
 // best[i] = max(best[i], dot(x[i], x[last])), the dot in sequence without fma.
@@ -408,6 +416,7 @@ struct SplitRows {
   const void* xs;
   const float* xn;
   size_t nx, slab;
+  bool f16 = false;  // fp16 halves (else bf16; emh_halves.h)
 };
 // Positions per chunk of scatter_add's chunked counting sort.
 constexpr int TALLY_CP = 256;
@@ -435,6 +444,7 @@ struct SplitCents {
   const void* cs;
   const uint32_t* part;
   int nparts;
+  bool f16 = false;  // fp16 halves (else bf16)
 };
 // pre: x's rows already split, pc: the centroids (used when the call takes
 // the split-operand screen; see split_screen).
@@ -456,13 +466,15 @@ bool top1_screens(emh_ctx* c, size_t n, size_t d, size_t k, bool ip);
 // Whether a top-1 call of n rows (and of any fewer) can tally the labels it
 // writes: the screen with d % 4 == 0, or the latency-bound exact scan.
 bool top1_tallies(emh_ctx* c, size_t n, size_t d, size_t k, bool ip);
-// Split rows of x (n rows, or ids[lo..lo+n)) into bf16 halves in out,
-// slab-major, with their |x|^2 in norm; with part, each of the
+// Split rows of x (n rows, or ids[lo..lo+n)) into halves in out (fp16 with
+// f16, else bf16; emh_halves.h), slab-major, with their |x|^2 in norm; with
+// part, each of the
 // halves_blocks(n) blocks leaves the largest |x|^2 of its rows and the
 // largest cnorm in part[2 b], part[2 b + 1] (emh_screen4.hip). Bytes of out:
 // halves_bytes(n, d).
 void launch_halves(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids, size_t lo,
-                   size_t n, void* out, float* norm, const float* cnorm, uint32_t* part);
+                   size_t n, void* out, float* norm, const float* cnorm, uint32_t* part,
+                   bool f16 = false);
 inline size_t halves_bytes(size_t n, size_t d) { return n * ((d + 31) / 32) * 128; }
 inline size_t halves_blocks(size_t n) { return (n + 7) / 8; }
 // out[0], out[1] = the largest part[2 i], part[2 i + 1] over i < nparts (f32

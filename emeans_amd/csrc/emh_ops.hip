@@ -271,7 +271,7 @@ __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __r
                                              char* __restrict__ csplit,
                                              uint32_t* __restrict__ cpart,
                                              uint32_t* __restrict__ zero_words, size_t nzero,
-                                             float* __restrict__ readout) {
+                                             float* __restrict__ readout, int f16) {
   // EC rows of min(d, ECH) + 4 floats (norms, or readout): the rounded
   // squares; with csplit or readout, then as many for the values.
   extern __shared__ __attribute__((aligned(16))) float sq[];
@@ -349,7 +349,7 @@ __global__ __launch_bounds__(256) void k_ema(float* __restrict__ pos, float* __r
                                       t + 2 < len ? vr[t + 2] : 0.0f,
                                       t + 3 < len ? vr[t + 3] : 0.0f);
         uint2 hi, lw;
-        split_quad(v4, hi, lw);
+        split_quad(v4, hi, lw, f16 != 0);
         const size_t col = c0 + (size_t)t;
         char* o = csplit + ((col >> 5) * k + j0 + cc) * SLAB_BYTES + quad_hi_offset((int)(col & 31) >> 2);
         *reinterpret_cast<uint2*>(o) = hi;
@@ -544,7 +544,7 @@ __global__ __launch_bounds__(256) void k_split_fused(float* __restrict__ pos,
                                                      const uint32_t* __restrict__ pairs, size_t d,
                                                      size_t k, float* __restrict__ norms,
                                                      char* __restrict__ csplit,
-                                                     uint32_t* __restrict__ cpart) {
+                                                     uint32_t* __restrict__ cpart, int f16) {
   extern __shared__ __attribute__((aligned(16))) float sl[];
   __shared__ int diff;
   __shared__ float nv[2];
@@ -602,7 +602,7 @@ __global__ __launch_bounds__(256) void k_split_fused(float* __restrict__ pos,
                                     c4 + 2 < len ? vr[c4 + 2] : 0.0f,
                                     c4 + 3 < len ? vr[c4 + 3] : 0.0f);
       uint2 hv, lv;
-      split_quad(v4, hv, lv);
+      split_quad(v4, hv, lv, f16 != 0);
       char* o = csplit + ((size_t)(c4 >> 5) * k + (r ? t : s)) * SLAB_BYTES +
                 quad_hi_offset((c4 & 31) >> 2);
       *reinterpret_cast<uint2*>(o) = hv;
@@ -667,7 +667,7 @@ void launch_normalize_rows(emh_ctx* c, const float* src, size_t rows, size_t d, 
 void launch_ema(emh_ctx* c, float* pos, float* usage, const float* sums, const uint32_t* counts,
                 size_t k, size_t d, float alpha, float decay, int replace, float* norms,
                 bool clear_screen_words, uint32_t* tally, bool zero_counts, void* csplit,
-                uint32_t* cpart, uint32_t* zero_words, size_t nzero, float* readout) {
+                uint32_t* cpart, uint32_t* zero_words, size_t nzero, float* readout, bool f16) {
   if (k == 0) return;
   EMH_ENSURE(!csplit || (norms && cpart), "ema: the centroid halves need the norms and maxima");
   EMH_ENSURE(!readout || (!norms && !csplit && d <= (size_t)ECH),
@@ -678,7 +678,8 @@ void launch_ema(emh_ctx* c, float* pos, float* usage, const float* sums, const u
   hipLaunchKernelGGL(k_ema, grid1(k, EC), dim3(256), lds, c->stream, pos, usage, sums, counts, k,
                      d, alpha, decay, replace, norms, clear_screen_words ? c->small : nullptr,
                      tally, zero_counts ? const_cast<uint32_t*>(counts) : nullptr,
-                     (char*)csplit, cpart, zero_words, zero_words ? nzero : 0, readout);
+                     (char*)csplit, cpart, zero_words, zero_words ? nzero : 0, readout,
+                     f16 ? 1 : 0);
   EMH_HIP(hipGetLastError());
 }
 
@@ -727,12 +728,12 @@ void launch_check_finite(emh_ctx* c, const float* v, size_t n, uint32_t* flag) {
 
 void launch_split_fused(emh_ctx* c, float* pos, float* usage, const uint32_t* pairs_dev,
                         size_t npairs, size_t d, size_t k, float* norms, void* csplit,
-                        uint32_t* cpart) {
+                        uint32_t* cpart, bool f16) {
   if (npairs == 0) return;
   EMH_ENSURE(d >= 1 && d <= SPLIT_FUSED_MAX_D && norms, "split_fused: shape out of range");
   const size_t lds = 4 * (size_t)ema_row((int)d) * sizeof(float);
   hipLaunchKernelGGL(k_split_fused, dim3((unsigned)npairs), dim3(256), lds, c->stream, pos, usage,
-                     pairs_dev, d, k, norms, (char*)csplit, cpart);
+                     pairs_dev, d, k, norms, (char*)csplit, cpart, f16 ? 1 : 0);
   EMH_HIP(hipGetLastError());
 }
 

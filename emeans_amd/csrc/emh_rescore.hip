@@ -108,7 +108,7 @@ __global__ __launch_bounds__(256) void k_verify(
     int nrows, const float* __restrict__ cents, const float* __restrict__ cnorm, int k, int ip,
     int kk, const Cand* __restrict__ cand, int parts, const float* __restrict__ xnorm,
     uint32_t* __restrict__ labels, float* __restrict__ scores, uint32_t* __restrict__ fb,
-    uint32_t* __restrict__ small, int bf3) {
+    uint32_t* __restrict__ small, int bound) {
   constexpr int PMAX = R * (KNN ? L : C1 + 1);  // pairs (+ the |x|^2 chain per top-1 row)
   __shared__ Cand cst[R * MAX_PARTS * L];
   __shared__ uint32_t prow[PMAX], pcid[PMAX];
@@ -168,7 +168,7 @@ __global__ __launch_bounds__(256) void k_verify(
     int state = 0, nc = 0;
     if (rowid[tid] != NONE) {
       const float E = screen_bound(xnorm[r0 + tid], __uint_as_float(small[SW_CMAX2]),
-                                   __uint_as_float(small[SW_CNMAX]), d, l2, bf3 != 0, bf3 == 2);
+                                   __uint_as_float(small[SW_CNMAX]), d, l2, bound);
       bool complete;
       if (KNN) {
         thr = key[kk - 1] + 2.0f * E;
@@ -372,7 +372,7 @@ __global__ __launch_bounds__(256) void k_check1(
     int nrows, const float* __restrict__ cents, const float* __restrict__ cnorm, int ip,
     const Cand* __restrict__ cand, int parts, const float* __restrict__ xnorm,
     uint32_t* __restrict__ labels, float* __restrict__ scores, uint32_t* __restrict__ fb,
-    uint32_t* __restrict__ small, int bf3, uint32_t* __restrict__ tcnt,
+    uint32_t* __restrict__ small, int bound, uint32_t* __restrict__ tcnt,
     uint32_t* __restrict__ tcounts, size_t tlo, size_t tstride) {
   __shared__ v4f stage[2][CSLOT * CDP4];
   __shared__ uint32_t xrow[CR];  // x row of each settled row, NONE otherwise
@@ -426,7 +426,7 @@ __global__ __launch_bounds__(256) void k_check1(
     int cj = 0, cert = 1;
     if (vrow) {
       const float E = screen_bound(xn, __uint_as_float(small[SW_CMAX2]),
-                                   __uint_as_float(small[SW_CNMAX]), d, l2, bf3 != 0, bf3 == 2);
+                                   __uint_as_float(small[SW_CNMAX]), d, l2, bound);
       const float thr = best + 2.0f * E;
 #pragma unroll
       for (int e = 0; e < L; e++)
@@ -697,14 +697,15 @@ __global__ __launch_bounds__(256) void k_margin(
   const float kx = ip ? -acc : cnorm[cd.id] - 2.0f * acc;
   float edot = 0.f;
   const float E = screen_bound(xnorm[r], __uint_as_float(small[SW_CMAX2]),
-                               __uint_as_float(small[SW_CNMAX]), d, !ip, bound != 0, bound == 2,
-                               &edot);
+                               __uint_as_float(small[SW_CNMAX]), d, !ip, bound, &edot);
   if (!isfinite(kx) || !isfinite(E) || !(E > 0.f) || !(edot > 0.f)) return;
   const float dk = fabsf(cd.key - kx);
   const float ratio = dk / E;
   const float u = 5.9604645e-08f;
   const float allow = (ip ? 0.f : 1.0000002f * u * (fabsf(cd.key) + fabsf(kx))) +
-                      (bound == 2 ? 7.63e-6f * fabsf(cd.key) + 8.9e-44f : 0.f);
+                      (bound == BOUND_BF16_TAGGED || bound == BOUND_F16_TAGGED
+                           ? 7.63e-6f * fabsf(cd.key) + 8.9e-44f
+                           : 0.f);
   const float dot_ratio = fmaxf(dk - allow, 0.f) / ((ip ? 1.0f : 2.0f) * edot);
   atomicAdd(&out[0], 1ull);
   if (ratio > 1.0f) atomicAdd(&out[1], 1ull);
@@ -747,25 +748,24 @@ void launch_margin(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32
 void launch_verify1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
                     size_t lo, size_t n, const float* cents, const float* cnorm, size_t k, bool ip,
                     const Cand* cand, int parts, const float* xnorm, uint32_t* labels,
-                    float* scores, uint32_t* fb, bool tagged, const LabelTally* tally, int L) {
+                    float* scores, uint32_t* fb, int bound, const LabelTally* tally, int L) {
   const dim3 g((unsigned)((n + R1 - 1) / R1));
-  // The bound follows the screen's arithmetic: 0 f32, 1 bf16, 2 bf16 with tagged keys.
-  const int bf3 = c->screen == SCREEN_F32 ? 0 : tagged ? 2 : 1;
   static_assert(TALLY_CP % CR == 0, "a check block's rows lie in one tally chunk");
   EMH_ENSURE(!tally || (d % 4 == 0 && lo >= tally->lo && (lo - tally->lo) % TALLY_CP == 0),
              "check: a tally needs d %% 4 == 0 and chunk-aligned positions");
-  EMH_ENSURE(L == L1 || (L == L1S && d % 4 == 0), "check: lists of %d entries", L);
+  EMH_ENSURE(L == L1 || L == L1F || (L == L1S && d % 4 == 0), "check: lists of %d entries", L);
   if (d % 4 == 0)
-    hipLaunchKernelGGL(L == L1S ? k_check1<L1S> : k_check1<L1>,
+    hipLaunchKernelGGL(L == L1S ? k_check1<L1S> : L == L1F ? k_check1<L1F> : k_check1<L1>,
                        dim3((unsigned)((n + CR - 1) / CR)), dim3(256), 0, c->stream, x,
                        nx, (int)d, ids, lo, (int)n, cents, cnorm, ip ? 1 : 0, cand, parts, xnorm,
-                       labels, scores, fb, c->small, bf3, tally ? tally->cnt : nullptr,
+                       labels, scores, fb, c->small, bound, tally ? tally->cnt : nullptr,
                        tally ? tally->counts : nullptr, tally ? tally->lo : 0,
                        tally ? tally->stride : 0);
   else
-    hipLaunchKernelGGL((k_verify<L1, R1, false, false>), g, dim3(256), 0, c->stream, x, nx,
-                       (int)d, ids, lo, (int)n, cents, cnorm, (int)k, ip ? 1 : 0, 1, cand, parts,
-                       xnorm, labels, scores, fb, c->small, bf3);
+    hipLaunchKernelGGL((L == L1F ? k_verify<L1F, R1, false, false> : k_verify<L1, R1, false, false>),
+                       g, dim3(256), 0, c->stream, x, nx, (int)d, ids, lo, (int)n, cents, cnorm,
+                       (int)k, ip ? 1 : 0, 1, cand, parts, xnorm, labels, scores, fb, c->small,
+                       bound);
   EMH_HIP(hipGetLastError());
 }
 
@@ -773,15 +773,15 @@ void launch_verifyk(emh_ctx* c, const float* q, size_t m, const float* data, siz
                     size_t kk, const Cand* cand, int parts, const float* xnorm, uint32_t* ids,
                     float* sims, uint32_t* fb) {
   const dim3 g((unsigned)((m + RK - 1) / RK));
-  const int bf3 = c->screen != SCREEN_F32;
+  const int bound = c->screen == SCREEN_F32 ? BOUND_F32 : BOUND_BF16;
   if (d % 4 == 0)
     hipLaunchKernelGGL((k_verify<LK, RK, true, true>), g, dim3(256), 0, c->stream, q, m, (int)d,
                        nullptr, (size_t)0, (int)m, data, nullptr, (int)n, 1, (int)kk, cand, parts,
-                       xnorm, ids, sims, fb, c->small, bf3);
+                       xnorm, ids, sims, fb, c->small, bound);
   else
     hipLaunchKernelGGL((k_verify<LK, RK, true, false>), g, dim3(256), 0, c->stream, q, m,
                        (int)d, nullptr, (size_t)0, (int)m, data, nullptr, (int)n, 1, (int)kk,
-                       cand, parts, xnorm, ids, sims, fb, c->small, bf3);
+                       cand, parts, xnorm, ids, sims, fb, c->small, bound);
   EMH_HIP(hipGetLastError());
 }
 

@@ -39,7 +39,7 @@
 namespace emh {
 namespace {
 
-// The 128 x 128 screens in the context's arithmetic (SCREEN_BF3 or SCREEN_F32).
+// The 128 x 128 screens in the context's arithmetic (f32 in SCREEN_F32, else bf16).
 void launch_screen_t1(emh_ctx* c, const ScreenArgs& a, bool ip) {
   if (c->screen == SCREEN_F32)
     launch_screen_t1_f32(c, a, ip);
@@ -64,7 +64,7 @@ int choose_parts(int row_tiles, int ntiles, int cus, int per_cu = 2) {
 
 namespace {
 // The screen's launch geometry for n rows against k centroids. split: the
-// call may take the split-operand screen (k_screen4: bf16 arithmetic, k >= 64
+// call may take the split-operand screen (k_screen4: fp16 or bf16, k >= 64
 // and at most MAX_PARTS tiles of 256 centroids, one tile per part with
 // tagged keys; any d >= 32). Otherwise (and for the no-allocation entry, which
 // has no room to split a selection) the large-tile screen that splits its
@@ -143,8 +143,13 @@ struct Top1Screen {
   uint32_t* fb = nullptr;
   float* xnorm = nullptr;
   bool tagged = false;
-  int L = L1;  // entries per part list: L1S for the sorted insert's lists
+  bool f16 = false;  // the split-operand screen ran in fp16 two-pass arithmetic
+  int L = L1;  // entries per part list: L1S for the sorted insert's, L1F for the fp16 screen's
 };
+
+// The split-operand screen's arithmetic: fp16 two-pass in SCREEN_F16, else
+// bf16 three-pass.
+bool split_f16(const emh_ctx* c) { return c->screen == SCREEN_F16; }
 
 Top1Screen screen_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
                        size_t lo, size_t n, const float* cents, const float* cnorm, size_t k,
@@ -154,7 +159,8 @@ Top1Screen screen_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const ui
   s.g = top1_geom(c, n, d, k, ip, !ar, small_exact);
   if (!s.g.screen) return s;
   const Top1Geom& g = s.g;
-  const size_t cbytes = (size_t)g.parts * n * L1 * sizeof(Cand);
+  const bool f16 = g.split && split_f16(c);
+  const size_t cbytes = (size_t)g.parts * n * (f16 ? L1F : L1) * sizeof(Cand);
   s.cand = (Cand*)(ar ? ar->take(cbytes) : c->cand.get(cbytes));
   s.fb = (uint32_t*)(ar ? ar->take(n * 4) : c->fblist.get(n * 4));
   s.xnorm = (float*)(ar ? ar->take(n * 4) : c->xnorm.get(n * 4));
@@ -162,11 +168,14 @@ Top1Screen screen_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const ui
     launch_fill_u32(c, c->small, 3, 0);
   const unsigned blocks = (unsigned)(g.row_tiles * g.parts);
   s.tagged = g.big && g.tpp == 1;
-  s.L = g.big && !s.tagged ? L1S : L1;
+  s.L = f16 ? L1F : g.big && !s.tagged ? L1S : L1;
   if (g.split) {
     // The centroids' halves and the bound's centroid maxima (the caller's,
     // split ahead, or split here), then the rows' halves (the caller's, or
-    // this selection's).
+    // this selection's), all in the call's format.
+    EMH_ENSURE(!pre || pre->f16 == f16, "top1: rows split in the other format");
+    EMH_ENSURE(!pc || pc->f16 == f16, "top1: centroids split in the other format");
+    s.f16 = f16;
     const void* cs;
     const uint32_t* part;
     int nparts;
@@ -178,14 +187,14 @@ Top1Screen screen_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const ui
       void* cw = c->csplit.get(halves_bytes(k, d));
       uint32_t* pw = (uint32_t*)c->csplit_part.get(halves_blocks(k) * 8);
       launch_halves(c, cents, k, d, nullptr, 0, k, cw, (float*)c->csplit_norm.get(k * 4),
-                    ip ? nullptr : cnorm, pw);
+                    ip ? nullptr : cnorm, pw, f16);
       cs = cw;
       part = pw;
       nparts = (int)halves_blocks(k);
     }
     Screen4Args a{blocks,   nullptr,  0,      nullptr, 0,       d,       nullptr,
                   0,        n,        cs,     k * 128, cnorm,   k,       1,
-                  g.parts,  g.ntiles, s.cand, s.xnorm, part,    nparts};
+                  g.parts,  g.ntiles, s.cand, s.xnorm, part,    nparts,  f16};
     if (pre) {
       a.xs = pre->xs;
       a.xslab = pre->slab;
@@ -195,7 +204,7 @@ Top1Screen screen_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const ui
       a.lo = lo;
     } else {
       void* xs = c->xsplit.get(halves_bytes(n, d));
-      launch_halves(c, x, nx, d, ids, lo, n, xs, s.xnorm, nullptr, nullptr);
+      launch_halves(c, x, nx, d, ids, lo, n, xs, s.xnorm, nullptr, nullptr, f16);
       a.xs = xs;
       a.xslab = n * 128;
       a.xn = s.xnorm;
@@ -219,8 +228,12 @@ Top1Screen screen_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const ui
   return s;
 }
 
-// The check's bound arithmetic: 0 f32 screen, 1 bf16, 2 bf16 with tagged keys.
-int bound_kind(emh_ctx* c, bool tagged) { return c->screen == SCREEN_F32 ? 0 : tagged ? 2 : 1; }
+// The check's bound arithmetic: the screen's (BoundKind).
+int bound_kind(const emh_ctx* c, const Top1Screen& s) {
+  if (c->screen == SCREEN_F32) return BOUND_F32;
+  if (s.f16) return BOUND_F16_TAGGED;
+  return s.tagged ? BOUND_BF16_TAGGED : BOUND_BF16;
+}
 }  // namespace
 
 void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids, size_t lo,
@@ -244,7 +257,7 @@ void launch_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t
     return;
   }
   launch_verify1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, s.cand, s.g.parts, s.xnorm, labels,
-                 scores, s.fb, s.tagged, tally, s.L);
+                 scores, s.fb, bound_kind(c, s), tally, s.L);
   launch_exact1(c, x, nx, d, ids, lo, n, s.fb, cents, cnorm, k, ip, labels, scores, ar, tally);
 }
 
@@ -259,12 +272,13 @@ void screen_margin_top1(emh_ctx* c, const float* x, size_t nx, size_t d, const u
       screen_top1(c, x, nx, d, ids, lo, n, cents, cnorm, k, ip, false, nullptr, nullptr, nullptr,
                   false);
   if (!s.g.screen) return;  // variant 0: no screen, nothing to measure
-  out->variant = s.g.big ? (s.tagged ? EMH_SCREEN_BIG_TAGGED : EMH_SCREEN_BIG_SORTED)
-                         : (c->screen == SCREEN_F32 ? EMH_SCREEN_SMALL_F32 : EMH_SCREEN_SMALL_BF16);
+  out->variant = s.f16     ? EMH_SCREEN_BIG_F16
+                 : s.g.big ? (s.tagged ? EMH_SCREEN_BIG_TAGGED : EMH_SCREEN_BIG_SORTED)
+                           : (c->screen == SCREEN_F32 ? EMH_SCREEN_SMALL_F32 : EMH_SCREEN_SMALL_BF16);
   out->parts = s.g.parts;
   out->tiles_per_part = s.g.tpp;
   launch_margin(c, x, nx, d, ids, lo, n, cents, cnorm, ip, s.cand, s.g.parts, s.L, s.xnorm,
-                bound_kind(c, s.tagged), out);
+                bound_kind(c, s), out);
 }
 
 void launch_topk(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,
@@ -287,8 +301,8 @@ void launch_topk(emh_ctx* c, const float* q, size_t m, const float* data, size_t
       rep->variant = EMH_SCREEN_BIG_KNN;
       rep->parts = parts;
       rep->tiles_per_part = 0;
-      launch_margin(c, q, m, d, nullptr, 0, m, data, nullptr, true, cand, parts, LK, xnorm, 1,
-                    rep);
+      launch_margin(c, q, m, d, nullptr, 0, m, data, nullptr, true, cand, parts, LK, xnorm,
+                    BOUND_BF16, rep);
       return;
     }
     uint32_t* fb = (uint32_t*)c->fblist.get(m * 4);
@@ -325,7 +339,7 @@ void launch_topk(emh_ctx* c, const float* q, size_t m, const float* data, size_t
     rep->parts = parts;
     rep->tiles_per_part = tpp;
     launch_margin(c, q, m, d, nullptr, 0, m, data, nullptr, true, cand, parts, LK, xnorm,
-                  c->screen != SCREEN_F32 ? 1 : 0, rep);
+                  c->screen != SCREEN_F32 ? BOUND_BF16 : BOUND_F32, rep);
     return;
   }
   launch_verifyk(c, q, m, data, n, d, kk, cand, parts, xnorm, ids, sims, fb);

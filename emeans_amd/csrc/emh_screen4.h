@@ -1,6 +1,6 @@
-// The large-tile bf16 top-1 screen over operands split ahead of time
-// (k_screen4), and the kernel that splits rows or centroids into bf16 halves
-// (k_halves). Shared by emh_screen4.hip (launchers) and nothing else.
+// The large-tile top-1 screen over operands split ahead of time (k_screen4),
+// and the kernel that splits rows or centroids into halves (k_halves).
+// Shared by emh_screen4.hip (launchers) and nothing else.
 //
 // k_screen3 splits every slab it stages (f32 loads, three conversions per
 // element, LDS stores), once per row tile and centroid part, and runs its
@@ -18,8 +18,11 @@
 //    one line;
 //  - a step's DMAs for the next slab go out between its groups of MFMAs, so
 //    one wave's loads are issued while the other wave on its SIMD runs MFMAs.
-// The MFMA sequence per accumulator (per 16 dimensions: hi.hi, hi.lo, lo.hi)
-// is k_screen3's, so the keys are the same; the error bound is unchanged.
+// Two arithmetics, by the halves' format: bf16 three-pass (per 16 dimensions
+// hi.hi, hi.lo, lo.hi: k_screen3's sequence, so the same keys and bound) and
+// fp16 two-pass (centroid hi against row hi, then row lo: a third fewer
+// MFMAs and operand reads, within a bound 2.7 times the bf16 one at d = 768;
+// the centroids' lo halves are not read).
 #pragma once
 
 #include <type_traits>
@@ -94,7 +97,8 @@ __device__ __forceinline__ void load32(const float* p, int col, int d, float (&v
 }
 
 // Split rows ids[lo + g] (lo + g without ids; an id >= nx reads row 0) for
-// g < n into out, in selection order and slab-major: slab j of row g at
+// g < n into out (fp16 halves when f16, else bf16), in selection order and
+// slab-major: slab j of row g at
 // out + (j n + g) 128 bytes. norm[g] = the row's |x|^2 (f32, summed in any
 // order: the screen bound's input). With part: block b writes the largest
 // |x|^2 of its rows and, with cnorm, the largest cnorm[g] (f32 bits; a NaN or
@@ -111,7 +115,7 @@ __global__ __launch_bounds__(256) void k_halves(const float* __restrict__ x, siz
                                                 size_t n, char* __restrict__ out,
                                                 float* __restrict__ norm,
                                                 const float* __restrict__ cnorm,
-                                                uint32_t* __restrict__ part) {
+                                                uint32_t* __restrict__ part, int f16) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int d32 = (d + 31) >> 5, nseg = (d32 + 7) >> 3;
   const int js = lane >> 3, c4 = lane & 7;
@@ -155,7 +159,7 @@ __global__ __launch_bounds__(256) void k_halves(const float* __restrict__ x, siz
       sq[i] = fmaf(v[i].z, v[i].z, sq[i]);
       sq[i] = fmaf(v[i].w, v[i].w, sq[i]);
       uint2 hi, lw;
-      split_quad(v[i], hi, lw);
+      split_quad(v[i], hi, lw, f16 != 0);
       if (valid[i]) {
         char* o = out + ((size_t)j * n + g[i]) * SLAB_BYTES + hoff;
         *reinterpret_cast<uint2*>(o) = hi;
@@ -204,7 +208,7 @@ using StageNo = std::integral_constant<int, I>;
 // s % 2. Step s waits for its own DMAs, passes a barrier (every wave's DMAs of
 // step s are in, and every wave is done with stage (s + 1) % 2), then runs
 // its MFMAs while it issues the DMAs of step s + 1 into the other stage.
-template <int L, bool L2, int NW>
+template <int L, bool L2, int NW, bool F16>
 __global__ __launch_bounds__(NW * 64, 1) void k_screen4(
     const char* __restrict__ xs, size_t xslab, const float* __restrict__ xn, size_t nx, int d,
     const uint32_t* __restrict__ ids, size_t lo, int nrows, const char* __restrict__ cs,
@@ -281,24 +285,26 @@ __global__ __launch_bounds__(NW * 64, 1) void k_screen4(
   // half h takes dimensions 16 kk + 8 h .. + 7 (chunk 4 kk + h of the hi
   // half, 4 kk + 2 + h of the lo half).
   const int sw = swz(li);  // rows wr * RW + y * 32 + li: swz(row) = sw
+  // Operand registers: 8 halves of one format (fp16 or bf16).
+  typedef std::conditional_t<F16, v8h, v8bf> Op;
   struct Rows {
-    v8bf bh[WN], bl[WN];
+    Op bh[WN], bl[WN];
   };
   auto read_rows = [&](const char* X, int kk, Rows& o) __attribute__((always_inline)) {
     const int oh = ((4 * kk + h) ^ sw) << 4, ol = ((4 * kk + 2 + h) ^ sw) << 4;
 #pragma unroll
     for (int y = 0; y < WN; y++) {
       const char* p = X + (wr * RW + y * 32 + li) * SLAB_BYTES;
-      o.bh[y] = *reinterpret_cast<const v8bf*>(p + oh);
-      o.bl[y] = *reinterpret_cast<const v8bf*>(p + ol);
+      o.bh[y] = *reinterpret_cast<const Op*>(p + oh);
+      o.bl[y] = *reinterpret_cast<const Op*>(p + ol);
     }
   };
-  v8bf ah[WA], al[WA];  // centroid operands: each refreshed right after its MFMAs
+  Op ah[WA], al[WA];  // centroid operands: each refreshed right after its MFMAs (al: bf16)
   auto read_cent = [&](const char* X, int kk, int a) __attribute__((always_inline)) {
     const int oh = ((4 * kk + h) ^ sw) << 4, ol = ((4 * kk + 2 + h) ^ sw) << 4;
     const char* p = X + S4_HALF + (wc * 128 + a * 32 + li) * SLAB_BYTES;
-    ah[a] = *reinterpret_cast<const v8bf*>(p + oh);
-    al[a] = *reinterpret_cast<const v8bf*>(p + ol);
+    ah[a] = *reinterpret_cast<const Op*>(p + oh);
+    if (!F16) al[a] = *reinterpret_cast<const Op*>(p + ol);
   };
 
   float lkey[WN][L];  // per-row lists, filled by the fold after the loop
@@ -343,7 +349,8 @@ __global__ __launch_bounds__(NW * 64, 1) void k_screen4(
         const size_t id = ids ? (size_t)ids[p] : p;
         xv = xn[id < nx ? id : 0];
       }
-      thr_e[y] = 2.0f * 1.0078125f * screen_bound(xv, cm2, cnm, d, L2, true, true);
+      thr_e[y] = 2.0f * 1.0078125f *
+                 screen_bound(xv, cm2, cnm, d, L2, F16 ? BOUND_F16_TAGGED : BOUND_BF16_TAGGED);
     }
   }
   auto threshold = [&](float m, int y) __attribute__((always_inline)) {
@@ -423,16 +430,23 @@ __global__ __launch_bounds__(NW * 64, 1) void k_screen4(
   };
 
   constexpr int PER = 2 * ND + (L2 ? 1 : 0);  // DMAs per step per wave
+  auto mfma = [](const Op& p, const Op& q, const v16f& c) __attribute__((always_inline)) {
+    if constexpr (F16)
+      return __builtin_amdgcn_mfma_f32_32x32x16_f16(p, q, c, 0, 0, 0);
+    else
+      return __builtin_amdgcn_mfma_f32_32x32x16_bf16(p, q, c, 0, 0, 0);
+  };
+  // One centroid block's MFMAs of a 16-dimension step: hi.hi, hi.lo, then
+  // (bf16) lo.hi.
   auto mfma6 = [&](int a, const Rows& b) __attribute__((always_inline)) {
 #pragma unroll
-    for (int y = 0; y < WN; y++)
-      acc[a][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[a], b.bh[y], acc[a][y], 0, 0, 0);
+    for (int y = 0; y < WN; y++) acc[a][y] = mfma(ah[a], b.bh[y], acc[a][y]);
 #pragma unroll
-    for (int y = 0; y < WN; y++)
-      acc[a][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[a], b.bl[y], acc[a][y], 0, 0, 0);
+    for (int y = 0; y < WN; y++) acc[a][y] = mfma(ah[a], b.bl[y], acc[a][y]);
+    if constexpr (!F16) {
 #pragma unroll
-    for (int y = 0; y < WN; y++)
-      acc[a][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[a], b.bh[y], acc[a][y], 0, 0, 0);
+      for (int y = 0; y < WN; y++) acc[a][y] = mfma(al[a], b.bh[y], acc[a][y]);
+    }
   };
   // Prologue: steps 0 and 1 into stages 0 and 1; step 0's first operands.
 #pragma unroll

@@ -1,5 +1,6 @@
-// Instantiations of the split-operand large-tile screen (k_screen4) and the
-// kernel that splits rows into bf16 halves (k_halves).
+// Instantiations of the split-operand large-tile screen (k_screen4: fp16
+// two-pass or bf16 three-pass) and the kernel that splits rows into halves
+// (k_halves).
 #include <algorithm>
 
 #include "emh_screen4.h"
@@ -11,7 +12,8 @@ void launch_screen4(emh_ctx* c, const Screen4Args& a, bool ip) {
   // and keeps one tile per part.
   EMH_ENSURE(a.nx < (1u << 25) && a.k < (1u << 25), "screen: more than 2^25 rows or centroids");
   EMH_ENSURE(a.tpp == 1 && a.parts == a.ntiles, "screen: one tile per part");
-  auto kern = ip ? k_screen4<L1, false, 8> : k_screen4<L1, true, 8>;
+  auto kern = a.f16 ? (ip ? k_screen4<L1F, false, 8, true> : k_screen4<L1F, true, 8, true>)
+                    : (ip ? k_screen4<L1, false, 8, false> : k_screen4<L1, true, 8, false>);
   hipLaunchKernelGGL(kern, dim3(a.blocks), dim3(512), 0, c->stream, (const char*)a.xs, a.xslab,
                      a.xn, a.nx, (int)a.d, a.ids, a.lo, (int)a.n, (const char*)a.cs, a.cslab,
                      a.cnorm, (int)a.k, a.tpp, a.parts, a.ntiles, a.cand, a.xnorm, a.part,
@@ -61,12 +63,13 @@ void launch_part_max(emh_ctx* c, const uint32_t* part, size_t nparts, uint32_t* 
 }
 
 void launch_halves(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids, size_t lo,
-                   size_t n, void* out, float* norm, const float* cnorm, uint32_t* part) {
+                   size_t n, void* out, float* norm, const float* cnorm, uint32_t* part,
+                   bool f16) {
   if (n == 0) return;
   EMH_ENSURE(d >= 1 && n < (1u << 31), "halves: shape out of range");
   auto kern = d % 4 == 0 ? k_halves<true> : k_halves<false>;
   hipLaunchKernelGGL(kern, dim3((unsigned)halves_blocks(n)), dim3(256), 0, c->stream, x, nx,
-                     (int)d, ids, lo, n, (char*)out, norm, cnorm, part);
+                     (int)d, ids, lo, n, (char*)out, norm, cnorm, part, f16 ? 1 : 0);
   EMH_HIP(hipGetLastError());
 }
 

@@ -124,7 +124,7 @@ __global__ __launch_bounds__(512, 1) void k_screen4kn(
     if (blockIdx.x == 0 && tid == 0) small[SW_CMAX2] = ma;
     const float cm2 = __uint_as_float(ma);
     const float xv = qown < (uint32_t)m ? qn[qown] : 0.f;
-    thr_e = 2.0f * 1.0078125f * screen_bound(xv, cm2, 0.f, d, false, true, false);
+    thr_e = 2.0f * 1.0078125f * screen_bound(xv, cm2, 0.f, d, false, BOUND_BF16);
   }
 
   float lkey[L];
@@ -339,8 +339,9 @@ __global__ __launch_bounds__(512, 1) void k_screen4kn(
 }  // namespace
 
 bool screen4kn_fits(emh_ctx* c, size_t m, size_t n, size_t d) {
-  return c->screen == SCREEN_BF3 && d >= 32 && m >= 256 && n >= 512 && m < (1u << 25) &&
-         n < (1u << 25);
+  // (bf16 three-pass in every mode but SCREEN_OFF and SCREEN_F32)
+  return c->screen != SCREEN_OFF && c->screen != SCREEN_F32 && d >= 32 && m >= 256 && n >= 512 &&
+         m < (1u << 25) && n < (1u << 25);
 }
 
 int screen4kn(emh_ctx* c, const float* q, size_t m, const float* data, size_t n, size_t d,

@@ -18,6 +18,7 @@ constexpr int LDK = BK + 4;  // f32 screen: padded LDS row (floats), conflict-fr
 
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
 // Work item of block `bid` of `nb`: blocks are dealt round-robin to the 8 XCDs
 // (consecutive ids land on different XCDs), so number each XCD's blocks
@@ -849,6 +850,7 @@ struct Screen4Args {
   float* xnorm;
   const uint32_t* part;  // the centroid split's per-block maxima (launch_halves' part)
   int nparts;
+  bool f16;  // both operands in fp16 halves: the two-pass screen (else bf16, three passes)
 };
 void launch_screen4(emh_ctx* c, const Screen4Args& a, bool ip);
 // The 128 x 128 top-1 screen (emh_screen_t1_{bf3,f32}.hip) and the kNN screen

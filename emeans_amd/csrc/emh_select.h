@@ -10,6 +10,7 @@ namespace emh {
 constexpr uint32_t NONE = 0xffffffffu;
 constexpr int L1 = 6;    // top-1: the smallest screen keys each part keeps
 constexpr int L1S = 5;   // ... with the sorted insert (parts of several 256-centroid tiles)
+constexpr int L1F = 10;  // ... on the fp16 two-pass screen (its bound admits more near-ties)
 constexpr int C1 = 16;   // top-1: most candidates a row sends to the exact chains
 constexpr int LK = 24;   // top-k list: kk <= 16 plus 7 spare + the bound
 constexpr int KMAX = 16;  // largest kk of the screened top-k (emeans-core/src/knn.rs:16)
@@ -70,6 +71,14 @@ __device__ __forceinline__ void insert_nb(float (&key)[L], uint32_t (&id)[L], fl
   id[0] = c[0] ? j : id[0];
 }
 
+// The screens' arithmetic, as the bound follows it.
+enum BoundKind : int {
+  BOUND_F32 = 0,         // f32 MFMA screen
+  BOUND_BF16 = 1,        // bf16 three-pass screen
+  BOUND_BF16_TAGGED = 2, // the same with tagged keys (k_screen4, k_screen3 one tile per part)
+  BOUND_F16_TAGGED = 3,  // fp16 two-pass screen with tagged keys (k_screen4 on fp16 halves)
+};
+
 // Screen error bound E on |key' - key| for one row (see emh_screen.hip):
 // xn and cmax2 are squared norms summed in any order (relative error <= gamma_d,
 // absorbed by the (1 + g) factors); cnmax bounds the given centroid norms.
@@ -78,19 +87,25 @@ __device__ __forceinline__ void insert_nb(float (&key)[L], uint32_t (&id)[L], fl
 //   f32 screen: the MFMA's sum in any order, taken at 2 gamma_d S, with a
 //   denormal-flush floor of d 2^-124, and 2^-126 sqrt(d) (|x| + cmax) for
 //   elements below 2^-126 that the MFMA may take as zero;
-//   bf16 screen (bf3): the split (x ~ xh + xl, c ~ ch + cl, the xl.cl product
+//   bf16 screen: the split (x ~ xh + xl, c ~ ch + cl, the xl.cl product
 //   dropped): <= 3.05 * 2^-16 S, plus 2^-133 per element in the bf16
 //   subnormal range, <= 2^-133 sqrt(d) (|x| + cmax) for the three products;
-//   the MFMA accumulation: M = 6 ceil(d / 32) MFMAs in a chain, each within
-//   16 u (|C| + sum |p|) (v_mfma_f32_32x32x16_bf16 rounds each product to a
-//   2^-26 grid relative to the largest term, then rounds the sum once:
-//   <= 5.25 u; measured <= 4.9 u), so <= gamma(16 M) * 1.02 S (the three
-//   passes' |products| sum to <= 1.02 S); underflow: (3d + M) 2^-124.
+//   fp16 screen (xh.ch + xl.ch, fp16 halves as emh_halves.h states, products
+//   exact in f32): per element |x||c - ch| + |ch||x - xh - xl| <=
+//   (2^-11 + 2^-22 (1 + 2^-11)) |x c| + 2^-25 (1.0011) (|x| + |c|) + 2^-50,
+//   so <= 4.89e-4 S + 2.9836e-8 sqrt(d) (|x| + cmax) + d 2^-50; valid while
+//   every element is below 65520 in magnitude, which |x| <= 32768 and
+//   cmax <= 32768 ensure: beyond that the bound is NaN (the exact scan);
+//   the MFMA accumulation: M MFMAs in a chain (6 ceil(d / 32) bf16, 4 ceil(d
+//   / 32) fp16), each within 16 u (|C| + sum |p|) (v_mfma_f32_32x32x16_bf16
+//   and _f16 round each product to a grid relative to the largest term, then
+//   round the sum once; measured <= 5.9 u for both, with exponents spread
+//   over 2^-20 .. 2^20 and f16 subnormal inputs), so <= gamma(16 M) * 1.02 S
+//   (the passes' |products| sum to <= 1.02 S); underflow: (3d + M) 2^-124.
 // With edot_out, also the bound's dot term (unscaled, before the L2 key and
 // tag allowances): the part that rests on the split and the MFMA model.
 __device__ __forceinline__ float screen_bound(float xn, float cmax2, float cnmax, int d, bool l2,
-                                              bool bf3, bool tagged = false,
-                                              float* edot_out = nullptr) {
+                                              int kind, float* edot_out = nullptr) {
   const float u = 5.9604645e-08f;  // 2^-24
   const float du = (float)d * u;
   const float g = du / (1.0f - du);
@@ -101,7 +116,16 @@ __device__ __forceinline__ float screen_bound(float xn, float cmax2, float cnmax
   const float xa = sqrtf(xn + uf) * (1.0f + g), ca = sqrtf(cmax2 + uf) * (1.0f + g);
   const float S = xa * ca;
   float edot;
-  if (bf3) {
+  if (kind == BOUND_F16_TAGGED) {
+    const float m = (float)(4 * ((d + 31) / 32));  // MFMAs per dot
+    const float mu = 16.0f * m * u;
+    const float gm = mu / (1.0f - mu);
+    edot = (g + 1.02f * gm + 4.8900e-4f) * S                  // 2^-11 + 2^-22 (1 + 2^-11)
+           + 2.9836e-8f * sqrtf((float)d) * (xa + ca)         // 2^-25 (1.0011)
+           + (float)d * 8.8818e-16f                           // d 2^-50
+           + (float)(3 * d + (int)m) * 4.7019774e-38f;        // 2^-124
+    if (!(xa <= 32768.0f && ca <= 32768.0f)) edot = __builtin_nanf("");
+  } else if (kind != BOUND_F32) {
     const float m = (float)(6 * ((d + 31) / 32));  // MFMAs per dot
     const float mu = 16.0f * m * u;
     const float gm = mu / (1.0f - mu);
@@ -114,10 +138,11 @@ __device__ __forceinline__ float screen_bound(float xn, float cmax2, float cnmax
   }
   if (edot_out) *edot_out = edot;
   float e = l2 ? 2.0f * edot + 2.0f * u * (cnmax + 2.0f * S) : edot;
-  // Tagged keys (the single-tile large-tile screen) carry a 6-bit column tag
+  // Tagged keys (the single-tile large-tile screens) carry a 6-bit column tag
   // in their low mantissa bits: |tagged - key| <= 63 ulp < 2^-17 |key|, with
   // |key| <= S (IP) or cnmax + 2S (L2), plus 63 subnormal ulps (< 2^-143).
-  if (tagged) e += 7.63e-6f * (l2 ? cnmax + 2.0f * S : S) + 8.9e-44f;
+  if (kind == BOUND_BF16_TAGGED || kind == BOUND_F16_TAGGED)
+    e += 7.63e-6f * (l2 ? cnmax + 2.0f * S : S) + 8.9e-44f;
   return e * 1.125f;
 }
 
@@ -144,12 +169,13 @@ __device__ __forceinline__ void merge_parts(const Cand* c, int parts, float (&ke
 }
 
 // ---- emh_rescore.hip: merge, bound and re-score the screen's lists; xnorm[r]
-// is row lo + r's |x|^2 summed in any order (the bound's input).
+// is row lo + r's |x|^2 summed in any order (the bound's input); bound: the
+// screen's arithmetic (BoundKind).
 void launch_verify1(emh_ctx* c, const float* x, size_t nx, size_t d, const uint32_t* ids,
                     size_t lo, size_t n, const float* cents, const float* cnorm, size_t k, bool ip,
                     const Cand* cand, int parts, const float* xnorm, uint32_t* labels,
-                    float* scores, uint32_t* fb, bool tagged = false,
-                    const LabelTally* tally = nullptr, int L = L1);
+                    float* scores, uint32_t* fb, int bound, const LabelTally* tally = nullptr,
+                    int L = L1);
 // The kNN screen over split operands (emh_screen4kn.hip): whether it takes a
 // call, and the call's screen (candidate lists [m][parts][LK] and the queries'
 // |q|^2, in the context's scratch); returns the parts.

@@ -120,7 +120,7 @@ __global__ __launch_bounds__(UT) void k_update_small(
     float* __restrict__ acc, float* __restrict__ pos, float* __restrict__ usage, float alpha,
     float decay, int replace, float* __restrict__ norms, char* __restrict__ csplit,
     uint32_t* __restrict__ cpart, float* __restrict__ readout, uint32_t* __restrict__ tally,
-    uint32_t* __restrict__ small) {
+    uint32_t* __restrict__ small, int f16) {
   __shared__ __attribute__((aligned(16))) SmallLds L;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, nw = (int)(blockDim.x >> 6);
   const size_t j = blockIdx.x;
@@ -221,7 +221,7 @@ __global__ __launch_bounds__(UT) void k_update_small(
   // The halves, with the zero columns of the last slab.
   if (csplit && tid < (int)(((d + 31) & ~(size_t)31) / 4)) {
     uint2 h, l;
-    split_quad(v, h, l);  // zeros past d
+    split_quad(v, h, l, f16 != 0);  // zeros past d
     const size_t col = 4 * (size_t)tid;
     char* o = csplit + ((col >> 5) * k + j) * SLAB_BYTES + quad_hi_offset((int)(col & 31) >> 2);
     *reinterpret_cast<uint2*>(o) = h;
@@ -273,7 +273,7 @@ void launch_update_small(emh_ctx* c, const float* x, size_t nx, size_t d, const 
                          size_t lo, size_t hi, const uint32_t* labels, size_t k, uint32_t* counts,
                          uint32_t* tcnt, size_t ntcnt, float* acc, float* pos, float* usage,
                          float alpha, float decay, int replace, float* norms, void* csplit,
-                         uint32_t* cpart, float* readout, uint32_t* tally) {
+                         uint32_t* cpart, float* readout, uint32_t* tally, bool f16) {
   const size_t n = hi > lo ? hi - lo : 0;
   EMH_ENSURE(update_small(n, d, readout != nullptr) && tally && (norms != nullptr) != (readout != nullptr) &&
                  (!csplit || (norms && cpart)),
@@ -282,7 +282,8 @@ void launch_update_small(emh_ctx* c, const float* x, size_t nx, size_t d, const 
   const unsigned threads = (unsigned)std::max<size_t>(64, (d / 4 + 63) / 64 * 64);
   hipLaunchKernelGGL(k_update_small, dim3((unsigned)k), dim3(threads), 0, c->stream, x, nx, d, ids,
                      lo, hi, labels, k, counts, tcnt, tcnt ? ntcnt : 0, acc, pos, usage, alpha,
-                     decay, replace, norms, (char*)csplit, cpart, readout, tally, c->small);
+                     decay, replace, norms, (char*)csplit, cpart, readout, tally, c->small,
+                     f16 ? 1 : 0);
   EMH_HIP(hipGetLastError());
 }
 

@@ -80,7 +80,8 @@ int emh_read_u32(emh_ctx* ctx, const emh_buf* b, size_t lo, size_t hi, uint32_t*
  * device (at most 1 GB a device, released with the device's last context), and
  * the context that takes it waits on the device for the work the other
  * contexts had queued when it was freed; a buffer whose address went out
- * (emh_buf_ptr) is freed at once. */
+ * (emh_buf_ptr) is freed at once. The handle is gone after the call, also
+ * when it fails. */
 int emh_free(emh_ctx* ctx, emh_buf* b);
 /* A non-owning view of caller device memory (for example a torch tensor) as a
  * buffer; freeing the view does not free the memory. kind: 0 f32, 1 u32. */
@@ -359,6 +360,7 @@ float emh_host_numpy_sum_f32(const float* a, uint64_t n);
 #define EMH_SCREEN_SMALL_BF16 3  /* 128 x 128 bf16 screen (d % 4 != 0, and small kNN calls) */
 #define EMH_SCREEN_SMALL_F32 4   /* 128 x 128 f32 screen (emh_set_screen(ctx, 2)) */
 #define EMH_SCREEN_BIG_KNN 5     /* kNN: 128 x 256 bf16 screen over operands split once */
+#define EMH_SCREEN_BIG_F16 6     /* large-tile fp16 two-pass screen, one tile per part, tagged keys */
 typedef struct emh_screen_report {
   int variant;          /* EMH_SCREEN_* */
   int parts;            /* centroid (or data row) parts per row tile */
@@ -384,9 +386,12 @@ int emh_screen_margin_topk(emh_ctx* ctx, const emh_buf* queries, size_t m, const
  * (the screen's misses; EMEANS_CUDA_SCREEN_STATS analogue, emeans-cuda lib.rs:278-287). */
 uint64_t emh_fallback_rows(emh_ctx* ctx);
 /* Select the top-1 / top-k path: 1 = MFMA screen in bf16 three-pass arithmetic
- * + exact check (default), 2 = MFMA screen in f32 arithmetic + exact check,
- * 0 = exact kernels only (the reference "FP32 kernel alone", emeans-cuda
- * tests/contract.rs:27-37). Results are the same bits in every mode. */
+ * + exact check (default), 3 = the same with the split-operand top-1 screen
+ * (k_screen4) in fp16 two-pass arithmetic (a third fewer MFMAs, a bound 2.7
+ * times looser at d = 768; rows or centroids beyond |x| = 32768 take the exact
+ * scan), 2 = MFMA screen in f32 arithmetic + exact check, 0 = exact kernels
+ * only (the reference "FP32 kernel alone", emeans-cuda tests/contract.rs:27-37).
+ * Results are the same bits in every mode. */
 int emh_set_screen(emh_ctx* ctx, int on);
 /* Top-1 calls of at most `items` exact items (rows x max(ceil(k / 64), 2))
  * run the exact kernels alone even when the mode screens (default 4096: there

@@ -77,7 +77,7 @@ def _margin(dev, x, c, metric, tag, variant=None, ids=None):
     if variant is not None:
         assert r["variant"] == variant, (tag, r)
     if r["variant"] != "none":
-        assert r["pairs"] > 0, (tag, r)
+        assert r["pairs"] > 0 or "beyond range" in tag, (tag, r)
         assert r["over"] == 0 and r["max_ratio"] <= 1.0, (tag, r)
         assert r["max_dot_ratio"] <= 0.5, (tag, r)
     return r
@@ -106,7 +106,7 @@ def _crowds(k, d, seed):
     return c, groups
 
 
-@pytest.mark.parametrize("mode", [1, 2], ids=["bf16x3", "f32"])
+@pytest.mark.parametrize("mode", [1, 2, 3], ids=["bf16x3", "f32", "f16x2"])
 @pytest.mark.parametrize("metric", ["ip", "l2"])
 @pytest.mark.parametrize("d", [36, 99, 768, 2500])
 def test_margin_near_tie_crowds(dev, mode, metric, d):
@@ -117,7 +117,7 @@ def test_margin_near_tie_crowds(dev, mode, metric, d):
     x = (rows * scale[:, None]).astype(np.float32)
     dev.set_screen(mode)
     try:
-        want = "small_f32" if mode == 2 else "big_tagged"
+        want = {1: "big_tagged", 2: "small_f32", 3: "big_f16"}[mode]
         _margin(dev, x, c, metric, f"crowds d={d} {metric} screen={mode}", want)
     finally:
         dev.set_screen(1)
@@ -141,7 +141,7 @@ def test_margin_extreme_scales(dev, metric):
         cs = np.array([1e-18, 1.0, 1e15], np.float64)
     x = (base * xs[np.arange(n) % len(xs)][:, None]).astype(np.float32)
     c = (cb * cs[np.arange(k) % len(cs)][:, None]).astype(np.float32)
-    for mode in (1, 2):
+    for mode in (1, 2, 3):
         dev.set_screen(mode)
         try:
             _margin(dev, x, c, metric, f"extreme scales {metric} screen={mode}")
@@ -151,6 +151,52 @@ def test_margin_extreme_scales(dev, metric):
                 assert r["pairs"] == 0 and r["variant"] != "none", r
         finally:
             dev.set_screen(1)
+
+
+@pytest.mark.parametrize("metric", ["ip", "l2"])
+def test_margin_f16_ranges(dev, metric):
+    """The fp16 two-pass screen (mode 3) on rows from 1e-6 to 1e3 and
+    centroids from 1e-3 to 1e2 (32,768 rows x 512 centroids: the
+    split-operand screen): every entry within the bound. Centroids beyond
+    |c| = 32768 make the bound NaN, so no entry is measured and every row
+    takes the exact scan: the labels and scores still equal the exact
+    kernels' bits."""
+    n, d, k = 32768, 256, 512
+    base = _mix(n, d, 32, 0.3, True, 61)
+    cb = _mix(k, d, 32, 0.3, True, 62)
+    xs = np.array([1e-6, 1e-3, 1.0, 1e3], np.float64)
+    cs = np.array([1e-3, 1.0, 1e2], np.float64)
+    x = (base * xs[np.arange(n) % len(xs)][:, None]).astype(np.float32)
+    c = (cb * cs[np.arange(k) % len(cs)][:, None]).astype(np.float32)
+    dev.set_screen(3)
+    try:
+        _margin(dev, x, c, metric, f"f16 ranges {metric}", "big_f16")
+        big = (cb * np.float32(1e5)).astype(np.float32)
+        r = _margin(dev, x, big, metric, f"f16 beyond range {metric}", "big_f16")
+        assert r["pairs"] == 0, r
+        got = _top1(dev, x, big, metric)
+    finally:
+        dev.set_screen(1)
+    dev.set_screen(0)
+    try:
+        want = _top1(dev, x, big, metric)
+    finally:
+        dev.set_screen(1)
+    assert np.array_equal(got[0], want[0]) and got[1].tobytes() == want[1].tobytes()
+
+
+def _top1(dev, x, c, metric):
+    from emeans_amd import Mat, Select
+    n, d = x.shape
+    k = c.shape[0]
+    cb = dev.upload_f32(c)
+    cn = None
+    if metric == "l2":
+        cn = dev.zeros_f32(k)
+        dev.row_norms(cb, k, d, cn)
+    lab, sco = dev.zeros_u32(n), dev.zeros_f32(n)
+    dev.top1(Mat(dev.bind(x), d), Select(None, (0, n)), cb, cn, k, metric, lab, sco)
+    return dev.read_u32(lab), dev.read_f32(sco)
 
 
 def _args(dev, x, c):
@@ -208,6 +254,13 @@ def test_margin_headline_batch(dev):
     _margin(dev, x, c, "l2", "headline batch", "big_tagged", ids=ids)
     # An epoch's tail batch (3,392 rows: 56 large-tile blocks) takes the 128 x 128 screen.
     _margin(dev, x, c, "l2", "headline tail batch", "small_bf16", ids=ids[:3392].copy())
+    # The training run's arithmetic on the same batch: fp16 two-pass.
+    dev.set_screen(3)
+    try:
+        r = _margin(dev, x, c, "l2", "headline batch fp16", "big_f16", ids=ids)
+        assert r["pairs"] > 0, r
+    finally:
+        dev.set_screen(1)
 
 
 @pytest.mark.parametrize("mode", [1, 2], ids=["bf16x3", "f32"])

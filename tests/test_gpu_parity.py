@@ -24,7 +24,7 @@ def dev():
     d.close()
 
 
-@pytest.fixture(params=[1, 2], ids=["bf16x3", "f32"])
+@pytest.fixture(params=[1, 2, 3], ids=["bf16x3", "f32", "f16x2"])
 def screen(request, dev):
     """The MFMA screen's arithmetic: bf16 three-pass (default) or f32."""
     dev.set_screen(request.param)

@@ -112,26 +112,38 @@ def test_spherical_blobs_config(dev):
     assert a.mean_objective(True) == O.mean_objective(osc, True)
 
 
-def test_l2_gmm_mid_size(dev):
-    """A 40,000 x 256, k = 512 L2 run through the MFMA screen, with revival."""
+@pytest.mark.parametrize("mode", [1, 3], ids=["bf16x3", "f16x2"])
+def test_l2_gmm_mid_size(dev, mode):
+    """A 40,000 x 256, k = 512 L2 run through the MFMA screen, with revival,
+    in either arithmetic of the split-operand screen."""
     from emeans_amd import Config, synth
     x, _ = synth.gmm_zipf(n=40_000, d=256, comps=512, s=1.1, seed=5)
     cfg = Config(d=256, k=512, seed=11)
-    m, t, o = _train_both(dev, x, cfg)
+    dev.set_screen(mode)
+    try:
+        m, t, o = _train_both(dev, x, cfg)
+    finally:
+        dev.set_screen(1)
     _assert_same_run(m, t, o, "gmm-mid")
     assert sum(s.nsplit for s in m.iteration_stats()) > 0
 
 
-def test_headline_config_bit_exact(dev):
+@pytest.mark.parametrize("mode", [1, 3], ids=["bf16x3", "f16x2"])
+def test_headline_config_bit_exact(dev, mode):
     """200,000 x 768, k = 1024, exact FP32, L2, seed 0: the whole training run and
-    the final assignment equal the oracle's CPU run bit for bit."""
+    the final assignment equal the oracle's CPU run bit for bit (with either
+    arithmetic of the split-operand screen)."""
     from emeans_amd import Config, synth
     x, _ = synth.gmm_zipf(n=200_000, d=768, comps=1024, s=1.1, seed=0)
     cfg = Config(d=768, k=1024, seed=0)
-    m, t, o = _train_both(dev, x, cfg)
-    _assert_same_run(m, t, o, "headline")
-    _assert_same_model_file(dev, m, o, cfg, x)
-    a = m.assign(x)
+    dev.set_screen(mode)
+    try:
+        m, t, o = _train_both(dev, x, cfg)
+        _assert_same_run(m, t, o, "headline")
+        _assert_same_model_file(dev, m, o, cfg, x)
+        a = m.assign(x)
+    finally:
+        dev.set_screen(1)
     ol, osc = O.assign(x, 768, t.centroids, "l2")
     assert np.array_equal(a.labels, ol) and a.scores.tobytes() == osc.tobytes()
     assert a.mean_objective(False) == O.mean_objective(osc, False)
