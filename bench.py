@@ -59,12 +59,12 @@ METRIC = "train s & assign Mrows/s at 200k×768 k=1024 FP32; % of FP32 MFMA peak
 # profiles/k_screen_train_assign_200kx768_k1024_hbm_traffic.md): 89.2 MB per
 # 16,384-row batch launch (50.3 MB of split rows, the centroids once per XCD),
 # 335 MB per 65,536-row assignment chunk, 40 MB per epoch-tail batch (the
-# 128 x 128 screen). Measured at commit fbe7a7a; the run does not count it
+# 128 x 128 screen). Measured at commit 2b8405f; the run does not count it
 # again (counters need a profiler pass of their own), so the line names where
 # the figure comes from.
 SCREEN_TRAFFIC_BYTES = 95.6e6
 SCREEN_TRAFFIC_SOURCE = ("profiles/k_screen_train_assign_200kx768_k1024_hbm_traffic.md, "
-                         "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE at commit fbe7a7a")
+                         "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE at commit 2b8405f")
 # The screen's roofline times every PROFILE_EVERY-th launch of the timed steps
 # with HIP events (an event pair between two kernels costs the stream a few
 # microseconds; on every launch that was ~5 % of the headline step).
